@@ -1,0 +1,210 @@
+"""Benchmark: one scene-structured attention layer at the HunyuanVideo-1.5 480p 4-scene shape on one MI355X.
+
+Workload (one step = one pass of the hot path over one layer's synthetic inputs, already resident in HBM):
+4 scenes x 8 latent frames x 1590 tokens (30 x 53 latent grid) + 128 text tokens per scene, frame memory of 4 frames
+(representatives {0, 10, 21, 31}), shared frames at their adjacent positions (step >= shared_switch 5), scene RoPE
+over a 3D table, 16 heads x 128, bf16 q / k / v ~ N(0, 1). A step runs the layout kernel, the K/V pack-gather (RoPE
+on the keys), the varlen attention (RoPE on the Q load, output in place) and the text-padding write-back.
+
+value = useful attention TFLOP/s of the whole step (sum over scopes of 4 * Lq * Lk * H * D per step time).
+roofline: the attention kernel alone, timed with HIP events on the stream it runs on.
+cpu_baseline: the oracle's packing plus torch SDPA per scope in fp32 on the host cores, on a sample of heads.
+
+    python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--no-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = 'scene-attn TFLOP/s & % bf16 MFMA peak; ms/layer, HunyuanVideo-1.5 480p 4-scene'
+PEAK_BF16_TFLOPS = 2516.6      # MI355X dense bf16 MFMA (256 CU x 2.4 GHz x 4096 FLOP/clk)
+PEAK_HBM_GBS = 8000.0          # MI355X HBM3E
+
+LENGTHS, T, COUNTS, H, D = [8, 8, 8, 8], 1590, [128] * 4, 16, 128
+REPS = [0, 10, 21, 31]
+GRID = (32, 30, 53)
+
+
+def rope_table(F, Hh, Ww, D, theta=1e4):
+    """3D RoPE table (temporal / height / width pair groups, interleaved real pairs), fp32 [F*Hh*Ww, D]"""
+    import torch
+    f, y, x = torch.meshgrid(torch.arange(F), torch.arange(Hh), torch.arange(Ww), indexing='ij')
+    nt, ny = D // 8, 3 * D // 16
+    groups = [(f, nt), (y, ny), (x, D // 2 - nt - ny)]
+    ang = torch.cat([p.reshape(-1, 1).float() * (theta ** (-torch.arange(n).float() / n)) for p, n in groups], 1)
+    return ang.cos().repeat_interleave(2, 1).contiguous(), ang.sin().repeat_interleave(2, 1).contiguous()
+
+
+def extra_from_reps(lengths, reps):
+    out, lo = {}, 0
+    for j, n in enumerate(lengths):
+        out[j] = sorted(f for f in reps if not lo <= f < lo + n)
+        lo += n
+    return out
+
+
+def time_events(fn, reps, stream):
+    import torch
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record(stream)
+    for _ in range(reps):
+        fn()
+    b.record(stream)
+    b.synchronize()
+    return a.elapsed_time(b) / reps
+
+
+def cpu_baseline(heads=4, runs=3):
+    """the oracle's packing + per-scope fp32 SDPA on the host CPU, for `heads` of the 16 heads (median of runs)"""
+    import numpy as np
+    import torch
+    from oracle import attention as OA
+    from oracle import layout as OL
+    torch.set_num_threads(os.cpu_count())
+    lay = OL.SceneLayout(LENGTHS, halo=0, extra=extra_from_reps(LENGTHS, REPS))
+    S, Le = sum(LENGTHS) * T, sum(COUNTS)
+    g = torch.Generator().manual_seed(0)
+    q, k, v = (torch.randn(S, heads, D, generator=g) for _ in range(3))
+    eq, ek, ev = (torch.randn(Le, heads, D, generator=g) for _ in range(3))
+    cos, sin = rope_table(*GRID, D)
+
+    def run():
+        sc = OL.hunyuan_scopes(lay, T, COUNTS, Le, scene_rope=True, adjacent=True)
+        qp, kp, vp = OA.pack(sc, q, k, v, eq, ek, ev, cos, sin, mode='raw')
+        OA.packed_attention(qp, kp, vp, sc.cu_q, sc.cu_k)
+        return sc
+
+    sc = run()
+    ts = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        run()
+        ts.append(time.perf_counter() - t0)
+    t = float(np.median(ts))
+    flops = OA.useful_flops(sc.lq, sc.lk, heads, D)
+    cpu = platform.processor() or ''
+    try:
+        for line in open('/proc/cpuinfo'):
+            if line.startswith('model name'):
+                cpu = line.split(':', 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return dict(value=round(flops / t / 1e12, 4), unit='TFLOP/s', cores=torch.get_num_threads(), kind='port',
+                sample=f'full config-2 layer (layout, packing with RoPE, fp32 SDPA per scope) for {heads} of {H} heads; '
+                       f'median of {runs} runs after 1 warm-up: {t:.2f} s on {os.cpu_count()} logical CPUs ({cpu})',
+                seconds=round(t, 3))
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument('--gpus', type=int, default=1)
+    ap.add_argument('--steps', type=int, default=20)
+    ap.add_argument('--warmup', type=int, default=3)
+    ap.add_argument('--no-cpu', action='store_true', help='skip the CPU baseline leg')
+    ap.add_argument('--kernel-reps', type=int, default=10)
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get('WORLD_SIZE', '1')) != 1:
+        print('bench.py measures the single-GPU scene-attention path only: run it with --gpus 1 '
+              '(the multi-GPU K/V gathering / Ulysses paths are not part of this build)', file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from onereel_amd import scene
+    from onereel_amd.layout import SceneLayout
+
+    dev = torch.device('cuda:0')
+    torch.cuda.set_device(dev)
+    stream = torch.cuda.current_stream(dev)
+    lay = SceneLayout(LENGTHS, halo=0, extra=extra_from_reps(LENGTHS, REPS))
+    S, Le = sum(LENGTHS) * T, sum(COUNTS)
+    g = torch.Generator(device=dev).manual_seed(0)
+    q, k, v = (torch.randn(S, H, D, generator=g, device=dev).to(torch.bfloat16) for _ in range(3))
+    eq, ek, ev = (torch.randn(Le, H, D, generator=g, device=dev).to(torch.bfloat16) for _ in range(3))
+    cos, sin = (x.to(dev) for x in rope_table(*GRID, D))
+    plan = scene.ScopePlan(lay, T, COUNTS, Le, True, None, True, True, dev)
+    lq = [int(x) for x in (plan.cu_q[1:] - plan.cu_q[:-1]).tolist()]
+    lk = [int(x) for x in (plan.cu_k[1:] - plan.cu_k[:-1]).tolist()]
+    flops = float(sum(4.0 * a * b * H * D for a, b in zip(lq, lk)))
+    kbuf = torch.empty(plan.sum_k, H, D, dtype=torch.bfloat16, device=dev)
+    vbuf = torch.empty_like(kbuf)
+
+    def step():
+        plan.build()
+        return scene.scene_attention(plan, q, k, v, eq, ek, ev, cos, sin, mode='raw', fused=True, kbuf=kbuf,
+                                     vbuf=vbuf)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / args.steps
+
+    # per-kernel durations with HIP events on the launch stream
+    R = args.kernel_reps
+    ov = torch.empty_like(q)
+    ot = torch.empty(Le, H, D, dtype=torch.bfloat16, device=dev)
+    ws = plan.workspace(H, D)
+    attn = lambda: scene.varlen(q, kbuf, vbuf, plan.cu_q, plan.cu_k, plan.max_q, plan.max_k, out=ov,
+                                seg_q_src=plan.seg_q_src, q_text=eq, o_text=ot, n_q_video=plan.n_video,
+                                q_rope=plan.q_rope, cos=cos, sin=sin, sum_q=plan.sum_q, workspace=ws)
+    pack = lambda: scene.pack_rows(plan, k, ek, 'k', out=kbuf, b_video=v, b_text=ev, b_out=vbuf, cos=cos, sin=sin,
+                                   mode='raw')
+    qpk = torch.empty(plan.sum_q, H, D, dtype=torch.bfloat16, device=dev)
+    scat = lambda: scene.scatter(plan, qpk, ov, ot)
+    attn()
+    pack()
+    scat()
+    torch.cuda.synchronize()
+    t_attn = time_events(attn, R, stream)
+    t_pack = time_events(pack, R, stream)
+    t_layout = time_events(plan.build, R, stream)
+    t_scat = time_events(scat, R, stream)
+    row = H * D * 2
+    pack_bytes = 2 * 2 * plan.sum_k * row            # K and V rows read + written
+    scat_bytes = 2 * plan.sum_q * row                # packed rows read + written
+    kernels = {
+        'attention': dict(ms=round(t_attn, 4), tflops=round(flops / t_attn / 1e9, 1),
+                          frac_bf16_peak=round(flops / t_attn / 1e9 / PEAK_BF16_TFLOPS, 4)),
+        'pack_gather_kv': dict(ms=round(t_pack, 4), gbs=round(pack_bytes / t_pack / 1e6, 1),
+                               frac_hbm_peak=round(pack_bytes / t_pack / 1e6 / PEAK_HBM_GBS, 4), bytes=pack_bytes),
+        'layout': dict(us=round(t_layout * 1e3, 2), gbs=round(plan.index_bytes() / t_layout / 1e6, 1),
+                       bytes=plan.index_bytes()),
+        'scatter': dict(ms=round(t_scat, 4), gbs=round(scat_bytes / t_scat / 1e6, 1),
+                        frac_hbm_peak=round(scat_bytes / t_scat / 1e6 / PEAK_HBM_GBS, 4), bytes=scat_bytes),
+    }
+    traffic = None
+    tf = ROOT / 'profiles' / 'attention_traffic.json'
+    if tf.exists():
+        traffic = json.loads(tf.read_text()).get('hbm_bytes_per_launch')
+    value = flops / (ms * 1e-3) / 1e12
+    out = dict(metric=METRIC, value=round(value, 2), unit='TFLOP/s', n_gpus=1, steps=args.steps, warmup=args.warmup,
+               ms_per_step=round(ms, 4), higher_is_better=True, scaling='weak', vs_baseline=None, dtype='bf16',
+               data='synthetic',
+               config=dict(workload='hunyuan15-480p-4scene-scene-attention-layer', scenes=4, frames_per_scene=8,
+                           tokens_per_frame=T, text_per_scene=128, frame_memory=4, shared_pos='adjacent',
+                           scene_rope=True, heads=H, head_dim=D, sum_q=plan.sum_q, sum_k=plan.sum_k,
+                           useful_flop_per_step=flops, frac_bf16_peak_step=round(value / PEAK_BF16_TFLOPS, 4)),
+               roofline=dict(bound='mfma', achieved=round(flops / t_attn / 1e9, 1), peak=PEAK_BF16_TFLOPS,
+                             unit='TFLOP/s', frac=round(flops / t_attn / 1e9 / PEAK_BF16_TFLOPS, 4), traffic=traffic,
+                             kernel='attn_kernel<128> (+ its one-block planner, a few us)'),
+               kernels=kernels)
+    if not args.no_cpu:
+        out['cpu_baseline'] = cpu_baseline()
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == '__main__':
+    main()

@@ -1,0 +1,164 @@
+/*
+ * onereel_hip.h: C ABI of libonereel_hip.so, the MI355X (gfx950) scene-structured attention hot path.
+ *
+ * One DiT attention layer of OneReel's scene attention on one GPU runs as:
+ *   or_layout_build   scope layout on the device: cu_seqlens, per-row gather indices and scene-RoPE rows
+ *   or_pack_gather    K/V (or Q) rows of every scope packed densely, RoPE applied on the way
+ *   or_varlen_fwd     packed varlen attention (bf16 MFMA), optional RoPE on the Q load, optional in-place Q / O
+ *   or_scatter        packed output rows written back to token order, text padding rows zeroed
+ *
+ * Conventions: every tensor is caller-owned device memory passed as a raw pointer; rows are [row][head][dim] with a
+ * row stride in elements; bf16 is IEEE bfloat16 stored as uint16_t; index arrays are int32. Every launch goes on the
+ * given stream (a hipStream_t, NULL = the null stream) and nothing synchronises the device. Entry points return 0 on
+ * success and a negative code on a bad argument (-1) or a HIP error (-2); or_last_error() returns the message of the
+ * calling thread's last failure. The library allocates no device memory: or_varlen_fwd takes a caller workspace of
+ * or_varlen_workspace_size() bytes.
+ *
+ * Row space of the layout's index arrays: the virtual concatenation [video tokens ; text rows]. A video token row is
+ * frame * T + spatial (frame-major, F*T rows); text row t of the valid-first text sequence is encoded as F*T + t.
+ */
+#ifndef ONEREEL_HIP_H
+#define ONEREEL_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define OR_MAX_SCENES 64
+#define OR_MAX_EXTRA 512
+
+/* Scene layout of one request, host memory. Mirrors SceneLayout(lengths, halo, sides, extra)
+ * (src/onereel/layout.py:10-22) plus the scope options of the HunyuanVideo-1.5 processor: text counts per sentence
+ * (Context.counts / text_ranges, src/onereel/models/hunyuan15.py:64,87-89), scene_rope / rope_lengths (:47-48) and
+ * shared_pos resolved for the current step (:162: 'adjacent', or 'switch' at step >= shared_switch). */
+typedef struct or_layout_desc {
+  int32_t n_scenes;                      /* 1..OR_MAX_SCENES */
+  int32_t T;                             /* video tokens per latent frame */
+  int32_t halo;                          /* halo frames per neighbouring side */
+  int32_t sides;                         /* 0 'adj', 1 'prev', 2 'next' */
+  int32_t with_text;                     /* 1: joint scopes V_j, T_j (hunyuan15.py:153-170); 0: video-only scopes
+                                            (wan.py:113-119) */
+  int32_t scene_rope;                    /* temporal RoPE index restarts at every scene (+1 after scene 0) */
+  int32_t adjacent;                      /* shared frames' keys at their adjacent positions (_move_shared) */
+  int32_t n_rope_lengths;                /* 0: the scene lengths; else the rope_lengths entries */
+  int32_t text_rows;                     /* Le: rows of the text q/k/v (valid tokens first, padding after) */
+  int32_t lengths[OR_MAX_SCENES];        /* latent frames per scene, each > 0 */
+  int32_t rope_lengths[OR_MAX_SCENES];
+  int32_t counts[OR_MAX_SCENES];         /* valid text tokens of sentence j */
+  int32_t extra_ptr[OR_MAX_SCENES + 1];  /* CSR of SceneLayout.extra: frames extra[extra_ptr[j] .. extra_ptr[j+1]) */
+  int32_t extra[OR_MAX_EXTRA];
+} or_layout_desc;
+
+/* Sizes of a layout, computed on the host from the descriptor (validates it). */
+typedef struct or_layout_sizes {
+  int64_t n_seg;       /* 2 * n_scenes with text, n_scenes without */
+  int64_t sum_q;       /* packed query rows */
+  int64_t sum_k;       /* packed key / value rows */
+  int64_t max_q;
+  int64_t max_k;
+  int64_t n_video;     /* F * T */
+  int64_t max_rope_row;/* largest rotary-table row any index array names (-1 if none) */
+} or_layout_sizes;
+
+/* Outputs of or_layout_build, caller-allocated int32 device arrays; any pointer may be NULL to skip it. */
+typedef struct or_layout_out {
+  int32_t* cu_q;       /* [n_seg + 1] */
+  int32_t* cu_k;       /* [n_seg + 1] */
+  int32_t* seg_q_src;  /* [n_seg] source row of the segment's first query (its queries are contiguous there) */
+  int32_t* q_src;      /* [sum_q] query row of every packed query (= the row its output is written back to) */
+  int32_t* q_rope;     /* [sum_q] rotary-table row of a raw (unrotated) query, -1 for text rows */
+  int32_t* k_src;      /* [sum_k] key / value row of every packed key */
+  int32_t* k_rope;     /* [sum_k] rotary-table row of a raw key: own frames at their (scene) position, shared frames
+                          at their adjacent position when moved, else their own; -1 for text rows */
+  int32_t* k_move_a;   /* [sum_k] already-rotated keys: _move_shared's inverse-rotation row a*T+s, -1 if not moved */
+  int32_t* k_move_b;   /* [sum_k] already-rotated keys: _move_shared's rotation row (a+d)*T+s, -1 if not moved */
+} or_layout_out;
+
+/* Replaces the host-side layout logic of SceneLayout.shared_frames / key_frames (src/onereel/layout.py:54-78),
+ * comm.runs / frame_tokens (src/onereel/parallel/comm.py:84-85,115-123) and the sizes of attention.packed's
+ * cu_seqlens (src/onereel/attention.py:28-29,67-70). Host only, no device work. */
+int or_layout_plan(const or_layout_desc* desc, or_layout_sizes* sizes);
+
+/* Replaces _segments' scope order and rows (src/onereel/models/hunyuan15.py:153-170, :225 own_rows), cu_seqlens
+ * (src/onereel/attention.py:28-29), scene_rope_rows (hunyuan15.py:443-454), frame_position / adjacent_positions /
+ * shared_positions (hunyuan15.py:92-124) and _move_shared's table rows (hunyuan15.py:136-145). One kernel launch. */
+int or_layout_build(const or_layout_desc* desc, const or_layout_out* out, void* stream);
+
+/* Replaces the pack copies of Processor.scene / _segments / attention.packed (hunyuan15.py:164,168,225;
+ * attention.py:69) and, with rope, diffusers apply_rotary_emb on the keys (hunyuan15.py:189-190) and _move_shared
+ * (hunyuan15.py:148-150).
+ * For every packed row r: src = src_idx[r]; row = src < n_video ? a_video[src] : a_text[src - n_video] (and the same
+ * for b when b_out != NULL); a_out[r] = rotate(row), b_out[r] = row.
+ * rotate: rope_row[r] >= 0 and move_from == NULL: RoPE at table row rope_row[r];
+ *         move_from != NULL and move_from[r] >= 0: x = bf16(R(-move_from[r]) row), then bf16(R(rope_row[r]) x);
+ *         else: a copy. cos / sin: fp32 [n_rope_rows, D] (may be NULL when no row is rotated). */
+int or_pack_gather(const void* a_video, const void* a_text, const void* b_video, const void* b_text,
+                   int64_t src_row_stride, int64_t text_row_stride, int64_t n_video,
+                   const int32_t* src_idx, const int32_t* rope_row, const int32_t* move_from,
+                   const float* cos_table, const float* sin_table, int64_t n_rope_rows,
+                   int64_t n_rows, int32_t H, int32_t D, void* a_out, void* b_out, void* stream);
+
+/* Replaces the write-back of Processor.scene (hunyuan15.py:226,231-235) after attention.packed's split
+ * (attention.py:71): o_video[dst] / o_text[dst - n_video] = packed[r] for dst = dst_idx[r]; then the text rows
+ * [text_zero_from, text_rows) of o_text are zeroed (the padding rows of ot = eq.new_zeros). */
+int or_scatter(const void* packed, const int32_t* dst_idx, int64_t n_rows, int64_t n_video,
+               void* o_video, void* o_text, int64_t dst_row_stride, int64_t text_row_stride,
+               int64_t text_zero_from, int64_t text_rows, int32_t H, int32_t D, void* stream);
+
+/* Arguments of or_varlen_fwd. Segment s has queries [cu_q[s], cu_q[s+1]) of the packed query space and keys
+ * k[k_start .. k_start + k_len) with k_start = k_off ? k_off[s] : cu_k[s] and k_len = k_len ? k_len[s] :
+ * cu_k[s+1] - cu_k[s]. Query i of segment s is read from (and its output written to) source row
+ * (seg_q_src ? seg_q_src[s] : cu_q[s]) + i, a row of q / o when below n_q_video, else of q_text / o_text. */
+typedef struct or_varlen_args {
+  const void* q;            /* bf16 [.., H, D] rows with stride q_row_stride */
+  const void* q_text;       /* bf16 text query rows (may equal q when n_q_video covers every row) */
+  const void* k;            /* bf16 [Nk, H, D] */
+  const void* v;            /* bf16 [Nk, H, D] */
+  void* o;                  /* bf16 output rows, same row space as q */
+  void* o_text;
+  float* lse;               /* optional fp32 [H, sum_q]: natural-log log-sum-exp of the scaled scores */
+  const int32_t* cu_q;      /* [n_seg + 1] */
+  const int32_t* cu_k;      /* [n_seg + 1] or NULL with k_off and k_len */
+  const int32_t* k_off;     /* optional [n_seg] */
+  const int32_t* k_len;     /* optional [n_seg] (seqused_k) */
+  const int32_t* seg_q_src; /* optional [n_seg] */
+  const int32_t* q_rope;    /* optional [sum_q] rotary-table row per packed query (-1: none) */
+  const float* cos_table;   /* fp32 [n_rope_rows, D] when q_rope != NULL */
+  const float* sin_table;
+  int64_t n_rope_rows;
+  int64_t n_q_video;
+  int64_t q_row_stride;     /* elements between consecutive rows of q / q_text */
+  int64_t k_row_stride;     /* of k and v */
+  int64_t o_row_stride;     /* of o / o_text */
+  int32_t n_seg;
+  int32_t sum_q;
+  int32_t max_q;
+  int32_t max_k;
+  int32_t H;
+  int32_t D;                /* 64 or 128 */
+  float scale;              /* softmax scale, D^-0.5 in the reference */
+  void* workspace;          /* device scratch of or_varlen_workspace_size() bytes */
+  int64_t workspace_bytes;
+} or_varlen_args;
+
+/* Bytes of device workspace or_varlen_fwd needs for this many segments, packed queries and heads. */
+int64_t or_varlen_workspace_size(int32_t n_seg, int32_t sum_q, int32_t H, int32_t D);
+
+/* Replaces attention.varlen / flash_attn_varlen_func (src/onereel/attention.py:39-43), varlen_lse (:46-53) and
+ * overlapping_ranges' FA3 call with seqused_k (:78-83): non-causal softmax(q k^T * scale) v per segment, bf16 in and
+ * out, fp32 accumulation. Two launches: a tile planner and the attention kernel. */
+int or_varlen_fwd(const or_varlen_args* args, void* stream);
+
+/* Message of the calling thread's last failed call ("" if none). */
+const char* or_last_error(void);
+
+/* Library version string. */
+const char* or_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ONEREEL_HIP_H */

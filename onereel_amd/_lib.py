@@ -1,0 +1,96 @@
+"""ctypes binding of libonereel_hip.so (declared in include/onereel_hip.h).
+
+torch is imported first so that the library binds to the HIP runtime torch already loaded (one runtime per process;
+torch's streams are then valid handles for the library). There is no fallback: without the built library every entry
+point raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+
+import torch  # noqa: F401  (loads the HIP runtime the library binds to)
+
+LIB_PATH = Path(os.environ.get('ONEREEL_HIP_LIB', Path(__file__).resolve().parent / 'libonereel_hip.so'))
+
+OR_MAX_SCENES = 64
+OR_MAX_EXTRA = 512
+
+i32, i64, vp = ctypes.c_int32, ctypes.c_int64, ctypes.c_void_p
+
+
+class LayoutDesc(ctypes.Structure):
+    _fields_ = [('n_scenes', i32), ('T', i32), ('halo', i32), ('sides', i32), ('with_text', i32),
+                ('scene_rope', i32), ('adjacent', i32), ('n_rope_lengths', i32), ('text_rows', i32),
+                ('lengths', i32 * OR_MAX_SCENES), ('rope_lengths', i32 * OR_MAX_SCENES),
+                ('counts', i32 * OR_MAX_SCENES), ('extra_ptr', i32 * (OR_MAX_SCENES + 1)),
+                ('extra', i32 * OR_MAX_EXTRA)]
+
+
+class LayoutSizes(ctypes.Structure):
+    _fields_ = [('n_seg', i64), ('sum_q', i64), ('sum_k', i64), ('max_q', i64), ('max_k', i64), ('n_video', i64),
+                ('max_rope_row', i64)]
+
+
+class LayoutOut(ctypes.Structure):
+    _fields_ = [(n, vp) for n in ('cu_q', 'cu_k', 'seg_q_src', 'q_src', 'q_rope', 'k_src', 'k_rope', 'k_move_a',
+                                  'k_move_b')]
+
+
+class VarlenArgs(ctypes.Structure):
+    _fields_ = [('q', vp), ('q_text', vp), ('k', vp), ('v', vp), ('o', vp), ('o_text', vp), ('lse', vp),
+                ('cu_q', vp), ('cu_k', vp), ('k_off', vp), ('k_len', vp), ('seg_q_src', vp), ('q_rope', vp),
+                ('cos_table', vp), ('sin_table', vp), ('n_rope_rows', i64), ('n_q_video', i64),
+                ('q_row_stride', i64), ('k_row_stride', i64), ('o_row_stride', i64), ('n_seg', i32), ('sum_q', i32),
+                ('max_q', i32), ('max_k', i32), ('H', i32), ('D', i32), ('scale', ctypes.c_float),
+                ('workspace', vp), ('workspace_bytes', i64)]
+
+
+# every exported symbol with its ctypes signature: include/onereel_hip.h
+SIGNATURES = {
+    'or_layout_plan': (i32, [ctypes.POINTER(LayoutDesc), ctypes.POINTER(LayoutSizes)]),
+    'or_layout_build': (i32, [ctypes.POINTER(LayoutDesc), ctypes.POINTER(LayoutOut), vp]),
+    'or_pack_gather': (i32, [vp, vp, vp, vp, i64, i64, i64, vp, vp, vp, vp, vp, i64, i64, i32, i32, vp, vp, vp]),
+    'or_scatter': (i32, [vp, vp, i64, i64, vp, vp, i64, i64, i64, i64, i32, i32, vp]),
+    'or_varlen_workspace_size': (i64, [i32, i32, i32, i32]),
+    'or_varlen_fwd': (i32, [ctypes.POINTER(VarlenArgs), vp]),
+    'or_last_error': (ctypes.c_char_p, []),
+    'or_version': (ctypes.c_char_p, []),
+}
+
+_lib = None
+
+
+class HipPathError(RuntimeError):
+    """a library call failed (bad argument or HIP error); the message is the library's"""
+
+
+def lib():
+    """the loaded library; raises if it was not built (no CPU fallback exists)"""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(f'{LIB_PATH} is not built: run python -m onereel_amd.build (the HIP path has no '
+                               f'fallback)')
+        h = ctypes.CDLL(str(LIB_PATH))
+        for name, (res, args) in SIGNATURES.items():
+            f = getattr(h, name)
+            f.restype, f.argtypes = res, args
+        _lib = h
+    return _lib
+
+
+def check(rc: int, what: str):
+    if rc != 0:
+        msg = lib().or_last_error().decode()
+        raise HipPathError(f'{what} failed ({rc}): {msg}')
+
+
+def ptr(t):
+    """device pointer of a tensor, or None"""
+    return None if t is None else t.data_ptr()
+
+
+def stream_handle(device=None):
+    return torch.cuda.current_stream(device).cuda_stream

@@ -1,0 +1,58 @@
+"""Build libonereel_hip.so (gfx950) in-tree with hipcc: one object per HIP source, then one shared library.
+
+    python -m onereel_amd.build            # or __graft_entry__.build()
+"""
+from __future__ import annotations
+
+import os
+import subprocess
+import sys
+from concurrent.futures import ThreadPoolExecutor
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+CSRC = PKG / 'csrc'
+INCLUDE = PKG.parent / 'include'
+LIB = PKG / 'libonereel_hip.so'
+OBJ = PKG / 'csrc' / '_obj'
+SOURCES = ['layout.hip', 'gather.hip', 'attention.hip']
+ARCH = os.environ.get('ONEREEL_ARCH', 'gfx950')
+
+HIPCC = os.environ.get('HIPCC', '/opt/rocm/bin/hipcc')
+FLAGS = [f'--offload-arch={ARCH}', '-O3', '-std=c++17', '-fPIC', '-I', str(INCLUDE),
+         # packed-FP32 VALU ops are disabled on purpose; hipcc's host pass warns that it does not know the feature
+         '-Xclang', '-target-feature', '-Xclang', '-packed-fp32-ops',
+         '-Wno-unused-result', '-munsafe-fp-atomics']
+
+
+def _run(cmd):
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    noise = "'-packed-fp32-ops' is not a recognized feature"
+    err = '\n'.join(l for l in r.stderr.splitlines() if noise not in l)
+    if r.returncode != 0:
+        raise RuntimeError(f'build failed: {" ".join(cmd)}\n{err}')
+    return err
+
+
+def build(verbose: bool = False) -> Path:
+    OBJ.mkdir(exist_ok=True)
+    objs = [OBJ / (s.replace('.hip', '.o')) for s in SOURCES]
+
+    def one(src_obj):
+        src, obj = src_obj
+        return _run([HIPCC, *FLAGS, '-c', str(CSRC / src), '-o', str(obj)])
+
+    with ThreadPoolExecutor(max_workers=len(SOURCES)) as ex:
+        logs = list(ex.map(one, zip(SOURCES, objs)))
+    tmp = LIB.with_suffix('.so.tmp')
+    logs.append(_run([HIPCC, f'--offload-arch={ARCH}', '-shared', '-fPIC', *map(str, objs), '-o', str(tmp)]))
+    os.replace(tmp, LIB)
+    if verbose:
+        for l in logs:
+            if l.strip():
+                print(l, file=sys.stderr)
+    return LIB
+
+
+if __name__ == '__main__':
+    print(build(verbose=True))

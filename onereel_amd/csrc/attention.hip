@@ -1,0 +1,530 @@
+// Packed varlen attention forward for gfx950: non-causal softmax(q k^T * scale) v per segment, bf16 in and out, fp32
+// accumulation. Replaces flash_attn_varlen_func as src/onereel/attention.py:39-53,78-83 calls it.
+//
+// Design (CDNA4, 64-wide wavefronts, v_mfma_f32_32x32x16_bf16):
+// - A work item is (segment, head, 256-query tile); a block of 4 wavefronts takes one item at a time from a queue
+//   (persistent blocks, one per CU). A planner kernel orders the items longest segment first (LPT over the uneven
+//   scene lengths) and, inside a segment, head-major so that consecutive items share K/V in L2.
+// - Each wavefront owns 64 queries. It computes S^T = K Q^T (keys on the MFMA rows, queries on the columns), so a
+//   lane holds one query's scores: the running max, the exponentials and the row sum are in-lane except one
+//   exchange with lane ^ 32. The K rows of the A operand are permuted (pi below) so that lane half h holds keys
+//   16h .. 16h+15 of each 32-key block in register order, which makes P^T usable as the B operand of O^T = V^T P^T
+//   and makes the V^T operand 8 consecutive keys: one 16-byte LDS read from a transposed V tile.
+// - K and V^T tiles of 64 keys are double-buffered in LDS (XOR-swizzled 16-byte chunks); the next tile's global
+//   loads are in flight while the current tile computes.
+// - Softmax in base 2 with the scale folded into one FMA: p = 2^(s*c - m*c), c = scale * log2(e).
+// - Optional RoPE on the Q load (table row per packed query), with the rounding of diffusers apply_rotary_emb.
+#include <math.h>
+
+#include "common.h"
+
+namespace onereel {
+
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int kThreads = 256;   // 4 wavefronts
+constexpr int kBQ = 256;        // queries per work item
+constexpr int kWQ = 64;         // queries per wavefront
+constexpr int kBK = 64;         // keys per tile
+constexpr int kWsHeader = 64;   // int32 words before the item list
+constexpr int kPlanThreads = 1024;
+constexpr int kMaxPlanSeg = 4096;
+
+struct AttnArgs {
+  const uint16_t* q;
+  const uint16_t* q_text;
+  const uint16_t* k;
+  const uint16_t* v;
+  uint16_t* o;
+  uint16_t* o_text;
+  float* lse;
+  const int32_t* cu_q;
+  const int32_t* cu_k;
+  const int32_t* k_off;
+  const int32_t* k_len;
+  const int32_t* seg_q_src;
+  const int32_t* q_rope;
+  const float* cos_t;
+  const float* sin_t;
+  int64_t n_rope_rows;
+  int64_t n_q_video;
+  int64_t qs, ks, os;   // row strides (elements)
+  int32_t sum_q, H;
+  float c;              // scale * log2(e)
+  float scale;
+};
+
+__device__ __forceinline__ int seg_k_begin(const AttnArgs& a, int s) { return a.k_off ? a.k_off[s] : a.cu_k[s]; }
+__device__ __forceinline__ int seg_k_len(const AttnArgs& a, int s) {
+  return a.k_len ? a.k_len[s] : a.cu_k[s + 1] - a.cu_k[s];
+}
+
+// A-operand row permutation of the S^T MFMA: row i = 8g + 4h + c reads key 16h + 4g + c
+__device__ __forceinline__ int pi32(int i) { return ((i >> 2) & 1) * 16 + (i >> 3) * 4 + (i & 3); }
+
+// 16-byte chunk swizzles: K tile rows of CH chunks; V^T rows of 8 chunks (64 keys)
+template <int CH>
+__device__ __forceinline__ int swz_k(int r) {
+  return ((r & 3) | (((r >> 4) & 1) << 2) | (((r >> 2) & 1) << 3)) & (CH - 1);
+}
+__device__ __forceinline__ int swz_v(int d) { return (d + (d >> 3)) & 7; }
+
+// ------------------------------------------------------------------------------------------------------------------
+// planner: one block. Items sorted by segment key count (descending), then segment; per segment head-major.
+__device__ inline int plan_upper_bound(const int* a, int n, int x) {
+  int lo = 0, hi = n;
+  while (lo < hi) {
+    int mid = (lo + hi) >> 1;
+    if (a[mid] <= x) lo = mid + 1;
+    else hi = mid;
+  }
+  return lo;
+}
+
+__global__ __launch_bounds__(kPlanThreads) void plan_kernel(const int32_t* cu_q, const int32_t* cu_k,
+                                                            const int32_t* k_len, int n_seg, int H, int max_items,
+                                                            int32_t* ws) {
+  __shared__ unsigned long long key[kMaxPlanSeg];
+  __shared__ int off[kMaxPlanSeg + 1];
+  __shared__ int part[kPlanThreads];
+  const int tid = threadIdx.x;
+  int n2 = 1;
+  while (n2 < n_seg) n2 <<= 1;
+  for (int i = tid; i < n2; i += kPlanThreads) {
+    if (i < n_seg) {
+      int lk = k_len ? k_len[i] : cu_k[i + 1] - cu_k[i];
+      lk = lk < 0 ? 0 : lk;
+      key[i] = ((unsigned long long)(0x7fffffffu - (unsigned)lk) << 32) | (unsigned)i;
+    } else {
+      key[i] = ~0ull;
+    }
+  }
+  __syncthreads();
+  for (int k = 2; k <= n2; k <<= 1) {
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      for (int i = tid; i < n2; i += kPlanThreads) {
+        int ixj = i ^ j;
+        if (ixj > i) {
+          unsigned long long x = key[i], y = key[ixj];
+          bool up = (i & k) == 0;
+          if ((x > y) == up) {
+            key[i] = y;
+            key[ixj] = x;
+          }
+        }
+      }
+      __syncthreads();
+    }
+  }
+  // items per sorted segment, exclusive scan (each thread owns a run of consecutive entries)
+  const int per = (n_seg + kPlanThreads - 1) / kPlanThreads;
+  int local = 0;
+  for (int e = 0; e < per; ++e) {
+    int i = tid * per + e;
+    if (i < n_seg) {
+      int s = (int)(key[i] & 0xffffffffu);
+      int lq = cu_q[s + 1] - cu_q[s];
+      int tiles = lq > 0 ? (lq + kBQ - 1) / kBQ : 0;
+      off[i] = tiles * H;
+      local += tiles * H;
+    }
+  }
+  part[tid] = local;
+  __syncthreads();
+  for (int o = 1; o < kPlanThreads; o <<= 1) {
+    int x = tid >= o ? part[tid - o] : 0;
+    __syncthreads();
+    part[tid] += x;
+    __syncthreads();
+  }
+  int run = part[tid] - local;
+  for (int e = 0; e < per; ++e) {
+    int i = tid * per + e;
+    if (i < n_seg) {
+      int c = off[i];
+      off[i] = run;
+      run += c;
+    }
+  }
+  if (tid == kPlanThreads - 1) off[n_seg] = part[tid];
+  __syncthreads();
+  int total = off[n_seg];
+  if (total > max_items) total = max_items;  // cannot happen with the host's bound; keeps writes in range
+  if (tid == 0) {
+    ws[0] = 0;
+    ws[1] = total;
+  }
+  for (int it = tid; it < total; it += kPlanThreads) {
+    int i = plan_upper_bound(off, n_seg + 1, it) - 1;
+    int s = (int)(key[i] & 0xffffffffu);
+    int lq = cu_q[s + 1] - cu_q[s];
+    int tiles = (lq + kBQ - 1) / kBQ;
+    int local_it = it - off[i];
+    int head = local_it / tiles, t = local_it - head * tiles;
+    ws[kWsHeader + 2 * it] = s;
+    ws[kWsHeader + 2 * it + 1] = (t << 8) | head;
+  }
+}
+
+// ------------------------------------------------------------------------------------------------------------------
+// attention
+
+template <int D>
+struct Tile {
+  static constexpr int CH = D / 8;              // 16-byte chunks per K row
+  static constexpr int KS = D / 16;             // MFMA k-steps of S^T
+  static constexpr int DB = D / 32;             // 32-row blocks of O^T
+  static constexpr int KCH = kBK * CH / kThreads;        // K chunks staged per thread
+  static constexpr int VP = D / 2;                       // V column pairs
+  static constexpr int VKG = kThreads / VP;              // key groups of the V staging
+  static constexpr int VKEYS = kBK / VKG;                // keys per thread in the V staging
+};
+
+template <int D>
+struct Smem {
+  uint16_t k[2][kBK * D];
+  uint16_t vt[2][D * kBK];
+  int item;
+};
+
+template <int D>
+__device__ __forceinline__ void stage_load(const AttnArgs& a, int head, int k_beg, int Lk, int t, u32x4* kreg,
+                                           uint32_t* vreg) {
+  using C = Tile<D>;
+  const int tid = threadIdx.x;
+#pragma unroll
+  for (int i = 0; i < C::KCH; ++i) {
+    const int c = tid + kThreads * i;
+    const int row = c / C::CH, col = c % C::CH;
+    int key = t * kBK + row;
+    key = key < Lk ? key : Lk - 1;
+    kreg[i] = *(const u32x4*)(a.k + (int64_t)(k_beg + key) * a.ks + head * D + col * 8);
+  }
+  const int dp = tid % C::VP, kg = tid / C::VP;
+#pragma unroll
+  for (int e = 0; e < C::VKEYS; ++e) {
+    int key = t * kBK + kg * C::VKEYS + e;
+    key = key < Lk ? key : Lk - 1;
+    vreg[e] = *(const uint32_t*)(a.v + (int64_t)(k_beg + key) * a.ks + head * D + 2 * dp);
+  }
+}
+
+template <int D>
+__device__ __forceinline__ void stage_store(Smem<D>& sm, int buf, const u32x4* kreg, const uint32_t* vreg) {
+  using C = Tile<D>;
+  const int tid = threadIdx.x;
+#pragma unroll
+  for (int i = 0; i < C::KCH; ++i) {
+    const int c = tid + kThreads * i;
+    const int row = c / C::CH, col = c % C::CH;
+    *(u32x4*)(&sm.k[buf][row * D + ((col ^ swz_k<C::CH>(row)) * 8)]) = kreg[i];
+  }
+  const int dp = tid % C::VP, kg = tid / C::VP;
+#pragma unroll
+  for (int ch = 0; ch < C::VKEYS / 8; ++ch) {
+    u32x4 ev, od;
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      const uint32_t x = vreg[ch * 8 + 2 * p], y = vreg[ch * 8 + 2 * p + 1];
+      ev[p] = (x & 0xffffu) | (y << 16);
+      od[p] = (x >> 16) | (y & 0xffff0000u);
+    }
+    const int chunk = (kg * C::VKEYS) / 8 + ch;
+    const int d0 = 2 * dp, d1 = 2 * dp + 1;
+    *(u32x4*)(&sm.vt[buf][d0 * kBK + ((chunk ^ swz_v(d0)) * 8)]) = ev;
+    *(u32x4*)(&sm.vt[buf][d1 * kBK + ((chunk ^ swz_v(d1)) * 8)]) = od;
+  }
+}
+
+__device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
+
+__device__ __forceinline__ bf16x8 pack_p8(const f32x16& p, int base) {
+  u32x4 r;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) r[i] = pack2(p[base + 2 * i], p[base + 2 * i + 1]);
+  return as_bf16x8(r);
+}
+
+template <int D>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))) void attn_kernel(AttnArgs a,
+                                                                                                  int32_t* ws) {
+  using C = Tile<D>;
+  __shared__ __attribute__((aligned(16))) Smem<D> sm;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int l32 = lane & 31, h = lane >> 5;
+  const float NEG_INF = -__builtin_inff();
+
+  for (;;) {
+    if (tid == 0) sm.item = atomicAdd(&ws[0], 1);
+    __syncthreads();
+    const int it = sm.item;
+    __syncthreads();
+    if (it >= ws[1]) break;
+    const int seg = ws[kWsHeader + 2 * it];
+    const int packed_ht = ws[kWsHeader + 2 * it + 1];
+    const int head = packed_ht & 255, qt = packed_ht >> 8;
+    const int q_beg = a.cu_q[seg];
+    const int Lq = a.cu_q[seg + 1] - q_beg;
+    const int k_beg = seg_k_begin(a, seg);
+    const int Lk = seg_k_len(a, seg);
+    const int q_src0 = a.seg_q_src ? a.seg_q_src[seg] : q_beg;
+    const int q0 = qt * kBQ + w * kWQ;
+    const bool active = q0 < Lq;
+
+    // Q operand (B of S^T): lane holds query l32 of block qb, dims 16*ks + 8h .. +7
+    bf16x8 qreg[2][C::KS];
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) {
+      int i = q0 + qb * 32 + l32;
+      i = i < Lq ? i : Lq - 1;
+      i = i < 0 ? 0 : i;
+      const int64_t row = q_src0 + i;
+      const uint16_t* qp = (row < a.n_q_video ? a.q + row * a.qs : a.q_text + (row - a.n_q_video) * a.qs) + head * D;
+      int rr = a.q_rope ? a.q_rope[q_beg + i] : -1;
+      if (rr >= a.n_rope_rows) rr = -1;
+#pragma unroll
+      for (int ks = 0; ks < C::KS; ++ks) {
+        const int d = 16 * ks + 8 * h;
+        u32x4 x = *(const u32x4*)(qp + d);
+        if (rr >= 0) x = rotate8(x, a.cos_t, a.sin_t, (int64_t)rr * D + d, 1.0f);
+        qreg[qb][ks] = as_bf16x8(x);
+      }
+    }
+
+    f32x16 acc[2][C::DB];
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+      for (int db = 0; db < C::DB; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[qb][db][r] = 0.0f;
+    float m[2] = {NEG_INF, NEG_INF}, lsum[2] = {0.0f, 0.0f};
+
+    const int n_tiles = (Lk + kBK - 1) / kBK;
+    u32x4 kreg[C::KCH];
+    uint32_t vreg[C::VKEYS];
+    if (n_tiles > 0) {
+      stage_load<D>(a, head, k_beg, Lk, 0, kreg, vreg);
+      stage_store<D>(sm, 0, kreg, vreg);
+    }
+    __syncthreads();
+
+    for (int t = 0; t < n_tiles; ++t) {
+      const int buf = t & 1;
+      const bool more = t + 1 < n_tiles;
+      if (more) stage_load<D>(a, head, k_beg, Lk, t + 1, kreg, vreg);
+      if (active) {
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+          // S^T for the 32 keys kb*32 + 16h + r of this tile (both query blocks share the K operand)
+          f32x16 s[2];
+#pragma unroll
+          for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) s[qb][r] = 0.0f;
+#pragma unroll
+          for (int ks = 0; ks < C::KS; ++ks) {
+            const int row = kb * 32 + pi32(l32);
+            const int col = 2 * ks + h;
+            const bf16x8 ka = *(const bf16x8*)(&sm.k[buf][row * D + ((col ^ swz_k<C::CH>(row)) * 8)]);
+            s[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka, qreg[0][ks], s[0], 0, 0, 0);
+            s[1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka, qreg[1][ks], s[1], 0, 0, 0);
+          }
+          if (t * kBK + kb * 32 + 32 > Lk) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              const bool bad = t * kBK + kb * 32 + 16 * h + r >= Lk;
+              s[0][r] = bad ? NEG_INF : s[0][r];
+              s[1][r] = bad ? NEG_INF : s[1][r];
+            }
+          }
+          bf16x8 pb[2][2];  // [half][qb]
+#pragma unroll
+          for (int qb = 0; qb < 2; ++qb) {
+            float mx = s[qb][0];
+#pragma unroll
+            for (int r = 1; r < 16; ++r) mx = fmaxf(mx, s[qb][r]);
+            mx = fmaxf(mx, __shfl_xor(mx, 32));
+            // lazy rescale: the running max moves only when some query of the wavefront gains more than 2^8
+            // (p stays <= 256 otherwise: exact enough in fp32 sums and bf16 operands)
+            if (__any((mx - m[qb]) * a.c > 8.0f)) {
+              const float m_new = fmaxf(m[qb], mx);
+              const float alpha = __builtin_amdgcn_exp2f((m[qb] - m_new) * a.c);
+              m[qb] = m_new;
+              lsum[qb] *= alpha;
+#pragma unroll
+              for (int db = 0; db < C::DB; ++db)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[qb][db][r] *= alpha;
+            }
+            const float mc = m[qb] * a.c;
+            float ls = 0.0f;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[qb][r], a.c, -mc));
+              s[qb][r] = p;
+              ls += p;
+            }
+            lsum[qb] += ls;
+            pb[0][qb] = pack_p8(s[qb], 0);
+            pb[1][qb] = pack_p8(s[qb], 8);
+          }
+          // O^T[db] += V^T[d = db*32 + l32][keys kb*32 + 16h + 8*half .. +7] P^T
+#pragma unroll
+          for (int half = 0; half < 2; ++half) {
+            const int chunk = 4 * kb + 2 * h + half;
+#pragma unroll
+            for (int db = 0; db < C::DB; ++db) {
+              const int d = db * 32 + l32;
+              const bf16x8 va = *(const bf16x8*)(&sm.vt[buf][d * kBK + ((chunk ^ swz_v(d)) * 8)]);
+              acc[0][db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pb[half][0], acc[0][db], 0, 0, 0);
+              acc[1][db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pb[half][1], acc[1][db], 0, 0, 0);
+            }
+          }
+        }
+      }
+      if (more) stage_store<D>(sm, buf ^ 1, kreg, vreg);
+      __syncthreads();
+    }
+
+    // epilogue: combine the lane pair's row sums, normalise, store 4 consecutive dims per (db, group)
+    if (active) {
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb) {
+        const float ltot = lsum[qb] + __shfl_xor(lsum[qb], 32);
+        const int i = q0 + qb * 32 + l32;
+        if (i < Lq) {
+          const float inv = n_tiles > 0 ? 1.0f / ltot : 0.0f;
+          const int64_t row = q_src0 + i;
+          uint16_t* op = (row < a.n_q_video ? a.o + row * a.os : a.o_text + (row - a.n_q_video) * a.os) + head * D;
+#pragma unroll
+          for (int db = 0; db < C::DB; ++db)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+              const int d = db * 32 + 8 * g + 4 * h;
+              uint32_t lo = pack2(acc[qb][db][4 * g] * inv, acc[qb][db][4 * g + 1] * inv);
+              uint32_t hi = pack2(acc[qb][db][4 * g + 2] * inv, acc[qb][db][4 * g + 3] * inv);
+              *(uint2*)(op + d) = make_uint2(lo, hi);
+            }
+          if (a.lse && h == 0)
+            a.lse[(int64_t)head * a.sum_q + q_beg + i] =
+                n_tiles > 0 ? m[qb] * a.scale + logf(ltot) : NEG_INF;
+        }
+      }
+    }
+  }
+}
+
+struct DevInfo {
+  int cus = 0;
+  int occ128 = 0, occ64 = 0;
+};
+
+int dev_info(DevInfo& info) {
+  static thread_local int cached_dev = -1;
+  static thread_local DevInfo cached;
+  int dev = 0;
+  if (int rc = check_hip(hipGetDevice(&dev), "hipGetDevice")) return rc;
+  if (dev != cached_dev) {
+    DevInfo di;
+    if (int rc = check_hip(hipDeviceGetAttribute(&di.cus, hipDeviceAttributeMultiprocessorCount, dev),
+                           "hipDeviceGetAttribute"))
+      return rc;
+    if (int rc = check_hip(hipOccupancyMaxActiveBlocksPerMultiprocessor(&di.occ128, attn_kernel<128>, kThreads, 0),
+                           "hipOccupancyMaxActiveBlocksPerMultiprocessor"))
+      return rc;
+    if (int rc = check_hip(hipOccupancyMaxActiveBlocksPerMultiprocessor(&di.occ64, attn_kernel<64>, kThreads, 0),
+                           "hipOccupancyMaxActiveBlocksPerMultiprocessor"))
+      return rc;
+    cached = di;
+    cached_dev = dev;
+  }
+  info = cached;
+  return 0;
+}
+
+int64_t max_items_of(int32_t n_seg, int32_t sum_q, int32_t H) {
+  return ((int64_t)(sum_q + kBQ - 1) / kBQ + n_seg) * H;
+}
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+}  // namespace
+}  // namespace onereel
+
+using namespace onereel;
+
+extern "C" int64_t or_varlen_workspace_size(int32_t n_seg, int32_t sum_q, int32_t H, int32_t D) {
+  (void)D;
+  if (n_seg < 0 || sum_q < 0 || H < 1) return -1;
+  return (int64_t)(kWsHeader + 2 * max_items_of(n_seg, sum_q, H)) * 4;
+}
+
+extern "C" int or_varlen_fwd(const or_varlen_args* p, void* stream) {
+  if (!p) return fail_arg("or_varlen_fwd: args is NULL");
+  const or_varlen_args& x = *p;
+  if (x.D != 64 && x.D != 128) return fail_arg("or_varlen_fwd: head_dim %d not supported (64 or 128)", x.D);
+  if (x.H < 1 || x.H > 256) return fail_arg("or_varlen_fwd: H=%d outside [1, 256]", x.H);
+  if (x.n_seg < 1 || x.n_seg > kMaxPlanSeg) return fail_arg("or_varlen_fwd: n_seg=%d outside [1, %d]", x.n_seg, kMaxPlanSeg);
+  if (x.sum_q < 0) return fail_arg("or_varlen_fwd: sum_q < 0");
+  if (!x.q || !x.k || !x.v || !x.o || !x.cu_q) return fail_arg("or_varlen_fwd: q, k, v, o and cu_q are required");
+  if (!x.cu_k && !(x.k_off && x.k_len)) return fail_arg("or_varlen_fwd: need cu_k, or k_off with k_len");
+  if (x.q_rope && (!x.cos_table || !x.sin_table || x.n_rope_rows < 1))
+    return fail_arg("or_varlen_fwd: q_rope needs cos / sin tables");
+  if (x.q_row_stride < (int64_t)x.H * x.D || x.k_row_stride < (int64_t)x.H * x.D || x.o_row_stride < (int64_t)x.H * x.D)
+    return fail_arg("or_varlen_fwd: row strides must cover H * D elements");
+  if (x.q_row_stride % 8 || x.k_row_stride % 8 || x.o_row_stride % 8 || !aligned16(x.q) || !aligned16(x.k) ||
+      !aligned16(x.v) || !aligned16(x.o) || (x.q_text && !aligned16(x.q_text)) || (x.o_text && !aligned16(x.o_text)))
+    return fail_arg("or_varlen_fwd: pointers must be 16-byte aligned and row strides multiples of 8 elements");
+  if (x.cos_table && (((uintptr_t)x.cos_table | (uintptr_t)x.sin_table) & 15u))
+    return fail_arg("or_varlen_fwd: rotary tables must be 16-byte aligned");
+  const int64_t need = or_varlen_workspace_size(x.n_seg, x.sum_q, x.H, x.D);
+  if (!x.workspace || x.workspace_bytes < need)
+    return fail_arg("or_varlen_fwd: workspace of %lld bytes needed", (long long)need);
+  if (x.sum_q == 0) return 0;
+  DevInfo di;
+  if (int rc = dev_info(di)) return rc;
+  const int occ = x.D == 128 ? di.occ128 : di.occ64;
+  if (occ < 1) return fail_arg("or_varlen_fwd: attention kernel cannot be resident (occupancy 0)");
+  const int64_t max_items = max_items_of(x.n_seg, x.sum_q, x.H);
+  int64_t grid = (int64_t)di.cus * occ;
+  if (grid > max_items) grid = max_items;
+  AttnArgs a;
+  a.q = (const uint16_t*)x.q;
+  a.q_text = (const uint16_t*)(x.q_text ? x.q_text : x.q);
+  a.k = (const uint16_t*)x.k;
+  a.v = (const uint16_t*)x.v;
+  a.o = (uint16_t*)x.o;
+  a.o_text = (uint16_t*)(x.o_text ? x.o_text : x.o);
+  a.lse = x.lse;
+  a.cu_q = x.cu_q;
+  a.cu_k = x.cu_k;
+  a.k_off = x.k_off;
+  a.k_len = x.k_len;
+  a.seg_q_src = x.seg_q_src;
+  a.q_rope = x.q_rope;
+  a.cos_t = x.cos_table;
+  a.sin_t = x.sin_table;
+  a.n_rope_rows = x.q_rope ? x.n_rope_rows : 0;
+  a.n_q_video = x.seg_q_src ? x.n_q_video : ((int64_t)1 << 62);
+  a.qs = x.q_row_stride;
+  a.ks = x.k_row_stride;
+  a.os = x.o_row_stride;
+  a.sum_q = x.sum_q;
+  a.H = x.H;
+  a.scale = x.scale;
+  a.c = x.scale * 1.4426950408889634f;
+  int32_t* ws = (int32_t*)x.workspace;
+  hipStream_t st = (hipStream_t)stream;
+  hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(kPlanThreads), 0, st, x.cu_q, x.k_off ? x.k_off : x.cu_k,
+                     x.k_len, x.n_seg, x.H, (int)max_items, ws);
+  if (int rc = check_hip(hipGetLastError(), "plan_kernel launch")) return rc;
+  if (x.D == 128)
+    hipLaunchKernelGGL(attn_kernel<128>, dim3((unsigned)grid), dim3(kThreads), 0, st, a, ws);
+  else
+    hipLaunchKernelGGL(attn_kernel<64>, dim3((unsigned)grid), dim3(kThreads), 0, st, a, ws);
+  return check_hip(hipGetLastError(), "attn_kernel launch");
+}

@@ -1,0 +1,178 @@
+// Shared helpers of libonereel_hip: error reporting, bf16 conversion and the per-scene layout logic that both the
+// host planner (or_layout_plan) and the device layout kernel run, so that sizes and indices come from one code.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/onereel_hip.h"
+
+namespace onereel {
+
+// ---------------------------------------------------------------------------------------------------------------
+// errors
+void set_error(const char* fmt, ...);
+int fail_arg(const char* fmt, ...);   // records the message, returns -1
+int check_hip(hipError_t e, const char* what);  // 0 or -2 with the HIP error string
+
+// ---------------------------------------------------------------------------------------------------------------
+// bf16 (stored as uint16_t); conversions round to nearest even, as torch's .to(torch.bfloat16) does
+__host__ __device__ inline float bf2f(uint16_t h) {
+  union { uint32_t u; float f; } x;
+  x.u = (uint32_t)h << 16;
+  return x.f;
+}
+
+__host__ __device__ inline uint16_t f2bf(float f) {
+  union { uint32_t u; float f; } x;
+  x.f = f;
+  uint32_t u = x.u;
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);  // NaN stays a quiet NaN
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// scene layout: derived per-scene quantities, computed identically on host and device
+constexpr int kMaxShared = 1024;  // shared-frame entries over all scenes (halo + extra)
+
+struct LayoutDerived {
+  int n_scenes, T, F, with_text, scene_rope, adjacent, text_rows, n_rope;
+  int lo[OR_MAX_SCENES], hi[OR_MAX_SCENES];        // frame range of scene j (layout.py:43-45)
+  int t0[OR_MAX_SCENES], t1[OR_MAX_SCENES];        // text range of sentence j (hunyuan15.py:87-89)
+  int rope_start[OR_MAX_SCENES + 1];               // frame boundaries of the rope scenes
+  int sh_ptr[OR_MAX_SCENES + 1];                   // shared frames of scene j: sh[sh_ptr[j] .. sh_ptr[j+1])
+  int sh[kMaxShared];
+  int sh_dst[kMaxShared];                          // their temporal position when moved (adjacent)
+};
+
+// temporal RoPE index of frame f (hunyuan15.py:103-113); -1 when f lies past the rope scenes (IndexError there)
+__host__ __device__ inline int frame_position(const LayoutDerived& L, int f) {
+  if (!L.scene_rope) return f;
+  for (int s = 0; s < L.n_rope; ++s) {
+    int start = L.rope_start[s];
+    if (f < L.rope_start[s + 1]) return f - start + (start > 0 ? 1 : 0);
+  }
+  return -1;
+}
+
+// rotary-table row of video token `tok` under the scene's RoPE (scene_rope_rows, hunyuan15.py:443-454)
+__host__ __device__ inline int rope_row_of_token(const LayoutDerived& L, int tok) {
+  if (!L.scene_rope) return tok;
+  int f = tok / L.T;
+  return frame_position(L, f) * L.T + (tok - f * L.T);
+}
+
+// shared frames of scene j (layout.py:54-69) written to out (capacity cap); returns their count or -1 on overflow.
+// Halo first (previous neighbour's last `halo` frames, then the next one's first), then sorted(extra[j]) keeping
+// frames outside the scene that are not in the halo list (repeats inside extra[j] are kept, as the reference does).
+__host__ __device__ inline int scene_shared_frames(const or_layout_desc& d, const int* lo, const int* hi, int j,
+                                                   int* out, int cap) {
+  int n = 0;
+  const int k = d.halo;
+  if (k > 0) {
+    if (j > 0 && (d.sides == 0 || d.sides == 1)) {
+      int a = hi[j - 1] - k;
+      if (a < lo[j - 1]) a = lo[j - 1];
+      for (int f = a; f < hi[j - 1]; ++f) {
+        if (n >= cap) return -1;
+        out[n++] = f;
+      }
+    }
+    if (j + 1 < d.n_scenes && (d.sides == 0 || d.sides == 2)) {
+      int b = lo[j + 1] + k;
+      if (b > hi[j + 1]) b = hi[j + 1];
+      for (int f = lo[j + 1]; f < b; ++f) {
+        if (n >= cap) return -1;
+        out[n++] = f;
+      }
+    }
+  }
+  const int nh = n;
+  const int e0 = d.extra_ptr[j], e1 = d.extra_ptr[j + 1];
+  // insertion of sorted(extra[j]) after the halo, filtered as it goes (filter does not depend on the order)
+  for (int e = e0; e < e1; ++e) {
+    const int f = d.extra[e];
+    if (lo[j] <= f && f < hi[j]) continue;
+    bool in_halo = false;
+    for (int i = 0; i < nh; ++i) in_halo |= (out[i] == f);
+    if (in_halo) continue;
+    if (n >= cap) return -1;
+    int p = n++;
+    while (p > nh && out[p - 1] > f) {
+      out[p] = out[p - 1];
+      --p;
+    }
+    out[p] = f;
+  }
+  return n;
+}
+
+// temporal position of shared frame f of scene j when moved (shared_positions / adjacent_positions,
+// hunyuan15.py:92-124). `sh` holds the scene's n shared frames. A dict keyed by frame keeps a repeated frame's last
+// index, so the count of entries <= f (of the relevant group) fixes the position.
+__host__ __device__ inline int shared_dst(const LayoutDerived& L, int j, const int* sh, int n, int f) {
+  const int lo = L.lo[j], hi = L.hi[j];
+  if (L.scene_rope) {
+    int last = -1;
+    for (int g = lo; g < hi; ++g) {
+      int p = frame_position(L, g);
+      if (p > last) last = p;
+    }
+    int c = 0;
+    for (int i = 0; i < n; ++i) c += (sh[i] <= f);
+    return last + c;
+  }
+  if (f < lo) {
+    int nb = 0, c = 0;
+    for (int i = 0; i < n; ++i) {
+      nb += (sh[i] < lo);
+      c += (sh[i] <= f);
+    }
+    return lo - nb + c - 1;
+  }
+  int c = 0;
+  for (int i = 0; i < n; ++i) c += (sh[i] >= hi && sh[i] <= f);
+  return hi + c - 1;
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// RoPE of 8 consecutive bf16 (diffusers apply_rotary_emb, interleaved pairs (2i, 2i+1)), bit-identical to torch's
+// (x.float() * cos + rot(x).float() * sin).to(bfloat16) with rot(x) = (-x_odd, x_even)
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// (x0, x1) -> (x0*c0 - x1*s0, x1*c1 + x0*s1), each product and the sum rounded to fp32 separately
+__device__ __forceinline__ void rot_pair(float x0, float x1, float c0, float c1, float s0, float s1, float& y0, float& y1) {
+#pragma clang fp contract(off)
+  float a = x0 * c0;
+  float b = (-x1) * s0;
+  float c = x1 * c1;
+  float e = x0 * s1;
+  y0 = a + b;
+  y1 = c + e;
+}
+
+__device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+  return (uint32_t)f2bf(lo) | ((uint32_t)f2bf(hi) << 16);
+}
+
+// 8 bf16 in `v` rotated with the table entries at element offset `off` of rows `row` (sign +1) or its inverse (-1)
+__device__ __forceinline__ u32x4 rotate8(u32x4 v, const float* __restrict__ cos_t, const float* __restrict__ sin_t,
+                                int64_t off, float sign) {
+  f32x4 c0 = *(const f32x4*)(cos_t + off), c1 = *(const f32x4*)(cos_t + off + 4);
+  f32x4 s0 = *(const f32x4*)(sin_t + off), s1 = *(const f32x4*)(sin_t + off + 4);
+  float c[8] = {c0[0], c0[1], c0[2], c0[3], c1[0], c1[1], c1[2], c1[3]};
+  float s[8] = {s0[0], s0[1], s0[2], s0[3], s1[0], s1[1], s1[2], s1[3]};
+  u32x4 r;
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    float x0 = bf2f((uint16_t)(v[p] & 0xffffu)), x1 = bf2f((uint16_t)(v[p] >> 16));
+    float y0, y1;
+    rot_pair(x0, x1, c[2 * p], c[2 * p + 1], sign * s[2 * p], sign * s[2 * p + 1], y0, y1);
+    r[p] = pack2(y0, y1);
+  }
+  return r;
+}
+
+}  // namespace onereel

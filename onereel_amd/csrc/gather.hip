@@ -1,0 +1,196 @@
+// K/V (or Q) pack-gather with RoPE on the way, and the scatter of packed outputs back to token order.
+//
+// Reference: the copies that pack each scope (src/onereel/models/hunyuan15.py:164,168,225; src/onereel/attention.py:69),
+// diffusers apply_rotary_emb on the video q / k rows (hunyuan15.py:189-190), _move_shared (hunyuan15.py:148-150), and
+// the write-back ov[lo:hi] = o / ot[t0:t1] = o after o.split (hunyuan15.py:226,231-235; attention.py:71).
+//
+// Both kernels are HBM-bound row copies: one wavefront moves one row of H*D bf16 (4 KiB at 16 x 128) per step in
+// 16-byte lanes, all loads of a row issued before its stores. The rotation is done in fp32 as two rounded products
+// and a rounded sum per element (no fused multiply-add), then rounded to bf16 to nearest even: the same bits as
+// torch's x.float() * cos + rot(x).float() * sin followed by .to(bfloat16).
+#include "common.h"
+
+namespace onereel {
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / 64;
+constexpr int kMaxChunksPerLane = 8;  // rows up to 64 lanes * 8 * 8 elements = 4096 elements (H*D)
+
+struct GatherArgs {
+  const uint16_t* a_video;
+  const uint16_t* a_text;
+  const uint16_t* b_video;
+  const uint16_t* b_text;
+  int64_t src_stride, text_stride, n_video;
+  const int32_t* src_idx;
+  const int32_t* rope_row;
+  const int32_t* move_from;
+  const float* cos_t;
+  const float* sin_t;
+  int64_t n_rope_rows;
+  int64_t n_rows;
+  int H, D;
+  uint16_t* a_out;
+  uint16_t* b_out;
+};
+
+__global__ __launch_bounds__(kThreads) void pack_gather_kernel(GatherArgs g) {
+  const int lane = threadIdx.x & 63;
+  const int64_t wave = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6);
+  const int64_t n_waves = (int64_t)gridDim.x * kWaves;
+  const int row_elems = g.H * g.D;
+  const int chunks = row_elems >> 3;
+  for (int64_t r = wave; r < g.n_rows; r += n_waves) {
+    const int src = g.src_idx[r];
+    const bool text = src >= g.n_video;
+    const int64_t off = text ? (int64_t)(src - g.n_video) * g.text_stride : (int64_t)src * g.src_stride;
+    const uint16_t* a = (text ? g.a_text : g.a_video) + off;
+    const uint16_t* b = g.b_out ? (text ? g.b_text : g.b_video) + off : nullptr;
+    // table rows outside the table leave the row unrotated (the host validates them; this only keeps reads in bounds)
+    int rope = g.rope_row ? g.rope_row[r] : -1;
+    int mfrom = g.move_from ? g.move_from[r] : -1;
+    if (rope >= g.n_rope_rows || mfrom >= g.n_rope_rows) rope = mfrom = -1;
+    u32x4 va[kMaxChunksPerLane], vb[kMaxChunksPerLane];
+#pragma unroll
+    for (int i = 0; i < kMaxChunksPerLane; ++i) {
+      const int c = lane + 64 * i;
+      if (c < chunks) {
+        va[i] = *(const u32x4*)(a + 8 * c);
+        if (b) vb[i] = *(const u32x4*)(b + 8 * c);
+      }
+    }
+    uint16_t* ao = g.a_out + r * (int64_t)row_elems;
+    uint16_t* bo = g.b_out ? g.b_out + r * (int64_t)row_elems : nullptr;
+#pragma unroll
+    for (int i = 0; i < kMaxChunksPerLane; ++i) {
+      const int c = lane + 64 * i;
+      if (c < chunks) {
+        u32x4 x = va[i];
+        const int d0 = (8 * c) % g.D;
+        if (g.move_from) {
+          if (mfrom >= 0 && rope >= 0) {
+            x = rotate8(x, g.cos_t, g.sin_t, (int64_t)mfrom * g.D + d0, -1.0f);
+            x = rotate8(x, g.cos_t, g.sin_t, (int64_t)rope * g.D + d0, 1.0f);
+          }
+        } else if (rope >= 0) {
+          x = rotate8(x, g.cos_t, g.sin_t, (int64_t)rope * g.D + d0, 1.0f);
+        }
+        *(u32x4*)(ao + 8 * c) = x;
+        if (bo) *(u32x4*)(bo + 8 * c) = vb[i];
+      }
+    }
+  }
+}
+
+struct ScatterArgs {
+  const uint16_t* packed;
+  const int32_t* dst_idx;
+  int64_t n_rows, n_video;
+  uint16_t* o_video;
+  uint16_t* o_text;
+  int64_t dst_stride, text_stride, zero_from, text_rows;
+  int H, D;
+};
+
+__global__ __launch_bounds__(kThreads) void scatter_kernel(ScatterArgs g) {
+  const int lane = threadIdx.x & 63;
+  const int64_t wave = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6);
+  const int64_t n_waves = (int64_t)gridDim.x * kWaves;
+  const int row_elems = g.H * g.D;
+  const int chunks = row_elems >> 3;
+  const int64_t n_zero = g.text_rows > g.zero_from ? g.text_rows - g.zero_from : 0;
+  for (int64_t r = wave; r < g.n_rows + n_zero; r += n_waves) {
+    if (r < g.n_rows) {
+      const int dst = g.dst_idx[r];
+      uint16_t* o = dst >= g.n_video ? g.o_text + (int64_t)(dst - g.n_video) * g.text_stride
+                                     : g.o_video + (int64_t)dst * g.dst_stride;
+      const uint16_t* p = g.packed + r * (int64_t)row_elems;
+      u32x4 v[kMaxChunksPerLane];
+#pragma unroll
+      for (int i = 0; i < kMaxChunksPerLane; ++i) {
+        const int c = lane + 64 * i;
+        if (c < chunks) v[i] = *(const u32x4*)(p + 8 * c);
+      }
+#pragma unroll
+      for (int i = 0; i < kMaxChunksPerLane; ++i) {
+        const int c = lane + 64 * i;
+        if (c < chunks) *(u32x4*)(o + 8 * c) = v[i];
+      }
+    } else {
+      uint16_t* o = g.o_text + (g.zero_from + (r - g.n_rows)) * g.text_stride;
+      const u32x4 z = {0u, 0u, 0u, 0u};
+#pragma unroll
+      for (int i = 0; i < kMaxChunksPerLane; ++i) {
+        const int c = lane + 64 * i;
+        if (c < chunks) *(u32x4*)(o + 8 * c) = z;
+      }
+    }
+  }
+}
+
+int row_grid(int64_t rows) {
+  // enough waves to keep every CU's memory pipes busy; the kernels loop over the rest
+  int64_t blocks = (rows + kWaves - 1) / kWaves;
+  if (blocks > 256 * 16) blocks = 256 * 16;
+  return (int)(blocks < 1 ? 1 : blocks);
+}
+
+int check_row_shape(int H, int D, const char* who) {
+  if (H < 1 || D < 8 || D % 8 != 0) return fail_arg("%s: need H >= 1 and D a multiple of 8 (H=%d D=%d)", who, H, D);
+  if ((int64_t)H * D > 64 * 8 * kMaxChunksPerLane)
+    return fail_arg("%s: rows of H*D=%d elements exceed the maximum %d", who, H * D, 64 * 8 * kMaxChunksPerLane);
+  return 0;
+}
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+}  // namespace
+}  // namespace onereel
+
+using namespace onereel;
+
+extern "C" int or_pack_gather(const void* a_video, const void* a_text, const void* b_video, const void* b_text,
+                              int64_t src_row_stride, int64_t text_row_stride, int64_t n_video,
+                              const int32_t* src_idx, const int32_t* rope_row, const int32_t* move_from,
+                              const float* cos_table, const float* sin_table, int64_t n_rope_rows, int64_t n_rows,
+                              int32_t H, int32_t D, void* a_out, void* b_out, void* stream) {
+  if (int rc = check_row_shape(H, D, "or_pack_gather")) return rc;
+  if (n_rows < 0) return fail_arg("or_pack_gather: n_rows < 0");
+  if (n_rows == 0) return 0;
+  if (!a_video || !src_idx || !a_out) return fail_arg("or_pack_gather: a_video, src_idx and a_out are required");
+  if (b_out && !b_video) return fail_arg("or_pack_gather: b_out given without b_video");
+  if ((rope_row || move_from) && (!cos_table || !sin_table || n_rope_rows < 1))
+    return fail_arg("or_pack_gather: rotation needs cos / sin tables");
+  if (move_from && !rope_row) return fail_arg("or_pack_gather: move_from needs rope_row (the second rotation)");
+  if (!aligned16(a_video) || !aligned16(a_out) || (a_text && !aligned16(a_text)) || (b_video && !aligned16(b_video)) ||
+      (b_text && !aligned16(b_text)) || (b_out && !aligned16(b_out)) || src_row_stride % 8 || text_row_stride % 8)
+    return fail_arg("or_pack_gather: pointers must be 16-byte aligned and row strides multiples of 8 elements");
+  GatherArgs g{(const uint16_t*)a_video, (const uint16_t*)(a_text ? a_text : a_video),
+               (const uint16_t*)b_video, (const uint16_t*)(b_text ? b_text : b_video),
+               src_row_stride, text_row_stride, n_video, src_idx, rope_row, move_from, cos_table, sin_table,
+               n_rope_rows, n_rows, H, D, (uint16_t*)a_out, (uint16_t*)b_out};
+  hipLaunchKernelGGL(pack_gather_kernel, dim3(row_grid(n_rows)), dim3(kThreads), 0, (hipStream_t)stream, g);
+  return check_hip(hipGetLastError(), "pack_gather_kernel launch");
+}
+
+extern "C" int or_scatter(const void* packed, const int32_t* dst_idx, int64_t n_rows, int64_t n_video,
+                          void* o_video, void* o_text, int64_t dst_row_stride, int64_t text_row_stride,
+                          int64_t text_zero_from, int64_t text_rows, int32_t H, int32_t D, void* stream) {
+  if (int rc = check_row_shape(H, D, "or_scatter")) return rc;
+  if (n_rows < 0 || text_zero_from < 0) return fail_arg("or_scatter: negative row count");
+  const int64_t n_zero = text_rows > text_zero_from ? text_rows - text_zero_from : 0;
+  if (n_rows + n_zero == 0) return 0;
+  if ((n_rows && (!packed || !dst_idx)) || (!o_video && !o_text))
+    return fail_arg("or_scatter: packed, dst_idx and an output are required");
+  if (n_zero && !o_text) return fail_arg("or_scatter: zeroing text rows needs o_text");
+  if ((packed && !aligned16(packed)) || (o_video && !aligned16(o_video)) || (o_text && !aligned16(o_text)) ||
+      dst_row_stride % 8 || text_row_stride % 8)
+    return fail_arg("or_scatter: pointers must be 16-byte aligned and row strides multiples of 8 elements");
+  ScatterArgs g{(const uint16_t*)packed, dst_idx, n_rows, n_video, (uint16_t*)o_video,
+                (uint16_t*)(o_text ? o_text : o_video), dst_row_stride, text_row_stride, text_zero_from, text_rows,
+                H, D};
+  hipLaunchKernelGGL(scatter_kernel, dim3(row_grid(n_rows + n_zero)), dim3(kThreads), 0, (hipStream_t)stream, g);
+  return check_hip(hipGetLastError(), "scatter_kernel launch");
+}

@@ -1,0 +1,156 @@
+"""HunyuanVideo-1.5 scene attention on one MI355X: the drop-in attention processor (src/onereel/models/hunyuan15.py).
+
+`Processor.__call__` keeps the diffusers processor signature (hunyuan15.py:177-210): the QKV projections and the
+RMSNorms run as the model's own torch modules; the scene-attention layer (RoPE, scope packing, varlen attention,
+write-back) runs as HIP kernels through `onereel_amd.scene`, with the scene RoPE fused into the K pack and the Q
+load. The multi-GPU modes of the reference (K/V gathering, Ulysses, ring), subject links and the bounded memory are
+not part of this build.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+
+import torch
+
+from .frame_memory import FrameMemory
+from .layout import SceneLayout
+from .scene import ScopePlan, scene_attention
+
+
+@dataclass
+class Context:
+    """the fields of the reference Context (hunyuan15.py:34-79) that the single-GPU scene path reads"""
+    layout: SceneLayout
+    mode: str = 'scene'
+    cfg: bool = True
+    shared_pos: str = 'source'           # 'source' | 'adjacent' | 'switch' (adjacent from step shared_switch on)
+    shared_switch: int = 10
+    scene_rope: bool = False             # temporal RoPE index restarts at every scene (+1 after scene 0)
+    rope_lengths: list = None            # scene lengths for scene_rope (default: the attention layout's)
+    frame_memory: FrameMemory = None
+    T: int = 0
+    fwd: int = 0
+    counts: dict = field(default_factory=dict)   # CFG branch (True = cond) -> MLLM tokens per sentence
+    fused: bool = True                   # Q read and outputs written in place (False: the reference's packed flow)
+    _cache: dict = field(default_factory=dict)
+    _rot_full: tuple = None
+
+    def step(self) -> int:
+        return (self.fwd - 1) // 2 if self.cfg else self.fwd - 1
+
+    def cond(self) -> bool:
+        return (self.fwd - 1) % 2 == 0 if self.cfg else True
+
+    def text_ranges(self) -> list:
+        c, out = 0, []
+        for n in self.counts[self.cond()]:
+            out.append((c, c + n))
+            c += n
+        return out
+
+    def adjacent(self) -> bool:
+        """shared frames at their adjacent positions in this step (hunyuan15.py:162)"""
+        return self.shared_pos == 'adjacent' or (self.shared_pos == 'switch' and self.step() >= self.shared_switch)
+
+
+def adjacent_positions(lay: SceneLayout, j: int) -> list:
+    """shared_pos = 'adjacent' (global RoPE): per shared frame of scene j, its temporal position (hunyuan15.py:92-100)"""
+    lo, hi = lay.ranges[j]
+    shared = lay.shared_frames(j)
+    before, after = sorted(f for f in shared if f < lo), sorted(f for f in shared if f >= hi)
+    pos = {f: lo - len(before) + i for i, f in enumerate(before)}
+    pos.update({f: hi + i for i, f in enumerate(after)})
+    return [pos[f] for f in shared]
+
+
+def frame_position(ctx: Context, f: int) -> int:
+    """temporal RoPE index of latent frame f (hunyuan15.py:103-113)"""
+    if not ctx.scene_rope:
+        return f
+    start = 0
+    for n in list(ctx.rope_lengths or ctx.layout.lengths):
+        if f < start + n:
+            return f - start + (start > 0)
+        start += n
+    raise IndexError(f)
+
+
+def shared_positions(ctx: Context, j: int) -> list:
+    """per shared frame of scene j, its temporal RoPE index under shared_pos = 'adjacent' (hunyuan15.py:116-124)"""
+    lay = ctx.layout
+    if not ctx.scene_rope:
+        return adjacent_positions(lay, j)
+    shared = lay.shared_frames(j)
+    last = max(frame_position(ctx, f) for f in lay.frames[j])
+    pos = {f: last + 1 + i for i, f in enumerate(sorted(shared))}
+    return [pos[f] for f in shared]
+
+
+def _key(ctx: Context, Le: int, adjacent: bool, moves: bool, device):
+    lay = ctx.layout
+    return ('plan', tuple(lay.lengths), lay.halo, lay.sides, tuple((j, tuple(v)) for j, v in sorted(lay.extra.items())),
+            ctx.T, tuple(ctx.counts[ctx.cond()]), Le, ctx.scene_rope, tuple(ctx.rope_lengths or ()), adjacent, moves,
+            str(device))
+
+
+def scope_plan(ctx: Context, Le: int, device, moves: bool = False) -> ScopePlan:
+    """the device layout of this step's scopes, cached per (layout, extra, counts, step mode)"""
+    adjacent = ctx.adjacent()
+    key = _key(ctx, Le, adjacent, moves, device)
+    if key not in ctx._cache:
+        ctx._cache[key] = ScopePlan(ctx.layout, ctx.T, ctx.counts[ctx.cond()], Le, ctx.scene_rope, ctx.rope_lengths,
+                                    adjacent, True, device, moves=moves)
+    return ctx._cache[key]
+
+
+def scene_rope_rows(ctx: Context, device) -> torch.Tensor:
+    """per video token row, its rotary row at the frame index within its scene (hunyuan15.py:443-454), built by the
+    device layout kernel (the queries of the video-only scopes, in token order)"""
+    lengths = list(ctx.rope_lengths or ctx.layout.lengths)
+    key = ('scene_rope', tuple(lengths), ctx.T, str(device))
+    if key not in ctx._cache:
+        plan = ScopePlan(SceneLayout(lengths, halo=0), ctx.T, None, 0, True, None, False, False, device)
+        ctx._cache[key] = plan.q_rope.long()
+    return ctx._cache[key]
+
+
+class Processor:
+    """the HunyuanVideo-1.5 attention processor with scene attention (hunyuan15.py:173-251), one GPU"""
+
+    def __init__(self, ctx: Context, layer: int):
+        self.ctx, self.layer = ctx, layer
+
+    def __call__(self, attn, hidden_states, encoder_hidden_states=None, attention_mask=None, image_rotary_emb=None):
+        ctx = self.ctx
+        cos, sin = image_rotary_emb
+        ctx._rot_full = image_rotary_emb
+        q, k, v = (f(hidden_states).unflatten(2, (attn.heads, -1)) for f in (attn.to_q, attn.to_k, attn.to_v))
+        q, k = attn.norm_q(q), attn.norm_k(k)
+        q, k, v = (x[0].to(torch.bfloat16) for x in (q, k, v))
+        eq, ek, ev = (f(encoder_hidden_states).unflatten(2, (attn.heads, -1))
+                      for f in (attn.add_q_proj, attn.add_k_proj, attn.add_v_proj))
+        if attn.norm_added_q is not None:
+            eq = attn.norm_added_q(eq)
+        if attn.norm_added_k is not None:
+            ek = attn.norm_added_k(ek)
+        eq, ek, ev = (x[0].to(torch.bfloat16) for x in (eq, ek, ev))
+        hs, ehs = self.scene_raw(q, k, v, eq, ek, ev, cos, sin)
+        hs = attn.to_out[1](attn.to_out[0](hs.flatten(1, 2)[None].to(hidden_states.dtype)))
+        ehs = attn.to_add_out(ehs.flatten(1, 2)[None].to(hidden_states.dtype))
+        return hs, ehs
+
+    def scene_raw(self, q, k, v, eq, ek, ev, cos, sin):
+        """scene attention of q / k BEFORE RoPE: rotation fused into the kernels (video rows rotated at their scene
+        rotary rows, moved shared keys at their adjacent rows, text rows not rotated)"""
+        ctx = self.ctx
+        plan = scope_plan(ctx, eq.shape[0], q.device)
+        return scene_attention(plan, q, k, v, eq, ek, ev, cos, sin, mode='raw', fused=ctx.fused)
+
+    def scene(self, q, k, v, eq, ek, ev):
+        """the reference's entry (hunyuan15.py:212-251): q / k already rotated; shared keys re-rotated by
+        _move_shared's two rotations through ctx._rot_full when the shared frames sit at adjacent positions"""
+        ctx = self.ctx
+        adjacent = ctx.adjacent()
+        plan = scope_plan(ctx, eq.shape[0], q.device, moves=adjacent)
+        cos, sin = ctx._rot_full if adjacent else (None, None)
+        return scene_attention(plan, q, k, v, eq, ek, ev, cos, sin, mode='rotated', fused=ctx.fused)

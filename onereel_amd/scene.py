@@ -1,0 +1,278 @@
+"""The scene-attention layer engine: device layout, K/V pack-gather, varlen attention and write-back.
+
+One layer of `Processor.scene` on one GPU (src/onereel/models/hunyuan15.py:212-251) runs here as at most four
+launches on the caller's current stream, with no host synchronisation:
+
+    ScopePlan.build      or_layout_build   cu_seqlens, gather rows, RoPE rows (cached per layout and step mode)
+    pack_kv              or_pack_gather    K (rotated on the way) and V rows of every scope, one pass
+    attention            or_varlen_fwd     Q read in place (rotated on the load), output written in place
+    zero text padding    or_scatter        ot rows past the valid text (ot = eq.new_zeros in the reference)
+
+`mode` says what q / k hold: 'raw' (before RoPE: the fused path, the table row of every query and key comes from
+the layout), 'rotated' (already rotated, as the reference's `scene` receives them: shared keys are re-rotated by
+_move_shared's two rotations when the shared frames are moved), or 'none' (no RoPE at all).
+"""
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _lib as L
+from .layout import SceneLayout
+
+MODES = ('raw', 'rotated', 'none')
+
+
+def _desc(lay: SceneLayout, T: int, counts, text_rows: int, scene_rope: bool, rope_lengths, adjacent: bool,
+          with_text: bool) -> L.LayoutDesc:
+    d = L.LayoutDesc()
+    n = lay.n_scenes
+    if n > L.OR_MAX_SCENES:
+        raise ValueError(f'{n} scenes exceed the maximum {L.OR_MAX_SCENES}')
+    d.n_scenes, d.T, d.halo = n, int(T), int(lay.halo)
+    d.sides = ('adj', 'prev', 'next').index(lay.sides)
+    d.with_text, d.scene_rope, d.adjacent = int(with_text), int(scene_rope), int(adjacent)
+    d.text_rows = int(text_rows)
+    for j, x in enumerate(lay.lengths):
+        d.lengths[j] = int(x)
+    counts = list(counts) if with_text else [0] * n
+    if len(counts) != n:
+        raise ValueError(f'{len(counts)} sentence counts for {n} scenes')
+    for j, c in enumerate(counts):
+        d.counts[j] = int(c)
+    rl = list(rope_lengths) if rope_lengths else []
+    if len(rl) > L.OR_MAX_SCENES:
+        raise ValueError('too many rope_lengths')
+    d.n_rope_lengths = len(rl)
+    for s, x in enumerate(rl):
+        d.rope_lengths[s] = int(x)
+    e = 0
+    d.extra_ptr[0] = 0
+    for j in range(n):
+        fr = list(lay.extra.get(j, ()))
+        if e + len(fr) > L.OR_MAX_EXTRA:
+            raise ValueError(f'more than {L.OR_MAX_EXTRA} extra frames')
+        for f in fr:
+            d.extra[e] = int(f)
+            e += 1
+        d.extra_ptr[j + 1] = e
+    return d
+
+
+class ScopePlan:
+    """The packed layout of one request's scopes, built on the device by `or_layout_build`.
+
+    Attributes (int32 device tensors): cu_q, cu_k [n_seg+1], seg_q_src [n_seg], q_src / q_rope [sum_q], k_src /
+    k_rope [sum_k], and for mode 'rotated' with moved shared frames k_move_a / k_move_b [sum_k]. Host ints: n_seg,
+    sum_q, sum_k, max_q, max_k, n_video, text_rows, max_rope_row."""
+
+    def __init__(self, lay: SceneLayout, T: int, counts=None, text_rows: int | None = None, scene_rope=False,
+                 rope_lengths=None, adjacent=False, with_text=True, device=None, moves=False):
+        counts = list(counts) if counts is not None else [0] * lay.n_scenes
+        if text_rows is None:
+            text_rows = sum(counts) if with_text else 0
+        self.layout, self.T, self.counts, self.text_rows = lay, int(T), counts, int(text_rows)
+        self.scene_rope, self.adjacent, self.with_text = bool(scene_rope), bool(adjacent), bool(with_text)
+        self.desc = _desc(lay, T, counts, text_rows, scene_rope, rope_lengths, adjacent, with_text)
+        sz = L.LayoutSizes()
+        L.check(L.lib().or_layout_plan(ctypes.byref(self.desc), ctypes.byref(sz)), 'or_layout_plan')
+        self.n_seg, self.sum_q, self.sum_k = sz.n_seg, sz.sum_q, sz.sum_k
+        self.max_q, self.max_k, self.n_video, self.max_rope_row = sz.max_q, sz.max_k, sz.n_video, sz.max_rope_row
+        dev = torch.device(device) if device is not None else torch.device('cuda', torch.cuda.current_device())
+        new = lambda n: torch.empty(int(n), dtype=torch.int32, device=dev)
+        self.cu_q, self.cu_k, self.seg_q_src = new(self.n_seg + 1), new(self.n_seg + 1), new(self.n_seg)
+        self.q_src, self.q_rope = new(self.sum_q), new(self.sum_q)
+        self.k_src, self.k_rope = new(self.sum_k), new(self.sum_k)
+        self.k_move_a = new(self.sum_k) if moves and adjacent else None
+        self.k_move_b = new(self.sum_k) if moves and adjacent else None
+        self.device = dev
+        self._ws = {}
+        self.build()
+
+    def build(self):
+        """(re)run the layout kernel on the current stream"""
+        out = L.LayoutOut(*(L.ptr(t) for t in (self.cu_q, self.cu_k, self.seg_q_src, self.q_src, self.q_rope,
+                                                self.k_src, self.k_rope, self.k_move_a, self.k_move_b)))
+        with torch.cuda.device(self.device):
+            L.check(L.lib().or_layout_build(ctypes.byref(self.desc), ctypes.byref(out), L.stream_handle()),
+                    'or_layout_build')
+        return self
+
+    def workspace(self, H: int, D: int) -> torch.Tensor:
+        if H not in self._ws:
+            n = L.lib().or_varlen_workspace_size(int(self.n_seg), int(self.sum_q), int(H), int(D))
+            self._ws[H] = torch.empty(int(n), dtype=torch.uint8, device=self.device)
+        return self._ws[H]
+
+    def index_bytes(self) -> int:
+        """bytes the layout kernel writes"""
+        n = 2 * (self.n_seg + 1) + self.n_seg + 2 * self.sum_q + 2 * self.sum_k
+        if self.k_move_a is not None:
+            n += 2 * self.sum_k
+        return 4 * n
+
+
+def _rows2d(x: torch.Tensor, H: int, D: int):
+    """(tensor, row stride) of a [rows, H, D] view whose (H, D) part is contiguous"""
+    if x.dim() != 3 or x.shape[1] != H or x.shape[2] != D:
+        raise ValueError(f'expected [rows, {H}, {D}], got {tuple(x.shape)}')
+    if x.stride(2) != 1 or x.stride(1) != D:
+        raise ValueError('heads and head dims must be contiguous')
+    return x, x.stride(0)
+
+
+def _check_bf16(*xs):
+    for x in xs:
+        if x is not None and (x.dtype != torch.bfloat16 or not x.is_cuda):
+            raise TypeError(f'expected a bf16 GPU tensor, got {x.dtype} on {x.device}')
+
+
+def _tables(cos, sin, D):
+    if cos is None:
+        return None, None, 0
+    if cos.dim() != 2 or cos.shape[1] != D or sin.shape != cos.shape:
+        raise ValueError(f'rotary tables must be [rows, {D}]')
+    cos = cos.to(torch.float32).contiguous()
+    sin = sin.to(torch.float32).contiguous()
+    return cos, sin, cos.shape[0]
+
+
+def pack_rows(plan: ScopePlan, video: torch.Tensor, text: torch.Tensor | None, which: str, out=None,
+              b_video=None, b_text=None, b_out=None, cos=None, sin=None, mode='none'):
+    """Gather the packed rows of the plan's queries (which='q') or keys (which='k') from [video ; text]; with b_*,
+    the value rows of the same keys in the same pass. Keys / queries are rotated per `mode`."""
+    H, D = video.shape[1], video.shape[2]
+    _check_bf16(video, text, b_video, b_text)
+    _, vs = _rows2d(video, H, D)
+    ts = _rows2d(text, H, D)[1] if text is not None and text.shape[0] else vs
+    if b_video is not None:
+        if _rows2d(b_video, H, D)[1] != vs or (b_text is not None and b_text.shape[0] and b_text.stride(0) != ts):
+            raise ValueError('value rows must have the strides of the key rows')
+    n = plan.sum_q if which == 'q' else plan.sum_k
+    src = plan.q_src if which == 'q' else plan.k_src
+    rope = move = None
+    if mode == 'raw':
+        rope = plan.q_rope if which == 'q' else plan.k_rope
+    elif mode == 'rotated' and which == 'k' and plan.adjacent:
+        if plan.k_move_a is None:
+            raise ValueError('plan was built without move rows (moves=True)')
+        rope, move = plan.k_move_b, plan.k_move_a
+    elif mode not in MODES:
+        raise ValueError(mode)
+    cos, sin, n_rows = _tables(cos, sin, D) if rope is not None else (None, None, 0)
+    if rope is not None and cos is None:
+        raise ValueError('RoPE needs the (cos, sin) tables')
+    if rope is not None and plan.max_rope_row >= n_rows:
+        raise ValueError(f'layout needs rotary row {plan.max_rope_row} but the table has {n_rows} rows')
+    out = out if out is not None else torch.empty(n, H, D, dtype=video.dtype, device=video.device)
+    if b_video is not None and b_out is None:
+        b_out = torch.empty(n, H, D, dtype=video.dtype, device=video.device)
+    L.check(L.lib().or_pack_gather(video.data_ptr(), L.ptr(text if text is not None and text.shape[0] else None),
+                                   L.ptr(b_video), L.ptr(b_text if b_text is not None and b_text.shape[0] else None),
+                                   vs, ts, plan.n_video, src.data_ptr(), L.ptr(rope), L.ptr(move),
+                                   L.ptr(cos), L.ptr(sin), n_rows, n, H, D, out.data_ptr(), L.ptr(b_out),
+                                   L.stream_handle(video.device)), 'or_pack_gather')
+    return (out, b_out) if b_video is not None else out
+
+
+def varlen(q, k, v, cu_q, cu_k, max_q, max_k, *, k_off=None, k_len=None, out=None, lse=None, seg_q_src=None,
+           q_text=None, o_text=None, n_q_video=None, q_rope=None, cos=None, sin=None, sum_q=None, workspace=None,
+           scale=None):
+    """or_varlen_fwd on torch tensors. Returns out (allocated [Nq, H, D] when not given)."""
+    H, D = k.shape[1], k.shape[2]
+    _check_bf16(q, k, v, q_text, out, o_text)
+    _, qs = _rows2d(q, H, D)
+    _, ks = _rows2d(k, H, D)
+    if _rows2d(v, H, D)[1] != ks:
+        raise ValueError('k and v must have the same row stride')
+    if q_text is not None and q_text.shape[0] and q_text.stride(0) != qs:
+        raise ValueError('q and q_text must have the same row stride')
+    n_seg = (cu_q.numel() - 1)
+    for t in (cu_q, cu_k, k_off, k_len, seg_q_src, q_rope):
+        if t is not None and (t.dtype != torch.int32 or not t.is_cuda or not t.is_contiguous()):
+            raise TypeError('index arrays must be contiguous int32 GPU tensors')
+    if sum_q is None:
+        sum_q = q.shape[0] if seg_q_src is None else None
+        if sum_q is None:
+            raise ValueError('sum_q is required with seg_q_src')
+    if out is None:
+        out = torch.empty(q.shape[0], H, D, dtype=torch.bfloat16, device=q.device)
+    _, os_ = _rows2d(out, H, D)
+    if o_text is not None and o_text.shape[0] and o_text.stride(0) != os_:
+        raise ValueError('o and o_text must have the same row stride')
+    cos, sin, n_rope_rows = _tables(cos, sin, D) if q_rope is not None else (None, None, 0)
+    if workspace is None:
+        nb = L.lib().or_varlen_workspace_size(int(n_seg), int(sum_q), int(H), int(D))
+        workspace = torch.empty(int(nb), dtype=torch.uint8, device=q.device)
+    a = L.VarlenArgs()
+    a.q, a.q_text, a.k, a.v = q.data_ptr(), L.ptr(q_text if q_text is not None and q_text.shape[0] else None), \
+        k.data_ptr(), v.data_ptr()
+    a.o, a.o_text, a.lse = out.data_ptr(), L.ptr(o_text if o_text is not None and o_text.shape[0] else None), \
+        L.ptr(lse)
+    a.cu_q, a.cu_k, a.k_off, a.k_len = L.ptr(cu_q), L.ptr(cu_k), L.ptr(k_off), L.ptr(k_len)
+    a.seg_q_src, a.q_rope, a.cos_table, a.sin_table = L.ptr(seg_q_src), L.ptr(q_rope), L.ptr(cos), L.ptr(sin)
+    a.n_rope_rows = n_rope_rows
+    a.n_q_video = q.shape[0] if n_q_video is None else int(n_q_video)
+    a.q_row_stride, a.k_row_stride, a.o_row_stride = qs, ks, os_
+    a.n_seg, a.sum_q, a.max_q, a.max_k, a.H, a.D = int(n_seg), int(sum_q), int(max_q), int(max_k), H, D
+    a.scale = float(D ** -0.5 if scale is None else scale)
+    a.workspace, a.workspace_bytes = workspace.data_ptr(), workspace.numel()
+    L.check(L.lib().or_varlen_fwd(ctypes.byref(a), L.stream_handle(q.device)), 'or_varlen_fwd')
+    return out
+
+
+def scatter(plan: ScopePlan, packed: torch.Tensor, ov: torch.Tensor, ot: torch.Tensor | None):
+    """write packed outputs back to token order (ov rows / ot rows), and zero ot's rows past the valid text"""
+    H, D = packed.shape[1], packed.shape[2]
+    _check_bf16(packed, ov, ot)
+    _, vs = _rows2d(ov, H, D)
+    ts = _rows2d(ot, H, D)[1] if ot is not None and ot.shape[0] else vs
+    valid = sum(plan.counts) if plan.with_text else 0
+    Le = ot.shape[0] if ot is not None else 0
+    L.check(L.lib().or_scatter(packed.data_ptr(), plan.q_src.data_ptr(), plan.sum_q, plan.n_video, ov.data_ptr(),
+                               L.ptr(ot if Le else None), vs, ts, valid, Le, H, D, L.stream_handle(packed.device)),
+            'or_scatter')
+    return ov, ot
+
+
+def zero_text_padding(plan: ScopePlan, ot: torch.Tensor):
+    """ot rows [sum(counts), Le) = 0 (the reference's ot = eq.new_zeros leaves them so)"""
+    H, D = ot.shape[1], ot.shape[2]
+    valid = sum(plan.counts) if plan.with_text else 0
+    if ot.shape[0] <= valid:
+        return ot
+    _, ts = _rows2d(ot, H, D)
+    L.check(L.lib().or_scatter(None, None, 0, plan.n_video, None, ot.data_ptr(), ts, ts, valid, ot.shape[0], H, D,
+                               L.stream_handle(ot.device)), 'or_scatter')
+    return ot
+
+
+def scene_attention(plan: ScopePlan, q, k, v, eq, ek, ev, cos=None, sin=None, mode='raw', fused=True,
+                    kbuf=None, vbuf=None):
+    """(ov, ot) of one scene-attention layer. q / k / v [F*T, H, D] and eq / ek / ev [Le, H, D] bf16 on the GPU.
+
+    fused=True: K/V packed once, Q read in place, outputs written in place. fused=False: the reference's data flow
+    (Q, K, V packed, one varlen call on packed tensors, write-back by the scatter kernel)."""
+    if mode not in MODES:
+        raise ValueError(mode)
+    H, D = q.shape[1], q.shape[2]
+    if q.shape[0] != plan.n_video:
+        raise ValueError(f'{q.shape[0]} video rows, layout has {plan.n_video}')
+    if plan.with_text and eq.shape[0] != plan.text_rows:
+        raise ValueError(f'{eq.shape[0]} text rows, layout has {plan.text_rows}')
+    kp, vp = pack_rows(plan, k, ek, 'k', out=kbuf, b_video=v, b_text=ev, b_out=vbuf, cos=cos, sin=sin, mode=mode)
+    ov = torch.empty_like(q)
+    ot = torch.empty(eq.shape[0], H, D, dtype=q.dtype, device=q.device) if eq is not None else None
+    qmode = 'raw' if mode == 'raw' else 'none'
+    if fused:
+        varlen(q, kp, vp, plan.cu_q, plan.cu_k, plan.max_q, plan.max_k, out=ov, seg_q_src=plan.seg_q_src,
+               q_text=eq, o_text=ot, n_q_video=plan.n_video, q_rope=plan.q_rope if qmode == 'raw' else None,
+               cos=cos, sin=sin, sum_q=plan.sum_q, workspace=plan.workspace(H, D))
+        if ot is not None:
+            zero_text_padding(plan, ot)
+    else:
+        qp = pack_rows(plan, q, eq, 'q', cos=cos, sin=sin, mode=qmode)
+        op = varlen(qp, kp, vp, plan.cu_q, plan.cu_k, plan.max_q, plan.max_k, workspace=plan.workspace(H, D))
+        scatter(plan, op, ov, ot)
+    return ov, ot

@@ -1,0 +1,238 @@
+"""GPU parity of the attention kernel and of the whole scene-attention layer against the fp32 oracle, through the
+C ABI. Tolerance (bf16 kernel vs fp32 reference on the same packing): max-abs <= 2e-2 and mean-abs <= 2e-3."""
+import numpy as np
+import pytest
+import torch
+
+from helpers import assert_close, attn_rows_reference, layout_case, rand_bf16, sample_rows
+from onereel_amd import _lib as L
+from onereel_amd import attention as A
+from onereel_amd import hunyuan15 as HY
+from onereel_amd import scene
+from onereel_amd import wan as W
+from onereel_amd.layout import SceneLayout
+from oracle import attention as OA
+from oracle import layout as OL
+
+pytestmark = [pytest.mark.gpu, pytest.mark.skipif(not torch.cuda.is_available(), reason='needs the GPU')]
+DEV = 'cuda'
+
+
+def _segments_case(lq, lk, H, D, seed):
+    q = rand_bf16((sum(lq), H, D), seed)
+    k = rand_bf16((sum(lk), H, D), seed + 1)
+    v = rand_bf16((sum(lk), H, D), seed + 2)
+    return q, k, v, np.cumsum([0] + lq), np.cumsum([0] + lk)
+
+
+@pytest.mark.parametrize('D', [64, 128])
+@pytest.mark.parametrize('lq,lk,H', [
+    ([1], [1], 1),
+    ([5, 1, 17], [9, 3, 30], 2),
+    ([63, 64, 65], [64, 63, 129], 3),
+    ([256, 257, 300, 7], [1000, 64, 65, 2049], 2),
+    ([0, 40, 0, 12], [5, 77, 9, 200], 4),          # empty query segments
+])
+def test_varlen_matches_fp32_reference(lq, lk, H, D):
+    print(f'varlen lq={lq} lk={lk} H={H} D={D}', flush=True)
+    q, k, v, cq, ck = _segments_case(lq, lk, H, D, 11)
+    o = A.varlen(q.to(DEV), k.to(DEV), v.to(DEV), torch.tensor(cq, dtype=torch.int32, device=DEV),
+                 torch.tensor(ck, dtype=torch.int32, device=DEV), max(lq), max(lk))
+    ref = OA.packed_attention(q, k, v, cq, ck)
+    assert_close(o.cpu(), ref, what='varlen')
+
+
+def test_varlen_lse_and_packed_api():
+    lq, lk, H, D = [70, 3, 129], [90, 300, 5], 2, 128
+    q, k, v, cq, ck = _segments_case(lq, lk, H, D, 21)
+    o, lse = A.varlen_lse(q.to(DEV), k.to(DEV), v.to(DEV), torch.tensor(cq, dtype=torch.int32, device=DEV),
+                          torch.tensor(ck, dtype=torch.int32, device=DEV), max(lq), max(lk))
+    ref = OA.packed_attention(q, k, v, cq, ck)
+    assert_close(o.cpu(), ref, what='varlen_lse out')
+    for s in range(3):
+        qs, ks = q[cq[s]:cq[s + 1]].float(), k[ck[s]:ck[s + 1]].float()
+        lref = torch.logsumexp(torch.einsum('qhd,khd->hqk', qs, ks) * D ** -0.5, -1)
+        assert (lse[:, cq[s]:cq[s + 1]].cpu() - lref).abs().max() < 2e-3
+    segs = [(q[cq[s]:cq[s + 1]].to(DEV), k[ck[s]:ck[s + 1]].to(DEV), v[ck[s]:ck[s + 1]].to(DEV)) for s in range(3)]
+    outs = A.packed(segs)
+    assert [x.shape[0] for x in outs] == lq
+    assert_close(torch.cat(outs).cpu(), ref, what='packed')
+    outs = A.packed_lse(segs)
+    assert torch.allclose(torch.cat([l for _, l in outs], 1), lse)
+
+
+def test_dense_and_overlapping_ranges():
+    H, D = 2, 128
+    q = rand_bf16((2, 150, H, D), 31)
+    k = rand_bf16((2, 170, H, D), 32)
+    v = rand_bf16((2, 170, H, D), 33)
+    o = A.dense(q.to(DEV), k.to(DEV), v.to(DEV)).cpu()
+    for b in range(2):
+        ref = OA.packed_attention(q[b], k[b], v[b], [0, 150], [0, 170])
+        assert_close(o[b], ref, what='dense')
+    # Wan-style overlapping key ranges read in place: scene j reads frames [lo, hi + 2)
+    T = 40
+    lay = OL.SceneLayout([3, 4, 2], halo=2, sides='next')
+    S = lay.n_frames * T
+    qq, kk, vv = (rand_bf16((S, H, D), s) for s in (41, 42, 43))
+    qr, kr = OL.wan_ranges(lay, T)
+    o = A.overlapping_ranges(qq.to(DEV), kk.to(DEV), vv.to(DEV), qr, kr).cpu()
+    cq = [0] + [b for _, b in qr]
+    ref = OA.packed_attention(qq, kk, vv, cq, None, k_off=[a for a, _ in kr], k_len=[b - a for a, b in kr])
+    assert_close(o, ref, what='overlapping_ranges')
+
+
+def _layer_inputs(case, seed=0):
+    H, D, T = case['H'], case['D'], case['T']
+    S = sum(case['lengths']) * T
+    q, k, v = (rand_bf16((S, H, D), seed + i) for i in range(3))
+    eq, ek, ev = (rand_bf16((case['Le'], H, D), seed + 3 + i) for i in range(3))
+    F, Hh, Ww = case['table']
+    cos, sin = OA.rope_table_3d(F, Hh, Ww, D)
+    return q, k, v, eq, ek, ev, cos, sin
+
+
+@pytest.mark.parametrize('name,per_seg', [('config1', None), ('config2', 48), ('config3', 48), ('config4_K12', 24)])
+@pytest.mark.parametrize('adjacent', [False, True])
+def test_scene_layer_matches_oracle(name, per_seg, adjacent):
+    """the fused layer (K/V pack with RoPE, Q RoPE on the load, in-place output) against the oracle's packing plus
+    per-scope fp32 attention; full outputs for config 1, sampled query rows (every segment's first / last rows
+    included) at the full-size configs"""
+    case = layout_case(name)
+    print(f'layer {name} adjacent={adjacent}', flush=True)
+    q, k, v, eq, ek, ev, cos, sin = _layer_inputs(case)
+    lay = SceneLayout(case['lengths'], halo=case['halo'], sides=case['sides'], extra=case['extra'])
+    plan = scene.ScopePlan(lay, case['T'], case['counts'], case['Le'], case['scene_rope'], None, adjacent, True, DEV)
+    g = [x.to(DEV) for x in (q, k, v, eq, ek, ev, cos, sin)]
+    ov, ot = scene.scene_attention(plan, *g[:6], g[6], g[7], mode='raw', fused=True)
+    olay = OL.SceneLayout(case['lengths'], case['halo'], case['sides'], case['extra'])
+    sc = OL.hunyuan_scopes(olay, case['T'], case['counts'], case['Le'], scene_rope=case['scene_rope'],
+                           adjacent=adjacent)
+    qp, kp, vp = OA.pack(sc, q, k, v, eq, ek, ev, cos, sin, mode='raw')
+    rows = np.arange(int(sc.cu_q[-1])) if per_seg is None else sample_rows(sc.cu_q, per_seg)
+    ref = attn_rows_reference(qp, kp, vp, sc.cu_q, sc.cu_k, rows)
+    got = torch.cat([ov, ot]).cpu()[torch.as_tensor(sc.q_src[rows])]
+    assert_close(got, ref, what=f'{name} layer')
+    valid = sum(case['counts'])
+    if case['Le'] > valid:
+        assert ot[valid:].abs().max().item() == 0
+
+
+@pytest.mark.parametrize('adjacent', [False, True])
+def test_scene_layer_reference_flow_and_rotated_inputs(adjacent):
+    """fused=False (Q/K/V packed, varlen on packed tensors, scatter) and mode 'rotated' (already rotated q / k, shared
+    keys re-rotated by _move_shared's two rotations) give the oracle's result; text padding rows stay zero"""
+    case = dict(layout_case('config1'), Le=40)
+    q, k, v, eq, ek, ev, cos, sin = _layer_inputs(case, 5)
+    lay = SceneLayout(case['lengths'], halo=0, extra=case['extra'])
+    olay = OL.SceneLayout(case['lengths'], 0, 'adj', case['extra'])
+    sc = OL.hunyuan_scopes(olay, case['T'], case['counts'], case['Le'], scene_rope=True, adjacent=adjacent)
+    plan = scene.ScopePlan(lay, case['T'], case['counts'], case['Le'], True, None, adjacent, True, DEV, moves=True)
+    g = [x.to(DEV) for x in (q, k, v, eq, ek, ev, cos, sin)]
+    rv, rt = OA.scene_layer(sc, q, k, v, eq, ek, ev, cos, sin, mode='raw')
+    ov, ot = scene.scene_attention(plan, *g, mode='raw', fused=False)
+    assert_close(ov.cpu(), rv, what='unfused video')
+    assert_close(ot.cpu(), rt, what='unfused text')
+    assert ot[32:].abs().max().item() == 0
+    # already-rotated inputs, as the reference's Processor.scene receives them
+    rows = torch.as_tensor(OL.scene_rope_rows(olay, case['T']))
+    qr = OA.apply_rotary_emb(q, cos[rows], sin[rows])
+    kr = OA.apply_rotary_emb(k, cos[rows], sin[rows])
+    rv2, rt2 = OA.scene_layer(sc, qr, kr, v, eq, ek, ev, cos, sin, mode='rotated')
+    for fused in (True, False):
+        ov2, ot2 = scene.scene_attention(plan, qr.to(DEV), kr.to(DEV), *g[2:], mode='rotated', fused=fused)
+        assert_close(ov2.cpu(), rv2, what=f'rotated video fused={fused}')
+        assert_close(ot2.cpu(), rt2, what=f'rotated text fused={fused}')
+
+
+class _Attn(torch.nn.Module):
+    """the attention-module attributes a diffusers HunyuanVideo-1.5 block hands its processor"""
+
+    def __init__(self, C, H, gen):
+        super().__init__()
+        self.heads = H
+        mk = lambda: torch.nn.Linear(C, C, dtype=torch.bfloat16)
+        self.to_q, self.to_k, self.to_v = mk(), mk(), mk()
+        self.add_q_proj, self.add_k_proj, self.add_v_proj = mk(), mk(), mk()
+        self.norm_q = torch.nn.RMSNorm(C // H, eps=1e-6, dtype=torch.bfloat16)
+        self.norm_k = torch.nn.RMSNorm(C // H, eps=1e-6, dtype=torch.bfloat16)
+        self.norm_added_q = torch.nn.RMSNorm(C // H, eps=1e-6, dtype=torch.bfloat16)
+        self.norm_added_k = None
+        self.to_out = torch.nn.ModuleList([mk(), torch.nn.Dropout(0.0)])
+        self.to_add_out = mk()
+        with torch.no_grad():
+            for p in self.parameters():
+                p.copy_(torch.randn(p.shape, generator=gen) * 0.05)
+
+
+@torch.no_grad()
+def test_processor_call_matches_oracle_layer():
+    """Processor.__call__ (diffusers signature) = projections -> oracle layer (RoPE + scopes + attention) -> outputs,
+    at step >= shared_switch (moved shared frames) with scene RoPE"""
+    gen = torch.Generator().manual_seed(3)
+    H, D, T = 2, 64, 16
+    C = H * D
+    lay = SceneLayout([3, 2, 3], halo=0, extra={0: [4, 7], 1: [0, 7], 2: [0, 4]})
+    counts = [5, 3, 4]
+    Le = 14
+    attn = _Attn(C, H, gen)
+    hs = (torch.randn(1, lay.n_frames * T, C, generator=gen) * 0.5).bfloat16()
+    ehs = (torch.randn(1, Le, C, generator=gen) * 0.5).bfloat16()
+    cos, sin = OA.rope_table_3d(lay.n_frames, 4, 4, D)
+    ctx = HY.Context(lay, T=T, scene_rope=True, shared_pos='switch', shared_switch=1, cfg=False)
+    ctx.counts = {True: counts}
+    ctx.fwd = 2                                                            # step 1 >= switch: adjacent
+    proc = HY.Processor(ctx, 0)
+    attn_g = _Attn(C, H, torch.Generator().manual_seed(3)).to(DEV)
+    attn_g.load_state_dict(attn.state_dict())
+    out, eout = proc(attn_g, hs.to(DEV), ehs.to(DEV), None, (cos.to(DEV), sin.to(DEV)))
+    # reference: the same projections on the CPU, the oracle's layer, the same output projections
+    q, k, v = (f(hs).unflatten(2, (H, -1)) for f in (attn.to_q, attn.to_k, attn.to_v))
+    q, k = attn.norm_q(q), attn.norm_k(k)
+    eq, ek, ev = (f(ehs).unflatten(2, (H, -1)) for f in (attn.add_q_proj, attn.add_k_proj, attn.add_v_proj))
+    eq = attn.norm_added_q(eq)
+    sc = OL.hunyuan_scopes(OL.SceneLayout([3, 2, 3], 0, 'adj', lay.extra), T, counts, Le, scene_rope=True,
+                           adjacent=True)
+    rv, rt = OA.scene_layer(sc, q[0].bfloat16(), k[0].bfloat16(), v[0].bfloat16(), eq[0].bfloat16(),
+                            ek[0].bfloat16(), ev[0].bfloat16(), cos, sin, mode='raw')
+    assert_close(proc.scene_raw(*(x[0].bfloat16().to(DEV) for x in (q, k, v, eq, ek, ev)), cos.to(DEV),
+                                sin.to(DEV))[0].cpu(), rv, what='scene_raw')
+    ref_out = attn.to_out[1](attn.to_out[0](rv.bfloat16().flatten(1, 2)[None]))
+    ref_eout = attn.to_add_out(rt.bfloat16().flatten(1, 2)[None])
+    assert_close(out.cpu(), ref_out, max_abs=5e-2, mean_abs=5e-3, what='processor hs')
+    assert_close(eout.cpu(), ref_eout, max_abs=5e-2, mean_abs=5e-3, what='processor ehs')
+    assert HY.scene_rope_rows(ctx, DEV).cpu().tolist() == OL.scene_rope_rows(OL.SceneLayout([3, 2, 3], 0), T).tolist()
+
+
+@torch.no_grad()
+def test_wan_self_and_cross_ranges():
+    H, D, T = 3, 128, 24
+    ctx = W.Context(SceneLayout([3, 4, 2], halo=2, sides='next'), T=T, text_len=20)
+    S = 9 * T
+    q, k, v = (rand_bf16((S, H, D), s) for s in (51, 52, 53))
+    o = W.self_ranges(ctx, q.to(DEV), k.to(DEV), v.to(DEV)).cpu()
+    qr, kr = OL.wan_ranges(OL.SceneLayout([3, 4, 2], 2, 'next'), T)
+    ref = OA.packed_attention(q, k, v, [0] + [b for _, b in qr], None, k_off=[a for a, _ in kr],
+                              k_len=[b - a for a, b in kr])
+    assert_close(o, ref, what='wan self zero-copy')
+    # with frame-memory extras: packed video-only scopes
+    ctx.layout = SceneLayout([3, 4, 2], halo=0, extra={0: [5, 8], 1: [0], 2: [1, 4]})
+    o = W.self_ranges(ctx, q.to(DEV), k.to(DEV), v.to(DEV)).cpu()
+    sc = OL.hunyuan_scopes(OL.SceneLayout([3, 4, 2], 0, 'adj', ctx.layout.extra), T, [0, 0, 0], 0, with_text=False)
+    qp, kp, vp = OA.pack(sc, q, k, v, q[:0], k[:0], v[:0], mode='none')
+    ref = OA.write_back(sc, OA.packed_attention(qp, kp, vp, sc.cu_q, sc.cu_k), 0)[0]
+    assert_close(o, ref, what='wan self packed')
+    # cross-attention: scene j reads sentence j
+    e = rand_bf16((60, H, D), 54)
+    ev = rand_bf16((60, H, D), 55)
+    o = W.cross_ranges(ctx, q.to(DEV), e.to(DEV), ev.to(DEV)).cpu()
+    cq = [0, 3 * T, 7 * T, 9 * T]
+    ref = OA.packed_attention(q, e, ev, cq, None, k_off=[0, 20, 40], k_len=[20, 20, 20])
+    assert_close(o, ref, what='wan cross')
+
+
+def test_native_library_is_the_in_tree_build():
+    """the HIP path runs from the in-tree libonereel_hip.so (no fallback exists)"""
+    L.lib()
+    maps = open('/proc/self/maps').read()
+    assert str(L.LIB_PATH) in maps

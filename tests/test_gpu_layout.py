@@ -1,0 +1,140 @@
+"""GPU parity, bit-exact: the layout kernel, the K/V/Q pack-gather (with RoPE and _move_shared) and the scatter
+against the oracle, through the C ABI, at the BASELINE layouts' full sizes and on edge-case layouts."""
+import numpy as np
+import pytest
+import torch
+
+from helpers import bits, layout_case, rand_bf16
+from onereel_amd.layout import SceneLayout
+from onereel_amd.scene import ScopePlan, pack_rows, scatter
+from oracle import attention as OA
+from oracle import layout as OL
+
+pytestmark = [pytest.mark.gpu, pytest.mark.skipif(not torch.cuda.is_available(), reason='needs the GPU')]
+
+DEV = 'cuda'
+
+
+def _plans(case, adjacent, with_text=True):
+    lay = SceneLayout(case['lengths'], halo=case['halo'], sides=case['sides'], extra=case['extra'])
+    counts = case['counts'] if with_text else None
+    Le = case['Le'] if with_text else 0
+    plan = ScopePlan(lay, case['T'], counts, Le, case['scene_rope'], case['rope_lengths'], adjacent, with_text, DEV,
+                     moves=True)
+    olay = OL.SceneLayout(case['lengths'], case['halo'], case['sides'], case['extra'])
+    sc = OL.hunyuan_scopes(olay, case['T'], case['counts'] if with_text else [0] * len(case['lengths']), Le,
+                           scene_rope=case['scene_rope'], rope_lengths=case['rope_lengths'], adjacent=adjacent,
+                           with_text=with_text)
+    return plan, sc
+
+
+def _check_plan(plan, sc, adjacent):
+    torch.cuda.synchronize()
+    eq = lambda t, a: np.array_equal(t.cpu().numpy().astype(np.int64), np.asarray(a, np.int64))
+    assert eq(plan.cu_q, sc.cu_q) and eq(plan.cu_k, sc.cu_k)
+    first = [int(sc.q_src[a]) if b > a else -1 for a, b in zip(sc.cu_q[:-1], sc.cu_q[1:])]
+    got_first = plan.seg_q_src.cpu().numpy()
+    assert all(f == -1 or f == g for f, g in zip(first, got_first))
+    assert eq(plan.q_src, sc.q_src) and eq(plan.k_src, sc.k_src)
+    assert eq(plan.q_rope, sc.q_rope) and eq(plan.k_rope, sc.k_rope)
+    if adjacent:
+        assert eq(plan.k_move_a, sc.k_move_a) and eq(plan.k_move_b, sc.k_move_b)
+    assert (plan.n_seg, plan.sum_q, plan.sum_k) == (len(sc.lq), int(sc.cu_q[-1]), int(sc.cu_k[-1]))
+
+
+@pytest.mark.parametrize('name', ['config1', 'config2', 'config3', 'config4_K2', 'config4_K4', 'config4_K8',
+                                  'config4_K12'])
+@pytest.mark.parametrize('adjacent', [False, True])
+def test_layout_kernel_bit_exact_configs(name, adjacent):
+    case = layout_case(name)
+    print(f'layout {name} adjacent={adjacent}', flush=True)
+    plan, sc = _plans(case, adjacent)
+    _check_plan(plan, sc, adjacent)
+    if name == 'config2':
+        assert plan.cu_q.tolist() == [0, 12720, 12848, 25568, 25696, 38416, 38544, 51264, 51392]
+        assert plan.cu_k.tolist() == [0, 17618, 30466, 48084, 60932, 78550, 91398, 109016, 121864]
+
+
+def test_layout_kernel_bit_exact_random_layouts():
+    rng = np.random.default_rng(7)
+    for it in range(60):
+        n = int(rng.integers(1, 9))
+        lengths = rng.integers(1, 7, n).tolist()
+        F = sum(lengths)
+        extra = {j: rng.integers(0, F, int(rng.integers(0, 5))).tolist() for j in range(n) if rng.random() < 0.7}
+        rope_lengths = None
+        if rng.random() < 0.3:   # scene RoPE over different scene lengths than the attention layout
+            rl = []
+            left = F
+            while left > 0:
+                x = int(rng.integers(1, left + 1))
+                rl.append(x)
+                left -= x
+            rope_lengths = rl
+        case = dict(lengths=lengths, halo=int(rng.integers(0, 3)), sides=['adj', 'prev', 'next'][int(rng.integers(3))],
+                    extra=extra, T=int(rng.integers(1, 12)), counts=rng.integers(0, 6, n).tolist(),
+                    scene_rope=bool(rng.integers(2)), rope_lengths=rope_lengths)
+        case['Le'] = sum(case['counts']) + int(rng.integers(0, 3))
+        adjacent = bool(rng.integers(2))
+        with_text = bool(rng.integers(2))
+        plan, sc = _plans(case, adjacent, with_text)
+        _check_plan(plan, sc, adjacent)
+
+
+def test_layout_kernel_max_scenes():
+    lengths = [1 + (j % 3) for j in range(64)]
+    F = sum(lengths)
+    case = dict(lengths=lengths, halo=1, sides='adj', extra={j: [(7 * j) % F, (11 * j + 3) % F] for j in range(64)},
+                T=5, counts=[j % 4 for j in range(64)], Le=200, scene_rope=True, rope_lengths=None)
+    for adjacent in (False, True):
+        plan, sc = _plans(case, adjacent)
+        _check_plan(plan, sc, adjacent)
+
+
+def _tables(case):
+    F, Hh, Ww = case['table']
+    assert Hh * Ww == case['T']
+    return OA.rope_table_3d(F, Hh, Ww, case['D'])
+
+
+@pytest.mark.parametrize('name', ['config1', 'config2', 'config3'])
+@pytest.mark.parametrize('adjacent', [False, True])
+def test_pack_gather_bit_exact(name, adjacent):
+    case = layout_case(name)
+    print(f'pack {name} adjacent={adjacent}', flush=True)
+    H, D, T = case['H'], case['D'], case['T']
+    S = sum(case['lengths']) * T
+    plan, sc = _plans(case, adjacent)
+    cos, sin = _tables(case)
+    q, k, v = (rand_bf16((S, H, D), s) for s in (1, 2, 3))
+    eq, ek, ev = (rand_bf16((case['Le'], H, D), s) for s in (4, 5, 6))
+    gq, gk, gv, geq, gek, gev = (x.to(DEV) for x in (q, k, v, eq, ek, ev))
+    gcos, gsin = cos.to(DEV), sin.to(DEV)
+    for mode in ('raw', 'rotated', 'none'):
+        kp, vp = pack_rows(plan, gk, gek, 'k', b_video=gv, b_text=gev, cos=gcos, sin=gsin, mode=mode)
+        qp = pack_rows(plan, gq, geq, 'q', cos=gcos, sin=gsin, mode='raw' if mode == 'raw' else 'none')
+        rq, rk, rv = OA.pack(sc, q, k, v, eq, ek, ev, cos, sin, mode=mode)
+        torch.cuda.synchronize()
+        assert torch.equal(bits(vp.cpu()), bits(rv)), mode
+        assert torch.equal(bits(kp.cpu()), bits(rk)), mode
+        assert torch.equal(bits(qp.cpu()), bits(rq)), mode
+        del kp, vp, qp
+
+
+@pytest.mark.parametrize('name', ['config1', 'config2'])
+def test_scatter_bit_exact(name):
+    case = layout_case(name)
+    H, D, T = case['H'], case['D'], case['T']
+    S = sum(case['lengths']) * T
+    plan, sc = _plans(case, False)
+    o = rand_bf16((plan.sum_q, H, D), 9)
+    le_pad = case['Le'] + 3        # text rows past the valid tokens must come back zero
+    ov = torch.full((S, H, D), 7.0, dtype=torch.bfloat16, device=DEV)
+    ot = torch.full((le_pad, H, D), 7.0, dtype=torch.bfloat16, device=DEV)
+    plan2 = ScopePlan(SceneLayout(case['lengths'], halo=case['halo'], sides=case['sides'], extra=case['extra']), T,
+                      case['counts'], le_pad, case['scene_rope'], None, False, True, DEV)
+    scatter(plan2, o.to(DEV), ov, ot)
+    rv, rt = OA.write_back(sc, o, le_pad, torch.bfloat16)
+    torch.cuda.synchronize()
+    assert torch.equal(bits(ov.cpu()), bits(rv))
+    assert torch.equal(bits(ot.cpu()), bits(rt))

@@ -1,0 +1,169 @@
+"""CPU tests of the product's host side: the drop-in Python API against the reference's known answers, and the C ABI
+(every declared symbol exported, the host planner's sizes against the oracle, argument errors) without a GPU."""
+import ctypes
+import json
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from onereel_amd import _lib as L
+from onereel_amd import comm, hunyuan15 as HY
+from onereel_amd.frame_memory import FrameMemory
+from onereel_amd.layout import SceneLayout
+from onereel_amd.scene import _desc
+from oracle import layout as OL
+
+ROOT = Path(__file__).resolve().parents[1]
+GOLD = json.loads((ROOT / 'tests' / 'golden' / 'known_answers.json').read_text())
+RT, HD = GOLD['reference_tests'], GOLD['hand_derived']
+
+
+def _extra(d):
+    return {int(j): list(v) for j, v in d.items()}
+
+
+def test_layout_api_known_answers():
+    g = RT['halo_order']
+    lay = SceneLayout(g['lengths'], halo=2)
+    assert lay.halo_frames(0) == g['halo_frames']['0'] and lay.halo_frames(1) == g['halo_frames']['1']
+    assert lay.key_frames(1) == g['key_frames_1'] and list(lay.key_range(1)) == g['key_range_1']
+    assert SceneLayout(g['lengths'], halo=2, sides='next').halo_frames(1) == g['next_halo_frames_1']
+    assert SceneLayout.even(21, 3).lengths == RT['even_21_3']['lengths']
+    assert SceneLayout.even(20, 3).scene_of_frame().tolist() == [f * 3 // 20 for f in range(20)]
+    g = RT['extra_shared']
+    lay = SceneLayout(g['lengths'], halo=0, extra=_extra(g['extra']))
+    assert lay.shared_frames(0) == g['shared_frames_0'] and lay.key_frames(1) == g['key_frames_1']
+    assert [list(x) for x in comm.runs(RT['runs']['frames'])] == RT['runs']['out']
+    assert [list(x) for x in comm.frame_tokens([3, 4, 1, 2], 10)] == RT['frame_tokens']['out']
+    assert comm.merge([(5, 7), (0, 2), (2, 3), (6, 9)]) == [(0, 3), (5, 9)]
+    assert comm.clip([(0, 3), (5, 9)], 2, 6) == [(2, 3), (5, 6)]
+    with pytest.raises(AssertionError):
+        SceneLayout([2, 0])
+    with pytest.raises(AssertionError):
+        SceneLayout([2, 2], sides='both')
+
+
+def test_frame_memory_api():
+    g = RT['fallback_extra']
+    lay = SceneLayout(g['lengths'], halo=0)
+    fm = FrameMemory(budget=2, fallback=(1, 'adj'))
+    fm.reset(lay, n_layers=8)
+    assert fm.layer == 4 and lay.extra == _extra(g['extra'])
+    fm.begin_step(0)
+    fm.set_representatives([7, 1])
+    assert lay.extra == _extra(g['extra'])
+    fm.begin_step(1)
+    assert lay.extra == {0: [7], 1: [1, 7], 2: [1]}
+    g = RT['sink_extra']
+    lay = SceneLayout(g['lengths'], halo=0)
+    fm = FrameMemory(budget=3, fallback=(0, 'adj'), sink=(0,))
+    fm.reset(lay, n_layers=4)
+    assert lay.extra == _extra(g['extra']) and 0 not in fm.candidate_frames()
+    c = FrameMemory(budget=3, candidates='boundary')
+    c.reset(SceneLayout([4, 4, 4], halo=0), 4)
+    assert c.candidate_frames() == [0, 3, 4, 7, 8, 11]
+
+
+def test_position_helpers_known_answers():
+    g = HD['shared_pos_layout']
+    lay = SceneLayout(g['lengths'], halo=0, extra=_extra(g['extra']))
+    ctx = HY.Context(lay, T=24, scene_rope=True)
+    for j in range(4):
+        assert HY.adjacent_positions(lay, j) == g['adjacent_positions'][str(j)]
+        assert HY.shared_positions(ctx, j) == g['scene_rope_shared_positions'][str(j)]
+    for f, p in g['scene_rope_frame_position'].items():
+        assert HY.frame_position(ctx, int(f)) == p
+    ctx = HY.Context(lay, shared_pos='switch', shared_switch=5, cfg=True)
+    ctx.fwd = 10
+    assert ctx.step() == 4 and not ctx.adjacent()
+    ctx.fwd = 11
+    assert ctx.step() == 5 and ctx.adjacent() and ctx.cond()
+
+
+def _header_symbols():
+    text = (ROOT / 'include' / 'onereel_hip.h').read_text()
+    return sorted(set(re.findall(r'^\s*(?:int|int64_t|const char\*)\s+(or_\w+)\s*\(', text, re.M)))
+
+
+def test_library_exports_every_declared_symbol():
+    syms = _header_symbols()
+    assert len(syms) == 8, syms
+    h = ctypes.CDLL(str(L.LIB_PATH))
+    for s in syms:
+        assert hasattr(h, s), s
+    assert set(syms) == set(L.SIGNATURES)
+    assert L.lib().or_version().startswith(b'onereel_hip')
+
+
+def _random_layout(rng):
+    n = int(rng.integers(1, 7))
+    lengths = rng.integers(1, 6, n).tolist()
+    F = sum(lengths)
+    extra = {j: rng.integers(0, F, int(rng.integers(0, 4))).tolist() for j in range(n) if rng.random() < 0.7}
+    return SceneLayout(lengths, halo=int(rng.integers(0, 3)), sides=['adj', 'prev', 'next'][int(rng.integers(3))],
+                       extra=extra)
+
+
+def test_host_planner_sizes_match_oracle():
+    rng = np.random.default_rng(0)
+    for _ in range(200):
+        lay = _random_layout(rng)
+        T = int(rng.integers(1, 9))
+        counts = rng.integers(0, 5, lay.n_scenes).tolist()
+        Le = sum(counts) + int(rng.integers(0, 3))
+        scene_rope, adjacent, with_text = (bool(rng.integers(2)) for _ in range(3))
+        d = _desc(lay, T, counts, Le, scene_rope, None, adjacent, with_text)
+        sz = L.LayoutSizes()
+        L.check(L.lib().or_layout_plan(ctypes.byref(d), ctypes.byref(sz)), 'plan')
+        olay = OL.SceneLayout(lay.lengths, lay.halo, lay.sides, lay.extra)
+        sc = OL.hunyuan_scopes(olay, T, counts if with_text else [0] * lay.n_scenes, Le, scene_rope=scene_rope,
+                               adjacent=adjacent, with_text=with_text)
+        assert (sz.n_seg, sz.sum_q, sz.sum_k) == (len(sc.lq), int(sc.cu_q[-1]), int(sc.cu_k[-1]))
+        assert (sz.max_q, sz.max_k) == (max(sc.lq), max(sc.lk))
+        rows = np.concatenate([sc.q_rope, sc.k_rope, sc.k_move_a, sc.k_move_b])
+        assert sz.max_rope_row >= rows.max()
+
+
+@pytest.mark.parametrize('bad, msg', [
+    (dict(extra={0: [9]}), 'extra frame 9'),
+    (dict(T=0), 'T must be positive'),
+    (dict(counts=[5, 5], Le=4), 'text counts'),
+    (dict(n=65), 'scenes'),
+])
+def test_layout_argument_errors(bad, msg):
+    n = bad.get('n', 2)
+    if n > 64:
+        with pytest.raises(ValueError, match=msg):
+            _desc(SceneLayout([1] * n, halo=0), 4, [0] * n, 0, False, None, False, True)
+        return
+    lay = SceneLayout([2, 3], halo=0, extra=bad.get('extra', {}))
+    d = _desc(lay, bad.get('T', 4), bad.get('counts', [1, 1]), bad.get('Le', 2), False, None, False, True)
+    with pytest.raises(L.HipPathError, match=msg):
+        L.check(L.lib().or_layout_plan(ctypes.byref(d), ctypes.byref(L.LayoutSizes())), 'or_layout_plan')
+
+
+def test_varlen_argument_errors_without_gpu():
+    a = L.VarlenArgs()
+    a.D, a.H, a.n_seg = 96, 1, 1
+    with pytest.raises(L.HipPathError, match='head_dim 96'):
+        L.check(L.lib().or_varlen_fwd(ctypes.byref(a), None), 'or_varlen_fwd')
+    a.D = 128
+    with pytest.raises(L.HipPathError, match='required'):
+        L.check(L.lib().or_varlen_fwd(ctypes.byref(a), None), 'or_varlen_fwd')
+    with pytest.raises(L.HipPathError, match='H\\*D'):
+        L.check(L.lib().or_pack_gather(1, 1, None, None, 4096, 4096, 0, 1, None, None, None, None, 0, 1, 64, 128, 1,
+                                       None, None), 'or_pack_gather')
+    assert L.lib().or_varlen_workspace_size(8, 51392, 16, 128) > 0
+
+
+def test_product_has_no_cpu_fallback():
+    """the product package never imports the oracle, and its compute entry points refuse CPU tensors"""
+    for p in (ROOT / 'onereel_amd').rglob('*.py'):
+        assert not re.search(r'^\s*(from|import)\s+oracle', p.read_text(), re.M), p
+    from onereel_amd import scene
+    x = torch.zeros(4, 2, 64, dtype=torch.bfloat16)
+    with pytest.raises(TypeError, match='GPU'):
+        scene.varlen(x, x, x, torch.zeros(2, dtype=torch.int32), torch.zeros(2, dtype=torch.int32), 4, 4)

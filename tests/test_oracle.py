@@ -1,0 +1,267 @@
+"""Pins the CPU oracle (oracle/) before it is trusted as the checker of the HIP path.
+
+Sources of truth, none of them the oracle's own formulas: the reference's test known answers and hand-derived values
+(tests/golden/known_answers.json), textbook identities (complex multiplication for RoPE, an explicit float64 softmax
+for attention), the reference's RoPE-composition invariant (tests/test_shared_pos.py of the reference), and a brute-
+force masked attention over the scope definition (src/onereel/README.md:11-15).
+"""
+import json
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention as OA
+from oracle import layout as OL
+
+GOLD = json.loads((Path(__file__).parent / 'golden' / 'known_answers.json').read_text())
+RT, HD = GOLD['reference_tests'], GOLD['hand_derived']
+
+
+def _extra(d):
+    return {int(j): list(v) for j, v in d.items()}
+
+
+# ---------------------------------------------------------------------------------------------- layout known answers
+def test_even_and_scene_of_frame():
+    g = RT['even_21_3']
+    assert OL.SceneLayout.even(g['n_frames'], g['n_scenes']).lengths == g['lengths']
+    assert OL.SceneLayout.even(20, 3).scene_of_frame() == [f * 3 // 20 for f in range(20)]
+
+
+def test_halo_order_and_sides():
+    g = RT['halo_order']
+    lay = OL.SceneLayout(g['lengths'], halo=g['halo'])
+    for j, exp in g['halo_frames'].items():
+        assert lay.halo_frames(int(j)) == exp
+    assert lay.key_frames(1) == g['key_frames_1']
+    assert list(lay.key_range(1)) == g['key_range_1']
+    assert OL.SceneLayout(g['lengths'], halo=2, sides='next').halo_frames(1) == g['next_halo_frames_1']
+    assert OL.SceneLayout(g['lengths'], halo=2, sides='prev').halo_frames(1) == g['prev_halo_frames_1']
+    assert OL.SceneLayout(RT['halo_zero']['lengths'], halo=0).halo_frames(0) == []
+
+
+def test_runs_and_frame_tokens():
+    assert [list(r) for r in OL.runs(RT['runs']['frames'])] == RT['runs']['out']
+    g = RT['frame_tokens']
+    assert [list(r) for r in OL.frame_tokens(g['frames'], g['T'])] == g['out']
+
+
+def test_shared_frames_with_extra():
+    g = RT['extra_shared']
+    lay = OL.SceneLayout(g['lengths'], halo=0, extra=_extra(g['extra']))
+    assert lay.shared_frames(0) == g['shared_frames_0']
+    assert lay.key_frames(1) == g['key_frames_1']
+    assert lay.shared_frames(2) == g['shared_frames_2']
+
+
+@pytest.mark.parametrize('name', ['fallback_extra', 'sink_extra'])
+def test_frame_memory_fallback(name):
+    g = RT[name]
+    lay = OL.SceneLayout(g['lengths'], halo=0)
+    fm = OL.FrameMemoryExtra(budget=g['budget'], fallback=tuple(g['fallback']), sink=tuple(g['sink']))
+    fm.reset(lay)
+    assert lay.extra == _extra(g['extra'])
+
+
+def test_frame_memory_next_step_applies_reps():
+    """tests/test_onereel_frame_memory.py:19-36: same step unchanged, next step extra[j] = reps outside scene j"""
+    lay = OL.SceneLayout([3, 3, 3], halo=0)
+    fm = OL.FrameMemoryExtra(budget=2, fallback=(1, 'adj'))
+    fm.reset(lay)
+    fm.begin_step(0)
+    fm.propose([7, 1])
+    assert lay.extra == {0: [3], 1: [2, 6], 2: [5]}
+    fm.begin_step(1)
+    assert fm.history[-1] == [1, 7]
+    for j, (lo, hi) in enumerate(lay.ranges):
+        assert lay.extra[j] == [f for f in [1, 7] if not lo <= f < hi]
+
+
+def test_config2_extra_from_reps():
+    g = HD['config2_hunyuan480p']
+    lay = OL.SceneLayout(g['lengths'], halo=0)
+    fm = OL.FrameMemoryExtra(budget=4, fallback=(0, 'adj'))
+    fm.reset(lay)
+    fm.propose(g['reps'])
+    fm.begin_step(1)
+    assert lay.extra == _extra(g['extra'])
+    assert [list(x) for x in OL.frame_tokens(lay.key_frames(0), g['T'])] == g['key_frame_tokens_0']
+
+
+def test_shared_repeat_kept_as_reference():
+    """layout.py:69 filters extra[j] against the halo list only: a repeated extra frame stays repeated"""
+    lay = OL.SceneLayout([2, 2, 2], halo=1, extra={0: [5, 5, 2, 0]})
+    assert lay.shared_frames(0) == [2, 5, 5]
+
+
+# ---------------------------------------------------------------------------------------------- positions
+def test_positions_hand_derived():
+    g = HD['shared_pos_layout']
+    lay = OL.SceneLayout(g['lengths'], halo=0, extra=_extra(g['extra']))
+    for j in range(lay.n_scenes):
+        assert lay.shared_frames(j) == g['shared_frames'][str(j)]
+        assert OL.adjacent_positions(lay, j) == g['adjacent_positions'][str(j)]
+        assert OL.shared_positions(lay, j, False) == g['adjacent_positions'][str(j)]
+        assert OL.shared_positions(lay, j, True) == g['scene_rope_shared_positions'][str(j)]
+    for f, p in g['scene_rope_frame_position'].items():
+        assert OL.frame_position(lay, int(f), True) == p
+    assert OL.frame_position(lay, 17, False) == 17
+
+
+def test_scene_rope_rows_hand_and_brute():
+    g = HD['scene_rope_rows_3_3_T2']
+    assert OL.scene_rope_rows(OL.SceneLayout(g['lengths'], halo=0), g['T']).tolist() == g['rows']
+    lay = OL.SceneLayout([5, 2, 4], halo=0)
+    rows = OL.scene_rope_rows(lay, 3)
+    brute = [OL.frame_position(lay, t // 3, True) * 3 + t % 3 for t in range(lay.n_frames * 3)]
+    assert rows.tolist() == brute
+
+
+def test_adjacent_positions_with_repeats():
+    """a repeated shared frame takes the position of its last occurrence (dict semantics, hunyuan15.py:98-100)"""
+    lay = OL.SceneLayout([3, 3, 3], halo=0, extra={1: [0, 0, 7]})
+    assert lay.shared_frames(1) == [0, 0, 7]
+    assert OL.adjacent_positions(lay, 1) == [2, 2, 6]
+    assert OL.shared_positions(lay, 1, True) == [5, 5, 6]
+
+
+# ---------------------------------------------------------------------------------------------- scopes
+@pytest.mark.parametrize('variant', ['scene_rope_adjacent', 'scene_rope_source', 'global_adjacent'])
+def test_tiny_scopes_hand_derived(variant):
+    g = HD['tiny_scopes']
+    lay = OL.SceneLayout(g['lengths'], halo=g['halo'], extra=_extra(g['extra']))
+    sc = OL.hunyuan_scopes(lay, g['T'], g['counts'], g['text_rows'], scene_rope=variant.startswith('scene'),
+                           adjacent=variant.endswith('adjacent'))
+    assert sc.lq == g['lq'] and sc.lk == g['lk']
+    assert sc.cu_q.tolist() == g['cu_q'] and sc.cu_k.tolist() == g['cu_k']
+    assert sc.q_src.tolist() == g['q_src'] and sc.k_src.tolist() == g['k_src']
+    exp = g[variant]
+    assert sc.q_rope.tolist() == exp['q_rope']
+    assert sc.k_rope.tolist() == exp['k_rope']
+    if 'k_move_a' in exp:
+        assert sc.k_move_a.tolist() == exp['k_move_a'] and sc.k_move_b.tolist() == exp['k_move_b']
+
+
+def test_config_scope_sizes():
+    g = HD['config1_cpu_plumbing']
+    sc = OL.hunyuan_scopes(OL.SceneLayout(g['lengths'], halo=0, extra=_extra(g['extra'])), g['T'], g['counts'])
+    assert sc.lq == g['lq'] and sc.lk == g['lk']
+    assert OA.useful_flops(sc.lq, sc.lk, 2, 64) == pytest.approx(g['useful_flop_H2_D64'], rel=1e-3)
+    g = HD['config2_hunyuan480p']
+    sc = OL.hunyuan_scopes(OL.SceneLayout(g['lengths'], halo=0, extra=_extra(g['extra'])), g['T'], g['counts'],
+                           scene_rope=True, adjacent=True)
+    assert sc.cu_q.tolist() == g['cu_q'] and sc.cu_k.tolist() == g['cu_k']
+    assert (sc.max_q, sc.max_k) == (g['max_q'], g['max_k'])
+    assert OA.useful_flops(sc.lq, sc.lk, 16, 128) == pytest.approx(g['useful_flop_H16_D128'], rel=1e-4)
+    g = HD['config3_wan704']
+    lay = OL.SceneLayout(g['lengths'], halo=g['halo'], sides=g['sides'])
+    sc = OL.hunyuan_scopes(lay, g['T'], g['counts'])
+    assert sc.lq == g['lq'] and sc.lk == g['lk']
+    _, kr = OL.wan_ranges(lay, g['T'])
+    assert [[a // g['T'], b // g['T']] for a, b in kr] == g['wan_k_ranges_frames']
+    g = HD['config4_uneven_K12']
+    rng = np.random.default_rng(12)
+    lengths = rng.integers(2, 17, 12).tolist()
+    text = rng.integers(64, 257, 12).tolist()
+    assert lengths == g['lengths']
+    F = sum(lengths)
+    reps = sorted({int(x) for x in np.linspace(0, F - 1, 4).round()})
+    lay = OL.SceneLayout(lengths, halo=0)
+    fm = OL.FrameMemoryExtra(budget=4, fallback=(0, 'adj'))
+    fm.reset(lay)
+    fm.propose(reps)
+    fm.begin_step(1)
+    sc = OL.hunyuan_scopes(lay, 1590, text)
+    assert (int(sc.cu_q[-1]), int(sc.cu_k[-1])) == (g['sum_lq'], g['sum_lk'])
+    assert OA.useful_flops(sc.lq, sc.lk, 16, 128) == pytest.approx(g['useful_flop_H16_D128'], rel=1e-3)
+
+
+def test_scopes_brute_force_membership():
+    """every packed key row of V_j is a token of key_frames(j) or of sentence j, in the order own frames, shared
+    frames, text; every video token is a query of exactly one scope"""
+    lay = OL.SceneLayout([3, 4, 2], halo=1, sides='adj', extra={0: [8], 2: [0, 1]})
+    T, counts = 3, [2, 0, 3]
+    sc = OL.hunyuan_scopes(lay, T, counts, 7)
+    S = lay.n_frames * T
+    assert sorted(sc.q_src[sc.q_src < S].tolist()) == list(range(S))
+    tr = OL.text_ranges(counts)
+    for s, (kind, j) in enumerate(zip(sc.kind, sc.scene)):
+        keys = sc.k_src[sc.cu_k[s]:sc.cu_k[s + 1]].tolist()
+        frames = lay.key_frames(j) if kind == 'v' else lay.frames[j]
+        exp = [f * T + x for f in frames for x in range(T)] + [S + t for t in range(*tr[j])]
+        assert keys == exp
+
+
+# ---------------------------------------------------------------------------------------------- RoPE
+def test_rope_matches_complex_multiplication():
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(40, 3, 16, generator=g)
+    ang = torch.rand(40, 8, generator=g) * 6.0
+    cos, sin = ang.cos().repeat_interleave(2, 1), ang.sin().repeat_interleave(2, 1)
+    out = OA.apply_rotary_emb(x, cos, sin)
+    z = torch.view_as_complex(x.double().reshape(40, 3, 8, 2).contiguous())
+    w = torch.polar(torch.ones(40, 8, dtype=torch.float64), ang.double())[:, None]
+    ref = torch.view_as_real(z * w).reshape(40, 3, 16)
+    assert (out.double() - ref).abs().max() < 1e-5
+    assert OA.apply_rotary_emb(x.bfloat16(), cos, sin).dtype == torch.bfloat16
+
+
+@pytest.mark.parametrize('scene_rope', [False, True])
+def test_move_shared_composition_invariant(scene_rope):
+    """tests/test_shared_pos.py of the reference: a shared key rotated at its own frame and moved by _move_shared
+    equals the key rotated at its adjacent position (max err < 1e-4, fp32), on its synthetic 3D table"""
+    cos, sin = OA.rope_table_3d(30, 4, 6, 128)
+    T = 24
+    g = HD['shared_pos_layout']
+    lay = OL.SceneLayout(g['lengths'], halo=0, extra=_extra(g['extra']))
+    sc = OL.hunyuan_scopes(lay, T, [0] * 4, 0, scene_rope=scene_rope, adjacent=True, with_text=False)
+    src_rows = torch.as_tensor(OL.scene_rope_rows(lay, T) if scene_rope else np.arange(lay.n_frames * T))
+    gen = torch.Generator().manual_seed(0)
+    k0 = torch.randn(int(sc.cu_k[-1]), 2, 128, generator=gen)
+    ksrc = torch.as_tensor(sc.k_src)
+    rotated = OA.apply_rotary_emb(k0, cos[src_rows[ksrc]], sin[src_rows[ksrc]])
+    moved = OA.move_shared(rotated, sc.k_move_a, sc.k_move_b, cos, sin)
+    direct = OA.rotate_rows(k0, sc.k_rope, cos, sin)
+    assert (moved - direct).abs().max().item() < 1e-4
+    assert (torch.as_tensor(sc.k_move_a) >= 0).sum() == sum(len(lay.shared_frames(j)) for j in range(4)) * T
+
+
+# ---------------------------------------------------------------------------------------------- attention
+def test_packed_attention_matches_explicit_softmax():
+    g = torch.Generator().manual_seed(1)
+    lq, lk = [5, 1, 17], [9, 3, 30]
+    H, D = 2, 16
+    q = torch.randn(sum(lq), H, D, generator=g)
+    k = torch.randn(sum(lk), H, D, generator=g)
+    v = torch.randn(sum(lk), H, D, generator=g)
+    cq, ck = np.cumsum([0] + lq), np.cumsum([0] + lk)
+    out = OA.packed_attention(q, k, v, cq, ck)
+    for s in range(3):
+        qs, ks, vs = (x.double() for x in (q[cq[s]:cq[s + 1]], k[ck[s]:ck[s + 1]], v[ck[s]:ck[s + 1]]))
+        for h in range(H):
+            p = torch.exp((qs[:, h] @ ks[:, h].T) / D ** 0.5)
+            ref = (p / p.sum(1, keepdim=True)) @ vs[:, h]
+            assert (out[cq[s]:cq[s + 1], h].double() - ref).abs().max() < 1e-5
+
+
+@pytest.mark.parametrize('case', [
+    dict(lengths=[3, 3], halo=0, extra={0: [5], 1: [0]}, T=8, counts=[4, 4], Le=8),     # config-1 shape, smaller T
+    dict(lengths=[2, 3, 2], halo=1, extra={}, T=4, counts=[3, 0, 2], Le=7),             # halo, empty sentence, padding
+    dict(lengths=[4, 2], halo=2, sides='next', extra={}, T=5, counts=[2, 2], Le=4),
+])
+def test_packed_layer_equals_masked_brute_force(case):
+    """packed scopes + per-scope SDPA + write-back == dense masked softmax over the scope definition"""
+    lay = OL.SceneLayout(case['lengths'], halo=case['halo'], sides=case.get('sides', 'adj'), extra=case['extra'])
+    T, Le = case['T'], case['Le']
+    g = torch.Generator().manual_seed(2)
+    S, H, D = lay.n_frames * T, 2, 16
+    q, k, v = (torch.randn(S, H, D, generator=g) for _ in range(3))
+    eq, ek, ev = (torch.randn(Le, H, D, generator=g) for _ in range(3))
+    sc = OL.hunyuan_scopes(lay, T, case['counts'], Le)
+    ov, ot = OA.scene_layer(sc, q, k, v, eq, ek, ev, mode='none')
+    rv, rt = OA.masked_reference(lay, T, case['counts'], q, k, v, eq, ek, ev)
+    assert (ov - rv).abs().max() < 1e-5
+    assert (ot - rt).abs().max() < 1e-5
+    assert ot[sum(case['counts']):].abs().max() == 0 if Le > sum(case['counts']) else True
