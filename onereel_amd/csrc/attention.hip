@@ -472,6 +472,7 @@ extern "C" int or_varlen_fwd(const or_varlen_args* p, void* stream) {
   if (x.sum_q < 0) return fail_arg("or_varlen_fwd: sum_q < 0");
   if (!x.q || !x.k || !x.v || !x.o || !x.cu_q) return fail_arg("or_varlen_fwd: q, k, v, o and cu_q are required");
   if (!x.cu_k && !(x.k_off && x.k_len)) return fail_arg("or_varlen_fwd: need cu_k, or k_off with k_len");
+  if (x.k_off && !x.k_len) return fail_arg("or_varlen_fwd: k_off needs k_len (the per-segment key counts)");
   if (x.q_rope && (!x.cos_table || !x.sin_table || x.n_rope_rows < 1))
     return fail_arg("or_varlen_fwd: q_rope needs cos / sin tables");
   if (x.q_row_stride < (int64_t)x.H * x.D || x.k_row_stride < (int64_t)x.H * x.D || x.o_row_stride < (int64_t)x.H * x.D)
@@ -519,7 +520,8 @@ extern "C" int or_varlen_fwd(const or_varlen_args* p, void* stream) {
   a.c = x.scale * 1.4426950408889634f;
   int32_t* ws = (int32_t*)x.workspace;
   hipStream_t st = (hipStream_t)stream;
-  hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(kPlanThreads), 0, st, x.cu_q, x.k_off ? x.k_off : x.cu_k,
+  // the planner needs key counts only: k_len when given, else the cu_k differences
+  hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(kPlanThreads), 0, st, x.cu_q, x.k_len ? nullptr : x.cu_k,
                      x.k_len, x.n_seg, x.H, (int)max_items, ws);
   if (int rc = check_hip(hipGetLastError(), "plan_kernel launch")) return rc;
   if (x.D == 128)
