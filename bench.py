@@ -63,7 +63,7 @@ def time_events(fn, reps, stream):
     return a.elapsed_time(b) / reps
 
 
-def cpu_baseline(heads=4, runs=3):
+def cpu_baseline(heads=16, runs=3):
     """the oracle's packing + per-scope fp32 SDPA on the host CPU, for `heads` of the 16 heads (median of runs)"""
     import numpy as np
     import torch
