@@ -22,7 +22,9 @@ HIPCC = os.environ.get('HIPCC', '/opt/rocm/bin/hipcc')
 FLAGS = [f'--offload-arch={ARCH}', '-O3', '-std=c++17', '-fPIC', '-I', str(INCLUDE),
          # packed-FP32 VALU ops are disabled on purpose; hipcc's host pass warns that it does not know the feature
          '-Xclang', '-target-feature', '-Xclang', '-packed-fp32-ops',
-         '-Wno-unused-result', '-munsafe-fp-atomics']
+         # MFMA accumulators in VGPRs: the softmax rescales them with VALU ops, which cannot address AGPRs
+         '-mllvm', '-amdgpu-mfma-vgpr-form=1',
+         '-Wno-unused-result']
 
 
 def _run(cmd):

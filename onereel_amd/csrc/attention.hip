@@ -65,13 +65,6 @@ __device__ __forceinline__ int seg_k_len(const AttnArgs& a, int s) {
 // A-operand row permutation of the S^T MFMA: row i = 8g + 4h + c reads key 16h + 4g + c
 __device__ __forceinline__ int pi32(int i) { return ((i >> 2) & 1) * 16 + (i >> 3) * 4 + (i & 3); }
 
-// 16-byte chunk swizzles: K tile rows of CH chunks; V^T rows of 8 chunks (64 keys)
-template <int CH>
-__device__ __forceinline__ int swz_k(int r) {
-  return ((r & 3) | (((r >> 4) & 1) << 2) | (((r >> 2) & 1) << 3)) & (CH - 1);
-}
-__device__ __forceinline__ int swz_v(int d) { return (d + (d >> 3)) & 7; }
-
 // ------------------------------------------------------------------------------------------------------------------
 // planner: one block. Items sorted by segment key count (descending), then segment; per segment head-major.
 __device__ inline int plan_upper_bound(const int* a, int n, int x) {
@@ -174,78 +167,187 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(const int32_t* cu_q,
 
 template <int D>
 struct Tile {
-  static constexpr int CH = D / 8;              // 16-byte chunks per K row
-  static constexpr int KS = D / 16;             // MFMA k-steps of S^T
-  static constexpr int DB = D / 32;             // 32-row blocks of O^T
-  static constexpr int KCH = kBK * CH / kThreads;        // K chunks staged per thread
-  static constexpr int VP = D / 2;                       // V column pairs
-  static constexpr int VKG = kThreads / VP;              // key groups of the V staging
-  static constexpr int VKEYS = kBK / VKG;                // keys per thread in the V staging
+  static constexpr int CH = D / 8;               // 16-byte chunks per K / V row
+  static constexpr int KS = D / 16;              // MFMA k-steps of S^T
+  static constexpr int DB = D / 32;              // 32-row blocks of O^T
+  static constexpr int LOADS = kBK * CH / kThreads;  // 16-byte direct loads per lane per tile, for K and for V
 };
 
 template <int D>
 struct Smem {
   uint16_t k[2][kBK * D];
-  uint16_t vt[2][D * kBK];
+  uint16_t v[2][kBK * D];
   int item;
 };
 
-template <int D>
-__device__ __forceinline__ void stage_load(const AttnArgs& a, int head, int k_beg, int Lk, int t, u32x4* kreg,
-                                           uint32_t* vreg) {
-  using C = Tile<D>;
-  const int tid = threadIdx.x;
-#pragma unroll
-  for (int i = 0; i < C::KCH; ++i) {
-    const int c = tid + kThreads * i;
-    const int row = c / C::CH, col = c % C::CH;
-    int key = t * kBK + row;
-    key = key < Lk ? key : Lk - 1;
-    kreg[i] = *(const u32x4*)(a.k + (int64_t)(k_beg + key) * a.ks + head * D + col * 8);
-  }
-  const int dp = tid % C::VP, kg = tid / C::VP;
-#pragma unroll
-  for (int e = 0; e < C::VKEYS; ++e) {
-    int key = t * kBK + kg * C::VKEYS + e;
-    key = key < Lk ? key : Lk - 1;
-    vreg[e] = *(const uint32_t*)(a.v + (int64_t)(k_beg + key) * a.ks + head * D + 2 * dp);
-  }
+// chunk swizzles (XOR on the 16-byte chunk index of a row). K: the S^T operand reads rows pi(l) of one chunk column,
+// spread over distinct chunks for every 16 consecutive lanes. V: the transpose read takes 4 consecutive rows x 32
+// bytes per 16 lanes; shifting each row by 2 chunks keeps them on distinct banks.
+template <int CH>
+__device__ __forceinline__ int swz_k(int r) {
+  return ((r & 3) | (((r >> 4) & 1) << 2) | (((r >> 2) & 1) << 3)) & (CH - 1);
+}
+template <int CH>
+__device__ __forceinline__ int swz_v(int r) {
+  return (2 * (r & 3)) & (CH - 1);
 }
 
+// HBM -> LDS copy of one K and one V tile (64 keys), 16 bytes per lane, lane-linear in LDS; the swizzle is applied by
+// choosing which global chunk each lane fetches. Keys past Lk re-read the last key (finite data, masked later).
 template <int D>
-__device__ __forceinline__ void stage_store(Smem<D>& sm, int buf, const u32x4* kreg, const uint32_t* vreg) {
+__device__ __forceinline__ void load_tile(const AttnArgs& a, Smem<D>& sm, int buf, int head, int k_beg, int Lk,
+                                          int t) {
   using C = Tile<D>;
-  const int tid = threadIdx.x;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
 #pragma unroll
-  for (int i = 0; i < C::KCH; ++i) {
-    const int c = tid + kThreads * i;
-    const int row = c / C::CH, col = c % C::CH;
-    *(u32x4*)(&sm.k[buf][row * D + ((col ^ swz_k<C::CH>(row)) * 8)]) = kreg[i];
-  }
-  const int dp = tid % C::VP, kg = tid / C::VP;
-#pragma unroll
-  for (int ch = 0; ch < C::VKEYS / 8; ++ch) {
-    u32x4 ev, od;
-#pragma unroll
-    for (int p = 0; p < 4; ++p) {
-      const uint32_t x = vreg[ch * 8 + 2 * p], y = vreg[ch * 8 + 2 * p + 1];
-      ev[p] = (x & 0xffffu) | (y << 16);
-      od[p] = (x >> 16) | (y & 0xffff0000u);
-    }
-    const int chunk = (kg * C::VKEYS) / 8 + ch;
-    const int d0 = 2 * dp, d1 = 2 * dp + 1;
-    *(u32x4*)(&sm.vt[buf][d0 * kBK + ((chunk ^ swz_v(d0)) * 8)]) = ev;
-    *(u32x4*)(&sm.vt[buf][d1 * kBK + ((chunk ^ swz_v(d1)) * 8)]) = od;
+  for (int i = 0; i < C::LOADS; ++i) {
+    const int base = (i * (kThreads / 64) + w) * 64;     // first LDS slot of this wavefront's instruction
+    const int slot = base + lane;
+    const int row = slot / C::CH, phys = slot % C::CH;
+    int key = t * kBK + row;
+    key = key < Lk ? key : Lk - 1;
+    const int64_t g = (int64_t)(k_beg + key) * a.ks + head * D;
+    __builtin_amdgcn_global_load_lds((const void*)(a.k + g + (phys ^ swz_k<C::CH>(row)) * 8),
+                                     (__attribute__((address_space(3))) void*)&sm.k[buf][base * 8], 16, 0, 0);
+    __builtin_amdgcn_global_load_lds((const void*)(a.v + g + (phys ^ swz_v<C::CH>(row)) * 8),
+                                     (__attribute__((address_space(3))) void*)&sm.v[buf][base * 8], 16, 0, 0);
   }
 }
 
 __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
+
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// V^T operand of O^T = V^T P^T: lane l (row d = db*32 + l%32, half h) gets keys key0 + 0..7 (8 consecutive keys)
+// through two transpose reads. Within each 16-lane group, source lane r addresses row key0 + 4t + r/4 at dims
+// base_d + 4*(r%4), and lane i receives the 4 keys of dim base_d + i.
+template <int D>
+__device__ __forceinline__ bf16x8 read_vt(const uint16_t* vtile, int key0, int db, int lane) {
+  using C = Tile<D>;
+  const int r = lane & 15, g = lane >> 4;
+  const int base_d = db * 32 + 16 * (g & 1);
+  const int d0 = base_d + 4 * (r & 3);
+  u32x2 lo, hi;
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const int row = key0 + 4 * t + (r >> 2);
+    const int phys = (d0 >> 3) ^ swz_v<C::CH>(row);
+    const uint16_t* p = vtile + row * D + phys * 8 + (d0 & 7);
+    bf16x4 x = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((__attribute__((address_space(3))) bf16x4*)p);
+    (t == 0 ? lo : hi) = __builtin_bit_cast(u32x2, x);
+  }
+  u32x4 v = {lo[0], lo[1], hi[0], hi[1]};
+  return as_bf16x8(v);
+}
 
 __device__ __forceinline__ bf16x8 pack_p8(const f32x16& p, int base) {
   u32x4 r;
 #pragma unroll
   for (int i = 0; i < 4; ++i) r[i] = pack2(p[base + 2 * i], p[base + 2 * i + 1]);
   return as_bf16x8(r);
+}
+
+// max over the 32 keys of a query: in-lane over 16, then with lane ^ 32 (v_permlane32_swap)
+__device__ __forceinline__ float pair_max(float x) {
+  const int xi = __builtin_bit_cast(int, x);
+  auto sw = __builtin_amdgcn_permlane32_swap(xi, xi, false, false);
+  return fmaxf(__builtin_bit_cast(float, (int)sw[0]), __builtin_bit_cast(float, (int)sw[1]));
+}
+
+__device__ __forceinline__ float pair_sum(float x) {
+  const int xi = __builtin_bit_cast(int, x);
+  auto sw = __builtin_amdgcn_permlane32_swap(xi, xi, false, false);
+  return __builtin_bit_cast(float, (int)sw[0]) + __builtin_bit_cast(float, (int)sw[1]);
+}
+
+// S^T for the 32 keys kb*32 + 16h + r of the tile in `ktile`, both query blocks
+template <int D>
+__device__ __forceinline__ void qk_block(const uint16_t* ktile, int kb, const bf16x8 (&qreg)[2][D / 16], int l32,
+                                         int h, f32x16 (&s)[2]) {
+  using C = Tile<D>;
+#pragma unroll
+  for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) s[qb][r] = 0.0f;
+  const int row = kb * 32 + pi32(l32);
+#pragma unroll
+  for (int ks = 0; ks < C::KS; ++ks) {
+    const int col = 2 * ks + h;
+    const bf16x8 ka = *(const bf16x8*)(ktile + row * D + ((col ^ swz_k<C::CH>(row)) * 8));
+    s[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka, qreg[0][ks], s[0], 0, 0, 0);
+    s[1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka, qreg[1][ks], s[1], 0, 0, 0);
+  }
+}
+
+// online softmax of one 32-key block (in place: s becomes p), P^T operands out
+template <int D>
+__device__ __forceinline__ void softmax_block(f32x16 (&s)[2], int key_base, int Lk, int h, float c, float (&m)[2],
+                                              float (&lsum)[2], f32x16 (&acc)[2][D / 32], bf16x8 (&pb)[2][2]) {
+  using C = Tile<D>;
+  const float NEG_INF = -__builtin_inff();
+  if (key_base + 32 > Lk) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const bool bad = key_base + 16 * h + r >= Lk;
+      s[0][r] = bad ? NEG_INF : s[0][r];
+      s[1][r] = bad ? NEG_INF : s[1][r];
+    }
+  }
+  float mx[2];
+#pragma unroll
+  for (int qb = 0; qb < 2; ++qb) {
+    float x = fmaxf(s[qb][0], s[qb][1]);
+#pragma unroll
+    for (int r = 2; r < 16; r += 2) x = fmaxf(x, fmaxf(s[qb][r], s[qb][r + 1]));
+    mx[qb] = pair_max(x);
+  }
+  // lazy rescale: the running max moves only when some query of the wavefront gains more than 2^8 over it
+  // (p stays <= 256 otherwise: exact enough in fp32 sums and bf16 operands)
+  if (__any((mx[0] - m[0]) * c > 8.0f || (mx[1] - m[1]) * c > 8.0f)) {
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) {
+      const float m_new = fmaxf(m[qb], mx[qb]);
+      const float alpha = __builtin_amdgcn_exp2f((m[qb] - m_new) * c);
+      m[qb] = m_new;
+      lsum[qb] *= alpha;
+#pragma unroll
+      for (int db = 0; db < C::DB; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[qb][db][r] *= alpha;
+    }
+  }
+#pragma unroll
+  for (int qb = 0; qb < 2; ++qb) {
+    const float mc = m[qb] * c;
+    float ls = 0.0f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[qb][r], c, -mc));
+      s[qb][r] = p;
+      ls += p;
+    }
+    lsum[qb] += ls;
+    pb[0][qb] = pack_p8(s[qb], 0);
+    pb[1][qb] = pack_p8(s[qb], 8);
+  }
+}
+
+// O^T += V^T P^T for one 32-key block
+template <int D>
+__device__ __forceinline__ void pv_block(const uint16_t* vtile, int kb, int h, int lane, const bf16x8 (&pb)[2][2],
+                                         f32x16 (&acc)[2][D / 32]) {
+  using C = Tile<D>;
+#pragma unroll
+  for (int half = 0; half < 2; ++half) {
+    const int key0 = kb * 32 + 16 * h + 8 * half;
+#pragma unroll
+    for (int db = 0; db < C::DB; ++db) {
+      const bf16x8 va = read_vt<D>(vtile, key0, db, lane);
+      acc[0][db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pb[half][0], acc[0][db], 0, 0, 0);
+      acc[1][db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pb[half][1], acc[1][db], 0, 0, 0);
+    }
+  }
 }
 
 template <int D>
@@ -273,6 +375,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
     const int q_src0 = a.seg_q_src ? a.seg_q_src[seg] : q_beg;
     const int q0 = qt * kBQ + w * kWQ;
     const bool active = q0 < Lq;
+    const int n_tiles = (Lk + kBK - 1) / kBK;
+    if (n_tiles > 0) load_tile<D>(a, sm, 0, head, k_beg, Lk, 0);
 
     // Q operand (B of S^T): lane holds query l32 of block qb, dims 16*ks + 8h .. +7
     bf16x8 qreg[2][C::KS];
@@ -302,91 +406,25 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[qb][db][r] = 0.0f;
     float m[2] = {NEG_INF, NEG_INF}, lsum[2] = {0.0f, 0.0f};
-
-    const int n_tiles = (Lk + kBK - 1) / kBK;
-    u32x4 kreg[C::KCH];
-    uint32_t vreg[C::VKEYS];
-    if (n_tiles > 0) {
-      stage_load<D>(a, head, k_beg, Lk, 0, kreg, vreg);
-      stage_store<D>(sm, 0, kreg, vreg);
-    }
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
 
     for (int t = 0; t < n_tiles; ++t) {
       const int buf = t & 1;
-      const bool more = t + 1 < n_tiles;
-      if (more) stage_load<D>(a, head, k_beg, Lk, t + 1, kreg, vreg);
+      if (t + 1 < n_tiles) load_tile<D>(a, sm, buf ^ 1, head, k_beg, Lk, t + 1);
       if (active) {
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
-          // S^T for the 32 keys kb*32 + 16h + r of this tile (both query blocks share the K operand)
-          f32x16 s[2];
-#pragma unroll
-          for (int qb = 0; qb < 2; ++qb)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) s[qb][r] = 0.0f;
-#pragma unroll
-          for (int ks = 0; ks < C::KS; ++ks) {
-            const int row = kb * 32 + pi32(l32);
-            const int col = 2 * ks + h;
-            const bf16x8 ka = *(const bf16x8*)(&sm.k[buf][row * D + ((col ^ swz_k<C::CH>(row)) * 8)]);
-            s[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka, qreg[0][ks], s[0], 0, 0, 0);
-            s[1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka, qreg[1][ks], s[1], 0, 0, 0);
-          }
-          if (t * kBK + kb * 32 + 32 > Lk) {
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-              const bool bad = t * kBK + kb * 32 + 16 * h + r >= Lk;
-              s[0][r] = bad ? NEG_INF : s[0][r];
-              s[1][r] = bad ? NEG_INF : s[1][r];
-            }
-          }
-          bf16x8 pb[2][2];  // [half][qb]
-#pragma unroll
-          for (int qb = 0; qb < 2; ++qb) {
-            float mx = s[qb][0];
-#pragma unroll
-            for (int r = 1; r < 16; ++r) mx = fmaxf(mx, s[qb][r]);
-            mx = fmaxf(mx, __shfl_xor(mx, 32));
-            // lazy rescale: the running max moves only when some query of the wavefront gains more than 2^8
-            // (p stays <= 256 otherwise: exact enough in fp32 sums and bf16 operands)
-            if (__any((mx - m[qb]) * a.c > 8.0f)) {
-              const float m_new = fmaxf(m[qb], mx);
-              const float alpha = __builtin_amdgcn_exp2f((m[qb] - m_new) * a.c);
-              m[qb] = m_new;
-              lsum[qb] *= alpha;
-#pragma unroll
-              for (int db = 0; db < C::DB; ++db)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) acc[qb][db][r] *= alpha;
-            }
-            const float mc = m[qb] * a.c;
-            float ls = 0.0f;
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-              const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[qb][r], a.c, -mc));
-              s[qb][r] = p;
-              ls += p;
-            }
-            lsum[qb] += ls;
-            pb[0][qb] = pack_p8(s[qb], 0);
-            pb[1][qb] = pack_p8(s[qb], 8);
-          }
-          // O^T[db] += V^T[d = db*32 + l32][keys kb*32 + 16h + 8*half .. +7] P^T
-#pragma unroll
-          for (int half = 0; half < 2; ++half) {
-            const int chunk = 4 * kb + 2 * h + half;
-#pragma unroll
-            for (int db = 0; db < C::DB; ++db) {
-              const int d = db * 32 + l32;
-              const bf16x8 va = *(const bf16x8*)(&sm.vt[buf][d * kBK + ((chunk ^ swz_v(d)) * 8)]);
-              acc[0][db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pb[half][0], acc[0][db], 0, 0, 0);
-              acc[1][db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pb[half][1], acc[1][db], 0, 0, 0);
-            }
-          }
-        }
+        const uint16_t* kt = sm.k[buf];
+        const uint16_t* vt = sm.v[buf];
+        f32x16 s0[2], s1[2];
+        bf16x8 pb[2][2];
+        qk_block<D>(kt, 0, qreg, l32, h, s0);
+        qk_block<D>(kt, 1, qreg, l32, h, s1);          // in flight while block 0's softmax runs
+        softmax_block<D>(s0, t * kBK, Lk, h, a.c, m, lsum, acc, pb);
+        pv_block<D>(vt, 0, h, lane, pb, acc);
+        softmax_block<D>(s1, t * kBK + 32, Lk, h, a.c, m, lsum, acc, pb);
+        pv_block<D>(vt, 1, h, lane, pb, acc);
       }
-      if (more) stage_store<D>(sm, buf ^ 1, kreg, vreg);
+      __builtin_amdgcn_s_waitcnt(0);
       __syncthreads();
     }
 
@@ -394,7 +432,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
     if (active) {
 #pragma unroll
       for (int qb = 0; qb < 2; ++qb) {
-        const float ltot = lsum[qb] + __shfl_xor(lsum[qb], 32);
+        const float ltot = pair_sum(lsum[qb]);
         const int i = q0 + qb * 32 + l32;
         if (i < Lq) {
           const float inv = n_tiles > 0 ? 1.0f / ltot : 0.0f;
@@ -410,8 +448,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
               *(uint2*)(op + d) = make_uint2(lo, hi);
             }
           if (a.lse && h == 0)
-            a.lse[(int64_t)head * a.sum_q + q_beg + i] =
-                n_tiles > 0 ? m[qb] * a.scale + logf(ltot) : NEG_INF;
+            a.lse[(int64_t)head * a.sum_q + q_beg + i] = n_tiles > 0 ? m[qb] * a.scale + logf(ltot) : NEG_INF;
         }
       }
     }

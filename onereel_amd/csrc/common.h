@@ -153,8 +153,12 @@ __device__ __forceinline__ void rot_pair(float x0, float x1, float c0, float c1,
   y1 = c + e;
 }
 
+// two floats -> packed bf16 pair, round to nearest even (v_cvt_pk_bf16_f32 on gfx950)
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
-  return (uint32_t)f2bf(lo) | ((uint32_t)f2bf(hi) << 16);
+  f32x2_t f = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2_t));
 }
 
 // 8 bf16 in `v` rotated with the table entries at element offset `off` of rows `row` (sign +1) or its inverse (-1)
