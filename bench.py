@@ -112,6 +112,9 @@ def main():
     ap.add_argument('--warmup', type=int, default=3)
     ap.add_argument('--no-cpu', action='store_true', help='skip the CPU baseline leg')
     ap.add_argument('--kernel-reps', type=int, default=10)
+    ap.add_argument('--once', action='store_true',
+                    help='profiling mode: a 1 GiB device copy (counter calibration), then the layout, pack-gather, '
+                         'attention and scatter kernels once each; prints nothing else')
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get('WORLD_SIZE', '1')) != 1:
         print('bench.py measures the single-GPU scene-attention path only: run it with --gpus 1 '
@@ -137,6 +140,19 @@ def main():
     flops = float(sum(4.0 * a * b * H * D for a, b in zip(lq, lk)))
     kbuf = torch.empty(plan.sum_k, H, D, dtype=torch.bfloat16, device=dev)
     vbuf = torch.empty_like(kbuf)
+
+    if args.once:
+        src = torch.empty(1 << 29, dtype=torch.int16, device=dev)
+        dst = torch.empty_like(src)
+        dst.copy_(src)                           # 1 GiB read + 1 GiB written
+        torch.cuda.synchronize()
+        plan.build()
+        ov, ot = scene.scene_attention(plan, q, k, v, eq, ek, ev, cos, sin, mode='raw', fused=True, kbuf=kbuf,
+                                       vbuf=vbuf)
+        scene.scatter(plan, torch.zeros(plan.sum_q, H, D, dtype=torch.bfloat16, device=dev), ov, ot)
+        torch.cuda.synchronize()
+        print('once: copy 1 GiB, layout, pack_gather, plan + attention, scatter', flush=True)
+        return
 
     def step():
         plan.build()
