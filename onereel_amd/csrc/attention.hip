@@ -15,6 +15,7 @@
 // - Softmax in base 2 with the scale folded into one FMA: p = 2^(s*c - m*c), c = scale * log2(e).
 // - Optional RoPE on the Q load (table row per packed query), with the rounding of diffusers apply_rotary_emb.
 #include <math.h>
+#include <stdlib.h>
 
 #include "common.h"
 
@@ -26,8 +27,7 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kThreads = 256;   // 4 wavefronts
-constexpr int kBQ = 256;        // queries per work item
-constexpr int kWQ = 64;         // queries per wavefront
+constexpr int kMinBQ = 128;     // smallest work-item query tile of any kernel variant (sizes the item list)
 constexpr int kBK = 64;         // keys per tile
 constexpr int kWsHeader = 64;   // int32 words before the item list
 constexpr int kPlanThreads = 1024;
@@ -78,8 +78,8 @@ __device__ inline int plan_upper_bound(const int* a, int n, int x) {
 }
 
 __global__ __launch_bounds__(kPlanThreads) void plan_kernel(const int32_t* cu_q, const int32_t* cu_k,
-                                                            const int32_t* k_len, int n_seg, int H, int max_items,
-                                                            int32_t* ws) {
+                                                            const int32_t* k_len, int n_seg, int H, int bq,
+                                                            int max_items, int32_t* ws) {
   __shared__ unsigned long long key[kMaxPlanSeg];
   __shared__ int off[kMaxPlanSeg + 1];
   __shared__ int part[kPlanThreads];
@@ -120,7 +120,7 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(const int32_t* cu_q,
     if (i < n_seg) {
       int s = (int)(key[i] & 0xffffffffu);
       int lq = cu_q[s + 1] - cu_q[s];
-      int tiles = lq > 0 ? (lq + kBQ - 1) / kBQ : 0;
+      int tiles = lq > 0 ? (lq + bq - 1) / bq : 0;
       off[i] = tiles * H;
       local += tiles * H;
     }
@@ -154,7 +154,7 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(const int32_t* cu_q,
     int i = plan_upper_bound(off, n_seg + 1, it) - 1;
     int s = (int)(key[i] & 0xffffffffu);
     int lq = cu_q[s + 1] - cu_q[s];
-    int tiles = (lq + kBQ - 1) / kBQ;
+    int tiles = (lq + bq - 1) / bq;
     int local_it = it - off[i];
     int head = local_it / tiles, t = local_it - head * tiles;
     ws[kWsHeader + 2 * it] = s;
@@ -261,52 +261,63 @@ __device__ __forceinline__ float pair_sum(float x) {
   return __builtin_bit_cast(float, (int)sw[0]) + __builtin_bit_cast(float, (int)sw[1]);
 }
 
-// S^T for the 32 keys kb*32 + 16h + r of the tile in `ktile`, both query blocks
-template <int D>
-__device__ __forceinline__ void qk_block(const uint16_t* ktile, int kb, const bf16x8 (&qreg)[2][D / 16], int l32,
-                                         int h, f32x16 (&s)[2]) {
+// S^T of the two 32-key blocks of a tile (keys kb*32 + 16h + r), for the wavefront's NQ query blocks. The K operand
+// of each (block, k-step) is read once and used by every query block; 2*NQ independent accumulation chains.
+template <int D, int NQ>
+__device__ __forceinline__ void qk_tile(const uint16_t* ktile, const bf16x8 (&qreg)[NQ][D / 16], int l32, int h,
+                                        f32x16 (&s0)[NQ], f32x16 (&s1)[NQ]) {
   using C = Tile<D>;
 #pragma unroll
-  for (int qb = 0; qb < 2; ++qb)
+  for (int qb = 0; qb < NQ; ++qb)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) s[qb][r] = 0.0f;
-  const int row = kb * 32 + pi32(l32);
+    for (int r = 0; r < 16; ++r) {
+      s0[qb][r] = 0.0f;
+      s1[qb][r] = 0.0f;
+    }
+  const int row0 = pi32(l32), row1 = 32 + pi32(l32);
 #pragma unroll
   for (int ks = 0; ks < C::KS; ++ks) {
     const int col = 2 * ks + h;
-    const bf16x8 ka = *(const bf16x8*)(ktile + row * D + ((col ^ swz_k<C::CH>(row)) * 8));
-    s[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka, qreg[0][ks], s[0], 0, 0, 0);
-    s[1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka, qreg[1][ks], s[1], 0, 0, 0);
+    const bf16x8 k0 = *(const bf16x8*)(ktile + row0 * D + ((col ^ swz_k<C::CH>(row0)) * 8));
+    const bf16x8 k1 = *(const bf16x8*)(ktile + row1 * D + ((col ^ swz_k<C::CH>(row1)) * 8));
+#pragma unroll
+    for (int qb = 0; qb < NQ; ++qb) {
+      s0[qb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(k0, qreg[qb][ks], s0[qb], 0, 0, 0);
+      s1[qb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(k1, qreg[qb][ks], s1[qb], 0, 0, 0);
+    }
   }
 }
 
 // online softmax of one 32-key block (in place: s becomes p), P^T operands out
-template <int D>
-__device__ __forceinline__ void softmax_block(f32x16 (&s)[2], int key_base, int Lk, int h, float c, float (&m)[2],
-                                              float (&lsum)[2], f32x16 (&acc)[2][D / 32], bf16x8 (&pb)[2][2]) {
+template <int D, int NQ>
+__device__ __forceinline__ void softmax_block(f32x16 (&s)[NQ], int key_base, int Lk, int h, float c, float (&m)[NQ],
+                                              float (&lsum)[NQ], f32x16 (&acc)[NQ][D / 32],
+                                              bf16x8 (&pb)[2][NQ]) {
   using C = Tile<D>;
   const float NEG_INF = -__builtin_inff();
   if (key_base + 32 > Lk) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const bool bad = key_base + 16 * h + r >= Lk;
-      s[0][r] = bad ? NEG_INF : s[0][r];
-      s[1][r] = bad ? NEG_INF : s[1][r];
+#pragma unroll
+      for (int qb = 0; qb < NQ; ++qb) s[qb][r] = bad ? NEG_INF : s[qb][r];
     }
   }
-  float mx[2];
+  float mx[NQ];
+  bool grow = false;
 #pragma unroll
-  for (int qb = 0; qb < 2; ++qb) {
+  for (int qb = 0; qb < NQ; ++qb) {
     float x = fmaxf(s[qb][0], s[qb][1]);
 #pragma unroll
     for (int r = 2; r < 16; r += 2) x = fmaxf(x, fmaxf(s[qb][r], s[qb][r + 1]));
     mx[qb] = pair_max(x);
+    grow |= (mx[qb] - m[qb]) * c > 8.0f;
   }
   // lazy rescale: the running max moves only when some query of the wavefront gains more than 2^8 over it
   // (p stays <= 256 otherwise: exact enough in fp32 sums and bf16 operands)
-  if (__any((mx[0] - m[0]) * c > 8.0f || (mx[1] - m[1]) * c > 8.0f)) {
+  if (__any(grow)) {
 #pragma unroll
-    for (int qb = 0; qb < 2; ++qb) {
+    for (int qb = 0; qb < NQ; ++qb) {
       const float m_new = fmaxf(m[qb], mx[qb]);
       const float alpha = __builtin_amdgcn_exp2f((m[qb] - m_new) * c);
       m[qb] = m_new;
@@ -318,7 +329,7 @@ __device__ __forceinline__ void softmax_block(f32x16 (&s)[2], int key_base, int 
     }
   }
 #pragma unroll
-  for (int qb = 0; qb < 2; ++qb) {
+  for (int qb = 0; qb < NQ; ++qb) {
     const float mc = m[qb] * c;
     float ls = 0.0f;
 #pragma unroll
@@ -334,9 +345,9 @@ __device__ __forceinline__ void softmax_block(f32x16 (&s)[2], int key_base, int 
 }
 
 // O^T += V^T P^T for one 32-key block
-template <int D>
-__device__ __forceinline__ void pv_block(const uint16_t* vtile, int kb, int h, int lane, const bf16x8 (&pb)[2][2],
-                                         f32x16 (&acc)[2][D / 32]) {
+template <int D, int NQ>
+__device__ __forceinline__ void pv_block(const uint16_t* vtile, int kb, int h, int lane, const bf16x8 (&pb)[2][NQ],
+                                         f32x16 (&acc)[NQ][D / 32]) {
   using C = Tile<D>;
 #pragma unroll
   for (int half = 0; half < 2; ++half) {
@@ -344,16 +355,20 @@ __device__ __forceinline__ void pv_block(const uint16_t* vtile, int kb, int h, i
 #pragma unroll
     for (int db = 0; db < C::DB; ++db) {
       const bf16x8 va = read_vt<D>(vtile, key0, db, lane);
-      acc[0][db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pb[half][0], acc[0][db], 0, 0, 0);
-      acc[1][db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pb[half][1], acc[1][db], 0, 0, 0);
+#pragma unroll
+      for (int qb = 0; qb < NQ; ++qb)
+        acc[qb][db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pb[half][qb], acc[qb][db], 0, 0, 0);
     }
   }
 }
 
-template <int D>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))) void attn_kernel(AttnArgs a,
-                                                                                                  int32_t* ws) {
+// NQ = 1: 32 queries per wavefront, 128 per block, two blocks resident per CU (two wavefronts per SIMD overlap MFMA
+// and softmax); NQ = 2: 64 queries per wavefront, 256 per block, one block per CU.
+template <int D, int NQ>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(NQ == 1 ? 2 : 1, NQ == 1 ? 2 : 1)))
+void attn_kernel(AttnArgs a, int32_t* ws) {
   using C = Tile<D>;
+  constexpr int WQ = 32 * NQ, BQ = 4 * WQ;
   __shared__ __attribute__((aligned(16))) Smem<D> sm;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int l32 = lane & 31, h = lane >> 5;
@@ -373,15 +388,15 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
     const int k_beg = seg_k_begin(a, seg);
     const int Lk = seg_k_len(a, seg);
     const int q_src0 = a.seg_q_src ? a.seg_q_src[seg] : q_beg;
-    const int q0 = qt * kBQ + w * kWQ;
+    const int q0 = qt * BQ + w * WQ;
     const bool active = q0 < Lq;
     const int n_tiles = (Lk + kBK - 1) / kBK;
     if (n_tiles > 0) load_tile<D>(a, sm, 0, head, k_beg, Lk, 0);
 
     // Q operand (B of S^T): lane holds query l32 of block qb, dims 16*ks + 8h .. +7
-    bf16x8 qreg[2][C::KS];
+    bf16x8 qreg[NQ][C::KS];
 #pragma unroll
-    for (int qb = 0; qb < 2; ++qb) {
+    for (int qb = 0; qb < NQ; ++qb) {
       int i = q0 + qb * 32 + l32;
       i = i < Lq ? i : Lq - 1;
       i = i < 0 ? 0 : i;
@@ -398,14 +413,19 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
       }
     }
 
-    f32x16 acc[2][C::DB];
+    f32x16 acc[NQ][C::DB];
 #pragma unroll
-    for (int qb = 0; qb < 2; ++qb)
+    for (int qb = 0; qb < NQ; ++qb)
 #pragma unroll
       for (int db = 0; db < C::DB; ++db)
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[qb][db][r] = 0.0f;
-    float m[2] = {NEG_INF, NEG_INF}, lsum[2] = {0.0f, 0.0f};
+    float m[NQ], lsum[NQ];
+#pragma unroll
+    for (int qb = 0; qb < NQ; ++qb) {
+      m[qb] = NEG_INF;
+      lsum[qb] = 0.0f;
+    }
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
 
@@ -415,14 +435,13 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
       if (active) {
         const uint16_t* kt = sm.k[buf];
         const uint16_t* vt = sm.v[buf];
-        f32x16 s0[2], s1[2];
-        bf16x8 pb[2][2];
-        qk_block<D>(kt, 0, qreg, l32, h, s0);
-        qk_block<D>(kt, 1, qreg, l32, h, s1);          // in flight while block 0's softmax runs
-        softmax_block<D>(s0, t * kBK, Lk, h, a.c, m, lsum, acc, pb);
-        pv_block<D>(vt, 0, h, lane, pb, acc);
-        softmax_block<D>(s1, t * kBK + 32, Lk, h, a.c, m, lsum, acc, pb);
-        pv_block<D>(vt, 1, h, lane, pb, acc);
+        f32x16 s0[NQ], s1[NQ];
+        bf16x8 pb[2][NQ];
+        qk_tile<D, NQ>(kt, qreg, l32, h, s0, s1);
+        softmax_block<D, NQ>(s0, t * kBK, Lk, h, a.c, m, lsum, acc, pb);
+        pv_block<D, NQ>(vt, 0, h, lane, pb, acc);
+        softmax_block<D, NQ>(s1, t * kBK + 32, Lk, h, a.c, m, lsum, acc, pb);
+        pv_block<D, NQ>(vt, 1, h, lane, pb, acc);
       }
       __builtin_amdgcn_s_waitcnt(0);
       __syncthreads();
@@ -431,7 +450,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
     // epilogue: combine the lane pair's row sums, normalise, store 4 consecutive dims per (db, group)
     if (active) {
 #pragma unroll
-      for (int qb = 0; qb < 2; ++qb) {
+      for (int qb = 0; qb < NQ; ++qb) {
         const float ltot = pair_sum(lsum[qb]);
         const int i = q0 + qb * 32 + l32;
         if (i < Lq) {
@@ -455,9 +474,25 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
   }
 }
 
+typedef void (*AttnFn)(AttnArgs, int32_t*);
+
+// kernel variant: queries per wavefront (ONEREEL_ATTN_WQ = 32 or 64; default 32)
+int variant_nq() {
+  static int nq = [] {
+    const char* e = getenv("ONEREEL_ATTN_WQ");
+    return (e && atoi(e) == 64) ? 2 : 1;
+  }();
+  return nq;
+}
+
+AttnFn attn_fn(int D, int nq) {
+  if (D == 128) return nq == 2 ? attn_kernel<128, 2> : attn_kernel<128, 1>;
+  return nq == 2 ? attn_kernel<64, 2> : attn_kernel<64, 1>;
+}
+
 struct DevInfo {
   int cus = 0;
-  int occ128 = 0, occ64 = 0;
+  int occ[2][2] = {{0, 0}, {0, 0}};  // [D == 128][nq - 1]
 };
 
 int dev_info(DevInfo& info) {
@@ -470,12 +505,12 @@ int dev_info(DevInfo& info) {
     if (int rc = check_hip(hipDeviceGetAttribute(&di.cus, hipDeviceAttributeMultiprocessorCount, dev),
                            "hipDeviceGetAttribute"))
       return rc;
-    if (int rc = check_hip(hipOccupancyMaxActiveBlocksPerMultiprocessor(&di.occ128, attn_kernel<128>, kThreads, 0),
-                           "hipOccupancyMaxActiveBlocksPerMultiprocessor"))
-      return rc;
-    if (int rc = check_hip(hipOccupancyMaxActiveBlocksPerMultiprocessor(&di.occ64, attn_kernel<64>, kThreads, 0),
-                           "hipOccupancyMaxActiveBlocksPerMultiprocessor"))
-      return rc;
+    for (int d = 0; d < 2; ++d)
+      for (int n = 0; n < 2; ++n)
+        if (int rc = check_hip(hipOccupancyMaxActiveBlocksPerMultiprocessor(&di.occ[d][n],
+                                                                            attn_fn(d ? 128 : 64, n + 1), kThreads, 0),
+                               "hipOccupancyMaxActiveBlocksPerMultiprocessor"))
+          return rc;
     cached = di;
     cached_dev = dev;
   }
@@ -484,7 +519,7 @@ int dev_info(DevInfo& info) {
 }
 
 int64_t max_items_of(int32_t n_seg, int32_t sum_q, int32_t H) {
-  return ((int64_t)(sum_q + kBQ - 1) / kBQ + n_seg) * H;
+  return ((int64_t)(sum_q + kMinBQ - 1) / kMinBQ + n_seg) * H;
 }
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
@@ -525,7 +560,8 @@ extern "C" int or_varlen_fwd(const or_varlen_args* p, void* stream) {
   if (x.sum_q == 0) return 0;
   DevInfo di;
   if (int rc = dev_info(di)) return rc;
-  const int occ = x.D == 128 ? di.occ128 : di.occ64;
+  const int nq = variant_nq();
+  const int occ = di.occ[x.D == 128][nq - 1];
   if (occ < 1) return fail_arg("or_varlen_fwd: attention kernel cannot be resident (occupancy 0)");
   const int64_t max_items = max_items_of(x.n_seg, x.sum_q, x.H);
   int64_t grid = (int64_t)di.cus * occ;
@@ -559,11 +595,8 @@ extern "C" int or_varlen_fwd(const or_varlen_args* p, void* stream) {
   hipStream_t st = (hipStream_t)stream;
   // the planner needs key counts only: k_len when given, else the cu_k differences
   hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(kPlanThreads), 0, st, x.cu_q, x.k_len ? nullptr : x.cu_k,
-                     x.k_len, x.n_seg, x.H, (int)max_items, ws);
+                     x.k_len, x.n_seg, x.H, 128 * nq, (int)max_items, ws);
   if (int rc = check_hip(hipGetLastError(), "plan_kernel launch")) return rc;
-  if (x.D == 128)
-    hipLaunchKernelGGL(attn_kernel<128>, dim3((unsigned)grid), dim3(kThreads), 0, st, a, ws);
-  else
-    hipLaunchKernelGGL(attn_kernel<64>, dim3((unsigned)grid), dim3(kThreads), 0, st, a, ws);
+  hipLaunchKernelGGL(attn_fn(x.D, nq), dim3((unsigned)grid), dim3(kThreads), 0, st, a, ws);
   return check_hip(hipGetLastError(), "attn_kernel launch");
 }
