@@ -16,6 +16,8 @@ INCLUDE = PKG.parent / 'include'
 LIB = PKG / 'libonereel_hip.so'
 OBJ = PKG / 'csrc' / '_obj'
 SOURCES = ['layout.hip', 'gather.hip', 'attention.hip']
+# attention: no NaN operands reach the softmax max, so fmax needs no quieting of its inputs (v_max3_f32 directly)
+SOURCE_FLAGS = {'attention.hip': ['-fno-honor-nans']}
 ARCH = os.environ.get('ONEREEL_ARCH', 'gfx950')
 
 HIPCC = os.environ.get('HIPCC', '/opt/rocm/bin/hipcc')
@@ -42,7 +44,7 @@ def build(verbose: bool = False) -> Path:
 
     def one(src_obj):
         src, obj = src_obj
-        return _run([HIPCC, *FLAGS, '-c', str(CSRC / src), '-o', str(obj)])
+        return _run([HIPCC, *FLAGS, *SOURCE_FLAGS.get(src, []), '-c', str(CSRC / src), '-o', str(obj)])
 
     with ThreadPoolExecutor(max_workers=len(SOURCES)) as ex:
         logs = list(ex.map(one, zip(SOURCES, objs)))

@@ -474,25 +474,360 @@ void attn_kernel(AttnArgs a, int32_t* ws) {
   }
 }
 
-typedef void (*AttnFn)(AttnArgs, int32_t*);
+// ------------------------------------------------------------------------------------------------------------------
+// v4: software-pipelined kernel. Keys in blocks of 32 (one MFMA block); K and V blocks stream through two rings of
+// four LDS slots each, filled by buffer loads straight into LDS three iterations ahead (out-of-range rows of a
+// segment's last block read as zeros). Iteration j of a wavefront runs the softmax of block j on the VALU while the
+// MFMA unit computes S of block j + 1 (QK^T) and O += V P^T of block j - 1, so the exponentials overlap the matrix
+// work inside one wavefront as well as across the two wavefronts that share a SIMD.
 
-// kernel variant: queries per wavefront (ONEREEL_ATTN_WQ = 32 or 64; default 32)
-int variant_nq() {
-  static int nq = [] {
-    const char* e = getenv("ONEREEL_ATTN_WQ");
-    return (e && atoi(e) == 64) ? 2 : 1;
-  }();
-  return nq;
+constexpr int kBKB = 32;   // keys per ring slot
+constexpr int kRing = 4;   // slots per ring (K ring and V ring)
+
+template <int D>
+struct R4 {
+  static constexpr int CH = D / 8;                     // 16-byte chunks per row
+  static constexpr int KS = D / 16;                    // MFMA k-steps of S^T
+  static constexpr int DB = D / 32;                    // 32-row blocks of O^T
+  static constexpr int LPB = kBKB * CH / kThreads;     // buffer loads per lane for one K (or V) block
+  static constexpr int SLOT = kBKB * D;                // bf16 elements per slot
+  static constexpr int GROUP = 2 * LPB;                // loads per lane issued by one iteration (a K and a V block)
+};
+
+// s_waitcnt immediate that waits until at most n vector-memory operations of this wavefront are outstanding
+constexpr int vmcnt_imm(int n) { return (n & 0xF) | (0x7 << 4) | (0xF << 8) | ((n >> 4) << 14); }
+
+// K slot swizzle (XOR on the 16-byte chunk index of block-local row r): the 16 lanes that one b128 read services
+// together read 16 distinct chunk positions. V slot swizzle: the 32 lanes of one transposing b64 read cover the 64
+// banks once.
+template <int CH>
+__device__ __forceinline__ int swz4_k(int r) {
+  if constexpr (CH == 16) return (r & 3) | (((r >> 4) & 1) << 2) | (((r >> 2) & 1) << 3);
+  else return ((r >> 1) & 3) | (((r >> 4) & 1) << 2);
+}
+template <int CH>
+__device__ __forceinline__ int swz4_v(int r) {
+  if constexpr (CH == 16) return 4 * (r & 3);
+  else return 4 * ((r >> 1) & 1);
 }
 
-AttnFn attn_fn(int D, int nq) {
-  if (D == 128) return nq == 2 ? attn_kernel<128, 2> : attn_kernel<128, 1>;
-  return nq == 2 ? attn_kernel<64, 2> : attn_kernel<64, 1>;
+typedef __attribute__((address_space(3))) void lds_void;
+
+// the slots are eight distinct __shared__ arrays, so that the compiler can tell a read of one slot from the loads
+// still in flight into the others (and waits for those only where they alias)
+struct Ring {
+  uint16_t* k[kRing];
+  uint16_t* v[kRing];
+};
+
+// one K or V block (rows b*32 .. b*32+31 of the segment, head columns) into an LDS slot; rows at or past Lk read 0
+template <int D>
+__device__ __forceinline__ void ring_load(const uint16_t* seg_head, int64_t rs, int b, int Lk, const uint32_t* voff,
+                                          uint16_t* slot, int w) {
+  // bytes from the block's first row to the end of its last valid row (rows past Lk fall outside); branch-free
+  const int rows = min(max(Lk - b * kBKB, 0), kBKB);
+  const int rb = (int)rs * 2;
+  const uint32_t nrec = (uint32_t)max(rows * rb - rb + D * 2, 0);
+  const uint16_t* p = seg_head + (int64_t)max(b, 0) * kBKB * rs;
+  __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc((void*)p, (short)0, (int)nrec, 0x00020000);
+#pragma unroll
+  for (int i = 0; i < R4<D>::LPB; ++i)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)(slot + (i * kThreads + w * 64) * 8), 16, voff[i], 0, 0, 0);
+}
+
+template <int D>
+__device__ __forceinline__ bf16x8 ring_vt(const uint16_t* slot, uint32_t vaddr, int half) {
+  u32x2 lo, hi;
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const char* p = (const char*)slot + vaddr + (8 * half + 4 * t) * D * 2;
+    bf16x4 x = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((__attribute__((address_space(3))) bf16x4*)p);
+    (t == 0 ? lo : hi) = __builtin_bit_cast(u32x2, x);
+  }
+  u32x4 v = {lo[0], lo[1], hi[0], hi[1]};
+  return as_bf16x8(v);
+}
+
+template <int D>
+struct St4 {
+  bf16x8 q[R4<D>::KS];
+  f32x16 acc[R4<D>::DB];
+  f32x16 s[2];
+  bf16x8 p[2][2];     // [parity][half]
+  float m, mc, lsum;
+  uint32_t kaddr[R4<D>::KS];
+  uint32_t vaddr[R4<D>::DB];
+};
+
+__device__ __forceinline__ float max16(const f32x16& s) {
+  float x = fmaxf(fmaxf(s[0], s[1]), s[2]);
+#pragma unroll
+  for (int r = 3; r < 15; r += 2) x = fmaxf(fmaxf(x, s[r]), s[r + 1]);
+  return fmaxf(x, s[15]);
+}
+
+// iteration j (J = j mod 4, compile-time so that every slot is a distinct LDS object for the compiler)
+template <int D, int J>
+__device__ __forceinline__ void iter4(St4<D>& st, const Ring& rg, int j, int nb, int Lk, bool active,
+                                      const uint16_t* kh, const uint16_t* vh, int64_t rs,
+                                      const uint32_t (&voffk)[R4<D>::LPB], const uint32_t (&voffv)[R4<D>::LPB],
+                                      int w, int h, float c) {
+  using C = R4<D>;
+  constexpr int PAR = J & 1;
+  // blocks K(j+1) and V(j-1) have landed (the loads of the last two iterations may still be in flight), every
+  // wavefront is done with iteration j-1's slots
+  __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * C::GROUP));
+  asm volatile("s_barrier" ::: "memory");
+  ring_load<D>(kh, rs, j + kRing, Lk, voffk, rg.k[J], w);
+  ring_load<D>(vh, rs, j + 2, Lk, voffv, rg.v[(J + 2) % kRing], w);
+  if (!active) return;
+
+  bf16x8 kop[C::KS];
+#pragma unroll
+  for (int ks = 0; ks < C::KS; ++ks)
+    kop[ks] = *(const bf16x8*)((const char*)rg.k[(J + 1) % kRing] + st.kaddr[ks]);
+  bf16x8 vop[2][C::DB];
+#pragma unroll
+  for (int half = 0; half < 2; ++half)
+#pragma unroll
+    for (int db = 0; db < C::DB; ++db) vop[half][db] = ring_vt<D>(rg.v[(J + 3) % kRing], st.vaddr[db], half);
+
+  f32x16& s = st.s[PAR];
+  if (j == nb - 1 && (Lk & (kBKB - 1))) {
+    int valid = Lk - j * kBKB - 16 * h;
+    asm volatile("" : "+v"(valid));   // computed here, not hoisted out of the loop as 16 lane masks in SGPRs
+#pragma unroll
+    for (int r = 0; r < 16; ++r) s[r] = r < valid ? s[r] : -__builtin_inff();
+  }
+  const float mx = pair_max(max16(s));
+  const bool grow = __builtin_fmaf(mx, c, -st.mc) > 8.0f;
+  const bool any_grow = __any(grow);
+  float alpha = 1.0f;
+  if (any_grow) {
+    const float mn = fmaxf(st.m, mx);
+    alpha = __builtin_amdgcn_exp2f((st.m - mn) * c);
+    st.m = mn;
+    st.mc = mn * c;
+  }
+  const float mc = st.mc;
+
+  // matrix work: S(j+1) = K(j+1) Q^T, O += V(j-1) P(j-1)
+  f32x16& sn = st.s[PAR ^ 1];
+  const f32x16 zero = {};
+#pragma unroll
+  for (int ks = 0; ks < C::KS; ++ks) {
+    sn = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kop[ks], st.q[ks], ks == 0 ? zero : sn, 0, 0, 0);
+    const int half = ks / C::DB, db = ks % C::DB;
+    st.acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vop[half][db], st.p[PAR ^ 1][half], st.acc[db], 0, 0, 0);
+  }
+  // vector work: P(j) = 2^(s c - m c) as bf16 pairs, and its row sum from the rounded values
+  f32x16 e;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) e[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[r], c, -mc));
+  float ls = 0.0f;
+  const bf16x2_t one = {(__bf16)1.0f, (__bf16)1.0f};
+#pragma unroll
+  for (int half = 0; half < 2; ++half) {
+    u32x4 pk;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      // the dot2 operand is the scalar, not pk[i]: hipcc (ROCm 7.2) selects element 0 for a bit_cast of pk[i]
+      const uint32_t pw = pack2(e[8 * half + 2 * i], e[8 * half + 2 * i + 1]);
+      ls = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, pw), one, ls, false);
+      pk[i] = pw;
+    }
+    st.p[PAR][half] = as_bf16x8(pk);
+  }
+#pragma unroll
+  for (int i = 0; i < 2 * C::KS; ++i) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(0x002, 48 / (2 * C::KS), 0);
+  }
+  // keeps the exponentials in this scheduling region (next to the MFMAs) instead of being sunk past the branch
+  asm volatile("" ::"v"(st.p[PAR][0]), "v"(st.p[PAR][1]), "v"(ls));
+  if (any_grow) {
+#pragma unroll
+    for (int db = 0; db < C::DB; ++db)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) st.acc[db][r] *= alpha;
+    st.lsum *= alpha;
+  }
+  st.lsum += ls;
+}
+
+template <int D>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void attn4_kernel(AttnArgs a, int32_t* ws) {
+  using C = R4<D>;
+  constexpr int WQ = 32, BQ = 4 * WQ;
+  __shared__ __attribute__((aligned(16))) uint16_t k0[C::SLOT], k1[C::SLOT], k2[C::SLOT], k3[C::SLOT];
+  __shared__ __attribute__((aligned(16))) uint16_t v0[C::SLOT], v1[C::SLOT], v2[C::SLOT], v3[C::SLOT];
+  __shared__ int item_sh;
+  const Ring rg = {{k0, k1, k2, k3}, {v0, v1, v2, v3}};
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform: LDS destinations of the loads in SGPRs
+  const int l32 = lane & 31, h = lane >> 5;
+  const int64_t rs = a.ks;
+
+  // per-lane constants: global byte offsets of this lane's buffer loads within a block, LDS byte offsets of its reads
+  uint32_t voffk[C::LPB], voffv[C::LPB];
+#pragma unroll
+  for (int i = 0; i < C::LPB; ++i) {
+    const int slot = i * kThreads + w * 64 + lane;
+    const int row = slot / C::CH, phys = slot % C::CH;
+    voffk[i] = (uint32_t)(row * rs * 2 + (phys ^ swz4_k<C::CH>(row)) * 16);
+    voffv[i] = (uint32_t)(row * rs * 2 + (phys ^ swz4_v<C::CH>(row)) * 16);
+  }
+  St4<D> st;
+  {
+    const int row = pi32(l32);
+#pragma unroll
+    for (int ks = 0; ks < C::KS; ++ks) st.kaddr[ks] = (uint32_t)(row * D * 2 + (((2 * ks + h) ^ swz4_k<C::CH>(row)) * 16));
+    const int r = lane & 15, g = lane >> 4;
+    const int cp = 2 * (g & 1) + ((r >> 1) & 1);
+    const int mv = C::CH == 16 ? ((r >> 2) & 3) : ((r >> 3) & 1);
+#pragma unroll
+    for (int db = 0; db < C::DB; ++db)
+      st.vaddr[db] = (uint32_t)((16 * h + (r >> 2)) * D * 2 + (4 * (db ^ mv) + cp) * 16 + (r & 1) * 8);
+  }
+
+  for (;;) {
+    if (tid == 0) item_sh = atomicAdd(&ws[0], 1);
+    __syncthreads();
+    const int it = item_sh;
+    __syncthreads();
+    if (it >= ws[1]) break;
+    const int seg = ws[kWsHeader + 2 * it];
+    const int packed_ht = ws[kWsHeader + 2 * it + 1];
+    const int head = packed_ht & 255, qt = packed_ht >> 8;
+    const int q_beg = a.cu_q[seg];
+    const int Lq = a.cu_q[seg + 1] - q_beg;
+    const int k_beg = seg_k_begin(a, seg);
+    const int Lk = seg_k_len(a, seg) < 0 ? 0 : seg_k_len(a, seg);
+    const int q_src0 = a.seg_q_src ? a.seg_q_src[seg] : q_beg;
+    const int q0 = qt * BQ + w * WQ;
+    const bool active = q0 < Lq;
+    const int nb = (Lk + kBKB - 1) / kBKB;
+    const uint16_t* kh = a.k + (int64_t)k_beg * rs + head * D;
+    const uint16_t* vh = a.v + (int64_t)k_beg * rs + head * D;
+
+    if (active) {
+      const int i = q0 + l32 < Lq ? q0 + l32 : Lq - 1;
+      const int64_t row = q_src0 + i;
+      const uint16_t* qp = (row < a.n_q_video ? a.q + row * a.qs : a.q_text + (row - a.n_q_video) * a.qs) + head * D;
+      int rr = a.q_rope ? a.q_rope[q_beg + i] : -1;
+      if (rr >= a.n_rope_rows) rr = -1;
+#pragma unroll
+      for (int ks = 0; ks < C::KS; ++ks) {
+        const int d = 16 * ks + 8 * h;
+        u32x4 x = *(const u32x4*)(qp + d);
+        if (rr >= 0) x = rotate8(x, a.cos_t, a.sin_t, (int64_t)rr * D + d, 1.0f);
+        st.q[ks] = as_bf16x8(x);
+      }
+    }
+    // prologue loads: K(0); then the groups {K(1), V(-1)}, {K(2), V(0)}, {K(3), V(1)} (V(-1) fills its slot with
+    // zeros: iteration 0 multiplies it by P(-1) = 0)
+    ring_load<D>(kh, rs, 0, Lk, voffk, rg.k[0], w);
+    ring_load<D>(kh, rs, 1, Lk, voffk, rg.k[1], w);
+    ring_load<D>(vh, rs, -1, Lk, voffv, rg.v[3], w);
+    ring_load<D>(kh, rs, 2, Lk, voffk, rg.k[2], w);
+    ring_load<D>(vh, rs, 0, Lk, voffv, rg.v[0], w);
+    ring_load<D>(kh, rs, 3, Lk, voffk, rg.k[3], w);
+    ring_load<D>(vh, rs, 1, Lk, voffv, rg.v[1], w);
+
+#pragma unroll
+    for (int db = 0; db < C::DB; ++db)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) st.acc[db][r] = 0.0f;
+    {
+      const u32x4 z = {0u, 0u, 0u, 0u};
+      st.p[1][0] = as_bf16x8(z);
+      st.p[1][1] = as_bf16x8(z);
+    }
+    st.m = -__builtin_inff();
+    st.mc = -__builtin_inff();
+    st.lsum = 0.0f;
+    const float c = a.c;
+
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(3 * C::GROUP));
+    asm volatile("s_barrier" ::: "memory");
+    if (active) {
+      const f32x16 zero = {};
+#pragma unroll
+      for (int ks = 0; ks < C::KS; ++ks)
+        st.s[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(*(const bf16x8*)((const char*)rg.k[0] + st.kaddr[ks]),
+                                                         st.q[ks], ks == 0 ? zero : st.s[0], 0, 0, 0);
+    }
+    for (int j = 0; j < nb; j += kRing) {
+      iter4<D, 0>(st, rg, j, nb, Lk, active, kh, vh, rs, voffk, voffv, w, h, c);
+      if (j + 1 < nb) iter4<D, 1>(st, rg, j + 1, nb, Lk, active, kh, vh, rs, voffk, voffv, w, h, c);
+      if (j + 2 < nb) iter4<D, 2>(st, rg, j + 2, nb, Lk, active, kh, vh, rs, voffk, voffv, w, h, c);
+      if (j + 3 < nb) iter4<D, 3>(st, rg, j + 3, nb, Lk, active, kh, vh, rs, voffk, voffv, w, h, c);
+    }
+    // epilogue: O += V(nb-1) P(nb-1), then normalise and store
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+    asm volatile("s_barrier" ::: "memory");
+    if (active) {
+      const int last = nb - 1;
+      const int vs = (last + kRing) % kRing;
+      const uint16_t* vslot = vs == 0 ? rg.v[0] : vs == 1 ? rg.v[1] : vs == 2 ? rg.v[2] : rg.v[3];
+      const bool odd = (last & 1) != 0;
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        const bf16x8 pp = odd ? st.p[1][half] : st.p[0][half];
+#pragma unroll
+        for (int db = 0; db < C::DB; ++db)
+          st.acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ring_vt<D>(vslot, st.vaddr[db], half), pp,
+                                                              st.acc[db], 0, 0, 0);
+      }
+      const float ltot = pair_sum(st.lsum);
+      const int i = q0 + l32;
+      if (i < Lq) {
+        const float inv = nb > 0 ? 1.0f / ltot : 0.0f;
+        const int64_t row = q_src0 + i;
+        uint16_t* op = (row < a.n_q_video ? a.o + row * a.os : a.o_text + (row - a.n_q_video) * a.os) + head * D;
+#pragma unroll
+        for (int db = 0; db < C::DB; ++db)
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            const int d = db * 32 + 8 * g + 4 * h;
+            uint32_t lo = pack2(st.acc[db][4 * g] * inv, st.acc[db][4 * g + 1] * inv);
+            uint32_t hi = pack2(st.acc[db][4 * g + 2] * inv, st.acc[db][4 * g + 3] * inv);
+            *(uint2*)(op + d) = make_uint2(lo, hi);
+          }
+        if (a.lse && h == 0)
+          a.lse[(int64_t)head * a.sum_q + q_beg + i] = nb > 0 ? st.m * a.scale + logf(ltot) : -__builtin_inff();
+      }
+    }
+  }
+}
+
+typedef void (*AttnFn)(AttnArgs, int32_t*);
+
+// kernel variant (ONEREEL_ATTN_VARIANT): 0 = software-pipelined ring kernel (default), 1 = tile kernel with 32
+// queries per wavefront, 2 = tile kernel with 64 queries per wavefront
+constexpr int kVariants = 3;
+
+int variant() {
+  static int v = [] {
+    const char* e = getenv("ONEREEL_ATTN_VARIANT");
+    if (!e) return 0;
+    const int x = atoi(e);
+    return x >= 0 && x < kVariants ? x : 0;
+  }();
+  return v;
+}
+
+int variant_bq(int var) { return var == 2 ? 256 : 128; }
+
+AttnFn attn_fn(int D, int var) {
+  if (D == 128) return var == 0 ? attn4_kernel<128> : var == 1 ? attn_kernel<128, 1> : attn_kernel<128, 2>;
+  return var == 0 ? attn4_kernel<64> : var == 1 ? attn_kernel<64, 1> : attn_kernel<64, 2>;
 }
 
 struct DevInfo {
   int cus = 0;
-  int occ[2][2] = {{0, 0}, {0, 0}};  // [D == 128][nq - 1]
+  int occ[2][kVariants] = {};  // [D == 128][variant]
 };
 
 int dev_info(DevInfo& info) {
@@ -506,9 +841,9 @@ int dev_info(DevInfo& info) {
                            "hipDeviceGetAttribute"))
       return rc;
     for (int d = 0; d < 2; ++d)
-      for (int n = 0; n < 2; ++n)
-        if (int rc = check_hip(hipOccupancyMaxActiveBlocksPerMultiprocessor(&di.occ[d][n],
-                                                                            attn_fn(d ? 128 : 64, n + 1), kThreads, 0),
+      for (int n = 0; n < kVariants; ++n)
+        if (int rc = check_hip(hipOccupancyMaxActiveBlocksPerMultiprocessor(&di.occ[d][n], attn_fn(d ? 128 : 64, n),
+                                                                            kThreads, 0),
                                "hipOccupancyMaxActiveBlocksPerMultiprocessor"))
           return rc;
     cached = di;
@@ -560,8 +895,8 @@ extern "C" int or_varlen_fwd(const or_varlen_args* p, void* stream) {
   if (x.sum_q == 0) return 0;
   DevInfo di;
   if (int rc = dev_info(di)) return rc;
-  const int nq = variant_nq();
-  const int occ = di.occ[x.D == 128][nq - 1];
+  const int var = variant();
+  const int occ = di.occ[x.D == 128][var];
   if (occ < 1) return fail_arg("or_varlen_fwd: attention kernel cannot be resident (occupancy 0)");
   const int64_t max_items = max_items_of(x.n_seg, x.sum_q, x.H);
   int64_t grid = (int64_t)di.cus * occ;
@@ -595,8 +930,8 @@ extern "C" int or_varlen_fwd(const or_varlen_args* p, void* stream) {
   hipStream_t st = (hipStream_t)stream;
   // the planner needs key counts only: k_len when given, else the cu_k differences
   hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(kPlanThreads), 0, st, x.cu_q, x.k_len ? nullptr : x.cu_k,
-                     x.k_len, x.n_seg, x.H, 128 * nq, (int)max_items, ws);
+                     x.k_len, x.n_seg, x.H, variant_bq(var), (int)max_items, ws);
   if (int rc = check_hip(hipGetLastError(), "plan_kernel launch")) return rc;
-  hipLaunchKernelGGL(attn_fn(x.D, nq), dim3((unsigned)grid), dim3(kThreads), 0, st, a, ws);
+  hipLaunchKernelGGL(attn_fn(x.D, var), dim3((unsigned)grid), dim3(kThreads), 0, st, a, ws);
   return check_hip(hipGetLastError(), "attn_kernel launch");
 }
