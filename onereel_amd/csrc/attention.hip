@@ -475,21 +475,28 @@ void attn_kernel(AttnArgs a, int32_t* ws) {
 }
 
 // ------------------------------------------------------------------------------------------------------------------
-// v4: software-pipelined kernel. Keys in blocks of 32 (one MFMA block); K and V blocks stream through two rings of
-// four LDS slots each, filled by buffer loads straight into LDS three iterations ahead (out-of-range rows of a
-// segment's last block read as zeros). Iteration j of a wavefront runs the softmax of block j on the VALU while the
-// MFMA unit computes S of block j + 1 (QK^T) and O += V P^T of block j - 1, so the exponentials overlap the matrix
-// work inside one wavefront as well as across the two wavefronts that share a SIMD.
+// Ring kernel (the default): software-pipelined over blocks of 32 keys. K and V blocks stream through two rings of
+// four LDS slots each, filled by buffer loads straight into LDS (LDS DMA) three iterations ahead; rows past a
+// segment's end read as zeros. Iteration j of a wavefront runs the softmax of block j on the VALU while the MFMA unit
+// computes S of block j + 1 (QK^T) and O += V P^T of block j - 1, so the exponentials overlap the matrix work inside
+// one wavefront as well as across the two wavefronts that share a SIMD.
+//
+// Running max: P(j) is computed with the running max m as it stands; only when some probability of the block
+// exceeds 2^16 (its row-half sum exceeds 2^20, or overflows) does the wavefront take the max of the block, rescale O
+// and l by 2^((m_old - m_new) c) and recompute P(j). The first block of every item takes that path (m starts at
+// -1e30, a finite stand-in for -inf so that masked scores still give exactly 0).
 
 constexpr int kBKB = 32;   // keys per ring slot
 constexpr int kRing = 4;   // slots per ring (K ring and V ring)
+constexpr float kRescaleSum = 1048576.0f;   // 2^20
+constexpr float kMInit = -1e30f;
 
 template <int D>
 struct R4 {
   static constexpr int CH = D / 8;                     // 16-byte chunks per row
   static constexpr int KS = D / 16;                    // MFMA k-steps of S^T
   static constexpr int DB = D / 32;                    // 32-row blocks of O^T
-  static constexpr int LPB = kBKB * CH / kThreads;     // buffer loads per lane for one K (or V) block
+  static constexpr int LPB = kBKB * CH / kThreads;     // loads per lane for one K (or V) block
   static constexpr int SLOT = kBKB * D;                // bf16 elements per slot
   static constexpr int GROUP = 2 * LPB;                // loads per lane issued by one iteration (a K and a V block)
 };
@@ -511,29 +518,50 @@ __device__ __forceinline__ int swz4_v(int r) {
   else return 4 * ((r >> 1) & 1);
 }
 
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) void lds_void;
 
-// the slots are eight distinct __shared__ arrays, so that the compiler can tell a read of one slot from the loads
-// still in flight into the others (and waits for those only where they alias)
+__device__ __forceinline__ uint32_t lds_addr(const void* p) { return (uint32_t)(uintptr_t)(const lds_void*)p; }
+
+// the slots are distinct __shared__ arrays, addressed by compile-time index
 struct Ring {
   uint16_t* k[kRing];
   uint16_t* v[kRing];
 };
 
-// one K or V block (rows b*32 .. b*32+31 of the segment, head columns) into an LDS slot; rows at or past Lk read 0
-template <int D>
-__device__ __forceinline__ void ring_load(const uint16_t* seg_head, int64_t rs, int b, int Lk, const uint32_t* voff,
-                                          uint16_t* slot, int w) {
-  // bytes from the block's first row to the end of its last valid row (rows past Lk fall outside); branch-free
-  const int rows = min(max(Lk - b * kBKB, 0), kBKB);
-  const int rb = (int)rs * 2;
-  const uint32_t nrec = (uint32_t)max(rows * rb - rb + D * 2, 0);
-  const uint16_t* p = seg_head + (int64_t)max(b, 0) * kBKB * rs;
-  __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc((void*)p, (short)0, (int)nrec, 0x00020000);
+// One K or V block into an LDS slot: lane i of load n fetches 16 bytes at voff[n] from the block's first row into
+// LDS byte m0 + n * 4096 + 16 * lane (m0: the slot plus this wavefront's 1 KiB). The buffer descriptor's record
+// count ends at the segment's last row, so rows past it read 0. Inline asm: the compiler does not see these LDS
+// writes, so it adds no waits on them before unrelated LDS reads; the kernel waits with vmcnt and a barrier itself.
+template <int LPB>
+__device__ __forceinline__ void dma_block(uint64_t base, int32_t nrec, const uint32_t* voff, uint32_t m0) {
+  const i32x4 r = {(int32_t)(uint32_t)base, (int32_t)(uint32_t)(base >> 32), nrec, 0x00020000};
 #pragma unroll
-  for (int i = 0; i < R4<D>::LPB; ++i)
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)(slot + (i * kThreads + w * 64) * 8), 16, voff[i], 0, 0, 0);
+  for (int n = 0; n < LPB; ++n)
+    asm volatile("s_mov_b32 m0, %2\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voff[n]), "s"(r),
+                 "s"(m0 + n * kThreads * 16)
+                 : "memory");
 }
+
+// wait until at most N of this wavefront's loads are in flight, then synchronise the block
+template <int N>
+__device__ __forceinline__ void wait_loads_barrier() {
+  if constexpr (N == 0) asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+  else if constexpr (N == 4) asm volatile("s_waitcnt vmcnt(4)\n\ts_barrier" ::: "memory");
+  else if constexpr (N == 6) asm volatile("s_waitcnt vmcnt(6)\n\ts_barrier" ::: "memory");
+  else if constexpr (N == 8) asm volatile("s_waitcnt vmcnt(8)\n\ts_barrier" ::: "memory");
+  else asm volatile("s_waitcnt vmcnt(12)\n\ts_barrier" ::: "memory");
+}
+
+// Per-item stream of one segment-head's K or V rows: block b starts at base + b * bb bytes and holds rem0 - b * bb
+// valid bytes (clamped at 0).
+struct Stream {
+  uint64_t base;
+  int32_t rem0;
+  int32_t bb;
+  __device__ __forceinline__ uint64_t at(int b) const { return base + (uint64_t)(int64_t)b * (uint32_t)bb; }
+  __device__ __forceinline__ int32_t nrec(int b) const { return max(rem0 - b * bb, 0); }
+};
 
 template <int D>
 __device__ __forceinline__ bf16x8 ring_vt(const uint16_t* slot, uint32_t vaddr, int half) {
@@ -566,61 +594,9 @@ __device__ __forceinline__ float max16(const f32x16& s) {
   return fmaxf(x, s[15]);
 }
 
-// iteration j (J = j mod 4, compile-time so that every slot is a distinct LDS object for the compiler)
-template <int D, int J>
-__device__ __forceinline__ void iter4(St4<D>& st, const Ring& rg, int j, int nb, int Lk, bool active,
-                                      const uint16_t* kh, const uint16_t* vh, int64_t rs,
-                                      const uint32_t (&voffk)[R4<D>::LPB], const uint32_t (&voffv)[R4<D>::LPB],
-                                      int w, int h, float c) {
-  using C = R4<D>;
-  constexpr int PAR = J & 1;
-  // blocks K(j+1) and V(j-1) have landed (the loads of the last two iterations may still be in flight), every
-  // wavefront is done with iteration j-1's slots
-  __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * C::GROUP));
-  asm volatile("s_barrier" ::: "memory");
-  ring_load<D>(kh, rs, j + kRing, Lk, voffk, rg.k[J], w);
-  ring_load<D>(vh, rs, j + 2, Lk, voffv, rg.v[(J + 2) % kRing], w);
-  if (!active) return;
-
-  bf16x8 kop[C::KS];
-#pragma unroll
-  for (int ks = 0; ks < C::KS; ++ks)
-    kop[ks] = *(const bf16x8*)((const char*)rg.k[(J + 1) % kRing] + st.kaddr[ks]);
-  bf16x8 vop[2][C::DB];
-#pragma unroll
-  for (int half = 0; half < 2; ++half)
-#pragma unroll
-    for (int db = 0; db < C::DB; ++db) vop[half][db] = ring_vt<D>(rg.v[(J + 3) % kRing], st.vaddr[db], half);
-
-  f32x16& s = st.s[PAR];
-  if (j == nb - 1 && (Lk & (kBKB - 1))) {
-    int valid = Lk - j * kBKB - 16 * h;
-    asm volatile("" : "+v"(valid));   // computed here, not hoisted out of the loop as 16 lane masks in SGPRs
-#pragma unroll
-    for (int r = 0; r < 16; ++r) s[r] = r < valid ? s[r] : -__builtin_inff();
-  }
-  const float mx = pair_max(max16(s));
-  const bool grow = __builtin_fmaf(mx, c, -st.mc) > 8.0f;
-  const bool any_grow = __any(grow);
-  float alpha = 1.0f;
-  if (any_grow) {
-    const float mn = fmaxf(st.m, mx);
-    alpha = __builtin_amdgcn_exp2f((st.m - mn) * c);
-    st.m = mn;
-    st.mc = mn * c;
-  }
-  const float mc = st.mc;
-
-  // matrix work: S(j+1) = K(j+1) Q^T, O += V(j-1) P(j-1)
-  f32x16& sn = st.s[PAR ^ 1];
-  const f32x16 zero = {};
-#pragma unroll
-  for (int ks = 0; ks < C::KS; ++ks) {
-    sn = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kop[ks], st.q[ks], ks == 0 ? zero : sn, 0, 0, 0);
-    const int half = ks / C::DB, db = ks % C::DB;
-    st.acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vop[half][db], st.p[PAR ^ 1][half], st.acc[db], 0, 0, 0);
-  }
-  // vector work: P(j) = 2^(s c - m c) as bf16 pairs, and its row sum from the rounded values
+// P = 2^(s c - mc) rounded to bf16 pairs, and the sum of the rounded values (the numerator and the denominator of
+// the softmax use the same probabilities)
+__device__ __forceinline__ float exp_pack(const f32x16& s, float c, float mc, bf16x8 (&p)[2]) {
   f32x16 e;
 #pragma unroll
   for (int r = 0; r < 16; ++r) e[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[r], c, -mc));
@@ -636,16 +612,67 @@ __device__ __forceinline__ void iter4(St4<D>& st, const Ring& rg, int j, int nb,
       ls = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, pw), one, ls, false);
       pk[i] = pw;
     }
-    st.p[PAR][half] = as_bf16x8(pk);
+    p[half] = as_bf16x8(pk);
   }
+  return ls;
+}
+
+// iteration j (J = j mod 4, compile-time: the slots it touches are compile-time)
+template <int D, int J>
+__device__ __forceinline__ void iter4(St4<D>& st, const Ring& rg, int j, int nb, int Lk, bool active,
+                                      const Stream& ks, const Stream& vs, const uint32_t* voffk,
+                                      const uint32_t* voffv, uint32_t m0w, int h, float c) {
+  using C = R4<D>;
+  constexpr int PAR = J & 1;
+  // blocks K(j+1) and V(j-1) have landed (the loads of the last two iterations may still be in flight), and every
+  // wavefront is done with iteration j-1's slots
+  wait_loads_barrier<2 * C::GROUP>();
+  dma_block<C::LPB>(ks.at(j + kRing), ks.nrec(j + kRing), voffk, lds_addr(rg.k[J]) + m0w);
+  dma_block<C::LPB>(vs.at(j + 2), vs.nrec(j + 2), voffv, lds_addr(rg.v[(J + 2) % kRing]) + m0w);
+  if (!active) return;
+
+  bf16x8 kop[C::KS];
+#pragma unroll
+  for (int k = 0; k < C::KS; ++k) kop[k] = *(const bf16x8*)((const char*)rg.k[(J + 1) % kRing] + st.kaddr[k]);
+  bf16x8 vop[2][C::DB];
+#pragma unroll
+  for (int half = 0; half < 2; ++half)
+#pragma unroll
+    for (int db = 0; db < C::DB; ++db) vop[half][db] = ring_vt<D>(rg.v[(J + 3) % kRing], st.vaddr[db], half);
+
+  f32x16& s = st.s[PAR];
+  if (j == nb - 1 && (Lk & (kBKB - 1))) {
+    int valid = Lk - j * kBKB - 16 * h;
+    asm volatile("" : "+v"(valid));   // computed here, not hoisted out of the loop as 16 lane masks in SGPRs
+#pragma unroll
+    for (int r = 0; r < 16; ++r) s[r] = r < valid ? s[r] : -__builtin_inff();
+  }
+
+  // matrix work: S(j+1) = K(j+1) Q^T, O += V(j-1) P(j-1)
+  f32x16& sn = st.s[PAR ^ 1];
+  const f32x16 zero = {};
+#pragma unroll
+  for (int k = 0; k < C::KS; ++k) {
+    sn = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kop[k], st.q[k], k == 0 ? zero : sn, 0, 0, 0);
+    const int half = k / C::DB, db = k % C::DB;
+    st.acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vop[half][db], st.p[PAR ^ 1][half], st.acc[db], 0, 0, 0);
+  }
+  // vector work: P(j) with the running max
+  float ls = exp_pack(s, c, st.mc, st.p[PAR]);
 #pragma unroll
   for (int i = 0; i < 2 * C::KS; ++i) {
     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-    __builtin_amdgcn_sched_group_barrier(0x002, 48 / (2 * C::KS), 0);
+    __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
   }
-  // keeps the exponentials in this scheduling region (next to the MFMAs) instead of being sunk past the branch
+  // keeps P(j) in this scheduling region (next to the MFMAs) instead of being sunk past the branch
   asm volatile("" ::"v"(st.p[PAR][0]), "v"(st.p[PAR][1]), "v"(ls));
-  if (any_grow) {
+  if (__any(!(ls <= kRescaleSum))) {
+    const float mx = pair_max(max16(s));
+    const float mn = fmaxf(st.m, mx);
+    const float alpha = __builtin_amdgcn_exp2f((st.m - mn) * c);
+    st.m = mn;
+    st.mc = mn * c;
+    ls = exp_pack(s, c, st.mc, st.p[PAR]);
 #pragma unroll
     for (int db = 0; db < C::DB; ++db)
 #pragma unroll
@@ -665,24 +692,25 @@ void attn4_kernel(AttnArgs a, int32_t* ws) {
   __shared__ int item_sh;
   const Ring rg = {{k0, k1, k2, k3}, {v0, v1, v2, v3}};
   const int tid = threadIdx.x, lane = tid & 63;
-  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform: LDS destinations of the loads in SGPRs
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31, h = lane >> 5;
   const int64_t rs = a.ks;
+  const uint32_t m0w = (uint32_t)w * 64 * 16;   // this wavefront's 1 KiB of each load's destination
 
-  // per-lane constants: global byte offsets of this lane's buffer loads within a block, LDS byte offsets of its reads
+  // per-lane constants: byte offsets of this lane's loads within a block, and of its LDS operand reads
   uint32_t voffk[C::LPB], voffv[C::LPB];
 #pragma unroll
-  for (int i = 0; i < C::LPB; ++i) {
-    const int slot = i * kThreads + w * 64 + lane;
+  for (int n = 0; n < C::LPB; ++n) {
+    const int slot = n * kThreads + w * 64 + lane;
     const int row = slot / C::CH, phys = slot % C::CH;
-    voffk[i] = (uint32_t)(row * rs * 2 + (phys ^ swz4_k<C::CH>(row)) * 16);
-    voffv[i] = (uint32_t)(row * rs * 2 + (phys ^ swz4_v<C::CH>(row)) * 16);
+    voffk[n] = (uint32_t)(row * rs * 2 + (phys ^ swz4_k<C::CH>(row)) * 16);
+    voffv[n] = (uint32_t)(row * rs * 2 + (phys ^ swz4_v<C::CH>(row)) * 16);
   }
   St4<D> st;
   {
     const int row = pi32(l32);
 #pragma unroll
-    for (int ks = 0; ks < C::KS; ++ks) st.kaddr[ks] = (uint32_t)(row * D * 2 + (((2 * ks + h) ^ swz4_k<C::CH>(row)) * 16));
+    for (int k = 0; k < C::KS; ++k) st.kaddr[k] = (uint32_t)(row * D * 2 + (((2 * k + h) ^ swz4_k<C::CH>(row)) * 16));
     const int r = lane & 15, g = lane >> 4;
     const int cp = 2 * (g & 1) + ((r >> 1) & 1);
     const int mv = C::CH == 16 ? ((r >> 2) & 3) : ((r >> 3) & 1);
@@ -703,14 +731,21 @@ void attn4_kernel(AttnArgs a, int32_t* ws) {
     const int q_beg = a.cu_q[seg];
     const int Lq = a.cu_q[seg + 1] - q_beg;
     const int k_beg = seg_k_begin(a, seg);
-    const int Lk = seg_k_len(a, seg) < 0 ? 0 : seg_k_len(a, seg);
+    const int Lk = max(seg_k_len(a, seg), 0);
     const int q_src0 = a.seg_q_src ? a.seg_q_src[seg] : q_beg;
     const int q0 = qt * BQ + w * WQ;
     const bool active = q0 < Lq;
     const int nb = (Lk + kBKB - 1) / kBKB;
-    const uint16_t* kh = a.k + (int64_t)k_beg * rs + head * D;
-    const uint16_t* vh = a.v + (int64_t)k_beg * rs + head * D;
+    const int32_t rb = (int32_t)rs * 2;
+    const Stream ks = {(uint64_t)(a.k + (int64_t)k_beg * rs + head * D), Lk * rb - rb + D * 2, kBKB * rb};
+    const Stream vs = {(uint64_t)(a.v + (int64_t)k_beg * rs + head * D), Lk * rb - rb + D * 2, kBKB * rb};
 
+    // prologue: K(0) and the group {K(1), V(-1)} (V(-1) fills its slot with zeros: iteration 0 multiplies it by
+    // P(-1) = 0) are in flight while Q loads; every load so far is waited for (so the compiler's own waits for Q do
+    // not fall inside the loop), then the groups {K(2), V(0)} and {K(3), V(1)} go out
+    dma_block<C::LPB>(ks.at(0), ks.nrec(0), voffk, lds_addr(rg.k[0]) + m0w);
+    dma_block<C::LPB>(ks.at(1), ks.nrec(1), voffk, lds_addr(rg.k[1]) + m0w);
+    dma_block<C::LPB>(vs.at(0), 0, voffv, lds_addr(rg.v[3]) + m0w);
     if (active) {
       const int i = q0 + l32 < Lq ? q0 + l32 : Lq - 1;
       const int64_t row = q_src0 + i;
@@ -718,22 +753,18 @@ void attn4_kernel(AttnArgs a, int32_t* ws) {
       int rr = a.q_rope ? a.q_rope[q_beg + i] : -1;
       if (rr >= a.n_rope_rows) rr = -1;
 #pragma unroll
-      for (int ks = 0; ks < C::KS; ++ks) {
-        const int d = 16 * ks + 8 * h;
+      for (int k = 0; k < C::KS; ++k) {
+        const int d = 16 * k + 8 * h;
         u32x4 x = *(const u32x4*)(qp + d);
         if (rr >= 0) x = rotate8(x, a.cos_t, a.sin_t, (int64_t)rr * D + d, 1.0f);
-        st.q[ks] = as_bf16x8(x);
+        st.q[k] = as_bf16x8(x);
       }
     }
-    // prologue loads: K(0); then the groups {K(1), V(-1)}, {K(2), V(0)}, {K(3), V(1)} (V(-1) fills its slot with
-    // zeros: iteration 0 multiplies it by P(-1) = 0)
-    ring_load<D>(kh, rs, 0, Lk, voffk, rg.k[0], w);
-    ring_load<D>(kh, rs, 1, Lk, voffk, rg.k[1], w);
-    ring_load<D>(vh, rs, -1, Lk, voffv, rg.v[3], w);
-    ring_load<D>(kh, rs, 2, Lk, voffk, rg.k[2], w);
-    ring_load<D>(vh, rs, 0, Lk, voffv, rg.v[0], w);
-    ring_load<D>(kh, rs, 3, Lk, voffk, rg.k[3], w);
-    ring_load<D>(vh, rs, 1, Lk, voffv, rg.v[1], w);
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+    dma_block<C::LPB>(ks.at(2), ks.nrec(2), voffk, lds_addr(rg.k[2]) + m0w);
+    dma_block<C::LPB>(vs.at(0), vs.nrec(0), voffv, lds_addr(rg.v[0]) + m0w);
+    dma_block<C::LPB>(ks.at(3), ks.nrec(3), voffk, lds_addr(rg.k[3]) + m0w);
+    dma_block<C::LPB>(vs.at(1), vs.nrec(1), voffv, lds_addr(rg.v[1]) + m0w);
 
 #pragma unroll
     for (int db = 0; db < C::DB; ++db)
@@ -744,33 +775,31 @@ void attn4_kernel(AttnArgs a, int32_t* ws) {
       st.p[1][0] = as_bf16x8(z);
       st.p[1][1] = as_bf16x8(z);
     }
-    st.m = -__builtin_inff();
-    st.mc = -__builtin_inff();
+    st.m = kMInit;
+    st.mc = kMInit * a.c;
     st.lsum = 0.0f;
     const float c = a.c;
 
-    __builtin_amdgcn_s_waitcnt(vmcnt_imm(3 * C::GROUP));
     asm volatile("s_barrier" ::: "memory");
     if (active) {
       const f32x16 zero = {};
 #pragma unroll
-      for (int ks = 0; ks < C::KS; ++ks)
-        st.s[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(*(const bf16x8*)((const char*)rg.k[0] + st.kaddr[ks]),
-                                                         st.q[ks], ks == 0 ? zero : st.s[0], 0, 0, 0);
+      for (int k = 0; k < C::KS; ++k)
+        st.s[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(*(const bf16x8*)((const char*)rg.k[0] + st.kaddr[k]),
+                                                         st.q[k], k == 0 ? zero : st.s[0], 0, 0, 0);
     }
     for (int j = 0; j < nb; j += kRing) {
-      iter4<D, 0>(st, rg, j, nb, Lk, active, kh, vh, rs, voffk, voffv, w, h, c);
-      if (j + 1 < nb) iter4<D, 1>(st, rg, j + 1, nb, Lk, active, kh, vh, rs, voffk, voffv, w, h, c);
-      if (j + 2 < nb) iter4<D, 2>(st, rg, j + 2, nb, Lk, active, kh, vh, rs, voffk, voffv, w, h, c);
-      if (j + 3 < nb) iter4<D, 3>(st, rg, j + 3, nb, Lk, active, kh, vh, rs, voffk, voffv, w, h, c);
+      iter4<D, 0>(st, rg, j, nb, Lk, active, ks, vs, voffk, voffv, m0w, h, c);
+      if (j + 1 < nb) iter4<D, 1>(st, rg, j + 1, nb, Lk, active, ks, vs, voffk, voffv, m0w, h, c);
+      if (j + 2 < nb) iter4<D, 2>(st, rg, j + 2, nb, Lk, active, ks, vs, voffk, voffv, m0w, h, c);
+      if (j + 3 < nb) iter4<D, 3>(st, rg, j + 3, nb, Lk, active, ks, vs, voffk, voffv, m0w, h, c);
     }
     // epilogue: O += V(nb-1) P(nb-1), then normalise and store
-    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
-    asm volatile("s_barrier" ::: "memory");
+    wait_loads_barrier<0>();
     if (active) {
       const int last = nb - 1;
-      const int vs = (last + kRing) % kRing;
-      const uint16_t* vslot = vs == 0 ? rg.v[0] : vs == 1 ? rg.v[1] : vs == 2 ? rg.v[2] : rg.v[3];
+      const int vsl = (last + kRing) % kRing;
+      const uint16_t* vslot = vsl == 0 ? rg.v[0] : vsl == 1 ? rg.v[1] : vsl == 2 ? rg.v[2] : rg.v[3];
       const bool odd = (last & 1) != 0;
 #pragma unroll
       for (int half = 0; half < 2; ++half) {
@@ -889,6 +918,9 @@ extern "C" int or_varlen_fwd(const or_varlen_args* p, void* stream) {
     return fail_arg("or_varlen_fwd: pointers must be 16-byte aligned and row strides multiples of 8 elements");
   if (x.cos_table && (((uintptr_t)x.cos_table | (uintptr_t)x.sin_table) & 15u))
     return fail_arg("or_varlen_fwd: rotary tables must be 16-byte aligned");
+  if ((int64_t)(x.max_k + 8 * 32) * x.k_row_stride * 2 > 0x7fffffffLL)
+    return fail_arg("or_varlen_fwd: a segment's keys span more than 2 GiB (max_k %d x row stride %lld)", x.max_k,
+                    (long long)x.k_row_stride);
   const int64_t need = or_varlen_workspace_size(x.n_seg, x.sum_q, x.H, x.D);
   if (!x.workspace || x.workspace_bytes < need)
     return fail_arg("or_varlen_fwd: workspace of %lld bytes needed", (long long)need);
