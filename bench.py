@@ -215,7 +215,7 @@ def main():
                            useful_flop_per_step=flops, frac_bf16_peak_step=round(value / PEAK_BF16_TFLOPS, 4)),
                roofline=dict(bound='mfma', achieved=round(flops / t_attn / 1e9, 1), peak=PEAK_BF16_TFLOPS,
                              unit='TFLOP/s', frac=round(flops / t_attn / 1e9 / PEAK_BF16_TFLOPS, 4), traffic=traffic,
-                             kernel='attn_kernel<128> (+ its one-block planner, a few us)'),
+                             kernel='attn4_kernel<128> (+ plan_kernel, one block, ~10 us)'),
                kernels=kernels)
     if not args.no_cpu:
         out['cpu_baseline'] = cpu_baseline()
