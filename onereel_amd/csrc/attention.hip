@@ -2,9 +2,10 @@
 // accumulation. Replaces flash_attn_varlen_func as src/onereel/attention.py:39-53,78-83 calls it.
 //
 // Design (CDNA4, 64-wide wavefronts, v_mfma_f32_32x32x16_bf16):
-// - A work item is (segment, head, 256-query tile); a block of 4 wavefronts takes one item at a time from a queue
-//   (persistent blocks, one per CU). A planner kernel orders the items longest segment first (LPT over the uneven
-//   scene lengths) and, inside a segment, head-major so that consecutive items share K/V in L2.
+// - A work item is (segment, head, query tile); a block of 4 wavefronts takes one item at a time from a queue
+//   (persistent blocks). A planner kernel orders the items longest segment first (LPT over the uneven scene lengths)
+//   into eight queues, one per XCD, by head: the blocks of one XCD work on the same segment-head together and share
+//   its K/V in that XCD's L2. A block whose queue is empty takes items from the other queues.
 // - Each wavefront owns 64 queries. It computes S^T = K Q^T (keys on the MFMA rows, queries on the columns), so a
 //   lane holds one query's scores: the running max, the exponentials and the row sum are in-lane except one
 //   exchange with lane ^ 32. The K rows of the A operand are permuted (pi below) so that lane half h holds keys
@@ -29,7 +30,9 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 constexpr int kThreads = 256;   // 4 wavefronts
 constexpr int kMinBQ = 128;     // smallest work-item query tile of any kernel variant (sizes the item list)
 constexpr int kBK = 64;         // keys per tile
-constexpr int kWsHeader = 64;   // int32 words before the item list
+constexpr int kQueues = 8;      // item queues: one per XCD
+constexpr int kQueueWords = 32; // words per queue header (head counter, item count, first item), one 128-byte line
+constexpr int kWsHeader = kQueues * kQueueWords;   // int32 words before the item list
 constexpr int kPlanThreads = 1024;
 constexpr int kMaxPlanSeg = 4096;
 
@@ -66,7 +69,9 @@ __device__ __forceinline__ int seg_k_len(const AttnArgs& a, int s) {
 __device__ __forceinline__ int pi32(int i) { return ((i >> 2) & 1) * 16 + (i >> 3) * 4 + (i & 3); }
 
 // ------------------------------------------------------------------------------------------------------------------
-// planner: one block. Items sorted by segment key count (descending), then segment; per segment head-major.
+// planner: one block. Segments sorted by key count (descending), then index. Queue q holds the heads h with
+// h % 8 == q: for every sorted segment, those heads in order, each head's query tiles in order. Queue q's header at
+// ws[32 q]: [0] head counter, [1] item count, [2] index of its first item in the item list.
 __device__ inline int plan_upper_bound(const int* a, int n, int x) {
   int lo = 0, hi = n;
   while (lo < hi) {
@@ -144,11 +149,21 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(const int32_t* cu_q,
   }
   if (tid == kPlanThreads - 1) off[n_seg] = part[tid];
   __syncthreads();
-  int total = off[n_seg];
-  if (total > max_items) total = max_items;  // cannot happen with the host's bound; keeps writes in range
-  if (tid == 0) {
-    ws[0] = 0;
-    ws[1] = total;
+  // the host's bound guarantees that the items fit; if they did not, every queue stays empty and no item is written
+  const bool fits = off[n_seg] <= max_items;
+  const int total = fits ? off[n_seg] : 0;
+  // off[i] / H: query tiles of the sorted segments before i, each counted once
+  const int all_tiles = total / H;
+  auto heads_of = [&](int q) { return (H - q + kQueues - 1) / kQueues; };   // heads h < H with h % 8 == q
+  auto first_of = [&](int q) {
+    int b = 0;
+    for (int r = 0; r < q; ++r) b += all_tiles * heads_of(r);
+    return b;
+  };
+  if (tid < kQueues) {
+    ws[kQueueWords * tid] = 0;
+    ws[kQueueWords * tid + 1] = all_tiles * heads_of(tid);
+    ws[kQueueWords * tid + 2] = first_of(tid);
   }
   for (int it = tid; it < total; it += kPlanThreads) {
     int i = plan_upper_bound(off, n_seg + 1, it) - 1;
@@ -157,10 +172,28 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(const int32_t* cu_q,
     int tiles = (lq + bq - 1) / bq;
     int local_it = it - off[i];
     int head = local_it / tiles, t = local_it - head * tiles;
-    ws[kWsHeader + 2 * it] = s;
-    ws[kWsHeader + 2 * it + 1] = (t << 8) | head;
+    const int q = head % kQueues;
+    const int pos = first_of(q) + (off[i] / H) * heads_of(q) + (head / kQueues) * tiles + t;
+    ws[kWsHeader + 2 * pos] = s;
+    ws[kWsHeader + 2 * pos + 1] = (t << 8) | head;
   }
 }
+
+// next work item of a block (thread 0 calls it): from the queue of the block's XCD (read from HW_REG_XCC_ID), then
+// from the others in turn; -1 when every queue is empty. A queue's counter is read before the atomic so that
+// exhausted queues are not incremented further.
+__device__ inline int next_item(int32_t* ws, int xcc) {
+  for (int r = 0; r < kQueues; ++r) {
+    int32_t* hq = ws + kQueueWords * ((xcc + r) & (kQueues - 1));
+    const int n = hq[1];
+    if (__hip_atomic_load(hq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= n) continue;
+    const int x = atomicAdd(hq, 1);
+    if (x < n) return hq[2] + x;
+  }
+  return -1;
+}
+
+__device__ __forceinline__ int xcc_id() { return __builtin_amdgcn_s_getreg(0xf814) & (kQueues - 1); }  // HW_REG_XCC_ID
 
 // ------------------------------------------------------------------------------------------------------------------
 // attention
@@ -374,12 +407,13 @@ void attn_kernel(AttnArgs a, int32_t* ws) {
   const int l32 = lane & 31, h = lane >> 5;
   const float NEG_INF = -__builtin_inff();
 
+  const int xcc = xcc_id();
   for (;;) {
-    if (tid == 0) sm.item = atomicAdd(&ws[0], 1);
+    if (tid == 0) sm.item = next_item(ws, xcc);
     __syncthreads();
     const int it = sm.item;
     __syncthreads();
-    if (it >= ws[1]) break;
+    if (it < 0) break;
     const int seg = ws[kWsHeader + 2 * it];
     const int packed_ht = ws[kWsHeader + 2 * it + 1];
     const int head = packed_ht & 255, qt = packed_ht >> 8;
@@ -719,12 +753,13 @@ void attn4_kernel(AttnArgs a, int32_t* ws) {
       st.vaddr[db] = (uint32_t)((16 * h + (r >> 2)) * D * 2 + (4 * (db ^ mv) + cp) * 16 + (r & 1) * 8);
   }
 
+  const int xcc = xcc_id();
   for (;;) {
-    if (tid == 0) item_sh = atomicAdd(&ws[0], 1);
+    if (tid == 0) item_sh = next_item(ws, xcc);
     __syncthreads();
     const int it = item_sh;
     __syncthreads();
-    if (it >= ws[1]) break;
+    if (it < 0) break;
     const int seg = ws[kWsHeader + 2 * it];
     const int packed_ht = ws[kWsHeader + 2 * it + 1];
     const int head = packed_ht & 255, qt = packed_ht >> 8;
