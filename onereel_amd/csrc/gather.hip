@@ -5,9 +5,11 @@
 // the write-back ov[lo:hi] = o / ot[t0:t1] = o after o.split (hunyuan15.py:226,231-235; attention.py:71).
 //
 // Both kernels are HBM-bound row copies: one wavefront moves one row of H*D bf16 (4 KiB at 16 x 128) per step in
-// 16-byte lanes, all loads of a row issued before its stores. The rotation is done in fp32 as two rounded products
-// and a rounded sum per element (no fused multiply-add), then rounded to bf16 to nearest even: the same bits as
-// torch's x.float() * cos + rot(x).float() * sin followed by .to(bfloat16).
+// 16-byte lanes (the scatter two rows per step), all loads issued before the stores. Stores are non-temporal: the
+// packed rows and the token-order outputs are written once and read by the next kernel from HBM, so they bypass
+// the caches (about 10% and 25% faster than cached stores for the pack and the scatter). The rotation is done in
+// fp32 as two rounded products and a rounded sum per element (no fused multiply-add), then rounded to bf16 to
+// nearest even: the same bits as torch's x.float() * cos + rot(x).float() * sin followed by .to(bfloat16).
 #include "common.h"
 
 namespace onereel {
@@ -17,6 +19,9 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
 constexpr int kMaxChunksPerLane = 8;  // rows up to 64 lanes * 8 * 8 elements = 4096 elements (H*D)
+
+// 16-byte store that bypasses the caches (global_store_dwordx4 ... nt)
+__device__ __forceinline__ void store_nt(uint16_t* p, u32x4 v) { __builtin_nontemporal_store(v, (u32x4*)p); }
 
 struct GatherArgs {
   const uint16_t* a_video;
@@ -77,8 +82,8 @@ __global__ __launch_bounds__(kThreads) void pack_gather_kernel(GatherArgs g) {
         } else if (rope >= 0) {
           x = rotate8(x, g.cos_t, g.sin_t, (int64_t)rope * g.D + d0, 1.0f);
         }
-        *(u32x4*)(ao + 8 * c) = x;
-        if (bo) *(u32x4*)(bo + 8 * c) = vb[i];
+        store_nt(ao + 8 * c, x);
+        if (bo) store_nt(bo + 8 * c, vb[i]);
       }
     }
   }
@@ -94,6 +99,9 @@ struct ScatterArgs {
   int H, D;
 };
 
+constexpr int kScatterRows = 2;   // rows per wavefront step (loads of both in flight before the stores)
+
+// rows r < n_rows: packed row r -> token-order row dst_idx[r]; rows n_rows .. n_rows + n_zero: zeroed text rows
 __global__ __launch_bounds__(kThreads) void scatter_kernel(ScatterArgs g) {
   const int lane = threadIdx.x & 63;
   const int64_t wave = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6);
@@ -101,30 +109,38 @@ __global__ __launch_bounds__(kThreads) void scatter_kernel(ScatterArgs g) {
   const int row_elems = g.H * g.D;
   const int chunks = row_elems >> 3;
   const int64_t n_zero = g.text_rows > g.zero_from ? g.text_rows - g.zero_from : 0;
-  for (int64_t r = wave; r < g.n_rows + n_zero; r += n_waves) {
-    if (r < g.n_rows) {
-      const int dst = g.dst_idx[r];
-      uint16_t* o = dst >= g.n_video ? g.o_text + (int64_t)(dst - g.n_video) * g.text_stride
-                                     : g.o_video + (int64_t)dst * g.dst_stride;
-      const uint16_t* p = g.packed + r * (int64_t)row_elems;
-      u32x4 v[kMaxChunksPerLane];
+  const int64_t total = g.n_rows + n_zero;
+  for (int64_t r0 = wave * kScatterRows; r0 < total; r0 += n_waves * kScatterRows) {
+    u32x4 v[kScatterRows][kMaxChunksPerLane];
+    uint16_t* o[kScatterRows];
 #pragma unroll
-      for (int i = 0; i < kMaxChunksPerLane; ++i) {
-        const int c = lane + 64 * i;
-        if (c < chunks) v[i] = *(const u32x4*)(p + 8 * c);
+    for (int k = 0; k < kScatterRows; ++k) {
+      const int64_t r = r0 + k;
+      o[k] = nullptr;
+      if (r < g.n_rows) {
+        const int dst = g.dst_idx[r];
+        o[k] = dst >= g.n_video ? g.o_text + (int64_t)(dst - g.n_video) * g.text_stride
+                                : g.o_video + (int64_t)dst * g.dst_stride;
+        const uint16_t* p = g.packed + r * (int64_t)row_elems;
+#pragma unroll
+        for (int i = 0; i < kMaxChunksPerLane; ++i) {
+          const int c = lane + 64 * i;
+          if (c < chunks) v[k][i] = *(const u32x4*)(p + 8 * c);
+        }
+      } else if (r < total) {
+        o[k] = g.o_text + (g.zero_from + (r - g.n_rows)) * g.text_stride;
+#pragma unroll
+        for (int i = 0; i < kMaxChunksPerLane; ++i) v[k][i] = u32x4{0u, 0u, 0u, 0u};
       }
+    }
 #pragma unroll
-      for (int i = 0; i < kMaxChunksPerLane; ++i) {
-        const int c = lane + 64 * i;
-        if (c < chunks) *(u32x4*)(o + 8 * c) = v[i];
-      }
-    } else {
-      uint16_t* o = g.o_text + (g.zero_from + (r - g.n_rows)) * g.text_stride;
-      const u32x4 z = {0u, 0u, 0u, 0u};
+    for (int k = 0; k < kScatterRows; ++k) {
+      if (o[k]) {
 #pragma unroll
-      for (int i = 0; i < kMaxChunksPerLane; ++i) {
-        const int c = lane + 64 * i;
-        if (c < chunks) *(u32x4*)(o + 8 * c) = z;
+        for (int i = 0; i < kMaxChunksPerLane; ++i) {
+          const int c = lane + 64 * i;
+          if (c < chunks) store_nt(o[k] + 8 * c, v[k][i]);
+        }
       }
     }
   }

@@ -6,8 +6,9 @@
 // cu_seqlens (src/onereel/attention.py:28-29), scene_rope_rows (hunyuan15.py:443-454), frame_position /
 // adjacent_positions / shared_positions (hunyuan15.py:92-124), _move_shared's rows a, a + d (hunyuan15.py:136-145).
 //
-// Every block first derives the per-scene quantities in LDS (one thread per scene; a few hundred integer ops), then
-// the grid writes the per-row arrays with a grid-stride loop: int32 stores, fully coalesced, HBM-bound.
+// Every block first derives the per-scene quantities in LDS: its first wavefront does it alone, one lane per scene
+// (at most 64 scenes, 128 segments), with cross-lane prefix sums and no block barrier until the tables are complete.
+// Then the grid writes the per-row arrays with a grid-stride loop: int32 stores, fully coalesced.
 #include <stdarg.h>
 #include <stdio.h>
 #include <string.h>
@@ -86,20 +87,22 @@ int derive_host(const or_layout_desc& d, LayoutDerived& L) {
 // ---------------------------------------------------------------------------------------------------------------
 // device
 
-// exclusive prefix sum of v over the first n (<= kThreads) threads; every thread of the block must call it
-__device__ int block_exclusive_scan(int v, int n, int* scratch) {
-  const int tid = threadIdx.x;
-  scratch[tid] = tid < n ? v : 0;
-  __syncthreads();
-  for (int off = 1; off < kThreads; off <<= 1) {
-    int x = tid >= off ? scratch[tid - off] : 0;
-    __syncthreads();
-    scratch[tid] += x;
-    __syncthreads();
+// inclusive prefix sum over the 64 lanes of a wavefront
+__device__ inline int wave_scan(int v) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int x = __shfl_up(v, o, 64);
+    if (lane >= o) v += x;
   }
-  int incl = scratch[tid];
-  __syncthreads();
-  return incl - (tid < n ? v : 0);
+  return v;
+}
+
+// LDS writes of this wavefront's lanes become visible to its other lanes (no block barrier)
+__device__ inline void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
 __device__ inline int upper_bound(const int* a, int n, int x) {  // first i in [0, n) with a[i] > x
@@ -121,29 +124,30 @@ __global__ __launch_bounds__(kThreads) void layout_kernel(const or_layout_desc d
                                                           int64_t sum_q, int64_t sum_k) {
   __shared__ LayoutDerived L;
   __shared__ SegTable S;
-  __shared__ int scan[kThreads];
   __shared__ int sh_tmp[kMaxShared];
   const int tid = threadIdx.x;
   const int ns = d.n_scenes;
+  const int n_seg = d.with_text ? 2 * ns : ns;
 
-  // 1. frame / text / rope prefix sums
-  {
-    int len = tid < ns ? d.lengths[tid] : 0;
-    int lo = block_exclusive_scan(len, ns, scan);
-    int cnt = (tid < ns && d.with_text) ? d.counts[tid] : 0;
-    int t0 = block_exclusive_scan(cnt, ns, scan);
+  if (tid < 64) {
+    const int lane = tid;
+    // 1. frame / text / rope prefix sums (lane j: scene j)
+    const int len = lane < ns ? d.lengths[lane] : 0;
+    const int lo = wave_scan(len) - len;
+    const int cnt = (lane < ns && d.with_text) ? d.counts[lane] : 0;
+    const int t0 = wave_scan(cnt) - cnt;
     const int nr = d.n_rope_lengths > 0 ? d.n_rope_lengths : ns;
-    int rl = tid < nr ? (d.n_rope_lengths > 0 ? d.rope_lengths[tid] : d.lengths[tid]) : 0;
-    int rs = block_exclusive_scan(rl, nr, scan);
-    if (tid < ns) {
-      L.lo[tid] = lo;
-      L.hi[tid] = lo + len;
-      L.t0[tid] = t0;
-      L.t1[tid] = t0 + cnt;
+    const int rl = lane < nr ? (d.n_rope_lengths > 0 ? d.rope_lengths[lane] : d.lengths[lane]) : 0;
+    const int rs = wave_scan(rl) - rl;
+    if (lane < ns) {
+      L.lo[lane] = lo;
+      L.hi[lane] = lo + len;
+      L.t0[lane] = t0;
+      L.t1[lane] = t0 + cnt;
     }
-    if (tid < nr) L.rope_start[tid] = rs;
-    if (tid == nr - 1) L.rope_start[nr] = rs + rl;
-    if (tid == 0) {
+    if (lane < nr) L.rope_start[lane] = rs;
+    if (lane == nr - 1) L.rope_start[nr] = rs + rl;
+    if (lane == 0) {
       L.n_scenes = ns;
       L.T = d.T;
       L.with_text = d.with_text;
@@ -152,51 +156,52 @@ __global__ __launch_bounds__(kThreads) void layout_kernel(const or_layout_desc d
       L.text_rows = d.text_rows;
       L.n_rope = nr;
     }
-    if (tid == ns - 1) L.F = lo + len;
-  }
-  __syncthreads();
+    if (lane == ns - 1) L.F = lo + len;
+    wave_lds_sync();
 
-  // 2. shared frames per scene: upper-bound slots, then compaction
-  {
+    // 2. shared frames per scene: upper-bound slots, then compaction (host validation keeps them within kMaxShared)
     int ub = 0;
-    if (tid < ns) {
+    if (lane < ns) {
       const int k = d.halo;
-      if (k > 0 && tid > 0 && (d.sides == 0 || d.sides == 1)) ub += min(k, d.lengths[tid - 1]);
-      if (k > 0 && tid + 1 < ns && (d.sides == 0 || d.sides == 2)) ub += min(k, d.lengths[tid + 1]);
-      ub += d.extra_ptr[tid + 1] - d.extra_ptr[tid];
+      if (k > 0 && lane > 0 && (d.sides == 0 || d.sides == 1)) ub += min(k, d.lengths[lane - 1]);
+      if (k > 0 && lane + 1 < ns && (d.sides == 0 || d.sides == 2)) ub += min(k, d.lengths[lane + 1]);
+      ub += d.extra_ptr[lane + 1] - d.extra_ptr[lane];
     }
-    int off = block_exclusive_scan(ub, ns, scan);  // host validation keeps the total within kMaxShared
+    const int off = wave_scan(ub) - ub;
     int n = 0;
-    if (tid < ns) n = scene_shared_frames(d, L.lo, L.hi, tid, sh_tmp + off, ub);
-    int ptr = block_exclusive_scan(n, ns, scan);
-    if (tid < ns) {
-      L.sh_ptr[tid] = ptr;
+    if (lane < ns) n = scene_shared_frames(d, L.lo, L.hi, lane, sh_tmp + off, ub);
+    const int ptr = wave_scan(n) - n;
+    if (lane < ns) {
+      L.sh_ptr[lane] = ptr;
       for (int i = 0; i < n; ++i) L.sh[ptr + i] = sh_tmp[off + i];
     }
-    if (tid == ns - 1) L.sh_ptr[ns] = ptr + n;
-    __syncthreads();
-    if (tid < ns && d.adjacent) {
-      for (int i = 0; i < n; ++i) L.sh_dst[ptr + i] = shared_dst(L, tid, L.sh + ptr, n, L.sh[ptr + i]);
+    if (lane == ns - 1) L.sh_ptr[ns] = ptr + n;
+    wave_lds_sync();
+    if (lane < ns && d.adjacent) {
+      for (int i = 0; i < n; ++i) L.sh_dst[ptr + i] = shared_dst(L, lane, L.sh + ptr, n, L.sh[ptr + i]);
     }
-  }
-  __syncthreads();
+    wave_lds_sync();
 
-  // 3. segments and cu_seqlens
-  const int n_seg = d.with_text ? 2 * ns : ns;
-  {
-    int lq = 0, lk = 0;
-    if (tid < n_seg) seg_lengths(L, tid, &lq, &lk);
-    int cq = block_exclusive_scan(lq, n_seg, scan);
-    int ck = block_exclusive_scan(lk, n_seg, scan);
-    if (tid < n_seg) {
-      S.cu_q[tid] = cq;
-      S.cu_k[tid] = ck;
+    // 3. segments and cu_seqlens: lane l holds segments l and 64 + l
+    int lq0 = 0, lk0 = 0, lq1 = 0, lk1 = 0;
+    if (lane < n_seg) seg_lengths(L, lane, &lq0, &lk0);
+    if (64 + lane < n_seg) seg_lengths(L, 64 + lane, &lq1, &lk1);
+    const int cq0 = wave_scan(lq0), ck0 = wave_scan(lk0);
+    const int tq = __shfl(cq0, 63, 64), tk = __shfl(ck0, 63, 64);
+    const int cq1 = wave_scan(lq1) + tq, ck1 = wave_scan(lk1) + tk;
+    if (lane < n_seg) {
+      S.cu_q[lane] = cq0 - lq0;
+      S.cu_k[lane] = ck0 - lk0;
     }
-    if (tid == n_seg - 1) {
-      S.cu_q[n_seg] = cq + lq;
-      S.cu_k[n_seg] = ck + lk;
+    if (64 + lane < n_seg) {
+      S.cu_q[64 + lane] = cq1 - lq1;
+      S.cu_k[64 + lane] = ck1 - lk1;
     }
-    if (tid == 0) S.n_seg = n_seg;
+    if (lane == 63) {
+      S.cu_q[n_seg] = cq1;
+      S.cu_k[n_seg] = ck1;
+      S.n_seg = n_seg;
+    }
   }
   __syncthreads();
   if (blockIdx.x == 0) {
@@ -411,7 +416,7 @@ extern "C" int or_layout_build(const or_layout_desc* desc, const or_layout_out* 
   if (!out) return fail_arg("or_layout_build: out is NULL");
   RowOut ro{out->q_src, out->q_rope, out->k_src, out->k_rope, out->k_move_a, out->k_move_b};
   const int64_t total = sz.sum_q + sz.sum_k;
-  int64_t blocks = (total + kThreads * 4 - 1) / (kThreads * 4);  // about 4 rows per thread
+  int64_t blocks = (total + kThreads * 2 - 1) / (kThreads * 2);  // about 2 rows per thread
   if (blocks < 1) blocks = 1;
   if (blocks > 2048) blocks = 2048;
   hipLaunchKernelGGL(layout_kernel, dim3((unsigned)blocks), dim3(kThreads), 0, (hipStream_t)stream, *desc, ro,
