@@ -9,8 +9,11 @@ on the keys), the varlen attention (RoPE on the Q load, output in place) and the
 value = useful attention TFLOP/s of the whole step (sum over scopes of 4 * Lq * Lk * H * D per step time).
 roofline: the attention kernel alone, timed with HIP events on the stream it runs on.
 cpu_baseline: the oracle's packing plus torch SDPA per scope in fp32 on the host cores, on a sample of heads.
+gemm_reference: torch.matmul (hipBLASLt) of two bf16 16384 x 16384 N(0, 1) matrices in the same run: what the
+vendor's dense bf16 GEMM reaches on this GPU with data of the same distribution. MI355X throttles its clock under
+MFMA load (power limit), and MFMA power depends on the operand bits, so this is the practical MFMA ceiling here.
 
-    python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--no-cpu]
+    python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--no-cpu] [--no-gemm-ref]
 """
 from __future__ import annotations
 
@@ -63,6 +66,39 @@ def time_events(fn, reps, stream):
     return a.elapsed_time(b) / reps
 
 
+def time_cold(fn, reps, stream, flush):
+    """average duration of `reps` single calls, each after `flush` (not timed) evicted the L2 and the 256 MB last-level
+    cache, so that an HBM-bound kernel reads its inputs from HBM rather than from data the previous call left"""
+    import torch
+    total = 0.0
+    for _ in range(reps):
+        flush()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        fn()
+        b.record(stream)
+        b.synchronize()
+        total += a.elapsed_time(b)
+    return total / reps
+
+
+def gemm_reference(n=16384, reps=5):
+    """TFLOP/s of torch.matmul on bf16 N(0, 1) n x n matrices (hipBLASLt), best of three timings of `reps` calls"""
+    import torch
+    g = torch.Generator(device='cuda').manual_seed(1)
+    a = torch.randn(n, n, generator=g, device='cuda').to(torch.bfloat16)
+    b = torch.randn(n, n, generator=g, device='cuda').to(torch.bfloat16)
+    c = a @ b
+    torch.cuda.synchronize()
+    st = torch.cuda.current_stream()
+    ms = min(time_events(lambda: torch.matmul(a, b, out=c), reps, st) for _ in range(3))
+    tflops = 2.0 * n ** 3 / ms / 1e9
+    del a, b, c
+    torch.cuda.empty_cache()
+    return dict(what=f'torch.matmul bf16 {n}x{n}x{n}, N(0,1) inputs (hipBLASLt), same run', ms=round(ms, 4),
+                tflops=round(tflops, 1), frac_bf16_peak=round(tflops / PEAK_BF16_TFLOPS, 4))
+
+
 def cpu_baseline(heads=16, runs=3):
     """the oracle's packing + per-scope fp32 SDPA on the host CPU, for `heads` of the 16 heads (median of runs)"""
     import numpy as np
@@ -112,9 +148,11 @@ def main():
     ap.add_argument('--warmup', type=int, default=3)
     ap.add_argument('--no-cpu', action='store_true', help='skip the CPU baseline leg')
     ap.add_argument('--kernel-reps', type=int, default=10)
+    ap.add_argument('--no-gemm-ref', action='store_true', help='skip the bf16 GEMM reference')
     ap.add_argument('--once', action='store_true',
                     help='profiling mode: a 1 GiB device copy (counter calibration), then the layout, pack-gather, '
-                         'attention and scatter kernels once each; prints nothing else')
+                         'attention and scatter kernels once each, then one bf16 16384^3 torch.matmul (the GEMM '
+                         'reference); prints nothing else')
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get('WORLD_SIZE', '1')) != 1:
         print('bench.py measures the single-GPU scene-attention path only: run it with --gpus 1 '
@@ -151,7 +189,8 @@ def main():
                                        vbuf=vbuf)
         scene.scatter(plan, torch.zeros(plan.sum_q, H, D, dtype=torch.bfloat16, device=dev), ov, ot)
         torch.cuda.synchronize()
-        print('once: copy 1 GiB, layout, pack_gather, plan + attention, scatter', flush=True)
+        gemm_reference(reps=1)
+        print('once: copy 1 GiB, layout, pack_gather, plan + attention, scatter, bf16 GEMM reference', flush=True)
         return
 
     def step():
@@ -185,9 +224,14 @@ def main():
     scat()
     torch.cuda.synchronize()
     t_attn = time_events(attn, R, stream)
-    t_pack = time_events(pack, R, stream)
-    t_layout = time_events(plan.build, R, stream)
-    t_scat = time_events(scat, R, stream)
+    # HBM-bound kernels: each call timed alone after the caches were evicted (cold), and back to back (warm: inputs
+    # that fit the 256 MB last-level cache are then partly served from it)
+    evict = torch.ones(128 << 20, dtype=torch.int32, device=dev)
+    flush = lambda: evict.sum()   # reads 512 MB: the caches then hold clean lines of it, nothing to write back
+    t_pack, t_pack_w = time_cold(pack, R, stream, flush), time_events(pack, R, stream)
+    t_layout = time_cold(plan.build, R, stream, flush)
+    t_scat, t_scat_w = time_cold(scat, R, stream, flush), time_events(scat, R, stream)
+    del evict
     row = H * D * 2
     pack_bytes = 2 * 2 * plan.sum_k * row            # K and V rows read + written
     scat_bytes = 2 * plan.sum_q * row                # packed rows read + written
@@ -195,11 +239,13 @@ def main():
         'attention': dict(ms=round(t_attn, 4), tflops=round(flops / t_attn / 1e9, 1),
                           frac_bf16_peak=round(flops / t_attn / 1e9 / PEAK_BF16_TFLOPS, 4)),
         'pack_gather_kv': dict(ms=round(t_pack, 4), gbs=round(pack_bytes / t_pack / 1e6, 1),
-                               frac_hbm_peak=round(pack_bytes / t_pack / 1e6 / PEAK_HBM_GBS, 4), bytes=pack_bytes),
+                               frac_hbm_peak=round(pack_bytes / t_pack / 1e6 / PEAK_HBM_GBS, 4), bytes=pack_bytes,
+                               warm_ms=round(t_pack_w, 4), timing='cold caches, single calls'),
         'layout': dict(us=round(t_layout * 1e3, 2), gbs=round(plan.index_bytes() / t_layout / 1e6, 1),
-                       bytes=plan.index_bytes()),
+                       bytes=plan.index_bytes(), bound='launch latency (1.4 MB of int32 indices)'),
         'scatter': dict(ms=round(t_scat, 4), gbs=round(scat_bytes / t_scat / 1e6, 1),
-                        frac_hbm_peak=round(scat_bytes / t_scat / 1e6 / PEAK_HBM_GBS, 4), bytes=scat_bytes),
+                        frac_hbm_peak=round(scat_bytes / t_scat / 1e6 / PEAK_HBM_GBS, 4), bytes=scat_bytes,
+                        warm_ms=round(t_scat_w, 4), timing='cold caches, single calls'),
     }
     traffic = None
     tf = ROOT / 'profiles' / 'attention_traffic.json'
@@ -217,6 +263,8 @@ def main():
                              unit='TFLOP/s', frac=round(flops / t_attn / 1e9 / PEAK_BF16_TFLOPS, 4), traffic=traffic,
                              kernel='attn4_kernel<128> (+ plan_kernel, one block, ~10 us)'),
                kernels=kernels)
+    if not args.no_gemm_ref:
+        out['gemm_reference'] = gemm_reference()
     if not args.no_cpu:
         out['cpu_baseline'] = cpu_baseline()
     print(json.dumps(out), flush=True)
