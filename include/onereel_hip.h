@@ -6,6 +6,7 @@
  *   or_pack_gather    K/V (or Q) rows of every scope packed densely, RoPE applied on the way
  *   or_varlen_fwd     packed varlen attention (bf16 MFMA), optional RoPE on the Q load, optional in-place Q / O
  *   or_scatter        packed output rows written back to token order, text padding rows zeroed
+ *   or_lse_merge      log-sum-exp merge of two partial attention results (attention split over key sets)
  *
  * Conventions: every tensor is caller-owned device memory passed as a raw pointer; rows are [row][head][dim] with a
  * row stride in elements; bf16 is IEEE bfloat16 stored as uint16_t; index arrays are int32. Every launch goes on the
@@ -150,6 +151,15 @@ int64_t or_varlen_workspace_size(int32_t n_seg, int32_t sum_q, int32_t H, int32_
  * overlapping_ranges' FA3 call with seqused_k (:78-83): non-causal softmax(q k^T * scale) v per segment, bf16 in and
  * out, fp32 accumulation. Two launches: a tile planner and the attention kernel. */
 int or_varlen_fwd(const or_varlen_args* args, void* stream);
+
+/* Replaces the log-sum-exp merge of partial attention results: ring._merge (src/onereel/parallel/ring.py:63-70) and
+ * the merge in Processor._far_lse (src/onereel/models/hunyuan15.py:270-275). o: fp32 [n_rows, H, D] (row stride
+ * o_row_stride elements), lse: fp32 [H, n_rows], both updated in place with the partial result o_s: bf16
+ * [n_rows, H, D] (row stride os_row_stride), lse_s: fp32 [H, n_rows] (as or_varlen_fwd writes them). Per (row, head):
+ * m = max(lse, lse_s) (0 if infinite), w1 = exp(lse - m), w2 = exp(lse_s - m), o = o * (w1 / (w1 + w2)) +
+ * o_s * (w2 / (w1 + w2)), lse = m + log(w1 + w2). Two kernel launches. */
+int or_lse_merge(float* o, float* lse, const void* o_s, const float* lse_s, int64_t n_rows, int32_t H, int32_t D,
+                 int64_t o_row_stride, int64_t os_row_stride, void* stream);
 
 /* Message of the calling thread's last failed call ("" if none). */
 const char* or_last_error(void);

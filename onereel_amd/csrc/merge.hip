@@ -1,0 +1,104 @@
+// Log-sum-exp merge of partial attention results: the combine step of attention split over key sets.
+//
+// Reference: ring._merge (src/onereel/parallel/ring.py:63-70), which folds a partial (o_s, lse_s) into the running
+// fp32 (o, lse) of a ring step, and Processor._far_lse (src/onereel/models/hunyuan15.py:270-275), which merges the
+// local-key and the received-key halves of a scene's attention. Per query row n and head h:
+//   m   = max(lse, lse_s), replaced by 0 when infinite (both sides empty: -inf)
+//   w1  = exp(lse - m), w2 = exp(lse_s - m), den = w1 + w2
+//   o   = o * (w1 / den) + o_s * (w2 / den)      (two rounded products, then a rounded sum, as torch's mul_ / add_)
+//   lse = m + log(den)
+//
+// HBM-bound: per element 4 B of o read and written and 2 B of o_s read. One thread per 8 consecutive elements of a
+// (row, head) pair, each computing the pair's weights from its two lse scalars; a second launch then writes the new
+// lse (the first reads the old one in every thread of a pair).
+#include <math.h>
+
+#include "common.h"
+
+namespace onereel {
+
+namespace {
+
+constexpr int kThreads = 256;
+
+struct MergeArgs {
+  float* o;
+  float* lse;
+  const uint16_t* o_s;
+  const float* lse_s;
+  int64_t n_rows, o_stride, os_stride;   // row strides in elements
+  int H, D;
+};
+
+// one thread per 8 consecutive elements of one (row, head); D / 8 threads per pair
+__global__ __launch_bounds__(kThreads) void lse_merge_kernel(MergeArgs g) {
+  const int per = g.D >> 3;
+  const int64_t total = g.n_rows * g.H * per;
+  for (int64_t t = (int64_t)blockIdx.x * kThreads + threadIdx.x; t < total; t += (int64_t)gridDim.x * kThreads) {
+    const int64_t pair = t / per;
+    const int c = (int)(t - pair * per);
+    const int64_t n = pair / g.H;
+    const int h = (int)(pair - n * g.H);
+    const float l1 = g.lse[(int64_t)h * g.n_rows + n], l2 = g.lse_s[(int64_t)h * g.n_rows + n];
+    float m = fmaxf(l1, l2);
+    if (isinf(m)) m = 0.0f;
+    const float w1 = expf(l1 - m), w2 = expf(l2 - m);
+    const float den = w1 + w2;
+    const float a = w1 / den, b = w2 / den;
+    float* op = g.o + n * g.o_stride + (int64_t)h * g.D + 8 * c;
+    const uint16_t* sp = g.o_s + n * g.os_stride + (int64_t)h * g.D + 8 * c;
+    const u32x4 s = *(const u32x4*)sp;
+    f32x4 x0 = *(const f32x4*)op, x1 = *(const f32x4*)(op + 4);
+    float y[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma clang fp contract(off)
+      const float s_lo = bf2f((uint16_t)(s[i] & 0xffffu)), s_hi = bf2f((uint16_t)(s[i] >> 16));
+      const float xa = (i < 2 ? x0[2 * i] : x1[2 * i - 4]) * a;
+      const float xb = (i < 2 ? x0[2 * i + 1] : x1[2 * i - 3]) * a;
+      y[2 * i] = xa + s_lo * b;
+      y[2 * i + 1] = xb + s_hi * b;
+    }
+    *(f32x4*)op = f32x4{y[0], y[1], y[2], y[3]};
+    *(f32x4*)(op + 4) = f32x4{y[4], y[5], y[6], y[7]};
+  }
+}
+
+// lse = m + log(w1 + w2) per (head, row), after lse_merge_kernel has used the old values
+__global__ __launch_bounds__(kThreads) void lse_update_kernel(float* lse, const float* lse_s, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n; i += (int64_t)gridDim.x * kThreads) {
+    const float l1 = lse[i], l2 = lse_s[i];
+    float m = fmaxf(l1, l2);
+    if (isinf(m)) m = 0.0f;
+    lse[i] = m + logf(expf(l1 - m) + expf(l2 - m));
+  }
+}
+
+}  // namespace
+}  // namespace onereel
+
+using namespace onereel;
+
+extern "C" int or_lse_merge(float* o, float* lse, const void* o_s, const float* lse_s, int64_t n_rows, int32_t H,
+                            int32_t D, int64_t o_row_stride, int64_t os_row_stride, void* stream) {
+  if (n_rows < 0 || H < 1 || D < 8 || D % 8 != 0 || D > 512)
+    return fail_arg("or_lse_merge: need n_rows >= 0, H >= 1 and D a multiple of 8 in [8, 512] (H=%d D=%d)", H, D);
+  if (n_rows == 0) return 0;
+  if (!o || !lse || !o_s || !lse_s) return fail_arg("or_lse_merge: o, lse, o_s and lse_s are required");
+  if (o_row_stride < (int64_t)H * D || os_row_stride < (int64_t)H * D)
+    return fail_arg("or_lse_merge: row strides must cover H * D elements");
+  if (((uintptr_t)o | (uintptr_t)o_s) & 15u || o_row_stride % 4 || os_row_stride % 8)
+    return fail_arg("or_lse_merge: o and o_s must be 16-byte aligned, row strides multiples of 16 bytes");
+  MergeArgs g{o, lse, (const uint16_t*)o_s, lse_s, n_rows, o_row_stride, os_row_stride, H, D};
+  const int64_t total = n_rows * H * (D / 8);
+  int64_t blocks = (total + kThreads - 1) / kThreads;
+  if (blocks > 256 * 32) blocks = 256 * 32;
+  hipLaunchKernelGGL(lse_merge_kernel, dim3((unsigned)blocks), dim3(kThreads), 0, (hipStream_t)stream, g);
+  if (int rc = check_hip(hipGetLastError(), "lse_merge_kernel launch")) return rc;
+  const int64_t n_lse = n_rows * H;
+  int64_t lb = (n_lse + kThreads - 1) / kThreads;
+  if (lb > 256 * 8) lb = 256 * 8;
+  hipLaunchKernelGGL(lse_update_kernel, dim3((unsigned)lb), dim3(kThreads), 0, (hipStream_t)stream, lse, lse_s,
+                     n_lse);
+  return check_hip(hipGetLastError(), "lse_update_kernel launch");
+}

@@ -15,6 +15,8 @@ TEST INFRASTRUCTURE ONLY (see `oracle/__init__.py`). Restates:
                        torch.nn.functional.scaled_dot_product_attention per scope (no mask)
 - `scene_layer`        Processor.scene on one GPU (hunyuan15.py:212-251): ov[q rows] = video outputs, ot = zeros then
                        text outputs (rows past the valid text stay 0)
+- `merge_lse`          ring._merge (src/onereel/parallel/ring.py:63-70): a partial (o_s, lse_s) folded into the
+                       running fp32 (o, lse); the same weights as Processor._far_lse's merge (hunyuan15.py:270-275)
 """
 from __future__ import annotations
 
@@ -157,3 +159,29 @@ def masked_reference(lay, T, counts, q, k, v, eq, ek, ev):
     p = torch.softmax(s, -1).nan_to_num(0.0)
     o = torch.einsum('hqk,khd->qhd', p, vv)
     return o[:S], o[S:]
+
+
+def merge_lse(o, lse, o_s, lse_s):
+    """ring._merge (ring.py:63-70), out of place: o [N, H, D] fp32, lse [H, N] fp32, o_s [N, H, D] (cast to o's dtype,
+    as the reference's o_s.float()), lse_s [H, N] -> (o, lse) merged. m = max(lse, lse_s), 0 where infinite; w1 = exp(lse - m), w2 = exp(lse_s - m);
+    o * (w1 / den) + o_s * (w2 / den) with den = w1 + w2; lse = m + log(den). Pinned in tests/test_oracle.py by the
+    identity it exists for: merging attention over two disjoint key sets equals attention over their union."""
+    m = torch.maximum(lse, lse_s)
+    m = torch.where(torch.isinf(m), torch.zeros_like(m), m)
+    w1, w2 = torch.exp(lse - m), torch.exp(lse_s - m)
+    den = w1 + w2
+    out = o * (w1 / den).transpose(0, 1)[..., None] + o_s.to(o.dtype) * (w2 / den).transpose(0, 1)[..., None]
+    return out, m + torch.log(den)
+
+
+def attention_lse(q, k, v):
+    """dense attention of q [N, H, D] over k / v [M, H, D] in float64: (out [N, H, D], lse [H, N], natural log of the
+    scaled scores' exp-sum; -inf and out 0 when M == 0)"""
+    q, k, v = q.double(), k.double(), v.double()
+    D = q.shape[-1]
+    if k.shape[0] == 0:
+        return torch.zeros_like(q), torch.full((q.shape[1], q.shape[0]), -float('inf'), dtype=torch.float64)
+    s = torch.einsum('nhd,mhd->hnm', q, k) * D ** -0.5
+    lse = torch.logsumexp(s, -1)
+    out = torch.einsum('hnm,mhd->nhd', torch.softmax(s, -1), v)
+    return out, lse

@@ -237,3 +237,36 @@ def test_native_library_is_the_in_tree_build():
     L.lib()
     maps = open('/proc/self/maps').read()
     assert str(L.LIB_PATH) in maps
+
+
+@pytest.mark.parametrize('split', [0, 1, 300, 777])
+def test_lse_merge_of_two_key_sets(split):
+    """varlen_lse over keys [0, split) and [split, 777) of each segment, merged by or_lse_merge: equals the oracle's
+    ring._merge of the same partial results (fp32, 1e-5) and attention over all keys (bf16 tolerance)"""
+    print(f'lse merge split={split}', flush=True)
+    H, D, nk = 3, 128, 777
+    lq = [65, 130]
+    q = rand_bf16((sum(lq), H, D), 41)
+    k = rand_bf16((2 * nk, H, D), 42)
+    v = rand_bf16((2 * nk, H, D), 43)
+    cq = torch.tensor([0, lq[0], sum(lq)], dtype=torch.int32, device=DEV)
+
+    def part(a, b):
+        # an empty key set is passed as zero-length segments over a one-row buffer (the kernel's Lk = 0 path)
+        kk = torch.cat([k[s * nk + a:s * nk + b] for s in range(2)] + [k[:1]]).to(DEV)
+        vv = torch.cat([v[s * nk + a:s * nk + b] for s in range(2)] + [v[:1]]).to(DEV)
+        ck = torch.tensor([0, b - a, 2 * (b - a)], dtype=torch.int32, device=DEV)
+        return A.varlen_lse(q.to(DEV), kk, vv, cq, ck, max(lq), max(b - a, 1))
+
+    o1, l1 = part(0, split)
+    o2, l2 = part(split, nk)
+    ref_o, ref_l = OA.merge_lse(o1.float().cpu(), l1.cpu(), o2.cpu(), l2.cpu())
+    o, lse = o1.float(), l1.clone()
+    A.merge_lse(o, lse, o2, l2)
+    torch.cuda.synchronize()
+    assert (o.cpu() - ref_o).abs().max() < 1e-5 and (lse.cpu() - ref_l).abs().max() < 1e-5
+    full = OA.packed_attention(q, k, v, np.array([0, lq[0], sum(lq)]), np.array([0, nk, 2 * nk]))
+    assert_close(o.cpu(), full, what='merged attention')
+    if split in (0, nk):   # one side empty: the other side's result, unchanged
+        keep, other = (o2, l2) if split == 0 else (o1, l1)
+        assert torch.equal(o.cpu(), keep.float().cpu()) and torch.equal(lse.cpu(), other.cpu())

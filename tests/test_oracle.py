@@ -265,3 +265,38 @@ def test_packed_layer_equals_masked_brute_force(case):
     assert (ov - rv).abs().max() < 1e-5
     assert (ot - rt).abs().max() < 1e-5
     assert ot[sum(case['counts']):].abs().max() == 0 if Le > sum(case['counts']) else True
+
+
+# ------------------------------------------------------------------------------------------------ log-sum-exp merge
+@pytest.mark.parametrize('split', [0, 1, 37, 60, 61])
+def test_merge_lse_of_disjoint_key_sets_is_attention_over_their_union(split):
+    """attention over keys [0, split) and [split, 61), merged, equals attention over all 61 keys (float64); an empty
+    side (split 0 or 61) leaves the other side unchanged"""
+    g = torch.Generator().manual_seed(split)
+    q, k, v = (torch.randn(n, 3, 16, generator=g, dtype=torch.float64) for n in (9, 61, 61))
+    o1, l1 = OA.attention_lse(q, k[:split], v[:split])
+    o2, l2 = OA.attention_lse(q, k[split:], v[split:])
+    o, lse = OA.merge_lse(o1, l1, o2, l2)
+    ref_o, ref_l = OA.attention_lse(q, k, v)
+    assert (o - ref_o).abs().max() < 1e-12
+    assert (lse - ref_l).abs().max() < 1e-12
+
+
+def test_attention_lse_matches_packed_attention_and_logsumexp():
+    """the float64 dense helper agrees with the oracle's packed attention and with an explicit log(sum(exp))"""
+    g = torch.Generator().manual_seed(3)
+    q, k, v = (torch.randn(n, 2, 32, generator=g) for n in (7, 19, 19))
+    o, lse = OA.attention_lse(q, k, v)
+    ref = OA.packed_attention(q, k, v, np.array([0, 7]), np.array([0, 19]))
+    assert (o.float() - ref).abs().max() < 1e-5
+    s = torch.einsum('nhd,mhd->hnm', q.double(), k.double()) / 32 ** 0.5
+    assert (lse - s.exp().sum(-1).log()).abs().max() < 1e-10
+
+
+def test_merge_lse_first_step_of_a_ring():
+    """a ring starts from o = 0, lse = -inf: the first merge returns the partial result exactly"""
+    g = torch.Generator().manual_seed(5)
+    o_s = torch.randn(4, 2, 8, generator=g).to(torch.bfloat16)
+    l_s = torch.randn(2, 4, generator=g)
+    o, lse = OA.merge_lse(torch.zeros(4, 2, 8), torch.full((2, 4), -float('inf')), o_s, l_s)
+    assert torch.equal(o, o_s.float()) and torch.allclose(lse, l_s, atol=0, rtol=0)
