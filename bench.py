@@ -37,6 +37,28 @@ REPS = [0, 10, 21, 31]
 GRID = (32, 30, 53)
 
 
+def workload(name):
+    """scene-attention layer shapes: the HunyuanVideo-1.5 480p layer (the default and headline), the Wan2.2 704x1280
+    joint scopes, and the 12-scene uneven sweep point (lengths and text counts drawn from numpy's generator seeded 12)"""
+    if name == 'hunyuan480p':
+        return dict(workload='hunyuan15-480p-4scene-scene-attention-layer', lengths=LENGTHS, T=T, counts=COUNTS, H=H,
+                    D=D, halo=0, sides='adj', reps=REPS, grid=GRID, scene_rope=True, adjacent=True)
+    if name == 'wan704':
+        return dict(workload='wan22-704x1280-3scene-joint-scope-attention-layer', lengths=[11] * 3, T=880,
+                    counts=[128] * 3, H=24, D=128, halo=2, sides='next', reps=None, grid=(33, 22, 40),
+                    scene_rope=False, adjacent=False)
+    if name == 'uneven12':
+        import numpy as np
+        rng = np.random.default_rng(12)
+        lengths = rng.integers(2, 17, 12).tolist()
+        counts = rng.integers(64, 257, 12).tolist()
+        F = sum(lengths)
+        reps = sorted({int(x) for x in np.linspace(0, F - 1, 4).round()})
+        return dict(workload='uneven-12-scene-sweep-attention-layer', lengths=lengths, T=1590, counts=counts, H=16,
+                    D=128, halo=0, sides='adj', reps=reps, grid=(F, 30, 53), scene_rope=True, adjacent=True)
+    raise ValueError(name)
+
+
 def rope_table(F, Hh, Ww, D, theta=1e4):
     """3D RoPE table (temporal / height / width pair groups, interleaved real pairs), fp32 [F*Hh*Ww, D]"""
     import torch
@@ -141,14 +163,84 @@ def cpu_baseline(heads=16, runs=3):
                 seconds=round(t, 3))
 
 
+def run_dit(args):
+    """one forward of a random-init Wan2.2-TI2V-5B-shaped DiT (30 blocks, hidden 3072 = 24 x 128, FFN 14336, bf16
+    weights N(0, 0.02)) over 16 scenes x 15 latent frames x 880 tokens (22 x 40 grid) with frame memory 4 and 128
+    text tokens per scene: end-to-end ms per step (one transformer pass; classifier-free guidance would double it)"""
+    import torch
+    from onereel_amd import wan_dit as WD
+    from onereel_amd.layout import SceneLayout
+    dev = torch.device('cuda:0')
+    torch.cuda.set_device(dev)
+    lengths, Tw, text_len, grid = [15] * 16, 880, 128, (240, 22, 40)
+    F = sum(lengths)
+    reps = sorted({int(round(x)) for x in [i * (F - 1) / 3 for i in range(4)]})
+    lay = SceneLayout(lengths, halo=0, extra=extra_from_reps(lengths, reps))
+    cfg = WD.DiTConfig()
+    model = WD.WanDiT(cfg, lay, Tw, text_len, dev, seed=0)
+    g = torch.Generator(device=dev).manual_seed(0)
+    S = F * Tw
+    tokens = torch.randn(S, cfg.in_channels * cfg.patch, generator=g, device=dev).to(torch.bfloat16)
+    text = torch.randn(len(lengths) * text_len, cfg.text_dim, generator=g, device=dev).to(torch.bfloat16)
+    rot = tuple(x.to(dev) for x in WD.wan_rope_table(*grid, cfg.dim // cfg.heads))
+    steps = args.steps if args.steps is not None else 3
+    warmup = args.warmup if args.warmup is not None else 1
+    for _ in range(warmup):
+        model.forward(tokens, 500.0, text, rot)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        model.forward(tokens, 500.0, text, rot)
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    # one more pass with events around the attention processors (outside the timed steps)
+    marks = {'self': [], 'cross': []}
+
+    def timed(kind, fn):
+        def run(*a, **kw):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            out = fn(*a, **kw)
+            e1.record()
+            marks[kind].append((e0, e1))
+            return out
+        return run
+    p_self, p_cross = model.p_self, model.p_cross
+    model.p_self, model.p_cross = timed('self', p_self), timed('cross', p_cross)
+    model.forward(tokens, 500.0, text, rot)
+    torch.cuda.synchronize()
+    model.p_self, model.p_cross = p_self, p_cross
+    attn_ms = {k: sum(a.elapsed_time(b) for a, b in v) for k, v in marks.items()}
+    fl = model.flops(len(lengths) * text_len)
+    total = sum(fl.values())
+    out = dict(metric='Wan2.2-TI2V-5B-shaped DiT forward, ms/step (16 scenes x 15 frames x 880 tokens, frame memory 4)',
+               value=round(ms, 2), unit='ms', n_gpus=1, steps=steps, warmup=warmup, ms_per_step=round(ms, 2),
+               higher_is_better=False, scaling='weak', vs_baseline=None, dtype='bf16',
+               data='synthetic latent, text and timestep; random-init N(0, 0.02) bf16 weights',
+               config=dict(workload='wan22-ti2v-5b-dit-forward-16scene', blocks=cfg.blocks, hidden=cfg.dim,
+                           heads=cfg.heads, head_dim=cfg.dim // cfg.heads, ffn=cfg.ffn, scenes=len(lengths),
+                           frames_per_scene=15, tokens_per_frame=Tw, tokens=S, text_per_scene=text_len,
+                           frame_memory=reps, classifier_free_guidance=False),
+               flop_per_step={k: float(v) for k, v in fl.items()}, tflops=round(total / ms / 1e9, 1),
+               attention_ms=dict(self_processors=round(attn_ms['self'], 2), cross_processors=round(attn_ms['cross'], 2),
+                                 what='processor calls: QKV / output projections, _qk, layout, pack and varlen '
+                                      'kernels (self); projections and varlen (cross)'))
+    print(json.dumps(out), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument('--gpus', type=int, default=1)
-    ap.add_argument('--steps', type=int, default=20)
-    ap.add_argument('--warmup', type=int, default=3)
+    ap.add_argument('--steps', type=int, default=None, help='timed steps (default 20; 3 for wan-dit-step)')
+    ap.add_argument('--warmup', type=int, default=None, help='untimed steps first (default 3; 1 for wan-dit-step)')
     ap.add_argument('--no-cpu', action='store_true', help='skip the CPU baseline leg')
     ap.add_argument('--kernel-reps', type=int, default=10)
     ap.add_argument('--no-gemm-ref', action='store_true', help='skip the bf16 GEMM reference')
+    ap.add_argument('--workload', default='hunyuan480p', choices=['hunyuan480p', 'wan704', 'uneven12', 'wan-dit-step'],
+                    help='hunyuan480p (default, the headline): the HunyuanVideo-1.5 480p 4-scene layer; wan704 and '
+                         'uneven12: the same layer at the Wan2.2 704x1280 and 12-scene uneven shapes; wan-dit-step: '
+                         'one forward of a random-init Wan2.2-TI2V-5B-shaped DiT over 16 scenes x 15 frames x 880 '
+                         'tokens with frame memory 4 (end-to-end ms per step)')
     ap.add_argument('--once', action='store_true',
                     help='profiling mode: a 1 GiB device copy (counter calibration), then the layout, pack-gather, '
                          'attention and scatter kernels once each, then one bf16 16384^3 torch.matmul (the GEMM '
@@ -159,6 +251,14 @@ def main():
               '(the multi-GPU K/V gathering / Ulysses paths are not part of this build)', file=sys.stderr)
         sys.exit(2)
 
+    if args.workload == 'wan-dit-step':
+        return run_dit(args)
+    args.steps = 20 if args.steps is None else args.steps
+    args.warmup = 3 if args.warmup is None else args.warmup
+    W = workload(args.workload)
+    headline = args.workload == 'hunyuan480p'
+    T_, H_, D_ = W['T'], W['H'], W['D']
+
     import torch
     from onereel_amd import scene
     from onereel_amd.layout import SceneLayout
@@ -166,13 +266,15 @@ def main():
     dev = torch.device('cuda:0')
     torch.cuda.set_device(dev)
     stream = torch.cuda.current_stream(dev)
-    lay = SceneLayout(LENGTHS, halo=0, extra=extra_from_reps(LENGTHS, REPS))
-    S, Le = sum(LENGTHS) * T, sum(COUNTS)
+    extra = extra_from_reps(W['lengths'], W['reps']) if W['reps'] else {}
+    lay = SceneLayout(W['lengths'], halo=W['halo'], sides=W['sides'], extra=extra)
+    S, Le = sum(W['lengths']) * T_, sum(W['counts'])
     g = torch.Generator(device=dev).manual_seed(0)
-    q, k, v = (torch.randn(S, H, D, generator=g, device=dev).to(torch.bfloat16) for _ in range(3))
-    eq, ek, ev = (torch.randn(Le, H, D, generator=g, device=dev).to(torch.bfloat16) for _ in range(3))
-    cos, sin = (x.to(dev) for x in rope_table(*GRID, D))
-    plan = scene.ScopePlan(lay, T, COUNTS, Le, True, None, True, True, dev)
+    q, k, v = (torch.randn(S, H_, D_, generator=g, device=dev).to(torch.bfloat16) for _ in range(3))
+    eq, ek, ev = (torch.randn(Le, H_, D_, generator=g, device=dev).to(torch.bfloat16) for _ in range(3))
+    cos, sin = (x.to(dev) for x in rope_table(*W['grid'], D_))
+    plan = scene.ScopePlan(lay, T_, W['counts'], Le, W['scene_rope'], None, W['adjacent'], True, dev)
+    H, D = H_, D_
     lq = [int(x) for x in (plan.cu_q[1:] - plan.cu_q[:-1]).tolist()]
     lk = [int(x) for x in (plan.cu_k[1:] - plan.cu_k[:-1]).tolist()]
     flops = float(sum(4.0 * a * b * H * D for a, b in zip(lq, lk)))
@@ -189,7 +291,8 @@ def main():
                                        vbuf=vbuf)
         scene.scatter(plan, torch.zeros(plan.sum_q, H, D, dtype=torch.bfloat16, device=dev), ov, ot)
         torch.cuda.synchronize()
-        gemm_reference(reps=1)
+        if headline:
+            gemm_reference(reps=1)
         print('once: copy 1 GiB, layout, pack_gather, plan + attention, scatter, bf16 GEMM reference', flush=True)
         return
 
@@ -249,23 +352,25 @@ def main():
     }
     traffic = None
     tf = ROOT / 'profiles' / 'attention_traffic.json'
-    if tf.exists():
+    if headline and tf.exists():    # measured (PMC) on the headline layer only
         traffic = json.loads(tf.read_text()).get('hbm_bytes_per_launch')
     value = flops / (ms * 1e-3) / 1e12
-    out = dict(metric=METRIC, value=round(value, 2), unit='TFLOP/s', n_gpus=1, steps=args.steps, warmup=args.warmup,
+    metric = METRIC if headline else f'scene-attn TFLOP/s & % bf16 MFMA peak; ms/layer, {W["workload"]}'
+    out = dict(metric=metric, value=round(value, 2), unit='TFLOP/s', n_gpus=1, steps=args.steps, warmup=args.warmup,
                ms_per_step=round(ms, 4), higher_is_better=True, scaling='weak', vs_baseline=None, dtype='bf16',
                data='synthetic',
-               config=dict(workload='hunyuan15-480p-4scene-scene-attention-layer', scenes=4, frames_per_scene=8,
-                           tokens_per_frame=T, text_per_scene=128, frame_memory=4, shared_pos='adjacent',
-                           scene_rope=True, heads=H, head_dim=D, sum_q=plan.sum_q, sum_k=plan.sum_k,
+               config=dict(workload=W['workload'], scenes=len(W['lengths']), frames_per_scene=W['lengths'],
+                           tokens_per_frame=T_, text_per_scene=W['counts'], halo=W['halo'], sides=W['sides'],
+                           frame_memory=W['reps'], shared_pos='adjacent' if W['adjacent'] else 'source',
+                           scene_rope=W['scene_rope'], heads=H, head_dim=D, sum_q=plan.sum_q, sum_k=plan.sum_k,
                            useful_flop_per_step=flops, frac_bf16_peak_step=round(value / PEAK_BF16_TFLOPS, 4)),
                roofline=dict(bound='mfma', achieved=round(flops / t_attn / 1e9, 1), peak=PEAK_BF16_TFLOPS,
                              unit='TFLOP/s', frac=round(flops / t_attn / 1e9 / PEAK_BF16_TFLOPS, 4), traffic=traffic,
                              kernel='attn4_kernel<128> (+ plan_kernel, one block, ~10 us)'),
                kernels=kernels)
-    if not args.no_gemm_ref:
+    if headline and not args.no_gemm_ref:
         out['gemm_reference'] = gemm_reference()
-    if not args.no_cpu:
+    if headline and not args.no_cpu:
         out['cpu_baseline'] = cpu_baseline()
     print(json.dumps(out), flush=True)
 

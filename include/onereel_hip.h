@@ -7,6 +7,7 @@
  *   or_varlen_fwd     packed varlen attention (bf16 MFMA), optional RoPE on the Q load, optional in-place Q / O
  *   or_scatter        packed output rows written back to token order, text padding rows zeroed
  *   or_lse_merge      log-sum-exp merge of two partial attention results (attention split over key sets)
+ *   or_rmsnorm_rope   fused RMSNorm + interleaved RoPE of the Wan self-attention's queries and keys
  *
  * Conventions: every tensor is caller-owned device memory passed as a raw pointer; rows are [row][head][dim] with a
  * row stride in elements; bf16 is IEEE bfloat16 stored as uint16_t; index arrays are int32. Every launch goes on the
@@ -160,6 +161,17 @@ int or_varlen_fwd(const or_varlen_args* args, void* stream);
  * o_s * (w2 / (w1 + w2)), lse = m + log(w1 + w2). Two kernel launches. */
 int or_lse_merge(float* o, float* lse, const void* o_s, const float* lse_s, int64_t n_rows, int32_t H, int32_t D,
                  int64_t o_row_stride, int64_t os_row_stride, void* stream);
+
+/* Replaces _qk of the Wan self-attention (src/onereel/models/wan.py:64-74): RMSNorm over each token row's C = H * D
+ * elements with weight w (bf16 [C]) and eps, then diffusers' interleaved RoPE per head with c = cos[row, 2i],
+ * s = sin[row, 2i + 1] (cos[..., 0::2], sin[..., 1::2]): out[2i] = y[2i] c - y[2i+1] s, out[2i+1] = y[2i] s +
+ * y[2i+1] c; fp32 throughout, one rounding to bf16. q and k (k may be NULL) in one launch. Rows: bf16 with the given
+ * strides (elements); cos / sin: fp32 [n_rope_rows, D], table row rope_row[r] (rope_row NULL: row r; out of range:
+ * no rotation). D must divide 512 and C be a multiple of 512. */
+int or_rmsnorm_rope(const void* q, const void* k, const void* wq, const void* wk, int64_t q_row_stride,
+                    int64_t k_row_stride, int64_t n_rows, int32_t C, int32_t D, float eps, const float* cos_table,
+                    const float* sin_table, const int32_t* rope_row, int64_t n_rope_rows, void* q_out, void* k_out,
+                    int64_t qo_row_stride, int64_t ko_row_stride, void* stream);
 
 /* Message of the calling thread's last failed call ("" if none). */
 const char* or_last_error(void);

@@ -270,3 +270,27 @@ def test_lse_merge_of_two_key_sets(split):
     if split in (0, nk):   # one side empty: the other side's result, unchanged
         keep, other = (o2, l2) if split == 0 else (o1, l1)
         assert torch.equal(o.cpu(), keep.float().cpu()) and torch.equal(lse.cpu(), other.cpu())
+
+
+@pytest.mark.parametrize('S,heads,D', [(257, 24, 128), (64, 4, 128), (33, 16, 64)])
+def test_wan_qk_fused_norm_rope(S, heads, D):
+    """or_rmsnorm_rope (through wan._qk) against the oracle's fp32 restatement of _qk (wan.py:64-74): both fp32 with
+    one rounding, so they differ by at most one bf16 step and almost never; q and k read from strided views"""
+    print(f'wan _qk S={S} heads={heads} D={D}', flush=True)
+    from oracle import wan as OW
+    C = heads * D
+    g = torch.Generator().manual_seed(S)
+    qkv = (torch.randn(S, 3 * C, generator=g) * 3).to(torch.bfloat16)       # a fused projection: q / k are views
+    wq, wk = (torch.rand(C, generator=g) + 0.5).to(torch.bfloat16), (torch.rand(C, generator=g) + 0.5).to(torch.bfloat16)
+    ang = torch.randn(S, D // 2, generator=g)
+    cos, sin = ang.cos().repeat_interleave(2, 1), ang.sin().repeat_interleave(2, 1)
+    dev = qkv.to(DEV)
+    qo, ko = W._qk(dev[None, :, :C], dev[None, :, C:2 * C], wq.to(DEV), wk.to(DEV), 1e-6, cos[None, :, None].to(DEV),
+                   sin[None, :, None].to(DEV), heads)
+    assert qo.shape == (1, S, heads, D)
+    for got, x, w in ((qo, qkv[:, :C], wq), (ko, qkv[:, C:2 * C], wk)):
+        ref = OW.qk_norm_rope(x, w, 1e-6, cos, sin, heads)
+        got = got[0].cpu()
+        diff = (got.float() - ref.float()).abs()
+        assert (diff <= ref.float().abs() * 2 ** -7 + 1e-6).all(), diff.max()
+        assert (got.view(torch.int16) == ref.view(torch.int16)).float().mean() > 0.99

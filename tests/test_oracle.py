@@ -300,3 +300,24 @@ def test_merge_lse_first_step_of_a_ring():
     l_s = torch.randn(2, 4, generator=g)
     o, lse = OA.merge_lse(torch.zeros(4, 2, 8), torch.full((2, 4), -float('inf')), o_s, l_s)
     assert torch.equal(o, o_s.float()) and torch.allclose(lse, l_s, atol=0, rtol=0)
+
+
+# ------------------------------------------------------------------------------------------- Wan RMSNorm + RoPE
+def test_wan_qk_norm_rope_textbook_forms():
+    """unit RMS before the weight, and each head's pair rotation is the complex product (x1 + i x2)(c + i s); the
+    weight scales elementwise before the rotation"""
+    from oracle import wan as OW
+    g = torch.Generator().manual_seed(7)
+    S, H, D = 5, 4, 16
+    x = torch.randn(S, H * D, generator=g, dtype=torch.float64)
+    ang = torch.randn(S, D // 2, generator=g, dtype=torch.float64)
+    cos = ang.cos().repeat_interleave(2, 1)
+    sin = ang.sin().repeat_interleave(2, 1)
+    ones = torch.ones(H * D, dtype=torch.float64)
+    no_rot = OW.qk_norm_rope(x, ones, 0.0, torch.ones(S, D, dtype=torch.float64), torch.zeros(S, D, dtype=torch.float64), H)
+    assert torch.allclose(no_rot.reshape(S, -1).pow(2).mean(-1), torch.ones(S, dtype=torch.float64))
+    w = torch.rand(H * D, generator=g, dtype=torch.float64) + 0.5
+    out = OW.qk_norm_rope(x, w, 1e-6, cos, sin, H)
+    y = (x / (x.pow(2).mean(-1, keepdim=True) + 1e-6).sqrt() * w).view(S, H, D // 2, 2)
+    z = torch.complex(y[..., 0], y[..., 1]) * torch.polar(torch.ones_like(ang), ang)[:, None, :]
+    assert (out.view(S, H, D // 2, 2) - torch.stack([z.real, z.imag], -1)).abs().max() < 1e-12
