@@ -8,6 +8,8 @@
  *   or_scatter        packed output rows written back to token order, text padding rows zeroed
  *   or_lse_merge      log-sum-exp merge of two partial attention results (attention split over key sets)
  *   or_rmsnorm_rope   fused RMSNorm + interleaved RoPE of the Wan self-attention's queries and keys
+ *   or_frame_pool     frame memory: per-frame sums of hidden states (deterministic)
+ *   or_frame_select   frame memory: k-means (cosine) representatives and their medoids, one workgroup
  *
  * Conventions: every tensor is caller-owned device memory passed as a raw pointer; rows are [row][head][dim] with a
  * row stride in elements; bf16 is IEEE bfloat16 stored as uint16_t; index arrays are int32. Every launch goes on the
@@ -172,6 +174,21 @@ int or_rmsnorm_rope(const void* q, const void* k, const void* wq, const void* wk
                     int64_t k_row_stride, int64_t n_rows, int32_t C, int32_t D, float eps, const float* cos_table,
                     const float* sin_table, const int32_t* rope_row, int64_t n_rope_rows, void* q_out, void* k_out,
                     int64_t qo_row_stride, int64_t ko_row_stride, void* stream);
+
+/* Replaces the pooling of FrameMemory.collect (src/onereel/frame_memory.py:76-85, index_add_ of one layer's video rows
+ * into per-frame sums and counts): for the frame-major rows r of hs (bf16, row stride row_stride elements, C wide),
+ * frame (row0 + r) / T, sums[frame] += the row (fp32 [n_frames, C]) and counts[frame] += 1 (fp32 [n_frames]). Rows
+ * are added in row order: the result does not depend on scheduling. */
+int or_frame_pool(const void* hs, int64_t n_rows, int32_t C, int64_t row_stride, int64_t row0, int32_t T,
+                  int32_t n_frames, float* sums, float* counts, void* stream);
+
+/* Replaces FrameMemory.select (src/onereel/frame_memory.py:114-132): k-means with the dot product as similarity over
+ * the L2-normalised feature rows feats[cand[n]] (fp32 [n_frames, C]; cand: int32 [n_cand] device, each < n_frames):
+ * farthest-point initialisation from candidate 0, at most iters passes (stop when the centres do not change), then
+ * per non-empty cluster the member most similar to its centre (the first on ties). reps: int32 [k] device, the chosen
+ * frames ascending, -1 after them. work: fp32 [8, C] device scratch. One workgroup; k * C <= 32768. */
+int or_frame_select(const float* feats, int32_t n_frames, int32_t C, const int32_t* cand, int32_t n_cand, int32_t k,
+                    int32_t iters, int32_t* reps, float* work, void* stream);
 
 /* Message of the calling thread's last failed call ("" if none). */
 const char* or_last_error(void);

@@ -58,6 +58,8 @@ SIGNATURES = {
     'or_lse_merge': (i32, [vp, vp, vp, vp, i64, i32, i32, i64, i64, vp]),
     'or_rmsnorm_rope': (i32, [vp, vp, vp, vp, i64, i64, i64, i32, i32, ctypes.c_float, vp, vp, vp, i64, vp, vp, i64,
                               i64, vp]),
+    'or_frame_pool': (i32, [vp, i64, i32, i64, i64, i32, i32, vp, vp, vp]),
+    'or_frame_select': (i32, [vp, i32, i32, vp, i32, i32, i32, vp, vp, vp]),
     'or_last_error': (ctypes.c_char_p, []),
     'or_version': (ctypes.c_char_p, []),
 }

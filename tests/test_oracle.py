@@ -321,3 +321,51 @@ def test_wan_qk_norm_rope_textbook_forms():
     y = (x / (x.pow(2).mean(-1, keepdim=True) + 1e-6).sqrt() * w).view(S, H, D // 2, 2)
     z = torch.complex(y[..., 0], y[..., 1]) * torch.polar(torch.ones_like(ang), ang)[:, None, :]
     assert (out.view(S, H, D // 2, 2) - torch.stack([z.real, z.imag], -1)).abs().max() < 1e-12
+
+
+# ------------------------------------------------------------------------------------------------- frame memory
+def _groups(sizes, dim, noise, seed):
+    """frames in len(sizes) groups of near-identical unit features (the reference test's construction)"""
+    g = torch.Generator().manual_seed(seed)
+    base = torch.randn(len(sizes), dim, generator=g, dtype=torch.float64)
+    x = torch.cat([base[i].expand(n, -1) for i, n in enumerate(sizes)])
+    x = x + noise * torch.randn(x.shape, generator=g, dtype=torch.float64)
+    return torch.nn.functional.normalize(x, dim=-1)
+
+
+def test_frame_memory_select_one_medoid_per_group():
+    """tests/test_onereel_frame_memory.py:19-38: two groups of frames (5 and 4) give one representative each"""
+    from oracle import frame_memory as OF
+    feats = _groups([5, 4], 16, 0.01, 0)
+    reps = OF.select(feats, list(range(9)), 2)
+    assert len(reps) == 2 and min(reps) < 5 <= max(reps)
+
+
+@pytest.mark.parametrize('sizes,seed', [([5, 4], 1), ([7, 3, 9, 5], 2), ([1, 12, 6], 3)])
+def test_frame_memory_select_medoids_by_construction(sizes, seed):
+    """well-separated groups: each representative is the member of its group closest to the group's normalised mean"""
+    from oracle import frame_memory as OF
+    feats = _groups(sizes, 32, 0.05, seed)
+    reps = OF.select(feats, list(range(sum(sizes))), len(sizes))
+    exp, lo = [], 0
+    for n in sizes:
+        m = torch.nn.functional.normalize(feats[lo:lo + n].mean(0), dim=0)
+        exp.append(lo + int((feats[lo:lo + n] @ m).argmax()))
+        lo += n
+    assert reps == sorted(exp)
+
+
+def test_frame_memory_candidates_sink_and_pool():
+    """tests/test_onereel_frame_memory.py:41-60: boundary candidates, the sink excluded; pooling = per-frame sums"""
+    from oracle import frame_memory as OF
+    ranges = [(0, 4), (4, 8), (8, 12)]
+    assert OF.candidates(ranges, 12, 'boundary') == [0, 3, 4, 7, 8, 11]
+    assert 0 not in OF.candidates([(0, 3), (3, 6), (6, 9)], 9, 'all', sink=(0,))
+    g = torch.Generator().manual_seed(4)
+    feats = torch.nn.functional.normalize(torch.randn(12, 8, generator=g, dtype=torch.float64), dim=-1)
+    assert OF.select(feats, [0, 3, 4, 7, 8, 11], 3) == OF.select(feats, [0, 3, 4, 7, 8, 11], 3)
+    assert set(OF.select(feats, [0, 3, 4, 7, 8, 11], 3)) <= {0, 3, 4, 7, 8, 11}
+    hs = torch.randn(10, 3, generator=g)
+    frame = torch.tensor([0, 0, 1, 1, 1, -1, 2, 2, 2, 2])
+    s, c = OF.pool(frame, hs, 4)
+    assert torch.allclose(s[1], hs[2:5].double().sum(0)) and c.tolist() == [2, 3, 4, 0]
