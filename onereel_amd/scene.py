@@ -176,6 +176,37 @@ def pack_rows(plan: ScopePlan, video: torch.Tensor, text: torch.Tensor | None, w
     return (out, b_out) if b_video is not None else out
 
 
+def gather_rows(src: torch.Tensor, idx: torch.Tensor, b_src: torch.Tensor | None = None):
+    """rows idx of src [N, H, D] (and of b_src, same shape and stride) packed into new [len(idx), H, D] tensors in
+    one pass of or_pack_gather; idx: int32 GPU tensor of rows in [0, N)"""
+    N, H, D = src.shape
+    _check_bf16(src, b_src)
+    _, ss = _rows2d(src, H, D)
+    if b_src is not None and (b_src.shape != src.shape or _rows2d(b_src, H, D)[1] != ss):
+        raise ValueError('b_src must have the shape and row stride of src')
+    if idx.dtype != torch.int32 or not idx.is_cuda or not idx.is_contiguous():
+        raise TypeError('idx must be a contiguous int32 GPU tensor')
+    n = idx.numel()
+    out = torch.empty(n, H, D, dtype=src.dtype, device=src.device)
+    b_out = torch.empty_like(out) if b_src is not None else None
+    L.check(L.lib().or_pack_gather(src.data_ptr(), None, L.ptr(b_src), None, ss, ss, N, idx.data_ptr(), None, None,
+                                   None, None, 0, n, H, D, out.data_ptr(), L.ptr(b_out),
+                                   L.stream_handle(src.device)), 'or_pack_gather')
+    return (out, b_out) if b_src is not None else out
+
+
+def scatter_rows(packed: torch.Tensor, idx: torch.Tensor, out: torch.Tensor):
+    """out[idx[r]] = packed[r] for out [N, H, D] (rows not named keep their contents), one pass of or_scatter"""
+    n, H, D = packed.shape
+    _check_bf16(packed, out)
+    _, os_ = _rows2d(out, H, D)
+    if idx.dtype != torch.int32 or not idx.is_cuda or not idx.is_contiguous() or idx.numel() != n:
+        raise TypeError('idx must be a contiguous int32 GPU tensor with one entry per packed row')
+    L.check(L.lib().or_scatter(packed.data_ptr(), idx.data_ptr(), n, out.shape[0], out.data_ptr(), None, os_, os_, 0,
+                               0, H, D, L.stream_handle(out.device)), 'or_scatter')
+    return out
+
+
 def varlen(q, k, v, cu_q, cu_k, max_q, max_k, *, k_off=None, k_len=None, out=None, lse=None, seg_q_src=None,
            q_text=None, o_text=None, n_q_video=None, q_rope=None, cos=None, sin=None, sum_q=None, workspace=None,
            scale=None):

@@ -369,3 +369,41 @@ def test_frame_memory_candidates_sink_and_pool():
     frame = torch.tensor([0, 0, 1, 1, 1, -1, 2, 2, 2, 2])
     s, c = OF.pool(frame, hs, 4)
     assert torch.allclose(s[1], hs[2:5].double().sum(0)) and c.tolist() == [2, 3, 4, 0]
+
+
+# ------------------------------------------------------------------------------------------ bounded memory (per head)
+def test_memory_select_keeps_every_candidate_when_the_budget_covers_them():
+    """tests/test_onereel_memory.py:63-73 of the reference"""
+    from oracle import memory as OM
+    rows, _ = OM.boundary_rows([(0, 3), (3, 7), (7, 9)], 8)
+    k = torch.randn(9 * 8, 2, 32, generator=torch.Generator().manual_seed(1))
+    rep, valid = OM.select(k[rows], len(rows))
+    for h in range(2):
+        assert sorted(rep[h][valid[h]].tolist()) == list(range(len(rows)))
+
+
+def test_memory_select_representative_is_the_nearest_member():
+    """tests/test_onereel_memory.py:76-94 of the reference: every representative is at least as near its centroid as
+    any other member of its cluster (distances recomputed here)"""
+    from oracle import memory as OM
+    x = torch.randn(120, 3, 16, generator=torch.Generator().manual_seed(2))
+    rep, valid, c = OM.select(x, 12, centroids=True)
+    xn = torch.nn.functional.normalize(x.float().transpose(0, 1), dim=-1)
+    for h in range(3):
+        z = torch.cdist(xn[h], c[h]).argmin(-1)
+        reps = rep[h][valid[h]].tolist()
+        assert len(reps) == len(set(z.tolist()))          # one representative per non-empty cluster
+        for r in reps:
+            members = (z == z[r]).nonzero().flatten()
+            d = (xn[h, members] - c[h, z[r]]).pow(2).sum(-1)
+            assert d.min() >= (xn[h, r] - c[h, z[r]]).pow(2).sum() - 1e-6
+
+
+def test_memory_select_one_representative_per_separated_group():
+    from oracle import memory as OM
+    g = torch.Generator().manual_seed(3)
+    base = torch.randn(4, 2, 16, generator=g)
+    x = torch.cat([base[i].expand(10, -1, -1) for i in range(4)]) + 0.01 * torch.randn(40, 2, 16, generator=g)
+    rep, valid = OM.select(x, 4)
+    for h in range(2):
+        assert sorted(r // 10 for r in rep[h][valid[h]].tolist()) == [0, 1, 2, 3]
