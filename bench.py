@@ -228,6 +228,56 @@ def run_dit(args):
     print(json.dumps(out), flush=True)
 
 
+def run_frame_memory(args):
+    """frame memory at the DiT-step shape: pooling of one observed layer (16 scenes x 15 frames x 880 tokens x 3072
+    bf16, 1.3 GB) per frame, and the k-means choice of 4 representatives among the 240 frames; each call timed alone
+    with the caches evicted before it"""
+    import torch
+    from onereel_amd.frame_memory import FrameMemory
+    from onereel_amd.layout import SceneLayout
+    dev = torch.device('cuda:0')
+    torch.cuda.set_device(dev)
+    lengths, Tw, C = [15] * 16, 880, 3072
+    lay = SceneLayout(lengths, halo=0)
+    S = lay.n_frames * Tw
+    g = torch.Generator(device=dev).manual_seed(0)
+    hs = torch.randn(S, C, generator=g, device=dev).to(torch.bfloat16)
+    frame = torch.arange(S, device=dev) // Tw
+    fm = FrameMemory(budget=4)
+    fm.reset(lay, 30)
+    st = torch.cuda.current_stream(dev)
+    evict = torch.ones(128 << 20, dtype=torch.int32, device=dev)
+    flush = lambda: evict.sum()
+    reps = args.kernel_reps
+
+    def pool():
+        fm.sums, fm.counts = {}, {}
+        fm.collect(frame, hs, layer=15)
+    pool()
+    torch.cuda.synchronize()
+    # the sums buffers are allocated inside collect; time the kernel on preallocated buffers
+    sums, counts = fm.sums[15], fm.counts[15]
+    from onereel_amd import _lib as L
+    row0, T_ = fm._rows[next(iter(fm._rows))]
+    call = lambda: L.check(L.lib().or_frame_pool(hs.data_ptr(), S, C, hs.stride(0), row0, T_, lay.n_frames,
+                                                 sums.data_ptr(), counts.data_ptr(), st.cuda_stream), 'or_frame_pool')
+    t_pool = time_cold(call, reps, st, flush)
+    feats = torch.nn.functional.normalize(torch.randn(lay.n_frames, C, generator=g, device=dev), dim=-1)
+    fm.select(feats)
+    torch.cuda.synchronize()
+    t_sel = time_cold(lambda: fm.select(feats), reps, st, flush)
+    nbytes = S * C * 2
+    out = dict(metric='frame memory: per-frame pooling GB/s and k-means selection us (240 frames, 3072 features)',
+               value=round(nbytes / t_pool / 1e6, 1), unit='GB/s', n_gpus=1, steps=reps, warmup=1,
+               higher_is_better=True, dtype='bf16 in, fp32 sums', data='synthetic',
+               config=dict(workload='frame-memory-16scene', tokens=S, features=C, frames=lay.n_frames, budget=4),
+               pool=dict(ms=round(t_pool, 4), gbs=round(nbytes / t_pool / 1e6, 1),
+                         frac_hbm_peak=round(nbytes / t_pool / 1e6 / PEAK_HBM_GBS, 4), bytes=nbytes),
+               select=dict(us=round(t_sel * 1e3, 1), what='one or_frame_select launch plus the read-back of the 4 '
+                                                          'chosen frames (host sync)'))
+    print(json.dumps(out), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument('--gpus', type=int, default=1)
@@ -236,11 +286,13 @@ def main():
     ap.add_argument('--no-cpu', action='store_true', help='skip the CPU baseline leg')
     ap.add_argument('--kernel-reps', type=int, default=10)
     ap.add_argument('--no-gemm-ref', action='store_true', help='skip the bf16 GEMM reference')
-    ap.add_argument('--workload', default='hunyuan480p', choices=['hunyuan480p', 'wan704', 'uneven12', 'wan-dit-step'],
+    ap.add_argument('--workload', default='hunyuan480p',
+                    choices=['hunyuan480p', 'wan704', 'uneven12', 'wan-dit-step', 'frame-memory'],
                     help='hunyuan480p (default, the headline): the HunyuanVideo-1.5 480p 4-scene layer; wan704 and '
                          'uneven12: the same layer at the Wan2.2 704x1280 and 12-scene uneven shapes; wan-dit-step: '
                          'one forward of a random-init Wan2.2-TI2V-5B-shaped DiT over 16 scenes x 15 frames x 880 '
-                         'tokens with frame memory 4 (end-to-end ms per step)')
+                         'tokens with frame memory 4 (end-to-end ms per step); frame-memory: the pooling and '
+                         'selection kernels at that shape')
     ap.add_argument('--once', action='store_true',
                     help='profiling mode: a 1 GiB device copy (counter calibration), then the layout, pack-gather, '
                          'attention and scatter kernels once each, then one bf16 16384^3 torch.matmul (the GEMM '
@@ -253,6 +305,8 @@ def main():
 
     if args.workload == 'wan-dit-step':
         return run_dit(args)
+    if args.workload == 'frame-memory':
+        return run_frame_memory(args)
     args.steps = 20 if args.steps is None else args.steps
     args.warmup = 3 if args.warmup is None else args.warmup
     W = workload(args.workload)
@@ -345,7 +399,8 @@ def main():
                                frac_hbm_peak=round(pack_bytes / t_pack / 1e6 / PEAK_HBM_GBS, 4), bytes=pack_bytes,
                                warm_ms=round(t_pack_w, 4), timing='cold caches, single calls'),
         'layout': dict(us=round(t_layout * 1e3, 2), gbs=round(plan.index_bytes() / t_layout / 1e6, 1),
-                       bytes=plan.index_bytes(), bound='launch latency (1.4 MB of int32 indices)'),
+                       bytes=plan.index_bytes(),
+                       bound=f'launch latency ({plan.index_bytes() / 1e6:.1f} MB of int32 indices)'),
         'scatter': dict(ms=round(t_scat, 4), gbs=round(scat_bytes / t_scat / 1e6, 1),
                         frac_hbm_peak=round(scat_bytes / t_scat / 1e6 / PEAK_HBM_GBS, 4), bytes=scat_bytes,
                         warm_ms=round(t_scat_w, 4), timing='cold caches, single calls'),
