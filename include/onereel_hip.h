@@ -10,6 +10,7 @@
  *   or_rmsnorm_rope   fused RMSNorm + interleaved RoPE of the Wan self-attention's queries and keys
  *   or_frame_pool     frame memory: per-frame sums of hidden states (deterministic)
  *   or_frame_select   frame memory: k-means (cosine) representatives and their medoids, one workgroup
+ *   or_layernorm_modulate, or_gated_residual   the fused elementwise work of the Wan-shaped DiT block harness
  *
  * Conventions: every tensor is caller-owned device memory passed as a raw pointer; rows are [row][head][dim] with a
  * row stride in elements; bf16 is IEEE bfloat16 stored as uint16_t; index arrays are int32. Every launch goes on the
@@ -189,6 +190,19 @@ int or_frame_pool(const void* hs, int64_t n_rows, int32_t C, int64_t row_stride,
  * frames ascending, -1 after them. work: fp32 [8, C] device scratch. One workgroup; k * C <= 32768. */
 int or_frame_select(const float* feats, int32_t n_frames, int32_t C, const int32_t* cand, int32_t n_cand, int32_t k,
                     int32_t iters, int32_t* reps, float* work, void* stream);
+
+/* Replaces the LayerNorm + modulation chains of the Wan transformer block the reference's processors run in
+ * (diffusers' WanTransformerBlock, third-party; installed at src/onereel/models/wan.py:77-108): per bf16 row of C
+ * elements, y = (x - mean) * rstd, then * weight, + bias, * (1 + scale), + shift for each of those fp32 [C] vectors
+ * that is not NULL, in that order and in fp32; out = bf16(y). */
+int or_layernorm_modulate(const void* x, void* out, int64_t n_rows, int32_t C, int64_t x_row_stride,
+                          int64_t out_row_stride, float eps, const float* weight, const float* bias, const float* scale,
+                          const float* shift, void* stream);
+
+/* Replaces the block's residual adds (same block): x = bf16(float(x) + float(a) * gate), gate fp32 [C], or
+ * x = bf16(float(x) + float(a)) when gate is NULL; in place on x. */
+int or_gated_residual(void* x, const void* a, const float* gate, int64_t n_rows, int32_t C, int64_t x_row_stride,
+                      int64_t a_row_stride, void* stream);
 
 /* Message of the calling thread's last failed call ("" if none). */
 const char* or_last_error(void);

@@ -14,7 +14,8 @@ It runs the attention through onereel_amd.wan's processors:
   scopes);
 - cross-attention: the varlen kernel's zero-copy key ranges.
 
-GEMMs, LayerNorms and the elementwise modulation stay torch ops (hipBLASLt and torch's kernels). Shapes of
+GEMMs stay torch ops (hipBLASLt). The block's LayerNorm + modulation and gated residual adds are one HIP pass each
+(`or_layernorm_modulate`, `or_gated_residual`) instead of chains of torch kernels over fp32 temporaries. Shapes of
 Wan2.2-TI2V-5B: hidden 3072 = 24 heads x 128, FFN 14336, 30 blocks, eps 1e-6, patch (1, 2, 2) over 48 latent
 channels, text width 4096 projected to 3072.
 """
@@ -26,6 +27,7 @@ from dataclasses import dataclass
 import torch
 import torch.nn.functional as F
 
+from . import _lib as L
 from . import wan
 from .layout import SceneLayout
 
@@ -42,6 +44,42 @@ class DiTConfig:
     text_dim: int = 4096
     freq_dim: int = 256
     std: float = 0.02
+
+
+def _rows(x: torch.Tensor):
+    C = x.shape[-1]
+    x2 = x.reshape(-1, C)
+    if x.dtype != torch.bfloat16 or x2.stride(1) != 1:
+        raise ValueError('expected bf16 rows with contiguous elements')
+    return x2, C
+
+
+def _vec(t, C):
+    return None if t is None else t.reshape(C).to(torch.float32).contiguous()
+
+
+def layernorm_modulate(x, eps, weight=None, bias=None, scale=None, shift=None):
+    """bf16 [..., C] -> bf16 LayerNorm(x) [* weight + bias] [* (1 + scale) + shift], fp32 inside, one HIP pass (the
+    block's x.float() / layer_norm / modulation / .to(bf16) chain)"""
+    x2, C = _rows(x)
+    out = torch.empty(x2.shape, dtype=torch.bfloat16, device=x.device)
+    w, b, sc, sh = (_vec(t, C) for t in (weight, bias, scale, shift))
+    L.check(L.lib().or_layernorm_modulate(x2.data_ptr(), out.data_ptr(), x2.shape[0], C, x2.stride(0), C, float(eps),
+                                          L.ptr(w), L.ptr(b), L.ptr(sc), L.ptr(sh), L.stream_handle(x.device)),
+            'or_layernorm_modulate')
+    return out.view(x.shape)
+
+
+def gated_residual_(x, a, gate=None):
+    """x = bf16(float(x) + float(a) * gate) in place (x = x + a without a gate), one HIP pass"""
+    x2, C = _rows(x)
+    a2, Ca = _rows(a)
+    if Ca != C or a2.shape[0] != x2.shape[0]:
+        raise ValueError('x and a must have the same rows')
+    g = _vec(gate, C)
+    L.check(L.lib().or_gated_residual(x2.data_ptr(), a2.data_ptr(), L.ptr(g), x2.shape[0], C, x2.stride(0),
+                                      a2.stride(0), L.stream_handle(x.device)), 'or_gated_residual')
+    return x
 
 
 class Linear:
@@ -88,16 +126,16 @@ class Block:
         self.scale_shift_table = torch.randn(6, d, generator=gen, device=device) / d ** 0.5
 
     def __call__(self, x, text, temb6, rotary, p_self, p_cross):
-        """x [1, S, dim] bf16, text [1, L, dim] bf16, temb6 [6, dim] fp32"""
-        d, eps = self.cfg.dim, self.cfg.eps
+        """x [1, S, dim] bf16 (updated in place and returned), text [1, L, dim] bf16, temb6 [6, dim] fp32"""
+        eps = self.cfg.eps
         shift, scale, gate, c_shift, c_scale, c_gate = (self.scale_shift_table + temb6).chunk(6, 0)
-        n = (F.layer_norm(x.float(), (d,), eps=eps) * (1 + scale) + shift).to(x.dtype)
-        x = (x.float() + p_self(self.attn1, n, rotary_emb=rotary).float() * gate).to(x.dtype)
-        n = F.layer_norm(x.float(), (d,), self.norm2_w, self.norm2_b, eps).to(x.dtype)
-        x = x + p_cross(self.attn2, n, encoder_hidden_states=text)
-        n = (F.layer_norm(x.float(), (d,), eps=eps) * (1 + c_scale) + c_shift).to(x.dtype)
+        n = layernorm_modulate(x, eps, scale=scale, shift=shift)
+        gated_residual_(x, p_self(self.attn1, n, rotary_emb=rotary), gate)
+        n = layernorm_modulate(x, eps, weight=self.norm2_w, bias=self.norm2_b)
+        gated_residual_(x, p_cross(self.attn2, n, encoder_hidden_states=text))
+        n = layernorm_modulate(x, eps, scale=c_scale, shift=c_shift)
         f = self.ffn_out(F.gelu(self.ffn_in(n), approximate='tanh'))
-        return (x.float() + f.float() * c_gate).to(x.dtype)
+        return gated_residual_(x, f, c_gate)
 
 
 def timestep_features(t: float, n: int, device) -> torch.Tensor:
@@ -136,7 +174,7 @@ class WanDiT:
         for blk in self.blocks:
             x = blk(x, ctx_text, temb6, rotary, self.p_self, self.p_cross)
         shift, scale = (self.scale_shift_table + temb.float()[None]).chunk(2, 0)
-        x = (F.layer_norm(x.float(), (d,), eps=self.cfg.eps) * (1 + scale) + shift).to(x.dtype)
+        x = layernorm_modulate(x, self.cfg.eps, scale=scale, shift=shift)
         return self.proj_out(x)[0]
 
     def flops(self, text_rows: int) -> dict:

@@ -95,3 +95,29 @@ def test_two_block_forward_matches_oracle_processors():
     print(f'two-block forward rel-L2 {rel:.2e}', flush=True)
     assert rel < 2e-2
     assert out.shape == (sum(LENGTHS) * T, 16) and torch.isfinite(out).all()
+
+
+@pytest.mark.parametrize('S,C', [(257, 3072), (64, 512), (9, 1000)])
+def test_fused_layernorm_modulate_and_residual_match_torch(S, C):
+    """the block's fused passes against the torch expressions they replace: LayerNorm + modulation within one bf16
+    step (and > 99% bit-equal), the gated residual bit-exact"""
+    print(f'fused dit elementwise S={S} C={C}', flush=True)
+    import torch.nn.functional as F
+    g = torch.Generator(device=DEV).manual_seed(S)
+    x = (torch.randn(S, C, generator=g, device=DEV) * 2 + 0.5).to(torch.bfloat16)
+    a = torch.randn(S, C, generator=g, device=DEV).to(torch.bfloat16)
+    scale, shift, gate = (0.3 * torch.randn(1, C, generator=g, device=DEV) for _ in range(3))
+    w, b = 1 + 0.1 * torch.randn(C, generator=g, device=DEV), 0.1 * torch.randn(C, generator=g, device=DEV)
+    cases = [(WD.layernorm_modulate(x, 1e-6, scale=scale, shift=shift),
+              (F.layer_norm(x.float(), (C,), eps=1e-6) * (1 + scale) + shift).to(torch.bfloat16)),
+             (WD.layernorm_modulate(x, 1e-6, weight=w, bias=b),
+              F.layer_norm(x.float(), (C,), w, b, 1e-6).to(torch.bfloat16))]
+    for got, ref in cases:
+        diff = (got.float() - ref.float()).abs()
+        assert (diff <= ref.float().abs() * 2 ** -7 + 1e-6).all(), diff.max()
+        assert (got.view(torch.int16) == ref.view(torch.int16)).float().mean() > 0.99
+    for gt in (gate, None):
+        ref = (x.float() + a.float() * gt).to(torch.bfloat16) if gt is not None else x + a
+        y = x.clone()
+        WD.gated_residual_(y, a, gt)
+        assert torch.equal(y.view(torch.int16), ref.view(torch.int16))
