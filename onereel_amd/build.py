@@ -41,6 +41,8 @@ def _run(cmd):
 
 def build(verbose: bool = False) -> Path:
     OBJ.mkdir(exist_ok=True)
+    # the key loop of the 64-query attention kernel is generated asm
+    _run([sys.executable, str(CSRC / 'gen_attn_ring64.py'), '--out', str(CSRC / 'attn_ring64.inc')])
     objs = [OBJ / (s.replace('.hip', '.o')) for s in SOURCES]
 
     def one(src_obj):

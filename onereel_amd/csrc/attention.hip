@@ -19,6 +19,7 @@
 #include <stdlib.h>
 
 #include "common.h"
+#include "attn_ring64.inc"
 
 namespace onereel {
 
@@ -628,27 +629,24 @@ __device__ __forceinline__ float max16(const f32x16& s) {
   return fmaxf(x, s[15]);
 }
 
-// P = 2^(s c - mc) rounded to bf16 pairs, and the sum of the rounded values (the numerator and the denominator of
-// the softmax use the same probabilities)
+// P = 2^(s c - mc) rounded to bf16 pairs, and the fp32 sum of the unrounded values (as FlashAttention sums its fp32
+// P before the PV product). The sum uses v_add_f32, which issues under a running MFMA: v_dot2_f32_bf16 does not
+// (measured on gfx950: each dot2 between 32x32x16 MFMAs holds the matrix pipe for ~18 cycles).
 __device__ __forceinline__ float exp_pack(const f32x16& s, float c, float mc, bf16x8 (&p)[2]) {
   f32x16 e;
 #pragma unroll
   for (int r = 0; r < 16; ++r) e[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[r], c, -mc));
-  float ls = 0.0f;
-  const bf16x2_t one = {(__bf16)1.0f, (__bf16)1.0f};
+  float t[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) t[i] = (e[4 * i] + e[4 * i + 1]) + (e[4 * i + 2] + e[4 * i + 3]);
 #pragma unroll
   for (int half = 0; half < 2; ++half) {
     u32x4 pk;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      // the dot2 operand is the scalar, not pk[i]: hipcc (ROCm 7.2) selects element 0 for a bit_cast of pk[i]
-      const uint32_t pw = pack2(e[8 * half + 2 * i], e[8 * half + 2 * i + 1]);
-      ls = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, pw), one, ls, false);
-      pk[i] = pw;
-    }
+    for (int i = 0; i < 4; ++i) pk[i] = pack2(e[8 * half + 2 * i], e[8 * half + 2 * i + 1]);
     p[half] = as_bf16x8(pk);
   }
-  return ls;
+  return (t[0] + t[1]) + (t[2] + t[3]);
 }
 
 // iteration j (J = j mod 4, compile-time: the slots it touches are compile-time)
@@ -866,11 +864,135 @@ void attn4_kernel(AttnArgs a, int32_t* ws) {
   }
 }
 
+// ------------------------------------------------------------------------------------------------------------------
+// Ring kernel with 64 queries per wavefront (D = 128): every K and V operand read from LDS feeds two MFMAs (two
+// 32-query column blocks), so LDS reads per FLOP halve, and a block of four wavefronts covers 256 queries, so the K/V
+// stream per FLOP halves too. One wavefront per SIMD, one block per CU. The O accumulators (128 registers per lane)
+// live in AGPRs for the whole key loop, which is generated inline asm (gen_attn_ring64.py -> attn_ring64.inc): K and
+// V blocks of 32 keys stream through rings of ONEREEL_RING64 LDS slots each, the barrier sits in the middle of an
+// iteration so that the next iteration's operands are read during this one's MFMAs, and the epilogue normalises O and
+// stores it (rows past the segment masked off). The item queue, the Q load (with RoPE) and the lse store are C++.
+
+constexpr int kRing64 = ONEREEL_RING64;
+constexpr int kSlot64 = kBKB * 128;   // bf16 elements per slot
+
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void attn8_kernel(AttnArgs a, int32_t* ws) {
+  constexpr int D = 128, CH = 16, KS = 8, WQ = 64, BQ = 4 * WQ;
+  __shared__ __attribute__((aligned(1024))) uint16_t ring[2 * kRing64 * kSlot64];
+  __shared__ int item_sh;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l32 = lane & 31, h = lane >> 5;
+  const int64_t rs = a.ks;
+  const uint32_t lds0 = lds_addr(ring);
+  const uint32_t sbase = lds0 + (uint32_t)w * 64 * 16;
+
+  // LDS read addresses: K step k reads row pi(l32), 16-byte chunk (2k + h) ^ swz(row), i.e. kb ^ 32k; V^T step
+  // (half, db) reads from vb ^ 64 db (the generated code forms both from these bases)
+  const int krow = pi32(l32), ksw = swz4_k<CH>(krow);
+  const uint32_t kb = lds0 + krow * D * 2 + (uint32_t)((h ^ (ksw & 1)) * 16 + 32 * (ksw >> 1));
+  const int r = lane & 15, g = lane >> 4;
+  const int cp = 2 * (g & 1) + ((r >> 1) & 1), mv = (r >> 2) & 3;
+  const uint32_t vb = lds0 + (uint32_t)(kRing64 * kSlot64 * 2) + (16 * h + (r >> 2)) * D * 2 + cp * 16 + (r & 1) * 8 +
+                      64 * mv;
+  // DMA lane offsets within a block (row * stride + swizzled chunk), as attn4_kernel
+  uint32_t voff[4];
+#pragma unroll
+  for (int n = 0; n < 2; ++n) {
+    const int slot = n * kThreads + w * 64 + lane;
+    const int row = slot / CH, phys = slot % CH;
+    voff[n] = (uint32_t)(row * rs * 2 + (phys ^ swz4_k<CH>(row)) * 16);
+    voff[2 + n] = (uint32_t)(row * rs * 2 + (phys ^ swz4_v<CH>(row)) * 16);
+  }
+
+  const int xcc = xcc_id();
+  for (;;) {
+    if (tid == 0) item_sh = next_item(ws, xcc);
+    __syncthreads();
+    const int it = item_sh;
+    __syncthreads();
+    if (it < 0) break;
+    const int seg = ws[kWsHeader + 2 * it];
+    const int packed_ht = ws[kWsHeader + 2 * it + 1];
+    const int head = packed_ht & 255, qt = packed_ht >> 8;
+    const int q_beg = a.cu_q[seg];
+    const int Lq = a.cu_q[seg + 1] - q_beg;
+    const int k_beg = seg_k_begin(a, seg);
+    const int Lk = max(seg_k_len(a, seg), 0);
+    const int q_src0 = a.seg_q_src ? a.seg_q_src[seg] : q_beg;
+    const int q0 = qt * BQ + w * WQ;
+    const int nb = (Lk + kBKB - 1) / kBKB;
+
+    // Q operands (rows past the segment repeat its last row; their outputs are not stored) and output rows
+    bf16x8 q[2][KS];
+    uint64_t op[2];
+    int ok[2];
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) {
+      const int i0 = q0 + qb * 32 + l32;
+      const int i = min(i0, Lq - 1);
+      const int64_t row = q_src0 + i;
+      const uint16_t* qp = (row < a.n_q_video ? a.q + row * a.qs : a.q_text + (row - a.n_q_video) * a.qs) + head * D;
+      int rr = a.q_rope ? a.q_rope[q_beg + i] : -1;
+      if (rr >= a.n_rope_rows) rr = -1;
+#pragma unroll
+      for (int k = 0; k < KS; ++k) {
+        const int d = 16 * k + 8 * h;
+        u32x4 x = *(const u32x4*)(qp + d);
+        if (rr >= 0) x = rotate8(x, a.cos_t, a.sin_t, (int64_t)rr * D + d, 1.0f);
+        q[qb][k] = as_bf16x8(x);
+      }
+      uint16_t* o = (row < a.n_q_video ? a.o + row * a.os : a.o_text + (row - a.n_q_video) * a.os) + head * D + 4 * h;
+      op[qb] = (uint64_t)o;
+      ok[qb] = i0 < Lq;
+    }
+    if (nb == 0) {
+      // no keys: O = 0 and lse = -inf, as attn4_kernel
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb)
+        if (ok[qb]) {
+          uint16_t* o = (uint16_t*)op[qb];
+#pragma unroll
+          for (int db = 0; db < 4; ++db)
+#pragma unroll
+            for (int gg = 0; gg < 4; ++gg) *(uint2*)(o + db * 32 + 8 * gg) = make_uint2(0u, 0u);
+          if (a.lse && h == 0) a.lse[(int64_t)head * a.sum_q + q_beg + q0 + qb * 32 + l32] = -__builtin_inff();
+        }
+      continue;
+    }
+    const uint64_t kaddr = (uint64_t)(a.k + (int64_t)k_beg * rs + head * D);
+    const uint64_t vaddr = (uint64_t)(a.v + (int64_t)k_beg * rs + head * D);
+    const int32_t rb = (int32_t)rs * 2;
+    const int32_t rem0 = Lk * rb - rb + D * 2;
+    const int32_t bb = kBKB * rb;
+    const int valid = Lk - (nb - 1) * kBKB - 16 * h;
+    float mo0, mo1, lo0, lo1;
+    asm volatile(ONEREEL_RING64_ASM
+                 : [mo0] "=&v"(mo0), [mo1] "=&v"(mo1), [lo0] "=&v"(lo0), [lo1] "=&v"(lo1)
+                 : [q00] "a"(q[0][0]), [q01] "a"(q[0][1]), [q02] "a"(q[0][2]), [q03] "a"(q[0][3]),
+                   [q04] "a"(q[0][4]), [q05] "a"(q[0][5]), [q06] "a"(q[0][6]), [q07] "a"(q[0][7]),
+                   [q10] "a"(q[1][0]), [q11] "a"(q[1][1]), [q12] "a"(q[1][2]), [q13] "a"(q[1][3]),
+                   [q14] "a"(q[1][4]), [q15] "a"(q[1][5]), [q16] "a"(q[1][6]), [q17] "a"(q[1][7]),
+                   [c] "s"(a.c), [nb] "s"(nb), [valid] "v"(valid), [kb] "v"(kb), [vb] "v"(vb),
+                   [vk0] "v"(voff[0]), [vk1] "v"(voff[1]), [vv0] "v"(voff[2]), [vv1] "v"(voff[3]),
+                   [sbase] "s"(sbase), [bb] "s"(bb), [kb_lo] "s"((uint32_t)kaddr), [kb_hi] "s"((uint32_t)(kaddr >> 32)),
+                   [vb_lo] "s"((uint32_t)vaddr), [vb_hi] "s"((uint32_t)(vaddr >> 32)), [rem0] "s"(rem0),
+                   [op0] "v"(op[0]), [op1] "v"(op[1]), [ok0] "v"(ok[0]), [ok1] "v"(ok[1])
+                 : ONEREEL_RING64_CLOBBERS);
+    if (a.lse && h == 0) {
+      if (ok[0]) a.lse[(int64_t)head * a.sum_q + q_beg + q0 + l32] = mo0 * a.scale + logf(lo0);
+      if (ok[1]) a.lse[(int64_t)head * a.sum_q + q_beg + q0 + 32 + l32] = mo1 * a.scale + logf(lo1);
+    }
+  }
+}
+
 typedef void (*AttnFn)(AttnArgs, int32_t*);
 
 // kernel variant (ONEREEL_ATTN_VARIANT): 0 = software-pipelined ring kernel (default), 1 = tile kernel with 32
-// queries per wavefront, 2 = tile kernel with 64 queries per wavefront
-constexpr int kVariants = 3;
+// queries per wavefront, 2 = tile kernel with 64 queries per wavefront, 3 = ring kernel with 64 queries per wavefront
+// (D = 128; D = 64 runs variant 0)
+constexpr int kVariants = 4;
 
 int variant() {
   static int v = [] {
@@ -882,11 +1004,12 @@ int variant() {
   return v;
 }
 
-int variant_bq(int var) { return var == 2 ? 256 : 128; }
+int variant_bq(int var, int D) { return var == 2 || (var == 3 && D == 128) ? 256 : 128; }
 
 AttnFn attn_fn(int D, int var) {
-  if (D == 128) return var == 0 ? attn4_kernel<128> : var == 1 ? attn_kernel<128, 1> : attn_kernel<128, 2>;
-  return var == 0 ? attn4_kernel<64> : var == 1 ? attn_kernel<64, 1> : attn_kernel<64, 2>;
+  if (D == 128)
+    return var == 0 ? attn4_kernel<128> : var == 1 ? attn_kernel<128, 1> : var == 2 ? attn_kernel<128, 2> : attn8_kernel;
+  return var == 1 ? attn_kernel<64, 1> : var == 2 ? attn_kernel<64, 2> : attn4_kernel<64>;
 }
 
 struct DevInfo {
@@ -997,7 +1120,7 @@ extern "C" int or_varlen_fwd(const or_varlen_args* p, void* stream) {
   hipStream_t st = (hipStream_t)stream;
   // the planner needs key counts only: k_len when given, else the cu_k differences
   hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(kPlanThreads), 0, st, x.cu_q, x.k_len ? nullptr : x.cu_k,
-                     x.k_len, x.n_seg, x.H, variant_bq(var), (int)max_items, ws);
+                     x.k_len, x.n_seg, x.H, variant_bq(var, x.D), (int)max_items, ws);
   if (int rc = check_hip(hipGetLastError(), "plan_kernel launch")) return rc;
   hipLaunchKernelGGL(attn_fn(x.D, var), dim3((unsigned)grid), dim3(kThreads), 0, st, a, ws);
   return check_hip(hipGetLastError(), "attn_kernel launch");
