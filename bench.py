@@ -405,10 +405,14 @@ def main():
                         frac_hbm_peak=round(scat_bytes / t_scat / 1e6 / PEAK_HBM_GBS, 4), bytes=scat_bytes,
                         warm_ms=round(t_scat_w, 4), timing='cold caches, single calls'),
     }
+    # the kernel or_varlen_fwd runs for an O-only call: the 64-query ring kernel at head_dim 128
+    kname = 'attn8_kernel' if D == 128 else 'attn4_kernel<64>'
     traffic = None
     tf = ROOT / 'profiles' / 'attention_traffic.json'
-    if headline and tf.exists():    # measured (PMC) on the headline layer only
-        traffic = json.loads(tf.read_text()).get('hbm_bytes_per_launch')
+    if headline and tf.exists():    # measured (PMC) on the headline layer only, for the kernel that runs
+        rec = json.loads(tf.read_text())
+        if rec.get('kernel') == kname:
+            traffic = rec.get('hbm_bytes_per_launch')
     value = flops / (ms * 1e-3) / 1e12
     metric = METRIC if headline else f'scene-attn TFLOP/s & % bf16 MFMA peak; ms/layer, {W["workload"]}'
     out = dict(metric=metric, value=round(value, 2), unit='TFLOP/s', n_gpus=1, steps=args.steps, warmup=args.warmup,
@@ -421,7 +425,7 @@ def main():
                            useful_flop_per_step=flops, frac_bf16_peak_step=round(value / PEAK_BF16_TFLOPS, 4)),
                roofline=dict(bound='mfma', achieved=round(flops / t_attn / 1e9, 1), peak=PEAK_BF16_TFLOPS,
                              unit='TFLOP/s', frac=round(flops / t_attn / 1e9 / PEAK_BF16_TFLOPS, 4), traffic=traffic,
-                             kernel='attn4_kernel<128> (+ plan_kernel, one block, ~10 us)'),
+                             kernel=f'{kname} (+ plan_kernel, one block, ~10 us)'),
                kernels=kernels)
     if headline and not args.no_gemm_ref:
         out['gemm_reference'] = gemm_reference()

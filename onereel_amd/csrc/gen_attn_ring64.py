@@ -9,24 +9,26 @@ does not keep such a split from source (it moves accumulators between the regist
 emitted here with fixed registers:
 
     a0..a127    O^T accumulators, acc(qb, db) = a[64 qb + 16 db : +15]
-    v56..v119   S, s(par, qb) = v[56 + 32 par + 16 qb : +15] (par = key block parity; S(j+1) fills while S(j) is read)
-    v120..v151  P as bf16 pairs, p(par, qb, half) = v[120 + 16 par + 8 qb + 4 half : +3]
-    v152..v183  K operands of the 8 k-steps, v184..v215 V^T operands of the 8 (half, db) steps
-    v216..v255  softmax temporaries, running max / scaled max / row sums, LDS read addresses
+    v36..v99    S, s(par, qb) = v[36 + 32 par + 16 qb : +15] (par = key block parity; S(j+1) fills while S(j) is read)
+    v100..v131  P as bf16 pairs, p(par, qb, half) = v[100 + 16 par + 8 qb + 4 half : +3]
+    v132..v163  K operands of the 8 k-steps, v164..v195 V^T operands of the 8 (half, db) steps
+    v196..v227  -m per query block, broadcast over 16 registers: the first QK^T MFMA of a block accumulates onto it
+    v228..v254  softmax temporaries, running max, row sums, LDS read addresses
     s64..s83    K and V buffer descriptors, their remaining byte counts, loop counters, return address
-Q comes in as 16 AGPR operands (the compiler places them above a127).
+Q comes in as 16 AGPR operands (the compiler places them above a127), already multiplied by c = scale * log2(e), so
+S = c q k^T - m comes out of the MFMAs and P = 2^S needs one v_exp_f32 per score and no other VALU op.
 
 Schedule of iteration j (32 keys; R-slot rings of K and V blocks in LDS, 8 KiB per slot):
     phase A  MFMA steps k = 0..3: S(j+1) += K(j+1)_k Q_k^T for both query blocks, O += V(j-1)_k P(j-1)_k; the VALU
              computes P(j) of query block 0 in between; the LDS operands of steps 4..7 are read
-    mid      wait until this wavefront's loads of K(j+2), V(j) have landed, barrier, then DMA of K(j+R) into slot
-             j % R and of V(j+R-2) into slot (j-2) % R (both consumed by iteration j-1)
+    mid      wait until this wavefront's loads of K(j+2), V(j) have landed, barrier; DMA of K(j+R) into slot j % R and
+             of V(j+R-2) into slot (j-2) % R (both consumed by iteration j-1) goes out during phase B
     phase B  steps k = 4..7, P(j) of query block 1, and the LDS operands of steps 0..3 of iteration j+1
-    tail     if a row-half sum of P(j) exceeds 2^20 (or is not finite): out-of-line rescale (block max, O and l scaled
-             by 2^((m_old - m_new) c), P(j) recomputed); then l += row sums
-The generator inserts the LDS waits (lgkmcnt) from the order of the reads, and s_nop where a VALU or memory
-instruction would touch a register fewer than 12 wait states after an MFMA wrote it (the v_mfma_f32_32x32x16_bf16
-latency hipcc uses for gfx950).
+    tail     if a row-half sum of P(j) exceeds 2^20 (or is not finite): out-of-line rescale (m moves up by the block
+             max d, O and l scale by 2^-d, S(j), S(j+1) and -m shift by -d, P(j) recomputed); then l += row sums
+The running max starts at block 0's own maximum (prologue), so row sums never underflow and m only moves up.
+The generator inserts the LDS waits (lgkmcnt) from the order of the reads, and s_nop where gfx950 needs wait states
+between dependent instructions (see Emitter).
 """
 from __future__ import annotations
 
@@ -37,31 +39,55 @@ SLOT = 8192              # bytes per K or V block: 32 keys x 128 dims x bf16
 MFMA_WAIT = 12           # wait states between a 32x32x16 bf16 MFMA and a VALU / memory access to its result
 LGKM_MAX = 15
 
+
 # fixed registers
 def S(par, qb, r):
-    return 56 + 32 * par + 16 * qb + r
+    return 36 + 32 * par + 16 * qb + r
+
+
 def Sx(par, qb):
     b = S(par, qb, 0)
     return f'v[{b}:{b + 15}]'
+
+
 def P(par, qb, half, i):
-    return 120 + 16 * par + 8 * qb + 4 * half + i
+    return 100 + 16 * par + 8 * qb + 4 * half + i
+
+
 def Px(par, qb, half):
     b = P(par, qb, half, 0)
     return f'v[{b}:{b + 3}]'
+
+
 def KOP(k):
-    return 152 + 4 * k
+    return 132 + 4 * k
+
+
 def VOP(k):
-    return 184 + 4 * k
-T0, A0, TT, LS0, M0, MC0, LSUM0, KADDR0, VADDR0, E0 = 216, 224, 228, 229, 231, 233, 235, 237, 245, 249
+    return 164 + 4 * k
+
+
+def MCV(qb):
+    return 196 + 16 * qb
+
+
+T0, A0, TT, LS0, M0, LSUM0, KADDR0, VADDR0 = 228, 232, 236, 237, 239, 241, 243, 251
+FIRST_FIXED = 36
+
+
 def ACC(qb, db):
     b = 64 * qb + 16 * db
     return f'a[{b}:{b + 15}]'
+
 
 KRES, VRES = 64, 68             # s[64:67], s[68:71]
 KREM, VREM, SJ, SNB1, SRR, SVOFF = 72, 73, 74, 75, 76, 77
 SRA, SX, SEX = 78, 80, 82       # s[78:79], s[80:81], s[82:83]
 NEG_INF = '0xff800000'
-M_INIT = '0xf149f2ca'           # -1e30f: finite, so that masked keys give exactly 0
+
+
+def v(x):
+    return f'v{x}'
 
 
 class Emitter:
@@ -115,6 +141,11 @@ class Emitter:
             self.raw(f's_waitcnt lgkmcnt({min(after, LGKM_MAX)})')
             del self.lds[:last + 1]
 
+    def wait_lds_all(self):
+        if self.lds:
+            self.raw('s_waitcnt lgkmcnt(0)')
+            self.lds = []
+
     def _need(self, table, regs, waits):
         need = 0
         for r in regs:
@@ -165,30 +196,41 @@ class Kernel:
         self.VBASE = ring * SLOT      # V ring after the K ring
 
     # ---- pieces ------------------------------------------------------------------------------------------------
-    def dma_k(self, e, slot):
+    def dma(self, e, res, rem, vo, lds_off, zero=False, advance=True):
+        if zero:
+            e.raw(f's_mov_b32 s{res + 2}, 0')
         for n in range(2):
-            e.raw(f's_add_u32 m0, %[sbase], {slot * SLOT + n * 4096}')
-            e.raw('s_nop 0')
-            e.raw(f'buffer_load_dwordx4 %[vk{n}], s[{KRES}:{KRES + 3}], 0 offen lds')
-        e.raw(f's_add_u32 s{KRES}, s{KRES}, %[bb]')
-        e.raw(f's_addc_u32 s{KRES + 1}, s{KRES + 1}, 0')
-        e.raw(f's_sub_i32 s{KREM}, s{KREM}, %[bb]')
-        e.raw(f's_max_i32 s{KRES + 2}, s{KREM}, 0')
+            e.raw(f's_add_u32 m0, %[sbase], {lds_off + n * 4096}')
+            e.raw('s_nop 0')                      # gfx9: an SALU write of M0 and the LDS DMA reading it
+            e.raw(f'buffer_load_dwordx4 %[{vo}{n}], s[{res}:{res + 3}], 0 offen lds')
+        if zero:
+            e.raw(f's_max_i32 s{res + 2}, s{rem}, 0')
+        if advance:
+            e.raw(f's_add_u32 s{res}, s{res}, %[bb]')
+            e.raw(f's_addc_u32 s{res + 1}, s{res + 1}, 0')
+            e.raw(f's_sub_i32 s{rem}, s{rem}, %[bb]')
+            e.raw(f's_max_i32 s{res + 2}, s{rem}, 0')
+
+    def dma_k(self, e, slot):
+        self.dma(e, KRES, KREM, 'vk', slot * SLOT)
 
     def dma_v(self, e, slot, zero=False):
-        if zero:
-            e.raw(f's_mov_b32 s{VRES + 2}, 0')
-        for n in range(2):
-            e.raw(f's_add_u32 m0, %[sbase], {self.VBASE + slot * SLOT + n * 4096}')
-            e.raw('s_nop 0')
-            e.raw(f'buffer_load_dwordx4 %[vv{n}], s[{VRES}:{VRES + 3}], 0 offen lds')
-        if zero:
-            e.raw(f's_max_i32 s{VRES + 2}, s{VREM}, 0')
-            return
-        e.raw(f's_add_u32 s{VRES}, s{VRES}, %[bb]')
-        e.raw(f's_addc_u32 s{VRES + 1}, s{VRES + 1}, 0')
-        e.raw(f's_sub_i32 s{VREM}, s{VREM}, %[bb]')
-        e.raw(f's_max_i32 s{VRES + 2}, s{VREM}, 0')
+        self.dma(e, VRES, VREM, 'vv', self.VBASE + slot * SLOT, zero=zero, advance=not zero)
+
+    def dma_ops(self, J):
+        """the mid-iteration refill as side ops: K(j+R) into slot J, V(j+R-2) into slot (J-2) % R"""
+        R = self.R
+        ops = []
+        for res, rem, slot_off, vo in ((KRES, KREM, (J % R) * SLOT, 'vk'),
+                                       (VRES, VREM, self.VBASE + ((J - 2) % R) * SLOT, 'vv')):
+            for n in range(2):
+                ops.append(('m0', f's_add_u32 m0, %[sbase], {slot_off + n * 4096}'))
+                ops.append(('dma', f'buffer_load_dwordx4 %[{vo}{n}], s[{res}:{res + 3}], 0 offen lds'))
+            ops.append(('raw', f's_add_u32 s{res}, s{res}, %[bb]'))
+            ops.append(('raw', f's_addc_u32 s{res + 1}, s{res + 1}, 0'))
+            ops.append(('raw', f's_sub_i32 s{rem}, s{rem}, %[bb]'))
+            ops.append(('raw', f's_max_i32 s{res + 2}, s{rem}, 0'))
+        return ops
 
     def read_k(self, e, k, slot):
         e.ds_read(f'ds_read_b128 v[{KOP(k)}:{KOP(k) + 3}], v{KADDR0 + k} offset:{slot * SLOT}', [vr(KOP(k), 4)])
@@ -202,17 +244,14 @@ class Kernel:
                       [vr(lo, 2)])
 
     def softmax(self, par, qb):
-        """P(par, qb) = bf16(2^(s c - mc)) and LS(qb) = fp32 sum of the unrounded values: list of
-        (asm, reads, writes, transcendental)"""
-        T = lambda r: T0 + (r % 8)
-        v = lambda x: f'v{x}'
-
-        def fma(p):
-            return [(f'v_fma_f32 v{T(r)}, v{S(par, qb, r)}, %[c], -v{MC0 + qb}', [v(S(par, qb, r)), v(MC0 + qb)],
-                     [v(T(r))], False) for r in (2 * p, 2 * p + 1)]
+        """P(par, qb) = bf16(2^S) and LS(qb) = fp32 sum of the unrounded values: list of (asm, reads, writes, trans).
+        Each pair's cvt and adds come one pair behind its exponentials, so no transcendental result is read by the
+        next instruction."""
+        T = lambda r: T0 + (r % 4)
 
         def exp(p):
-            return [(f'v_exp_f32_e32 v{T(r)}, v{T(r)}', [v(T(r))], [v(T(r))], True) for r in (2 * p, 2 * p + 1)]
+            return [(f'v_exp_f32_e32 v{T(r)}, v{S(par, qb, r)}', [v(S(par, qb, r))], [v(T(r))], True)
+                    for r in (2 * p, 2 * p + 1)]
 
         def tail(p):
             r0, r1 = 2 * p, 2 * p + 1
@@ -227,140 +266,172 @@ class Kernel:
                             [v(A0 + p - 4)], False))
             return out
 
-        # the next pair's FMAs sit between a pair's exponentials and their first reader (no transcendental wait)
-        ops = fma(0)
+        ops = exp(0)
         for p in range(8):
-            ops += exp(p)
             if p + 1 < 8:
-                ops += fma(p + 1)
+                ops += exp(p + 1)
+            else:
+                ops.append((f'v_add_f32_e32 v{A0}, v{A0}, v{A0 + 1}', [v(A0), v(A0 + 1)], [v(A0)], False))
             ops += tail(p)
-        ops.append((f'v_add_f32_e32 v{A0}, v{A0}, v{A0 + 1}', [v(A0), v(A0 + 1)], [v(A0)], False))
         ops.append((f'v_add_f32_e32 v{A0 + 2}, v{A0 + 2}, v{A0 + 3}', [v(A0 + 2), v(A0 + 3)], [v(A0 + 2)], False))
         ops.append((f'v_add_f32_e32 v{LS0 + qb}, v{A0}, v{A0 + 2}', [v(A0), v(A0 + 2)], [v(LS0 + qb)], False))
         return ops
 
-    def mfma_s(self, e, par_next, qb, k):
-        c = '0' if k == 0 else Sx(par_next, qb)
-        e.mfma(Sx(par_next, qb), f'v[{KOP(k)}:{KOP(k) + 3}]', f'%[q{qb}{k}]', c, [vr(S(par_next, qb, 0), 16)],
-               [vr(KOP(k), 4)] + ([] if k == 0 else [vr(S(par_next, qb, 0), 16)]))
+    def mfma_s(self, e, par_next, qb, k, seed=None):
+        """S(par_next, qb) += K_k Q_k^T; the first step accumulates onto -m (or onto `seed`)"""
+        if k == 0:
+            c = seed if seed is not None else f'v[{MCV(qb)}:{MCV(qb) + 15}]'
+            reads = [vr(KOP(k), 4)] + ([] if seed is not None else [vr(MCV(qb), 16)])
+        else:
+            c = Sx(par_next, qb)
+            reads = [vr(KOP(k), 4), vr(S(par_next, qb, 0), 16)]
+        e.mfma(Sx(par_next, qb), f'v[{KOP(k)}:{KOP(k) + 3}]', f'%[q{qb}{k}]', c, [vr(S(par_next, qb, 0), 16)], reads)
 
     def mfma_pv(self, e, par_prev, qb, k):
         half, db = divmod(k, 4)
         e.mfma(ACC(qb, db), f'v[{VOP(k)}:{VOP(k) + 3}]', Px(par_prev, qb, half), ACC(qb, db), [],
                [vr(VOP(k), 4), vr(P(par_prev, qb, half, 0), 4)])
 
+    def row_max(self, e, par, qb, dst, tmp):
+        """dst = max over the query's 32 scores of block par (in-lane 16, then with lane ^ 32)"""
+        s = [S(par, qb, r) for r in range(16)]
+        e.valu(f'v_max3_f32 v{dst}, v{s[0]}, v{s[1]}, v{s[2]}', [v(s[0]), v(s[1]), v(s[2])], [v(dst)])
+        for r in range(3, 15, 2):
+            e.valu(f'v_max3_f32 v{dst}, v{dst}, v{s[r]}, v{s[r + 1]}', [v(dst), v(s[r]), v(s[r + 1])], [v(dst)])
+        e.valu(f'v_max_f32_e32 v{dst}, v{dst}, v{s[15]}', [v(dst), v(s[15])], [v(dst)])
+        e.valu(f'v_mov_b32_e32 v{tmp}, v{dst}', [v(dst)], [v(tmp)])
+        e.valu(f'v_permlane32_swap_b32_e32 v{dst}, v{tmp}', [v(dst), v(tmp)], [v(dst), v(tmp)], permlane=True)
+        e.valu(f'v_max_f32_e32 v{dst}, v{dst}, v{tmp}', [v(dst), v(tmp)], [v(dst)])
+
+    def mask(self, e, par):
+        """scores of keys past the segment's end -> -inf (S(j) of the segment's last block)"""
+        e.valu(f'v_mov_b32_e32 v{T0}, {NEG_INF}', [], [v(T0)])
+        for r in range(16):
+            e.valu(f'v_cmp_lt_i32_e32 vcc, {r}, %[valid]', [], [])
+            for qb in range(2):
+                e.valu(f'v_cndmask_b32_e32 v{S(par, qb, r)}, v{T0}, v{S(par, qb, r)}, vcc',
+                       [v(T0), v(S(par, qb, r))], [v(S(par, qb, r))])
+
     # ---- one iteration -------------------------------------------------------------------------------------------
     def body(self, e, J):
+        """one iteration: 32 MFMAs with the softmax, LDS reads and DMA spread between them. Every LDS operand is
+        read half an iteration ahead, so each phase starts with one lgkmcnt(0) and its MFMAs wait for nothing else."""
         R = self.R
         par, npar = J & 1, (J & 1) ^ 1
-        # mask S(j) on the segment's last block
         e.raw(f's_cmp_eq_u32 s{SJ}, s{SNB1}')
         e.raw(f's_cbranch_scc1 .Lmask{J}_%=')
         e.label(f'.Lmaskret{J}_%=')
         ks_now, vs_now = (J + 1) % R, (J - 1) % R          # slots of K(j+1), V(j-1)
         ks_next, vs_next = (J + 2) % R, J % R               # slots of K(j+2), V(j)
-        valu = self.softmax(par, 0)
-        valu_b = self.softmax(par, 1)
-        reads_a = []
-        for k in range(4, 8):
-            reads_a.append(('k', k, ks_now))
-            reads_a.append(('v', k, vs_now))
-        reads_b = []
-        for k in range(4):
-            reads_b.append(('k', k, ks_next))
-            reads_b.append(('v', k, vs_next))
 
-        def phase(ks, valu_ops, reads):
-            per = len(valu_ops) / 16.0
-            done = 0
-            for i, k in enumerate(ks):
-                for kind, qb in (('s', 0), ('s', 1), ('pv', 0), ('pv', 1)):
-                    if kind == 's':
-                        self.mfma_s(e, npar, qb, k)
-                    else:
-                        self.mfma_pv(e, npar, qb, k)
-                    n = len(e.lines)
-                    if reads:
-                        kind_r, kr, slot = reads.pop(0)
-                        if kind_r == 'k':
-                            self.read_k(e, kr, slot)
-                        else:
-                            self.read_v(e, kr, slot)
-                    slot_i = 4 * (i) + (0 if kind == 's' and qb == 0 else 1 if kind == 's' else 2 if qb == 0 else 3)
-                    target = int(round(per * (slot_i + 1)))
-                    while done < min(target, len(valu_ops)):
-                        s, rd, wr, tr = valu_ops[done]
-                        e.valu(s, rd, wr, trans=tr)
-                        done += 1
-            while done < len(valu_ops):
-                s, rd, wr, tr = valu_ops[done]
-                e.valu(s, rd, wr, trans=tr)
+        def reads(kslot, vslot, ks):
+            out = []
+            for k in ks:
+                out.append(('k', k, kslot))
+                out.append(('v', k, vslot))
+            return out
+
+        def emit_side(op, last_m0):
+            if op[0] == 'valu':
+                e.valu(op[1], op[2], op[3], trans=op[4])
+            elif op[0] == 'dma' and last_m0:
+                e.nop_to(1)
+                e.raw(op[1])
+            else:
+                e.raw(op[1])
+            return op[0] == 'm0'
+
+        def phase(ks, valu_ops, rd, dma):
+            e.wait_lds_all()
+            side = [('valu',) + op for op in valu_ops]
+            if dma:
+                # one VALU op between each M0 write and its load (gfx9 LDS-DMA M0 hazard)
+                merged, vi = [], 0
+                for op in dma:
+                    merged.append(op)
+                    if op[0] == 'm0' and vi < len(side):
+                        merged.append(side[vi])
+                        vi += 1
+                side = merged + side[vi:]
+            order = [(kind, qb, k) for k in ks for kind, qb in (('s', 0), ('s', 1), ('pv', 0), ('pv', 1))]
+            if ks[0] == 4:
+                # S(j+1) complete with 4 PV MFMAs still to go: the next iteration reads it without a wait
+                s_ops = [o for o in order if o[0] == 's']
+                pv_ops = [o for o in order if o[0] == 'pv']
+                order = s_ops[:4] + [x for pair in zip(s_ops[4:], pv_ops[:4]) for x in pair] + pv_ops[4:]
+            per = len(side) / 16.0
+            done, last_m0 = 0, False
+            for i, (kind, qb, k) in enumerate(order):
+                if kind == 's':
+                    self.mfma_s(e, npar, qb, k)
+                else:
+                    self.mfma_pv(e, npar, qb, k)
+                if rd:
+                    kr_kind, kr, slot = rd.pop(0)
+                    (self.read_k if kr_kind == 'k' else self.read_v)(e, kr, slot)
+                target = int(round(per * (i + 1)))
+                while done < min(target, len(side)):
+                    last_m0 = emit_side(side[done], last_m0)
+                    done += 1
+            while done < len(side):
+                last_m0 = emit_side(side[done], last_m0)
                 done += 1
 
-        phase([0, 1, 2, 3], valu, reads_a)
-        # mid: K(j+2), V(j) landed (this wavefront's loads) and visible (barrier); then refill the freed slots
+        phase([0, 1, 2, 3], self.softmax(par, 0), reads(ks_now, vs_now, range(4, 8)), None)
+        # mid: K(j+2), V(j) landed (this wavefront's loads) and visible (barrier); the refill of the freed slots goes
+        # out during phase B
         e.raw(f's_waitcnt vmcnt({4 * (R - 3)})')
         e.raw('s_barrier')
-        self.dma_k(e, J % R)
-        self.dma_v(e, (J - 2) % R)
-        phase([4, 5, 6, 7], valu_b, reads_b)
+        phase([4, 5, 6, 7], self.softmax(par, 1), reads(ks_next, vs_next, range(4)), self.dma_ops(J))
         # rescale check, row sums
-        e.valu(f'v_cmp_nge_f32_e32 vcc, s{SRR}, v{LS0}', [f'v{LS0}'])
-        e.valu(f'v_cmp_nge_f32_e64 s[{SX}:{SX + 1}], s{SRR}, v{LS0 + 1}', [f'v{LS0 + 1}'])
+        e.valu(f'v_cmp_nge_f32_e32 vcc, s{SRR}, v{LS0}', [v(LS0)])
+        e.valu(f'v_cmp_nge_f32_e64 s[{SX}:{SX + 1}], s{SRR}, v{LS0 + 1}', [v(LS0 + 1)])
         e.raw(f's_or_b64 vcc, vcc, s[{SX}:{SX + 1}]')
         e.raw(f's_getpc_b64 s[{SRA}:{SRA + 1}]')
         e.raw(f's_cbranch_vccnz .Lrescale{par}_%=')
-        e.valu(f'v_add_f32_e32 v{LSUM0}, v{LSUM0}, v{LS0}', [f'v{LSUM0}', f'v{LS0}'], [f'v{LSUM0}'])
-        e.valu(f'v_add_f32_e32 v{LSUM0 + 1}, v{LSUM0 + 1}, v{LS0 + 1}', [f'v{LSUM0 + 1}', f'v{LS0 + 1}'],
-               [f'v{LSUM0 + 1}'])
+        e.valu(f'v_add_f32_e32 v{LSUM0}, v{LSUM0}, v{LS0}', [v(LSUM0), v(LS0)], [v(LSUM0)])
+        e.valu(f'v_add_f32_e32 v{LSUM0 + 1}, v{LSUM0 + 1}, v{LS0 + 1}', [v(LSUM0 + 1), v(LS0 + 1)], [v(LSUM0 + 1)])
         e.raw(f's_add_u32 s{SJ}, s{SJ}, 1')
         e.raw(f's_cmp_ge_u32 s{SJ}, %[nb]')
         e.raw(f's_cbranch_scc1 .Lexit{J}_%=')
 
     def mask_block(self, J):
-        par = J & 1
-        # -inf goes through a VGPR: v_cndmask_b32_e32 reads VCC over the constant bus, which leaves no room for a literal
-        out = [f'.Lmask{J}_%=:', 's_nop 7', 's_nop 7', f'v_mov_b32_e32 v{E0}, {NEG_INF}']
-        for r in range(16):
-            out.append(f'v_cmp_lt_i32_e32 vcc, {r}, %[valid]')
-            for qb in range(2):
-                out.append(f'v_cndmask_b32_e32 v{S(par, qb, r)}, v{E0}, v{S(par, qb, r)}, vcc')
-        out.append(f's_branch .Lmaskret{J}_%=')
-        return out
+        e = Emitter()
+        e.label(f'.Lmask{J}_%=')
+        e.nop_to(MFMA_WAIT)
+        self.mask(e, J & 1)
+        e.raw(f's_branch .Lmaskret{J}_%=')
+        return e.lines
 
     def rescale_block(self, par):
-        """entered after the MFMAs of the iteration: 20 wait states before the accumulators are read or written"""
+        """entered after the MFMAs of the iteration (20 wait states before S or the accumulators are touched): the
+        running max moves up by d = max(block max, 0) >= 0; O and l scale by 2^-d; S(j), S(j+1) (accumulated onto the
+        old -m) and -m shift by -d; P(j) and its row sums are recomputed"""
+        npar = par ^ 1
         e = Emitter()
         e.label(f'.Lrescale{par}_%=')
         e.nop_to(20)
-        e0, e1 = E0, E0 + 1
-        v = lambda x: f'v{x}'
+        d, alpha = A0, A0 + 1            # free until the softmax recompute
         for qb in range(2):
-            s = [S(par, qb, r) for r in range(16)]
-            e.valu(f'v_max3_f32 v{e0}, v{s[0]}, v{s[1]}, v{s[2]}', [v(s[0]), v(s[1]), v(s[2])], [v(e0)])
-            for r in range(3, 15, 2):
-                e.valu(f'v_max3_f32 v{e0}, v{e0}, v{s[r]}, v{s[r + 1]}', [v(e0), v(s[r]), v(s[r + 1])], [v(e0)])
-            e.valu(f'v_max_f32_e32 v{e0}, v{e0}, v{s[15]}', [v(e0), v(s[15])], [v(e0)])
-            e.valu(f'v_mov_b32_e32 v{e1}, v{e0}', [v(e0)], [v(e1)])
-            e.valu(f'v_permlane32_swap_b32_e32 v{e0}, v{e1}', [v(e0), v(e1)], [v(e0), v(e1)], permlane=True)
-            e.valu(f'v_max_f32_e32 v{e0}, v{e0}, v{e1}', [v(e0), v(e1)], [v(e0)])            # block max of the query
-            e.valu(f'v_max_f32_e32 v{e0}, v{M0 + qb}, v{e0}', [v(M0 + qb), v(e0)], [v(e0)])  # new running max
-            e.valu(f'v_sub_f32_e32 v{e1}, v{M0 + qb}, v{e0}', [v(M0 + qb), v(e0)], [v(e1)])
-            e.valu(f'v_mul_f32_e32 v{e1}, %[c], v{e1}', [v(e1)], [v(e1)])
-            e.valu(f'v_exp_f32_e32 v{e1}, v{e1}', [v(e1)], [v(e1)], trans=True)           # alpha
-            e.valu(f'v_mov_b32_e32 v{M0 + qb}, v{e0}', [v(e0)], [v(M0 + qb)])
-            e.valu(f'v_mul_f32_e32 v{MC0 + qb}, %[c], v{e0}', [v(e0)], [v(MC0 + qb)])
-            for op, rd, wr, tr in self.softmax(par, qb):
-                e.valu(op, rd, wr, trans=tr)
-            e.valu(f'v_mul_f32_e32 v{LSUM0 + qb}, v{LSUM0 + qb}, v{e1}', [v(LSUM0 + qb), v(e1)], [v(LSUM0 + qb)])
+            self.row_max(e, par, qb, d, alpha)
+            e.valu(f'v_max_f32_e32 v{d}, 0, v{d}', [v(d)], [v(d)])
+            e.valu(f'v_exp_f32_e64 v{alpha}, -v{d}', [v(d)], [v(alpha)], trans=True)
+            e.valu(f'v_add_f32_e32 v{M0 + qb}, v{M0 + qb}, v{d}', [v(M0 + qb), v(d)], [v(M0 + qb)])
+            for r in range(16):
+                for reg in (S(par, qb, r), S(npar, qb, r), MCV(qb) + r):
+                    e.valu(f'v_sub_f32_e32 v{reg}, v{reg}, v{d}', [v(reg), v(d)], [v(reg)])
+            e.valu(f'v_mul_f32_e32 v{LSUM0 + qb}, v{LSUM0 + qb}, v{alpha}', [v(LSUM0 + qb), v(alpha)],
+                   [v(LSUM0 + qb)])
             for base in range(0, 64, 4):
                 acc = [64 * qb + base + i for i in range(4)]
                 for i in range(4):
                     e.valu(f'v_accvgpr_read_b32 v{T0 + i}, a{acc[i]}', [], [v(T0 + i)])
                 for i in range(4):
-                    e.valu(f'v_mul_f32_e32 v{T0 + i}, v{T0 + i}, v{e1}', [v(T0 + i), v(e1)], [v(T0 + i)])
+                    e.valu(f'v_mul_f32_e32 v{T0 + i}, v{T0 + i}, v{alpha}', [v(T0 + i), v(alpha)], [v(T0 + i)])
                 for i in range(4):
                     e.valu(f'v_accvgpr_write_b32 a{acc[i]}, v{T0 + i}', [v(T0 + i)], [f'a{acc[i]}'])
+            for op, rd, wr, tr in self.softmax(par, qb):
+                e.valu(op, rd, wr, trans=tr)
         e.nop_to(2)
         e.raw(f's_add_u32 s{SRA}, s{SRA}, 4')
         e.raw(f's_addc_u32 s{SRA + 1}, s{SRA + 1}, 0')
@@ -371,12 +442,12 @@ class Kernel:
         """O += V(nb-1) P(nb-1): steps 0..3 were prefetched by the last iteration, steps 4..7 are read from the slot
         whose byte offset is in s77"""
         e = Emitter()
-        e.lds = [self._regs_prefetch()[i] for i in range(len(self._regs_prefetch()))]
+        e.lds = self._regs_prefetch()
         e.label(f'.Lepi{par}_%=')
         for db in range(4):
-            e.raw(f'v_add_u32_e32 v{E0 + db}, s{SVOFF}, v{VADDR0 + db}')
+            e.raw(f'v_add_u32_e32 v{T0 + db}, s{SVOFF}, v{VADDR0 + db}')
         for k in range(4, 8):
-            self.read_v(e, k, 0, addr=f'v{E0 + k - 4}')
+            self.read_v(e, k, 0, addr=f'v{T0 + k - 4}')
         for k in range(8):
             for qb in range(2):
                 self.mfma_pv(e, par, qb, k)
@@ -392,17 +463,18 @@ class Kernel:
         return regs
 
     def store_block(self):
-        """O / l as bf16 to the output rows (rows past the segment masked off); 16 wait states after the last MFMA"""
+        """O / l as bf16 to the output rows (rows past the segment masked off); 16 wait states after the last MFMA.
+        Temporaries live in the S registers, which are dead here."""
         e = Emitter()
         e.label('.Lstore_%=')
         e.nop_to(16)
         e.raw('s_waitcnt vmcnt(0) lgkmcnt(0)')
-        x = [E0 + i for i in range(7)]
-        v = lambda r: f'v{r}'
+        x = [S(0, 0, i) for i in (0, 1, 2, 4, 5, 6, 7)]   # v[40:41] is the even-aligned store pair
         for qb in range(2):
             e.valu(f'v_mov_b32_e32 v{x[0]}, v{LSUM0 + qb}', [v(LSUM0 + qb)], [v(x[0])])
             e.valu(f'v_mov_b32_e32 v{x[1]}, v{LSUM0 + qb}', [v(LSUM0 + qb)], [v(x[1])])
-            e.valu(f'v_permlane32_swap_b32_e32 v{x[0]}, v{x[1]}', [v(x[0]), v(x[1])], [v(x[0]), v(x[1])], permlane=True)
+            e.valu(f'v_permlane32_swap_b32_e32 v{x[0]}, v{x[1]}', [v(x[0]), v(x[1])], [v(x[0]), v(x[1])],
+                   permlane=True)
             e.valu(f'v_add_f32_e32 v{x[0]}, v{x[0]}, v{x[1]}', [v(x[0]), v(x[1])], [v(x[0])])   # l of the query
             e.valu(f'v_mov_b32_e32 %[lo{qb}], v{x[0]}', [v(x[0])], [])
             e.valu(f'v_mov_b32_e32 %[mo{qb}], v{M0 + qb}', [v(M0 + qb)], [])
@@ -415,7 +487,8 @@ class Kernel:
                     for i in range(4):
                         e.valu(f'v_accvgpr_read_b32 v{x[3 + i]}, a{acc + i}', [], [v(x[3 + i])])
                     for i in range(4):
-                        e.valu(f'v_mul_f32_e32 v{x[3 + i]}, v{x[3 + i]}, v{x[2]}', [v(x[3 + i]), v(x[2])], [v(x[3 + i])])
+                        e.valu(f'v_mul_f32_e32 v{x[3 + i]}, v{x[3 + i]}, v{x[2]}', [v(x[3 + i]), v(x[2])],
+                               [v(x[3 + i])])
                     e.valu(f'v_cvt_pk_bf16_f32 v{x[3]}, v{x[3]}, v{x[4]}', [v(x[3]), v(x[4])], [v(x[3])])
                     e.valu(f'v_cvt_pk_bf16_f32 v{x[4]}, v{x[5]}, v{x[6]}', [v(x[5]), v(x[6])], [v(x[4])])
                     e.raw(f'global_store_dwordx2 %[op{qb}], v[{x[3]}:{x[4]}], off offset:{db * 64 + 16 * g}')
@@ -425,34 +498,28 @@ class Kernel:
     def prologue(self, e):
         R = self.R
         e.raw('s_waitcnt vmcnt(0) lgkmcnt(0)')
-        e.raw(f's_mov_b32 s{SRR}, 0x49800000')
+        e.raw(f's_mov_b32 s{SRR}, 0x49800000')      # 2^20
         e.raw(f's_mov_b32 s{SJ}, 0')
         e.raw(f's_sub_u32 s{SNB1}, %[nb], 1')
-        e.raw(f's_mov_b32 s{KRES}, %[kb_lo]')
-        e.raw(f's_mov_b32 s{KRES + 1}, %[kb_hi]')
-        e.raw(f's_mov_b32 s{KREM}, %[rem0]')
-        e.raw(f's_max_i32 s{KRES + 2}, s{KREM}, 0')
-        e.raw(f's_mov_b32 s{KRES + 3}, 0x20000')
-        e.raw(f's_mov_b32 s{VRES}, %[vb_lo]')
-        e.raw(f's_mov_b32 s{VRES + 1}, %[vb_hi]')
-        e.raw(f's_mov_b32 s{VREM}, %[rem0]')
-        e.raw(f's_max_i32 s{VRES + 2}, s{VREM}, 0')
-        e.raw(f's_mov_b32 s{VRES + 3}, 0x20000')
-        e.raw(f'v_mov_b32_e32 v{KADDR0}, %[kb]')
+        for res, rem, lo, hi in ((KRES, KREM, 'kb_lo', 'kb_hi'), (VRES, VREM, 'vb_lo', 'vb_hi')):
+            e.raw(f's_mov_b32 s{res}, %[{lo}]')
+            e.raw(f's_mov_b32 s{res + 1}, %[{hi}]')
+            e.raw(f's_mov_b32 s{rem}, %[rem0]')
+            e.raw(f's_max_i32 s{res + 2}, s{rem}, 0')
+            e.raw(f's_mov_b32 s{res + 3}, 0x20000')
+        e.valu(f'v_mov_b32_e32 v{KADDR0}, %[kb]', [], [v(KADDR0)])
         for k in range(1, 8):
-            e.raw(f'v_xor_b32_e32 v{KADDR0 + k}, {32 * k}, %[kb]')
-        e.raw(f'v_mov_b32_e32 v{VADDR0}, %[vb]')
+            e.valu(f'v_xor_b32_e32 v{KADDR0 + k}, {32 * k}, %[kb]', [], [v(KADDR0 + k)])
+        e.valu(f'v_mov_b32_e32 v{VADDR0}, %[vb]', [], [v(VADDR0)])
         for db in range(1, 4):
-            e.raw(f'v_xor_b32_e32 v{VADDR0 + db}, {64 * db}, %[vb]')
+            e.valu(f'v_xor_b32_e32 v{VADDR0 + db}, {64 * db}, %[vb]', [], [v(VADDR0 + db)])
         for qb in range(2):
-            e.raw(f'v_mov_b32_e32 v{M0 + qb}, {M_INIT}')
-            e.raw(f'v_mul_f32_e32 v{MC0 + qb}, %[c], v{M0 + qb}')
-            e.raw(f'v_mov_b32_e32 v{LSUM0 + qb}, 0')
+            e.valu(f'v_mov_b32_e32 v{LSUM0 + qb}, 0', [], [v(LSUM0 + qb)])
             for half in range(2):
                 for i in range(4):
-                    e.raw(f'v_mov_b32_e32 v{P(1, qb, half, i)}, 0')
+                    e.valu(f'v_mov_b32_e32 v{P(1, qb, half, i)}, 0', [], [v(P(1, qb, half, i))])
         for i in range(128):
-            e.raw(f'v_accvgpr_write_b32 a{i}, 0')
+            e.valu(f'v_accvgpr_write_b32 a{i}, 0', [], [f'a{i}'])
         # ring fill: K0 K1 V(-1) then K(b+2) V(b) for b = 0 .. R-3 (block b of K in slot b, of V in slot b)
         self.dma_k(e, 0)
         self.dma_k(e, 1)
@@ -462,54 +529,57 @@ class Kernel:
             self.dma_v(e, b)
         e.raw(f's_waitcnt vmcnt({4 * (R - 2)})')     # K0, K1 and V(-1) landed
         e.raw('s_barrier')
-        # S(0) = K(0) Q^T; the operands of iteration 0's steps 0..3 (K(1), V(-1)) are read behind it
+        # S(0) = K(0) Q^T (no offset yet); the operands of iteration 0's steps 0..3 (K(1), V(-1)) are read behind it
         for k in range(8):
             self.read_k(e, k, 0)
-        pre = []
-        for k in range(4):
-            pre.append(('k', k, 1))
-            pre.append(('v', k, R - 1))
+        pre = [('k', k, 1) if t == 0 else ('v', k, R - 1) for k in range(4) for t in range(2)]
         for k in range(8):
             for qb in range(2):
-                self.mfma_s(e, 0, qb, k)
-            if k >= 1 and k - 1 < 4:
+                self.mfma_s(e, 0, qb, k, seed='0')
+            if 1 <= k <= 4:
                 # K operand k-1 is consumed by both query blocks: its register can take iteration 0's step k-1
-                kind, kk, slot = pre.pop(0)
-                self.read_k(e, kk, slot)
-                kind, kk, slot = pre.pop(0)
-                self.read_v(e, kk, slot)
-        while pre:
-            kind, kk, slot = pre.pop(0)
-            if kind == 'k':
-                self.read_k(e, kk, slot)
-            else:
-                self.read_v(e, kk, slot)
+                for _ in range(2):
+                    kind, kk, slot = pre.pop(0)
+                    (self.read_k if kind == 'k' else self.read_v)(e, kk, slot)
+        # m = block 0's maximum (after the mask when block 0 is the last one); S(0) -= m; the -m seed of later blocks
+        e.nop_to(MFMA_WAIT)
+        e.raw(f's_cmp_eq_u32 s{SNB1}, 0')
+        e.raw('s_cbranch_scc0 .Lpmask_%=')
+        self.mask(e, 0)
+        e.label('.Lpmask_%=')
+        for qb in range(2):
+            self.row_max(e, 0, qb, M0 + qb, A0)
+            for r in range(16):
+                e.valu(f'v_sub_f32_e32 v{S(0, qb, r)}, v{S(0, qb, r)}, v{M0 + qb}', [v(S(0, qb, r)), v(M0 + qb)],
+                       [v(S(0, qb, r))])
+                e.valu(f'v_sub_f32_e32 v{MCV(qb) + r}, 0, v{M0 + qb}', [v(M0 + qb)], [v(MCV(qb) + r)])
 
     def generate(self):
         R = self.R
-        # the prefetch order at a body's start must match what both predecessors leave: the prologue issues K k, V k
-        # pairs for k = 0..3 in the same order as phase B
         e = Emitter()
         self.prologue(e)
         pro_lines = list(e.lines)
-        state = (dict(e.mfma_w), e.pos, list(e.lds))
+        # the prologue leaves the same prefetched reads outstanding as a body's phase B, in the same order
+        state = (dict(e.mfma_w), dict(e.valu_w), e.pos, list(e.lds))
         # bodies: run the whole ring twice so that body 0 sees the wrap-around hazards of body R-1
         for attempt in range(2):
             e2 = Emitter()
-            mw, pos, lds = state
+            mw, vw, pos, lds = state
             e2.mfma_w = {r: p - pos for r, p in mw.items()}
-            e2.pos = 0
+            e2.valu_w = {r: p - pos for r, p in vw.items()}
             e2.lds = [set(x) for x in lds]
             e2.label('.Lloop_%=')
             for J in range(R):
                 self.body(e2, J)
             e2.raw('s_branch .Lloop_%=')
             if attempt == 0:
-                # merge: the later (more constraining) of the prologue's and the last body's MFMA writes
-                merged = {r: p - e.pos for r, p in e.mfma_w.items()}
+                mw2 = {r: p - e.pos for r, p in e.mfma_w.items()}
+                vw2 = {r: p - e.pos for r, p in e.valu_w.items()}
                 for r, p in e2.mfma_w.items():
-                    merged[r] = max(merged.get(r, -10 ** 9), p - e2.pos)
-                state = (merged, 0, lds)
+                    mw2[r] = max(mw2.get(r, -10 ** 9), p - e2.pos)
+                for r, p in e2.valu_w.items():
+                    vw2[r] = max(vw2.get(r, -10 ** 9), p - e2.pos)
+                state = (mw2, vw2, 0, lds)
         lines = pro_lines + e2.lines
         for J in range(R):
             lines += [f'.Lexit{J}_%=:', f's_mov_b32 s{SVOFF}, {J * SLOT}', f's_branch .Lepi{J & 1}_%=']
@@ -527,7 +597,7 @@ def render(ring):
     k = Kernel(ring)
     lines = k.generate()
     body = '\n'.join(f'  "{l}\\n\\t"' if not l.endswith(':') else f'  "{l}\\n"' for l in lines)
-    clob = ', '.join(f'"v{i}"' for i in range(56, 256)) + ', ' + ', '.join(f'"a{i}"' for i in range(128))
+    clob = ', '.join(f'"v{i}"' for i in range(FIRST_FIXED, 256)) + ', ' + ', '.join(f'"a{i}"' for i in range(128))
     clob += ', ' + ', '.join(f'"s{i}"' for i in range(64, 84)) + ', "vcc", "scc", "memory"'
     hdr = f'''// Generated by gen_attn_ring64.py (ring of {ring} K and {ring} V slots): do not edit.
 // The key loop of attn8_kernel; operands and fixed registers are described in the generator.
