@@ -153,9 +153,8 @@ int64_t or_varlen_workspace_size(int32_t n_seg, int32_t sum_q, int32_t H, int32_
 
 /* Replaces attention.varlen / flash_attn_varlen_func (src/onereel/attention.py:39-43), varlen_lse (:46-53) and
  * overlapping_ranges' FA3 call with seqused_k (:78-83): non-causal softmax(q k^T * scale) v per segment, bf16 in and
- * out, fp32 accumulation. Two launches: a tile planner and the attention kernel. Without lse (and D = 128) the
- * kernel takes 64 queries per wavefront and multiplies q by scale * log2(e) on the load (one bf16 rounding); with
- * lse it applies the scale in fp32. */
+ * out, fp32 accumulation. Two launches: a tile planner and the attention kernel (64 queries per wavefront at
+ * D = 128, 32 at D = 64). */
 int or_varlen_fwd(const or_varlen_args* args, void* stream);
 
 /* Replaces the log-sum-exp merge of partial attention results: ring._merge (src/onereel/parallel/ring.py:63-70) and

@@ -876,31 +876,6 @@ void attn4_kernel(AttnArgs a, int32_t* ws) {
 constexpr int kRing64 = ONEREEL_RING64;
 constexpr int kSlot64 = kBKB * 128;   // bf16 elements per slot
 
-// 8 bf16 of a query row times c = scale * log2(e), rotated first when the row has a table entry (the rotation in
-// fp32 as rotate8), rounded once to bf16: the key loop's scores are then c q k^T straight out of the MFMAs
-__device__ __forceinline__ u32x4 q_scaled8(u32x4 x, const float* __restrict__ cos_t, const float* __restrict__ sin_t,
-                                           int64_t off, bool rope, float c) {
-  float y[8];
-#pragma unroll
-  for (int p = 0; p < 4; ++p) {
-    y[2 * p] = bf2f((uint16_t)(x[p] & 0xffffu));
-    y[2 * p + 1] = bf2f((uint16_t)(x[p] >> 16));
-  }
-  if (rope) {
-    const f32x4 c0 = *(const f32x4*)(cos_t + off), c1 = *(const f32x4*)(cos_t + off + 4);
-    const f32x4 s0 = *(const f32x4*)(sin_t + off), s1 = *(const f32x4*)(sin_t + off + 4);
-    const float cs[8] = {c0[0], c0[1], c0[2], c0[3], c1[0], c1[1], c1[2], c1[3]};
-    const float sn[8] = {s0[0], s0[1], s0[2], s0[3], s1[0], s1[1], s1[2], s1[3]};
-#pragma unroll
-    for (int p = 0; p < 4; ++p)
-      rot_pair(y[2 * p], y[2 * p + 1], cs[2 * p], cs[2 * p + 1], sn[2 * p], sn[2 * p + 1], y[2 * p], y[2 * p + 1]);
-  }
-  u32x4 r;
-#pragma unroll
-  for (int p = 0; p < 4; ++p) r[p] = pack2(y[2 * p] * c, y[2 * p + 1] * c);
-  return r;
-}
-
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void attn8_kernel(AttnArgs a, int32_t* ws) {
   constexpr int D = 128, CH = 16, KS = 8, WQ = 64, BQ = 4 * WQ;
@@ -964,7 +939,9 @@ void attn8_kernel(AttnArgs a, int32_t* ws) {
 #pragma unroll
       for (int k = 0; k < KS; ++k) {
         const int d = 16 * k + 8 * h;
-        q[qb][k] = as_bf16x8(q_scaled8(*(const u32x4*)(qp + d), a.cos_t, a.sin_t, (int64_t)rr * D + d, rr >= 0, a.c));
+        u32x4 x = *(const u32x4*)(qp + d);
+        if (rr >= 0) x = rotate8(x, a.cos_t, a.sin_t, (int64_t)rr * D + d, 1.0f);
+        q[qb][k] = as_bf16x8(x);
       }
       uint16_t* o = (row < a.n_q_video ? a.o + row * a.os : a.o_text + (row - a.n_q_video) * a.os) + head * D + 4 * h;
       op[qb] = (uint64_t)o;
@@ -990,51 +967,40 @@ void attn8_kernel(AttnArgs a, int32_t* ws) {
     const int32_t rem0 = Lk * rb - rb + D * 2;
     const int32_t bb = kBKB * rb;
     const int valid = Lk - (nb - 1) * kBKB - 16 * h;
-    float mo0, mo1, lo0, lo1;   // per query: the running max of c q k^T, and the row sum relative to it
+    float mo0, mo1, lo0, lo1;   // per query: the running max of q k^T, and the row sum relative to it
     asm volatile(ONEREEL_RING64_ASM
                  : [mo0] "=&v"(mo0), [mo1] "=&v"(mo1), [lo0] "=&v"(lo0), [lo1] "=&v"(lo1)
                  : [q00] "a"(q[0][0]), [q01] "a"(q[0][1]), [q02] "a"(q[0][2]), [q03] "a"(q[0][3]),
                    [q04] "a"(q[0][4]), [q05] "a"(q[0][5]), [q06] "a"(q[0][6]), [q07] "a"(q[0][7]),
                    [q10] "a"(q[1][0]), [q11] "a"(q[1][1]), [q12] "a"(q[1][2]), [q13] "a"(q[1][3]),
                    [q14] "a"(q[1][4]), [q15] "a"(q[1][5]), [q16] "a"(q[1][6]), [q17] "a"(q[1][7]),
-                   [nb] "s"(nb), [valid] "v"(valid), [kb] "v"(kb), [vb] "v"(vb),
+                   [c] "s"(a.c), [nb] "s"(nb), [valid] "v"(valid), [kb] "v"(kb), [vb] "v"(vb),
                    [vk0] "v"(voff[0]), [vk1] "v"(voff[1]), [vv0] "v"(voff[2]), [vv1] "v"(voff[3]),
                    [sbase] "s"(sbase), [bb] "s"(bb), [kb_lo] "s"((uint32_t)kaddr), [kb_hi] "s"((uint32_t)(kaddr >> 32)),
                    [vb_lo] "s"((uint32_t)vaddr), [vb_hi] "s"((uint32_t)(vaddr >> 32)), [rem0] "s"(rem0),
                    [op0] "v"(op[0]), [op1] "v"(op[1]), [ok0] "v"(ok[0]), [ok1] "v"(ok[1])
                  : ONEREEL_RING64_CLOBBERS);
     if (a.lse && h == 0) {
-      // natural-log lse of scale * q k^T: the max is in log2 units
-      constexpr float kLn2 = 0.69314718055994531f;
-      if (ok[0]) a.lse[(int64_t)head * a.sum_q + q_beg + q0 + l32] = mo0 * kLn2 + logf(lo0);
-      if (ok[1]) a.lse[(int64_t)head * a.sum_q + q_beg + q0 + 32 + l32] = mo1 * kLn2 + logf(lo1);
+      if (ok[0]) a.lse[(int64_t)head * a.sum_q + q_beg + q0 + l32] = mo0 * a.scale + logf(lo0);
+      if (ok[1]) a.lse[(int64_t)head * a.sum_q + q_beg + q0 + 32 + l32] = mo1 * a.scale + logf(lo1);
     }
   }
 }
 
 typedef void (*AttnFn)(AttnArgs, int32_t*);
 
-// kernel variant. By default a call without lse output takes the 64-query ring kernel (variant 3, D = 128), which
-// folds c = scale * log2(e) into Q (one bf16 rounding of c q); a call that asks for the log-sum-exp takes the ring
-// kernel that applies c in fp32 (variant 0), so that lse keeps fp32 precision for the merges that consume it.
-// ONEREEL_ATTN_VARIANT forces 0 = ring kernel, 1 / 2 = tile kernel with 32 / 64 queries per wavefront, 3 = 64-query
-// ring kernel (lse requests still go to variant 0); D = 64 runs variant 0 for 3.
+// kernel variant (ONEREEL_ATTN_VARIANT): 3 = ring kernel with 64 queries per wavefront (the default; D = 64 runs
+// variant 0), 0 = ring kernel with 32 queries per wavefront, 1 / 2 = tile kernel with 32 / 64 queries per wavefront
 constexpr int kVariants = 4;
 
-int forced_variant() {
+int variant() {
   static int v = [] {
     const char* e = getenv("ONEREEL_ATTN_VARIANT");
-    if (!e) return -1;
+    if (!e) return 3;
     const int x = atoi(e);
-    return x >= 0 && x < kVariants ? x : -1;
+    return x >= 0 && x < kVariants ? x : 3;
   }();
   return v;
-}
-
-int variant(bool want_lse) {
-  const int f = forced_variant();
-  const int v = f < 0 ? 3 : f;
-  return v == 3 && want_lse ? 0 : v;
 }
 
 int variant_bq(int var, int D) { return var == 2 || (var == 3 && D == 128) ? 256 : 128; }
@@ -1118,7 +1084,7 @@ extern "C" int or_varlen_fwd(const or_varlen_args* p, void* stream) {
   if (x.sum_q == 0) return 0;
   DevInfo di;
   if (int rc = dev_info(di)) return rc;
-  const int var = variant(x.lse != nullptr);
+  const int var = variant();
   const int occ = di.occ[x.D == 128][var];
   if (occ < 1) return fail_arg("or_varlen_fwd: attention kernel cannot be resident (occupancy 0)");
   const int64_t max_items = max_items_of(x.n_seg, x.sum_q, x.H);

@@ -15,8 +15,9 @@ emitted here with fixed registers:
     v196..v227  -m per query block, broadcast over 16 registers: the first QK^T MFMA of a block accumulates onto it
     v228..v254  softmax temporaries, running max, row sums, LDS read addresses
     s64..s83    K and V buffer descriptors, their remaining byte counts, loop counters, return address
-Q comes in as 16 AGPR operands (the compiler places them above a127), already multiplied by c = scale * log2(e), so
-S = c q k^T - m comes out of the MFMAs and P = 2^S needs one v_exp_f32 per score and no other VALU op.
+Q comes in as 16 AGPR operands (the compiler places them above a127). S = q k^T - m comes out of the MFMAs (the
+first of each block accumulates onto -m), so P = 2^(c S), c = scale * log2(e), takes one v_mul_f32 and one v_exp_f32
+per score: the fp32 scores of FlashAttention's exp2(s c - m c), with the subtraction folded into the accumulator.
 
 Schedule of iteration j (32 keys; R-slot rings of K and V blocks in LDS, 8 KiB per slot):
     phase A  MFMA steps k = 0..3: S(j+1) += K(j+1)_k Q_k^T for both query blocks, O += V(j-1)_k P(j-1)_k; the VALU
@@ -25,7 +26,7 @@ Schedule of iteration j (32 keys; R-slot rings of K and V blocks in LDS, 8 KiB p
              of V(j+R-2) into slot (j-2) % R (both consumed by iteration j-1) goes out during phase B
     phase B  steps k = 4..7, P(j) of query block 1, and the LDS operands of steps 0..3 of iteration j+1
     tail     if a row-half sum of P(j) exceeds 2^20 (or is not finite): out-of-line rescale (m moves up by the block
-             max d, O and l scale by 2^-d, S(j), S(j+1) and -m shift by -d, P(j) recomputed); then l += row sums
+             max d, O and l scale by 2^(-c d), S(j), S(j+1) and -m shift by -d, P(j) recomputed); then l += row sums
 The running max starts at block 0's own maximum (prologue), so row sums never underflow and m only moves up.
 The generator inserts the LDS waits (lgkmcnt) from the order of the reads, and s_nop where gfx950 needs wait states
 between dependent instructions (see Emitter).
@@ -244,14 +245,16 @@ class Kernel:
                       [vr(lo, 2)])
 
     def softmax(self, par, qb):
-        """P(par, qb) = bf16(2^S) and LS(qb) = fp32 sum of the unrounded values: list of (asm, reads, writes, trans).
-        Each pair's cvt and adds come one pair behind its exponentials, so no transcendental result is read by the
-        next instruction."""
+        """P(par, qb) = bf16(2^(c S)) and LS(qb) = fp32 sum of the unrounded values: list of (asm, reads, writes,
+        trans)"""
         T = lambda r: T0 + (r % 4)
 
-        def exp(p):
-            return [(f'v_exp_f32_e32 v{T(r)}, v{S(par, qb, r)}', [v(S(par, qb, r))], [v(T(r))], True)
+        def mul(p):
+            return [(f'v_mul_f32_e32 v{T(r)}, %[c], v{S(par, qb, r)}', [v(S(par, qb, r))], [v(T(r))], False)
                     for r in (2 * p, 2 * p + 1)]
+
+        def exp(p):
+            return [(f'v_exp_f32_e32 v{T(r)}, v{T(r)}', [v(T(r))], [v(T(r))], True) for r in (2 * p, 2 * p + 1)]
 
         def tail(p):
             r0, r1 = 2 * p, 2 * p + 1
@@ -266,13 +269,17 @@ class Kernel:
                             [v(A0 + p - 4)], False))
             return out
 
-        ops = exp(0)
+        # pair p: c*S, 2^(c*S) one pair ahead of its cvt and adds (no transcendental result is read by the next
+        # instruction); a pair's T registers are rewritten only after its tail has read them
+        ops = mul(0)
         for p in range(8):
+            ops += exp(p)
+            if p >= 1:
+                ops += tail(p - 1)
             if p + 1 < 8:
-                ops += exp(p + 1)
-            else:
-                ops.append((f'v_add_f32_e32 v{A0}, v{A0}, v{A0 + 1}', [v(A0), v(A0 + 1)], [v(A0)], False))
-            ops += tail(p)
+                ops += mul(p + 1)
+        ops.append((f'v_add_f32_e32 v{A0}, v{A0}, v{A0 + 1}', [v(A0), v(A0 + 1)], [v(A0)], False))
+        ops += tail(7)
         ops.append((f'v_add_f32_e32 v{A0 + 2}, v{A0 + 2}, v{A0 + 3}', [v(A0 + 2), v(A0 + 3)], [v(A0 + 2)], False))
         ops.append((f'v_add_f32_e32 v{LS0 + qb}, v{A0}, v{A0 + 2}', [v(A0), v(A0 + 2)], [v(LS0 + qb)], False))
         return ops
@@ -405,8 +412,8 @@ class Kernel:
 
     def rescale_block(self, par):
         """entered after the MFMAs of the iteration (20 wait states before S or the accumulators are touched): the
-        running max moves up by d = max(block max, 0) >= 0; O and l scale by 2^-d; S(j), S(j+1) (accumulated onto the
-        old -m) and -m shift by -d; P(j) and its row sums are recomputed"""
+        running max moves up by d = max(block max, 0) >= 0; O and l scale by 2^(-c d); S(j), S(j+1) (accumulated onto
+        the old -m) and -m shift by -d; P(j) and its row sums are recomputed"""
         npar = par ^ 1
         e = Emitter()
         e.label(f'.Lrescale{par}_%=')
@@ -415,7 +422,8 @@ class Kernel:
         for qb in range(2):
             self.row_max(e, par, qb, d, alpha)
             e.valu(f'v_max_f32_e32 v{d}, 0, v{d}', [v(d)], [v(d)])
-            e.valu(f'v_exp_f32_e64 v{alpha}, -v{d}', [v(d)], [v(alpha)], trans=True)
+            e.valu(f'v_mul_f32_e32 v{alpha}, %[c], v{d}', [v(d)], [v(alpha)])
+            e.valu(f'v_exp_f32_e64 v{alpha}, -v{alpha}', [v(alpha)], [v(alpha)], trans=True)
             e.valu(f'v_add_f32_e32 v{M0 + qb}, v{M0 + qb}, v{d}', [v(M0 + qb), v(d)], [v(M0 + qb)])
             for r in range(16):
                 for reg in (S(par, qb, r), S(npar, qb, r), MCV(qb) + r):

@@ -43,6 +43,30 @@ def test_varlen_matches_fp32_reference(lq, lk, H, D):
     assert_close(o.cpu(), ref, what='varlen')
 
 
+@pytest.mark.parametrize('D', [64, 128])
+@pytest.mark.parametrize('growth', [0.05, -0.0009])
+def test_varlen_running_max_moves(growth, D):
+    """keys scaled by (1 + growth * key index): with growth > 0 the scores keep rising along the keys, so the online
+    max moves up many times inside an item (rescale of O and l, the shifted scores and the -m seed); with growth < 0
+    the first block holds the maximum and later blocks underflow towards 0. Both kernels: O-only and with lse."""
+    lq, lk, H = [300, 64, 5], [1000, 77, 33], 2
+    print(f'varlen running max growth={growth} D={D}', flush=True)
+    q, k, v, cq, ck = _segments_case(lq, lk, H, D, 31)
+    for s in range(len(lk)):
+        f = 1.0 + growth * torch.arange(lk[s], dtype=torch.float32)
+        k[ck[s]:ck[s + 1]] = (k[ck[s]:ck[s + 1]].float() * f[:, None, None]).bfloat16()
+    ref = OA.packed_attention(q, k, v, cq, ck)
+    args = (q.to(DEV), k.to(DEV), v.to(DEV), torch.tensor(cq, dtype=torch.int32, device=DEV),
+            torch.tensor(ck, dtype=torch.int32, device=DEV), max(lq), max(lk))
+    assert_close(A.varlen(*args).cpu(), ref, what='varlen, moving max')
+    o, lse = A.varlen_lse(*args)
+    assert_close(o.cpu(), ref, what='varlen_lse, moving max')
+    for s in range(3):
+        qs, ks = q[cq[s]:cq[s + 1]].float(), k[ck[s]:ck[s + 1]].float()
+        lref = torch.logsumexp(torch.einsum('qhd,khd->hqk', qs, ks) * D ** -0.5, -1)
+        assert (lse[:, cq[s]:cq[s + 1]].cpu() - lref).abs().max() < 2e-3
+
+
 def test_varlen_lse_and_packed_api():
     lq, lk, H, D = [70, 3, 129], [90, 300, 5], 2, 128
     q, k, v, cq, ck = _segments_case(lq, lk, H, D, 21)
