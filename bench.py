@@ -37,9 +37,13 @@ REPS = [0, 10, 21, 31]
 GRID = (32, 30, 53)
 
 
+UNEVEN = ['uneven2', 'uneven4', 'uneven8', 'uneven12']
+
+
 def workload(name):
     """scene-attention layer shapes: the HunyuanVideo-1.5 480p layer (the default and headline), the Wan2.2 704x1280
-    joint scopes, and the 12-scene uneven sweep point (lengths and text counts drawn from numpy's generator seeded 12)"""
+    joint scopes, and the uneven sweep points with K = 2, 4, 8 or 12 scenes (lengths in [2, 16] frames and text counts
+    in [64, 256] drawn from numpy's generator seeded K)"""
     if name == 'hunyuan480p':
         return dict(workload='hunyuan15-480p-4scene-scene-attention-layer', lengths=LENGTHS, T=T, counts=COUNTS, H=H,
                     D=D, halo=0, sides='adj', reps=REPS, grid=GRID, scene_rope=True, adjacent=True)
@@ -47,14 +51,15 @@ def workload(name):
         return dict(workload='wan22-704x1280-3scene-joint-scope-attention-layer', lengths=[11] * 3, T=880,
                     counts=[128] * 3, H=24, D=128, halo=2, sides='next', reps=None, grid=(33, 22, 40),
                     scene_rope=False, adjacent=False)
-    if name == 'uneven12':
+    if name in UNEVEN:
         import numpy as np
-        rng = np.random.default_rng(12)
-        lengths = rng.integers(2, 17, 12).tolist()
-        counts = rng.integers(64, 257, 12).tolist()
+        K = int(name[len('uneven'):])
+        rng = np.random.default_rng(K)
+        lengths = rng.integers(2, 17, K).tolist()
+        counts = rng.integers(64, 257, K).tolist()
         F = sum(lengths)
         reps = sorted({int(x) for x in np.linspace(0, F - 1, 4).round()})
-        return dict(workload='uneven-12-scene-sweep-attention-layer', lengths=lengths, T=1590, counts=counts, H=16,
+        return dict(workload=f'uneven-{K}-scene-sweep-attention-layer', lengths=lengths, T=1590, counts=counts, H=16,
                     D=128, halo=0, sides='adj', reps=reps, grid=(F, 30, 53), scene_rope=True, adjacent=True)
     raise ValueError(name)
 
@@ -287,9 +292,10 @@ def main():
     ap.add_argument('--kernel-reps', type=int, default=10)
     ap.add_argument('--no-gemm-ref', action='store_true', help='skip the bf16 GEMM reference')
     ap.add_argument('--workload', default='hunyuan480p',
-                    choices=['hunyuan480p', 'wan704', 'uneven12', 'wan-dit-step', 'frame-memory'],
+                    choices=['hunyuan480p', 'wan704'] + UNEVEN + ['wan-dit-step', 'frame-memory'],
                     help='hunyuan480p (default, the headline): the HunyuanVideo-1.5 480p 4-scene layer; wan704 and '
-                         'uneven12: the same layer at the Wan2.2 704x1280 and 12-scene uneven shapes; wan-dit-step: '
+                         'unevenK: the same layer at the Wan2.2 704x1280 shape and at the K-scene uneven sweep points '
+                         '(K = 2, 4, 8, 12); wan-dit-step: '
                          'one forward of a random-init Wan2.2-TI2V-5B-shaped DiT over 16 scenes x 15 frames x 880 '
                          'tokens with frame memory 4 (end-to-end ms per step); frame-memory: the pooling and '
                          'selection kernels at that shape')
