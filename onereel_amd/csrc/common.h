@@ -114,9 +114,14 @@ __host__ __device__ inline int scene_shared_frames(const or_layout_desc& d, cons
 __host__ __device__ inline int shared_dst(const LayoutDerived& L, int j, const int* sh, int n, int f) {
   const int lo = L.lo[j], hi = L.hi[j];
   if (L.scene_rope) {
+    // the largest position among frames lo..hi-1: positions rise within a rope scene, so each rope scene that
+    // overlaps [lo, hi) peaks at its last overlapping frame (frames past the rope scenes have none)
     int last = -1;
-    for (int g = lo; g < hi; ++g) {
-      int p = frame_position(L, g);
+    for (int s = 0; s < L.n_rope; ++s) {
+      const int a = L.rope_start[s], b = L.rope_start[s + 1];
+      const int e = (hi < b ? hi : b) - 1;
+      if (e < a || e < lo) continue;
+      const int p = e - a + (a > 0 ? 1 : 0);
       if (p > last) last = p;
     }
     int c = 0;

@@ -8,7 +8,9 @@
 //
 // Every block first derives the per-scene quantities in LDS: its first wavefront does it alone, one lane per scene
 // (at most 64 scenes, 128 segments), with cross-lane prefix sums and no block barrier until the tables are complete.
-// Then the grid writes the per-row arrays with a grid-stride loop: int32 stores, fully coalesced.
+// The packed rows then split into runs that share every index but the spatial offset: one run per (segment, frame)
+// and one per (segment, sentence). A block takes one run at a time, derives its bases once, and writes its rows as
+// base + offset with coalesced int32 stores, so no per-row search or division is left.
 #include <stdarg.h>
 #include <stdio.h>
 #include <string.h>
@@ -22,11 +24,15 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kMaxSeg = 2 * OR_MAX_SCENES;
 
-// segment s: with text, V_j = 2j and T_j = 2j + 1; without, V_j = j
+// segment s: with text, V_j = 2j and T_j = 2j + 1; without, V_j = j. A segment's packed rows are runs: one per
+// frame (T rows of one source frame) and one for its text rows. cu_uq / cu_uk count the runs of the query and key
+// sides.
 struct SegTable {
   int n_seg;
   int cu_q[kMaxSeg + 1];
   int cu_k[kMaxSeg + 1];
+  int cu_uq[kMaxSeg + 1];
+  int cu_uk[kMaxSeg + 1];
 };
 
 __host__ __device__ inline int seg_scene(int with_text, int s) { return with_text ? s >> 1 : s; }
@@ -43,6 +49,20 @@ __host__ __device__ inline void seg_lengths(const LayoutDerived& L, int s, int* 
   } else {
     *lq = own;
     *lk = own + (L.sh_ptr[j + 1] - L.sh_ptr[j]) * L.T + txt;
+  }
+}
+
+// runs of segment s: query side (its own frames, or its sentence) and key side (own frames, shared frames, sentence)
+__host__ __device__ inline void seg_runs(const LayoutDerived& L, int s, int* uq, int* uk) {
+  const int j = seg_scene(L.with_text, s);
+  const int own = L.hi[j] - L.lo[j];
+  const int txt = L.t1[j] - L.t0[j] > 0 ? 1 : 0;
+  if (seg_is_text(L.with_text, s)) {
+    *uq = txt;
+    *uk = own + txt;
+  } else {
+    *uq = own;
+    *uk = own + (L.sh_ptr[j + 1] - L.sh_ptr[j]) + txt;
   }
 }
 
@@ -120,8 +140,7 @@ struct RowOut {
 };
 
 __global__ __launch_bounds__(kThreads) void layout_kernel(const or_layout_desc d, RowOut out, int32_t* cu_q_out,
-                                                          int32_t* cu_k_out, int32_t* seg_q_src_out,
-                                                          int64_t sum_q, int64_t sum_k) {
+                                                          int32_t* cu_k_out, int32_t* seg_q_src_out) {
   __shared__ LayoutDerived L;
   __shared__ SegTable S;
   __shared__ int sh_tmp[kMaxShared];
@@ -202,6 +221,23 @@ __global__ __launch_bounds__(kThreads) void layout_kernel(const or_layout_desc d
       S.cu_k[n_seg] = ck1;
       S.n_seg = n_seg;
     }
+    int uq0 = 0, uk0 = 0, uq1 = 0, uk1 = 0;
+    if (lane < n_seg) seg_runs(L, lane, &uq0, &uk0);
+    if (64 + lane < n_seg) seg_runs(L, 64 + lane, &uq1, &uk1);
+    const int rq0 = wave_scan(uq0), rk0 = wave_scan(uk0);
+    const int rq1 = wave_scan(uq1) + __shfl(rq0, 63, 64), rk1 = wave_scan(uk1) + __shfl(rk0, 63, 64);
+    if (lane < n_seg) {
+      S.cu_uq[lane] = rq0 - uq0;
+      S.cu_uk[lane] = rk0 - uk0;
+    }
+    if (64 + lane < n_seg) {
+      S.cu_uq[64 + lane] = rq1 - uq1;
+      S.cu_uk[64 + lane] = rk1 - uk1;
+    }
+    if (lane == 63) {
+      S.cu_uq[n_seg] = rq1;
+      S.cu_uk[n_seg] = rk1;
+    }
   }
   __syncthreads();
   if (blockIdx.x == 0) {
@@ -215,63 +251,65 @@ __global__ __launch_bounds__(kThreads) void layout_kernel(const or_layout_desc d
     }
   }
 
-  // 4. per-row arrays
+  // 4. per-row arrays, one run at a time
   const int T = L.T;
   const int n_video = L.F * T;
-  const int64_t total = sum_q + sum_k;
-  for (int64_t r = (int64_t)blockIdx.x * kThreads + tid; r < total; r += (int64_t)gridDim.x * kThreads) {
-    if (r < sum_q) {
-      const int rq = (int)r;
-      const int s = upper_bound(S.cu_q, n_seg + 1, rq) - 1;
-      const int o = rq - S.cu_q[s];
-      const int j = seg_scene(L.with_text, s);
-      int src, rope;
-      if (seg_is_text(L.with_text, s)) {
-        src = n_video + L.t0[j] + o;
-        rope = -1;
+  const int n_uq = S.cu_uq[n_seg], n_runs = n_uq + S.cu_uk[n_seg];
+  for (int u = blockIdx.x; u < n_runs; u += gridDim.x) {
+    // run bases (block-uniform): rows [row0, row0 + count) get src0 + x, and rope0 + x / ma0 + x / mb0 + x where
+    // those apply (-1 elsewhere)
+    const bool qside = u < n_uq;
+    const int* cu_u = qside ? S.cu_uq : S.cu_uk;
+    const int uu = qside ? u : u - n_uq;
+    const int s = upper_bound(cu_u, n_seg + 1, uu) - 1;
+    const int slot = uu - cu_u[s];
+    const int j = seg_scene(L.with_text, s);
+    const int own = L.hi[j] - L.lo[j];
+    const int nsh = seg_is_text(L.with_text, s) ? 0 : L.sh_ptr[j + 1] - L.sh_ptr[j];
+    const int nfr = qside ? (seg_is_text(L.with_text, s) ? 0 : own) : own + nsh;
+    int row0, count, src0, rope0 = -1, ma0 = -1, mb0 = -1;
+    bool rope = false, move = false;
+    if (slot < nfr) {
+      row0 = (qside ? S.cu_q[s] : S.cu_k[s]) + slot * T;
+      count = T;
+      rope = true;
+      int f;
+      if (slot < own) {
+        f = L.lo[j] + slot;
+        rope0 = L.scene_rope ? frame_position(L, f) * T : f * T;
       } else {
-        src = L.lo[j] * T + o;
-        rope = rope_row_of_token(L, src);
-      }
-      if (out.q_src) out.q_src[rq] = src;
-      if (out.q_rope) out.q_rope[rq] = rope;
-    } else {
-      const int rk = (int)(r - sum_q);
-      const int s = upper_bound(S.cu_k, n_seg + 1, rk) - 1;
-      const int o = rk - S.cu_k[s];
-      const int j = seg_scene(L.with_text, s);
-      const bool text_seg = seg_is_text(L.with_text, s);
-      const int own = L.hi[j] - L.lo[j];
-      const int nsh = text_seg ? 0 : L.sh_ptr[j + 1] - L.sh_ptr[j];
-      const int nvid = (own + nsh) * T;
-      int src, rope = -1, ma = -1, mb = -1;
-      if (o < nvid) {
-        const int i = o / T, sp = o - (o / T) * T;
-        if (i < own) {
-          src = (L.lo[j] + i) * T + sp;
-          rope = rope_row_of_token(L, src);
+        const int e = L.sh_ptr[j] + (slot - own);
+        f = L.sh[e];
+        if (L.adjacent) {
+          const int dst = L.sh_dst[e];
+          const int dd = dst - frame_position(L, f);
+          const int a = dd >= 0 ? 0 : -dd;
+          rope0 = dst * T;
+          ma0 = a * T;
+          mb0 = (a + dd) * T;
+          move = true;
         } else {
-          const int e = L.sh_ptr[j] + (i - own);
-          const int f = L.sh[e];
-          src = f * T + sp;
-          if (L.adjacent) {
-            const int dst = L.sh_dst[e];
-            const int dd = dst - frame_position(L, f);
-            const int a = dd >= 0 ? 0 : -dd;
-            rope = dst * T + sp;
-            ma = a * T + sp;
-            mb = (a + dd) * T + sp;
-          } else {
-            rope = rope_row_of_token(L, src);
-          }
+          rope0 = L.scene_rope ? frame_position(L, f) * T : f * T;
         }
-      } else {
-        src = n_video + L.t0[j] + (o - nvid);
       }
-      if (out.k_src) out.k_src[rk] = src;
-      if (out.k_rope) out.k_rope[rk] = rope;
-      if (out.k_move_a) out.k_move_a[rk] = ma;
-      if (out.k_move_b) out.k_move_b[rk] = mb;
+      src0 = f * T;
+    } else {
+      row0 = (qside ? S.cu_q[s] : S.cu_k[s]) + nfr * T;
+      count = L.t1[j] - L.t0[j];
+      src0 = n_video + L.t0[j];
+    }
+    if (qside) {
+      for (int x = tid; x < count; x += kThreads) {
+        if (out.q_src) out.q_src[row0 + x] = src0 + x;
+        if (out.q_rope) out.q_rope[row0 + x] = rope ? rope0 + x : -1;
+      }
+    } else {
+      for (int x = tid; x < count; x += kThreads) {
+        if (out.k_src) out.k_src[row0 + x] = src0 + x;
+        if (out.k_rope) out.k_rope[row0 + x] = rope ? rope0 + x : -1;
+        if (out.k_move_a) out.k_move_a[row0 + x] = move ? ma0 + x : -1;
+        if (out.k_move_b) out.k_move_b[row0 + x] = move ? mb0 + x : -1;
+      }
     }
   }
 }
@@ -411,15 +449,20 @@ extern "C" int or_layout_plan(const or_layout_desc* desc, or_layout_sizes* sizes
 
 extern "C" int or_layout_build(const or_layout_desc* desc, const or_layout_out* out, void* stream) {
   or_layout_sizes sz;
-  int rc = plan_impl(desc, &sz, nullptr);
+  static thread_local LayoutDerived L;
+  int rc = plan_impl(desc, &sz, &L);
   if (rc) return rc;
   if (!out) return fail_arg("or_layout_build: out is NULL");
   RowOut ro{out->q_src, out->q_rope, out->k_src, out->k_rope, out->k_move_a, out->k_move_b};
-  const int64_t total = sz.sum_q + sz.sum_k;
-  int64_t blocks = (total + kThreads * 2 - 1) / (kThreads * 2);  // about 2 rows per thread
-  if (blocks < 1) blocks = 1;
-  if (blocks > 2048) blocks = 2048;
+  // one block per run (frame or sentence of a segment), at most 2048
+  int64_t runs = 0;
+  for (int s = 0; s < sz.n_seg; ++s) {
+    int uq, uk;
+    seg_runs(L, s, &uq, &uk);
+    runs += uq + uk;
+  }
+  int64_t blocks = runs < 1 ? 1 : runs > 2048 ? 2048 : runs;
   hipLaunchKernelGGL(layout_kernel, dim3((unsigned)blocks), dim3(kThreads), 0, (hipStream_t)stream, *desc, ro,
-                     out->cu_q, out->cu_k, out->seg_q_src, sz.sum_q, sz.sum_k);
+                     out->cu_q, out->cu_k, out->seg_q_src);
   return check_hip(hipGetLastError(), "layout_kernel launch");
 }
