@@ -2,21 +2,22 @@
 // accumulation. Replaces flash_attn_varlen_func as src/onereel/attention.py:39-53,78-83 calls it.
 //
 // Design (CDNA4, 64-wide wavefronts, v_mfma_f32_32x32x16_bf16):
-// - A work item is (segment, head, query tile); a block of 4 wavefronts takes one item at a time from a queue
-//   (persistent blocks). A planner kernel orders the items longest segment first (LPT over the uneven scene lengths)
-//   into eight queues, one per XCD, by head: the blocks of one XCD work on the same segment-head together and share
-//   its K/V in that XCD's L2. A block whose queue is empty takes items from the other queues.
-// - Each wavefront owns 64 queries. It computes S^T = K Q^T (keys on the MFMA rows, queries on the columns), so a
-//   lane holds one query's scores: the running max, the exponentials and the row sum are in-lane except one
-//   exchange with lane ^ 32. The K rows of the A operand are permuted (pi below) so that lane half h holds keys
-//   16h .. 16h+15 of each 32-key block in register order, which makes P^T usable as the B operand of O^T = V^T P^T
-//   and makes the V^T operand 8 consecutive keys: one 16-byte LDS read from a transposed V tile.
-// - K and V^T tiles of 64 keys are double-buffered in LDS (XOR-swizzled 16-byte chunks); the next tile's global
-//   loads are in flight while the current tile computes.
-// - Softmax in base 2 with the scale folded into one FMA: p = 2^(s*c - m*c), c = scale * log2(e).
+// - A work item is (segment, head, query tile); a persistent block of 4 wavefronts takes one item at a time from a
+//   queue. A planner kernel orders the items longest segment first (LPT over the uneven scene lengths) into eight
+//   queues, one per XCD, by head: the blocks of one XCD work on the same segment-head together and share its K/V in
+//   that XCD's L2. A block whose queue is empty takes items from the other queues.
+// - Scores are computed transposed, S^T = K Q^T (keys on the MFMA rows, queries on the columns), so a lane holds one
+//   query's scores: the max, the exponentials and the row sum are in-lane apart from one exchange with lane ^ 32.
+//   The K rows of the A operand are permuted (pi32) so that lane half h holds keys 16h .. 16h+15 of each 32-key block
+//   in register order, which makes P^T usable as the B operand of O^T = V^T P^T and each V^T operand 8 consecutive
+//   keys of one transposing LDS read pair.
+// - K and V stream in blocks of 32 keys through rings of LDS slots, filled by LDS DMA (buffer_load ... lds) several
+//   blocks ahead; rows past a segment's end read as zeros.
+// - head_dim 128: attn8_kernel, 64 queries per wavefront (one wavefront per SIMD), O in AGPRs, key loop in generated
+//   asm. head_dim 64: attn4_kernel, 32 queries per wavefront, two wavefronts per SIMD.
+// - Softmax in base 2, p = 2^(c (s - m)) with c = scale * log2(e), and a running max m raised only when needed.
 // - Optional RoPE on the Q load (table row per packed query), with the rounding of diffusers apply_rotary_emb.
 #include <math.h>
-#include <stdlib.h>
 
 #include "common.h"
 #include "attn_ring64.inc"
@@ -29,8 +30,7 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kThreads = 256;   // 4 wavefronts
-constexpr int kMinBQ = 128;     // smallest work-item query tile of any kernel variant (sizes the item list)
-constexpr int kBK = 64;         // keys per tile
+constexpr int kMinBQ = 128;     // smallest work-item query tile of the two kernels (sizes the item list)
 constexpr int kQueues = 8;      // item queues: one per XCD
 constexpr int kQueueWords = 32; // words per queue header (head counter, item count, first item), one 128-byte line
 constexpr int kWsHeader = kQueues * kQueueWords;   // int32 words before the item list
@@ -199,88 +199,10 @@ __device__ __forceinline__ int xcc_id() { return __builtin_amdgcn_s_getreg(0xf81
 // ------------------------------------------------------------------------------------------------------------------
 // attention
 
-template <int D>
-struct Tile {
-  static constexpr int CH = D / 8;               // 16-byte chunks per K / V row
-  static constexpr int KS = D / 16;              // MFMA k-steps of S^T
-  static constexpr int DB = D / 32;              // 32-row blocks of O^T
-  static constexpr int LOADS = kBK * CH / kThreads;  // 16-byte direct loads per lane per tile, for K and for V
-};
-
-template <int D>
-struct Smem {
-  uint16_t k[2][kBK * D];
-  uint16_t v[2][kBK * D];
-  int item;
-};
-
-// chunk swizzles (XOR on the 16-byte chunk index of a row). K: the S^T operand reads rows pi(l) of one chunk column,
-// spread over distinct chunks for every 16 consecutive lanes. V: the transpose read takes 4 consecutive rows x 32
-// bytes per 16 lanes; shifting each row by 2 chunks keeps them on distinct banks.
-template <int CH>
-__device__ __forceinline__ int swz_k(int r) {
-  return ((r & 3) | (((r >> 4) & 1) << 2) | (((r >> 2) & 1) << 3)) & (CH - 1);
-}
-template <int CH>
-__device__ __forceinline__ int swz_v(int r) {
-  return (2 * (r & 3)) & (CH - 1);
-}
-
-// HBM -> LDS copy of one K and one V tile (64 keys), 16 bytes per lane, lane-linear in LDS; the swizzle is applied by
-// choosing which global chunk each lane fetches. Keys past Lk re-read the last key (finite data, masked later).
-template <int D>
-__device__ __forceinline__ void load_tile(const AttnArgs& a, Smem<D>& sm, int buf, int head, int k_beg, int Lk,
-                                          int t) {
-  using C = Tile<D>;
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-#pragma unroll
-  for (int i = 0; i < C::LOADS; ++i) {
-    const int base = (i * (kThreads / 64) + w) * 64;     // first LDS slot of this wavefront's instruction
-    const int slot = base + lane;
-    const int row = slot / C::CH, phys = slot % C::CH;
-    int key = t * kBK + row;
-    key = key < Lk ? key : Lk - 1;
-    const int64_t g = (int64_t)(k_beg + key) * a.ks + head * D;
-    __builtin_amdgcn_global_load_lds((const void*)(a.k + g + (phys ^ swz_k<C::CH>(row)) * 8),
-                                     (__attribute__((address_space(3))) void*)&sm.k[buf][base * 8], 16, 0, 0);
-    __builtin_amdgcn_global_load_lds((const void*)(a.v + g + (phys ^ swz_v<C::CH>(row)) * 8),
-                                     (__attribute__((address_space(3))) void*)&sm.v[buf][base * 8], 16, 0, 0);
-  }
-}
-
 __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
 
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-
-// V^T operand of O^T = V^T P^T: lane l (row d = db*32 + l%32, half h) gets keys key0 + 0..7 (8 consecutive keys)
-// through two transpose reads. Within each 16-lane group, source lane r addresses row key0 + 4t + r/4 at dims
-// base_d + 4*(r%4), and lane i receives the 4 keys of dim base_d + i.
-template <int D>
-__device__ __forceinline__ bf16x8 read_vt(const uint16_t* vtile, int key0, int db, int lane) {
-  using C = Tile<D>;
-  const int r = lane & 15, g = lane >> 4;
-  const int base_d = db * 32 + 16 * (g & 1);
-  const int d0 = base_d + 4 * (r & 3);
-  u32x2 lo, hi;
-#pragma unroll
-  for (int t = 0; t < 2; ++t) {
-    const int row = key0 + 4 * t + (r >> 2);
-    const int phys = (d0 >> 3) ^ swz_v<C::CH>(row);
-    const uint16_t* p = vtile + row * D + phys * 8 + (d0 & 7);
-    bf16x4 x = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((__attribute__((address_space(3))) bf16x4*)p);
-    (t == 0 ? lo : hi) = __builtin_bit_cast(u32x2, x);
-  }
-  u32x4 v = {lo[0], lo[1], hi[0], hi[1]};
-  return as_bf16x8(v);
-}
-
-__device__ __forceinline__ bf16x8 pack_p8(const f32x16& p, int base) {
-  u32x4 r;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) r[i] = pack2(p[base + 2 * i], p[base + 2 * i + 1]);
-  return as_bf16x8(r);
-}
 
 // max over the 32 keys of a query: in-lane over 16, then with lane ^ 32 (v_permlane32_swap)
 __device__ __forceinline__ float pair_max(float x) {
@@ -293,220 +215,6 @@ __device__ __forceinline__ float pair_sum(float x) {
   const int xi = __builtin_bit_cast(int, x);
   auto sw = __builtin_amdgcn_permlane32_swap(xi, xi, false, false);
   return __builtin_bit_cast(float, (int)sw[0]) + __builtin_bit_cast(float, (int)sw[1]);
-}
-
-// S^T of the two 32-key blocks of a tile (keys kb*32 + 16h + r), for the wavefront's NQ query blocks. The K operand
-// of each (block, k-step) is read once and used by every query block; 2*NQ independent accumulation chains.
-template <int D, int NQ>
-__device__ __forceinline__ void qk_tile(const uint16_t* ktile, const bf16x8 (&qreg)[NQ][D / 16], int l32, int h,
-                                        f32x16 (&s0)[NQ], f32x16 (&s1)[NQ]) {
-  using C = Tile<D>;
-#pragma unroll
-  for (int qb = 0; qb < NQ; ++qb)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      s0[qb][r] = 0.0f;
-      s1[qb][r] = 0.0f;
-    }
-  const int row0 = pi32(l32), row1 = 32 + pi32(l32);
-#pragma unroll
-  for (int ks = 0; ks < C::KS; ++ks) {
-    const int col = 2 * ks + h;
-    const bf16x8 k0 = *(const bf16x8*)(ktile + row0 * D + ((col ^ swz_k<C::CH>(row0)) * 8));
-    const bf16x8 k1 = *(const bf16x8*)(ktile + row1 * D + ((col ^ swz_k<C::CH>(row1)) * 8));
-#pragma unroll
-    for (int qb = 0; qb < NQ; ++qb) {
-      s0[qb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(k0, qreg[qb][ks], s0[qb], 0, 0, 0);
-      s1[qb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(k1, qreg[qb][ks], s1[qb], 0, 0, 0);
-    }
-  }
-}
-
-// online softmax of one 32-key block (in place: s becomes p), P^T operands out
-template <int D, int NQ>
-__device__ __forceinline__ void softmax_block(f32x16 (&s)[NQ], int key_base, int Lk, int h, float c, float (&m)[NQ],
-                                              float (&lsum)[NQ], f32x16 (&acc)[NQ][D / 32],
-                                              bf16x8 (&pb)[2][NQ]) {
-  using C = Tile<D>;
-  const float NEG_INF = -__builtin_inff();
-  if (key_base + 32 > Lk) {
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const bool bad = key_base + 16 * h + r >= Lk;
-#pragma unroll
-      for (int qb = 0; qb < NQ; ++qb) s[qb][r] = bad ? NEG_INF : s[qb][r];
-    }
-  }
-  float mx[NQ];
-  bool grow = false;
-#pragma unroll
-  for (int qb = 0; qb < NQ; ++qb) {
-    float x = fmaxf(s[qb][0], s[qb][1]);
-#pragma unroll
-    for (int r = 2; r < 16; r += 2) x = fmaxf(x, fmaxf(s[qb][r], s[qb][r + 1]));
-    mx[qb] = pair_max(x);
-    grow |= (mx[qb] - m[qb]) * c > 8.0f;
-  }
-  // lazy rescale: the running max moves only when some query of the wavefront gains more than 2^8 over it
-  // (p stays <= 256 otherwise: exact enough in fp32 sums and bf16 operands)
-  if (__any(grow)) {
-#pragma unroll
-    for (int qb = 0; qb < NQ; ++qb) {
-      const float m_new = fmaxf(m[qb], mx[qb]);
-      const float alpha = __builtin_amdgcn_exp2f((m[qb] - m_new) * c);
-      m[qb] = m_new;
-      lsum[qb] *= alpha;
-#pragma unroll
-      for (int db = 0; db < C::DB; ++db)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) acc[qb][db][r] *= alpha;
-    }
-  }
-#pragma unroll
-  for (int qb = 0; qb < NQ; ++qb) {
-    const float mc = m[qb] * c;
-    float ls = 0.0f;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[qb][r], c, -mc));
-      s[qb][r] = p;
-      ls += p;
-    }
-    lsum[qb] += ls;
-    pb[0][qb] = pack_p8(s[qb], 0);
-    pb[1][qb] = pack_p8(s[qb], 8);
-  }
-}
-
-// O^T += V^T P^T for one 32-key block
-template <int D, int NQ>
-__device__ __forceinline__ void pv_block(const uint16_t* vtile, int kb, int h, int lane, const bf16x8 (&pb)[2][NQ],
-                                         f32x16 (&acc)[NQ][D / 32]) {
-  using C = Tile<D>;
-#pragma unroll
-  for (int half = 0; half < 2; ++half) {
-    const int key0 = kb * 32 + 16 * h + 8 * half;
-#pragma unroll
-    for (int db = 0; db < C::DB; ++db) {
-      const bf16x8 va = read_vt<D>(vtile, key0, db, lane);
-#pragma unroll
-      for (int qb = 0; qb < NQ; ++qb)
-        acc[qb][db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pb[half][qb], acc[qb][db], 0, 0, 0);
-    }
-  }
-}
-
-// NQ = 1: 32 queries per wavefront, 128 per block, two blocks resident per CU (two wavefronts per SIMD overlap MFMA
-// and softmax); NQ = 2: 64 queries per wavefront, 256 per block, one block per CU.
-template <int D, int NQ>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(NQ == 1 ? 2 : 1, NQ == 1 ? 2 : 1)))
-void attn_kernel(AttnArgs a, int32_t* ws) {
-  using C = Tile<D>;
-  constexpr int WQ = 32 * NQ, BQ = 4 * WQ;
-  __shared__ __attribute__((aligned(16))) Smem<D> sm;
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int l32 = lane & 31, h = lane >> 5;
-  const float NEG_INF = -__builtin_inff();
-
-  const int xcc = xcc_id();
-  for (;;) {
-    if (tid == 0) sm.item = next_item(ws, xcc);
-    __syncthreads();
-    const int it = sm.item;
-    __syncthreads();
-    if (it < 0) break;
-    const int seg = ws[kWsHeader + 2 * it];
-    const int packed_ht = ws[kWsHeader + 2 * it + 1];
-    const int head = packed_ht & 255, qt = packed_ht >> 8;
-    const int q_beg = a.cu_q[seg];
-    const int Lq = a.cu_q[seg + 1] - q_beg;
-    const int k_beg = seg_k_begin(a, seg);
-    const int Lk = seg_k_len(a, seg);
-    const int q_src0 = a.seg_q_src ? a.seg_q_src[seg] : q_beg;
-    const int q0 = qt * BQ + w * WQ;
-    const bool active = q0 < Lq;
-    const int n_tiles = (Lk + kBK - 1) / kBK;
-    if (n_tiles > 0) load_tile<D>(a, sm, 0, head, k_beg, Lk, 0);
-
-    // Q operand (B of S^T): lane holds query l32 of block qb, dims 16*ks + 8h .. +7
-    bf16x8 qreg[NQ][C::KS];
-#pragma unroll
-    for (int qb = 0; qb < NQ; ++qb) {
-      int i = q0 + qb * 32 + l32;
-      i = i < Lq ? i : Lq - 1;
-      i = i < 0 ? 0 : i;
-      const int64_t row = q_src0 + i;
-      const uint16_t* qp = (row < a.n_q_video ? a.q + row * a.qs : a.q_text + (row - a.n_q_video) * a.qs) + head * D;
-      int rr = a.q_rope ? a.q_rope[q_beg + i] : -1;
-      if (rr >= a.n_rope_rows) rr = -1;
-#pragma unroll
-      for (int ks = 0; ks < C::KS; ++ks) {
-        const int d = 16 * ks + 8 * h;
-        u32x4 x = *(const u32x4*)(qp + d);
-        if (rr >= 0) x = rotate8(x, a.cos_t, a.sin_t, (int64_t)rr * D + d, 1.0f);
-        qreg[qb][ks] = as_bf16x8(x);
-      }
-    }
-
-    f32x16 acc[NQ][C::DB];
-#pragma unroll
-    for (int qb = 0; qb < NQ; ++qb)
-#pragma unroll
-      for (int db = 0; db < C::DB; ++db)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) acc[qb][db][r] = 0.0f;
-    float m[NQ], lsum[NQ];
-#pragma unroll
-    for (int qb = 0; qb < NQ; ++qb) {
-      m[qb] = NEG_INF;
-      lsum[qb] = 0.0f;
-    }
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-
-    for (int t = 0; t < n_tiles; ++t) {
-      const int buf = t & 1;
-      if (t + 1 < n_tiles) load_tile<D>(a, sm, buf ^ 1, head, k_beg, Lk, t + 1);
-      if (active) {
-        const uint16_t* kt = sm.k[buf];
-        const uint16_t* vt = sm.v[buf];
-        f32x16 s0[NQ], s1[NQ];
-        bf16x8 pb[2][NQ];
-        qk_tile<D, NQ>(kt, qreg, l32, h, s0, s1);
-        softmax_block<D, NQ>(s0, t * kBK, Lk, h, a.c, m, lsum, acc, pb);
-        pv_block<D, NQ>(vt, 0, h, lane, pb, acc);
-        softmax_block<D, NQ>(s1, t * kBK + 32, Lk, h, a.c, m, lsum, acc, pb);
-        pv_block<D, NQ>(vt, 1, h, lane, pb, acc);
-      }
-      __builtin_amdgcn_s_waitcnt(0);
-      __syncthreads();
-    }
-
-    // epilogue: combine the lane pair's row sums, normalise, store 4 consecutive dims per (db, group)
-    if (active) {
-#pragma unroll
-      for (int qb = 0; qb < NQ; ++qb) {
-        const float ltot = pair_sum(lsum[qb]);
-        const int i = q0 + qb * 32 + l32;
-        if (i < Lq) {
-          const float inv = n_tiles > 0 ? 1.0f / ltot : 0.0f;
-          const int64_t row = q_src0 + i;
-          uint16_t* op = (row < a.n_q_video ? a.o + row * a.os : a.o_text + (row - a.n_q_video) * a.os) + head * D;
-#pragma unroll
-          for (int db = 0; db < C::DB; ++db)
-#pragma unroll
-            for (int g = 0; g < 4; ++g) {
-              const int d = db * 32 + 8 * g + 4 * h;
-              uint32_t lo = pack2(acc[qb][db][4 * g] * inv, acc[qb][db][4 * g + 1] * inv);
-              uint32_t hi = pack2(acc[qb][db][4 * g + 2] * inv, acc[qb][db][4 * g + 3] * inv);
-              *(uint2*)(op + d) = make_uint2(lo, hi);
-            }
-          if (a.lse && h == 0)
-            a.lse[(int64_t)head * a.sum_q + q_beg + i] = n_tiles > 0 ? m[qb] * a.scale + logf(ltot) : NEG_INF;
-        }
-      }
-    }
-  }
 }
 
 // ------------------------------------------------------------------------------------------------------------------
@@ -989,31 +697,13 @@ void attn8_kernel(AttnArgs a, int32_t* ws) {
 
 typedef void (*AttnFn)(AttnArgs, int32_t*);
 
-// kernel variant (ONEREEL_ATTN_VARIANT): 3 = ring kernel with 64 queries per wavefront (the default; D = 64 runs
-// variant 0), 0 = ring kernel with 32 queries per wavefront, 1 / 2 = tile kernel with 32 / 64 queries per wavefront
-constexpr int kVariants = 4;
-
-int variant() {
-  static int v = [] {
-    const char* e = getenv("ONEREEL_ATTN_VARIANT");
-    if (!e) return 3;
-    const int x = atoi(e);
-    return x >= 0 && x < kVariants ? x : 3;
-  }();
-  return v;
-}
-
-int variant_bq(int var, int D) { return var == 2 || (var == 3 && D == 128) ? 256 : 128; }
-
-AttnFn attn_fn(int D, int var) {
-  if (D == 128)
-    return var == 0 ? attn4_kernel<128> : var == 1 ? attn_kernel<128, 1> : var == 2 ? attn_kernel<128, 2> : attn8_kernel;
-  return var == 1 ? attn_kernel<64, 1> : var == 2 ? attn_kernel<64, 2> : attn4_kernel<64>;
-}
+// head_dim 128 runs the 64-query kernel (256-query items), head_dim 64 the 32-query kernel (128-query items)
+AttnFn attn_fn(int D) { return D == 128 ? attn8_kernel : attn4_kernel<64>; }
+int item_bq(int D) { return D == 128 ? 256 : 128; }
 
 struct DevInfo {
   int cus = 0;
-  int occ[2][kVariants] = {};  // [D == 128][variant]
+  int occ[2] = {};  // resident blocks per CU, [D == 128]
 };
 
 int dev_info(DevInfo& info) {
@@ -1027,11 +717,9 @@ int dev_info(DevInfo& info) {
                            "hipDeviceGetAttribute"))
       return rc;
     for (int d = 0; d < 2; ++d)
-      for (int n = 0; n < kVariants; ++n)
-        if (int rc = check_hip(hipOccupancyMaxActiveBlocksPerMultiprocessor(&di.occ[d][n], attn_fn(d ? 128 : 64, n),
-                                                                            kThreads, 0),
-                               "hipOccupancyMaxActiveBlocksPerMultiprocessor"))
-          return rc;
+      if (int rc = check_hip(hipOccupancyMaxActiveBlocksPerMultiprocessor(&di.occ[d], attn_fn(d ? 128 : 64), kThreads, 0),
+                             "hipOccupancyMaxActiveBlocksPerMultiprocessor"))
+        return rc;
     cached = di;
     cached_dev = dev;
   }
@@ -1084,8 +772,7 @@ extern "C" int or_varlen_fwd(const or_varlen_args* p, void* stream) {
   if (x.sum_q == 0) return 0;
   DevInfo di;
   if (int rc = dev_info(di)) return rc;
-  const int var = variant();
-  const int occ = di.occ[x.D == 128][var];
+  const int occ = di.occ[x.D == 128];
   if (occ < 1) return fail_arg("or_varlen_fwd: attention kernel cannot be resident (occupancy 0)");
   const int64_t max_items = max_items_of(x.n_seg, x.sum_q, x.H);
   int64_t grid = (int64_t)di.cus * occ;
@@ -1119,8 +806,8 @@ extern "C" int or_varlen_fwd(const or_varlen_args* p, void* stream) {
   hipStream_t st = (hipStream_t)stream;
   // the planner needs key counts only: k_len when given, else the cu_k differences
   hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(kPlanThreads), 0, st, x.cu_q, x.k_len ? nullptr : x.cu_k,
-                     x.k_len, x.n_seg, x.H, variant_bq(var, x.D), (int)max_items, ws);
+                     x.k_len, x.n_seg, x.H, item_bq(x.D), (int)max_items, ws);
   if (int rc = check_hip(hipGetLastError(), "plan_kernel launch")) return rc;
-  hipLaunchKernelGGL(attn_fn(x.D, var), dim3((unsigned)grid), dim3(kThreads), 0, st, a, ws);
+  hipLaunchKernelGGL(attn_fn(x.D), dim3((unsigned)grid), dim3(kThreads), 0, st, a, ws);
   return check_hip(hipGetLastError(), "attn_kernel launch");
 }
