@@ -12,6 +12,8 @@ cpu_baseline: the oracle's packing plus torch SDPA per scope in fp32 on the host
 gemm_reference: torch.matmul (hipBLASLt) of two bf16 16384 x 16384 N(0, 1) matrices in the same run: what the
 vendor's dense bf16 GEMM reaches on this GPU with data of the same distribution. MI355X throttles its clock under
 MFMA load (power limit), and MFMA power depends on the operand bits, so this is the practical MFMA ceiling here.
+copy_reference: a device-to-device copy of the pack's size (torch copy_) with cold caches, in the same run: the
+practical ceiling of the HBM-bound pack and scatter kernels.
 
     python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--no-cpu] [--no-gemm-ref]
 """
@@ -124,6 +126,22 @@ def gemm_reference(n=16384, reps=5):
     torch.cuda.empty_cache()
     return dict(what=f'torch.matmul bf16 {n}x{n}x{n}, N(0,1) inputs (hipBLASLt), same run', ms=round(ms, 4),
                 tflops=round(tflops, 1), frac_bf16_peak=round(tflops / PEAK_BF16_TFLOPS, 4))
+
+
+def copy_reference(nbytes, reps, stream, flush):
+    """GB/s of a device-to-device copy of `nbytes` (torch copy_, the runtime's blit kernel), each call after a cache
+    eviction: what a plain read + write stream of the pack's size reaches on this GPU"""
+    import torch
+    src = torch.ones(nbytes // 2, dtype=torch.int16, device='cuda')
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    ms = time_cold(lambda: dst.copy_(src), reps, stream, flush)
+    gbs = 2 * (nbytes // 2) * 2 / ms / 1e6
+    del src, dst
+    torch.cuda.empty_cache()
+    return dict(what=f'device copy of {nbytes / 1e9:.3f} GB (torch copy_), cold caches, same run', ms=round(ms, 4),
+                gbs=round(gbs, 1), frac_hbm_peak=round(gbs / PEAK_HBM_GBS, 4))
 
 
 def cpu_baseline(heads=16, runs=3):
@@ -391,12 +409,13 @@ def main():
     # that fit the 256 MB last-level cache are then partly served from it)
     evict = torch.ones(128 << 20, dtype=torch.int32, device=dev)
     flush = lambda: evict.sum()   # reads 512 MB: the caches then hold clean lines of it, nothing to write back
+    row = H * D * 2
+    pack_bytes = 2 * 2 * plan.sum_k * row            # K and V rows read + written
     t_pack, t_pack_w = time_cold(pack, R, stream, flush), time_events(pack, R, stream)
     t_layout = time_cold(plan.build, R, stream, flush)
     t_scat, t_scat_w = time_cold(scat, R, stream, flush), time_events(scat, R, stream)
+    copy_ref = copy_reference(pack_bytes // 2, R, stream, flush) if headline else None
     del evict
-    row = H * D * 2
-    pack_bytes = 2 * 2 * plan.sum_k * row            # K and V rows read + written
     scat_bytes = 2 * plan.sum_q * row                # packed rows read + written
     kernels = {
         'attention': dict(ms=round(t_attn, 4), tflops=round(flops / t_attn / 1e9, 1),
@@ -433,6 +452,8 @@ def main():
                              unit='TFLOP/s', frac=round(flops / t_attn / 1e9 / PEAK_BF16_TFLOPS, 4), traffic=traffic,
                              kernel=f'{kname} (+ plan_kernel, one block, ~10 us)'),
                kernels=kernels)
+    if copy_ref:
+        out['copy_reference'] = copy_ref
     if headline and not args.no_gemm_ref:
         out['gemm_reference'] = gemm_reference()
     if headline and not args.no_cpu:
