@@ -190,6 +190,19 @@ def vr(lo, n=1):
     return ('v', lo, n)
 
 
+# relative cost of a side op ('valu', asm, reads, writes, trans) or ('m0' | 'dma' | 'raw', asm) when spreading the
+# side ops of a phase between its 16 MFMAs. A transcendental takes the VALU four times as long as an fp32 op, and an
+# LDS DMA issue holds the wavefront longer than an ALU op; these weights were the fastest of a sweep (trans 1.5-4,
+# dma 1-4, MFMA order): 2.7-3% faster than equal weights with S and PV MFMAs alternating by k-step.
+SIDE_COST = {'valu': 1.0, 'trans': 2.0, 'm0': 1.0, 'dma': 3.0, 'raw': 1.0}
+
+
+def side_cost(op):
+    if op[0] == 'valu':
+        return SIDE_COST['trans' if op[4] else 'valu']
+    return SIDE_COST[op[0]]
+
+
 class Kernel:
     def __init__(self, ring):
         assert ring in (4, 6, 8)
@@ -360,14 +373,14 @@ class Kernel:
                         merged.append(side[vi])
                         vi += 1
                 side = merged + side[vi:]
-            order = [(kind, qb, k) for k in ks for kind, qb in (('s', 0), ('s', 1), ('pv', 0), ('pv', 1))]
-            if ks[0] == 4:
-                # S(j+1) complete with 4 PV MFMAs still to go: the next iteration reads it without a wait
-                s_ops = [o for o in order if o[0] == 's']
-                pv_ops = [o for o in order if o[0] == 'pv']
-                order = s_ops[:4] + [x for pair in zip(s_ops[4:], pv_ops[:4]) for x in pair] + pv_ops[4:]
-            per = len(side) / 16.0
-            done, last_m0 = 0, False
+            # the eight S MFMAs of the phase (both column blocks, k-steps interleaved), then the eight PV MFMAs: S(j+1)
+            # is complete eight MFMAs before the next iteration's softmax reads it
+            order = ([('s', qb, k) for k in ks for qb in (0, 1)] +
+                     [('pv', qb, k) for k in ks for qb in (0, 1)])
+            # side ops go between the MFMAs in proportion to their issue cost (SIDE_COST)
+            cost = [side_cost(op) for op in side]
+            total = float(sum(cost))
+            done, spent, last_m0 = 0, 0.0, False
             for i, (kind, qb, k) in enumerate(order):
                 if kind == 's':
                     self.mfma_s(e, npar, qb, k)
@@ -376,9 +389,10 @@ class Kernel:
                 if rd:
                     kr_kind, kr, slot = rd.pop(0)
                     (self.read_k if kr_kind == 'k' else self.read_v)(e, kr, slot)
-                target = int(round(per * (i + 1)))
-                while done < min(target, len(side)):
+                target = total * (i + 1) / 16.0
+                while done < len(side) and spent + 0.5 * cost[done] < target:
                     last_m0 = emit_side(side[done], last_m0)
+                    spent += cost[done]
                     done += 1
             while done < len(side):
                 last_m0 = emit_side(side[done], last_m0)
