@@ -11,7 +11,7 @@
 // Here each is one pass: bf16 in, fp32 math in torch's order (no contraction), bf16 out.
 //
 // HBM-bound: LayerNorm + modulation reads and writes one bf16 row (4 B per element); the residual reads two rows
-// and writes one (6 B per element). One wavefront per row, 8 consecutive elements per lane and chunk.
+// and writes one (6 B per element). LayerNorm: one wavefront per row, 8 consecutive elements per lane and chunk.
 #include <math.h>
 
 #include "common.h"
@@ -50,66 +50,101 @@ __device__ __forceinline__ void unpack8(u32x4 v, float (&f)[8]) {
   }
 }
 
+// The per-column parameters (weight, bias, scale, shift: those given) are staged in LDS once per block; each
+// wavefront loads its next row while it reduces and writes the current one.
 template <int NCH>
 __global__ __launch_bounds__(kThreads) void layernorm_modulate_kernel(LnArgs g) {
 #pragma clang fp contract(off)
+  extern __shared__ __attribute__((aligned(16))) float prm[];
   const int lane = threadIdx.x & 63;
-  const int64_t wave = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6);
-  for (int64_t r = wave; r < g.n_rows; r += (int64_t)gridDim.x * kWaves) {
-    const uint16_t* xp = g.x + r * g.x_stride;
-    float v[NCH][8];
-    float s = 0.0f;
+  const int C = g.C;
+  const float* src[4] = {g.weight, g.bias, g.scale, g.shift};
+  int at[4];
+  int n_prm = 0;
+#pragma unroll
+  for (int a = 0; a < 4; ++a) at[a] = src[a] ? C * n_prm++ : -1;
+#pragma unroll
+  for (int a = 0; a < 4; ++a)
+    if (src[a])
+      for (int e = 4 * threadIdx.x; e < C; e += 4 * kThreads) *(f32x4*)(prm + at[a] + e) = *(const f32x4*)(src[a] + e);
+  __syncthreads();
+
+  const int64_t stride = (int64_t)gridDim.x * kWaves;
+  auto load = [&](u32x4 (&raw)[NCH], int64_t row) {
+    const uint16_t* xp = g.x + row * g.x_stride;
 #pragma unroll
     for (int i = 0; i < NCH; ++i) {
       const int e = 8 * (lane + 64 * i);
-      if (e < g.C) {
-        unpack8(*(const u32x4*)(xp + e), v[i]);
+      if (e < C) raw[i] = *(const u32x4*)(xp + e);
+    }
+  };
+  // the row's elements are unpacked from the raw bf16 words in each pass, so that only raw words stay live
+  auto process = [&](const u32x4 (&raw)[NCH], int64_t row) {
+    float s = 0.0f;
 #pragma unroll
-        for (int t = 0; t < 8; ++t) s += v[i][t];
+    for (int i = 0; i < NCH; ++i) {
+      if (8 * (lane + 64 * i) < C) {
+        float v[8];
+        unpack8(raw[i], v);
+#pragma unroll
+        for (int t = 0; t < 8; ++t) s += v[t];
       }
     }
-    const float mean = wave_sum(s) / (float)g.C;
+    const float mean = wave_sum(s) / (float)C;
     float q = 0.0f;
 #pragma unroll
     for (int i = 0; i < NCH; ++i) {
-      if (8 * (lane + 64 * i) < g.C) {
+      if (8 * (lane + 64 * i) < C) {
+        float v[8];
+        unpack8(raw[i], v);
 #pragma unroll
         for (int t = 0; t < 8; ++t) {
-          const float d = v[i][t] - mean;
+          const float d = v[t] - mean;
           q += d * d;
         }
       }
     }
-    const float rstd = 1.0f / sqrtf(wave_sum(q) / (float)g.C + g.eps);
-    uint16_t* op = g.out + r * g.out_stride;
+    const float rstd = 1.0f / sqrtf(wave_sum(q) / (float)C + g.eps);
+    uint16_t* op = g.out + row * g.out_stride;
 #pragma unroll
     for (int i = 0; i < NCH; ++i) {
       const int e = 8 * (lane + 64 * i);
-      if (e >= g.C) continue;
+      if (e >= C) continue;
       float y[8];
+      unpack8(raw[i], y);
 #pragma unroll
-      for (int t = 0; t < 8; ++t) y[t] = (v[i][t] - mean) * rstd;
-      if (g.weight) {
+      for (int t = 0; t < 8; ++t) y[t] = (y[t] - mean) * rstd;
 #pragma unroll
-        for (int t = 0; t < 8; ++t) y[t] = y[t] * g.weight[e + t];
-      }
-      if (g.bias) {
+      for (int a = 0; a < 4; ++a) {
+        if (at[a] < 0) continue;
+        const f32x4 p0 = *(const f32x4*)(prm + at[a] + e), p1 = *(const f32x4*)(prm + at[a] + e + 4);
+        const float pv[8] = {p0[0], p0[1], p0[2], p0[3], p1[0], p1[1], p1[2], p1[3]};
 #pragma unroll
-        for (int t = 0; t < 8; ++t) y[t] = y[t] + g.bias[e + t];
-      }
-      if (g.scale) {
-#pragma unroll
-        for (int t = 0; t < 8; ++t) y[t] = y[t] * (1.0f + g.scale[e + t]);
-      }
-      if (g.shift) {
-#pragma unroll
-        for (int t = 0; t < 8; ++t) y[t] = y[t] + g.shift[e + t];
+        for (int t = 0; t < 8; ++t) {
+          if (a == 0) y[t] = y[t] * pv[t];                  // weight
+          else if (a == 1) y[t] = y[t] + pv[t];             // bias
+          else if (a == 2) y[t] = y[t] * (1.0f + pv[t]);    // scale
+          else y[t] = y[t] + pv[t];                         // shift
+        }
       }
       u32x4 o;
 #pragma unroll
       for (int p = 0; p < 4; ++p) o[p] = pack2(y[2 * p], y[2 * p + 1]);
       *(u32x4*)(op + e) = o;
     }
+  };
+  // two rows in flight per wavefront: the next row loads while the current one is reduced and written
+  u32x4 ra[NCH], rb[NCH];
+  int64_t r = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6);
+  if (r < g.n_rows) load(ra, r);
+  while (r < g.n_rows) {
+    if (r + stride < g.n_rows) load(rb, r + stride);
+    process(ra, r);
+    r += stride;
+    if (r >= g.n_rows) break;
+    if (r + stride < g.n_rows) load(ra, r + stride);
+    process(rb, r);
+    r += stride;
   }
 }
 
@@ -167,6 +202,12 @@ extern "C" int or_layernorm_modulate(const void* x, void* out, int64_t n_rows, i
   if (!x || !out) return fail_arg("or_layernorm_modulate: x and out are required");
   if (!aligned16(x) || !aligned16(out) || x_row_stride % 8 || out_row_stride % 8)
     return fail_arg("or_layernorm_modulate: x and out must be 16-byte aligned rows");
+  const float* prm[4] = {weight, bias, scale, shift};
+  int n_prm = 0;
+  for (const float* a : prm) {
+    if (a && !aligned16(a)) return fail_arg("or_layernorm_modulate: weight, bias, scale and shift must be 16-byte aligned");
+    n_prm += a != nullptr;
+  }
   LnArgs g{(const uint16_t*)x, (uint16_t*)out, n_rows, x_row_stride, out_row_stride, weight, bias, scale, shift, C,
            eps};
   int64_t blocks = (n_rows + kWaves - 1) / kWaves;
@@ -174,11 +215,12 @@ extern "C" int or_layernorm_modulate(const void* x, void* out, int64_t n_rows, i
   hipStream_t st = (hipStream_t)stream;
   const int nch = (C + 511) / 512;
   const dim3 grid((unsigned)blocks), block(kThreads);
-  if (nch <= 2) hipLaunchKernelGGL(layernorm_modulate_kernel<2>, grid, block, 0, st, g);
-  else if (nch <= 4) hipLaunchKernelGGL(layernorm_modulate_kernel<4>, grid, block, 0, st, g);
-  else if (nch <= 6) hipLaunchKernelGGL(layernorm_modulate_kernel<6>, grid, block, 0, st, g);
-  else if (nch <= 8) hipLaunchKernelGGL(layernorm_modulate_kernel<8>, grid, block, 0, st, g);
-  else hipLaunchKernelGGL(layernorm_modulate_kernel<16>, grid, block, 0, st, g);
+  const size_t lds = (size_t)n_prm * C * sizeof(float);   // at most 4 x 8192 x 4 B = 128 KiB
+  if (nch <= 2) hipLaunchKernelGGL(layernorm_modulate_kernel<2>, grid, block, lds, st, g);
+  else if (nch <= 4) hipLaunchKernelGGL(layernorm_modulate_kernel<4>, grid, block, lds, st, g);
+  else if (nch <= 6) hipLaunchKernelGGL(layernorm_modulate_kernel<6>, grid, block, lds, st, g);
+  else if (nch <= 8) hipLaunchKernelGGL(layernorm_modulate_kernel<8>, grid, block, lds, st, g);
+  else hipLaunchKernelGGL(layernorm_modulate_kernel<16>, grid, block, lds, st, g);
   return check_hip(hipGetLastError(), "layernorm_modulate_kernel launch");
 }
 

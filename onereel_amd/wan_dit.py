@@ -55,7 +55,12 @@ def _rows(x: torch.Tensor):
 
 
 def _vec(t, C):
-    return None if t is None else t.reshape(C).to(torch.float32).contiguous()
+    """per-column parameter as a contiguous fp32 [C] vector at a 16-byte aligned address (the kernels read it in
+    16-byte pieces)"""
+    if t is None:
+        return None
+    v = t.reshape(C).to(torch.float32).contiguous()
+    return v if v.data_ptr() % 16 == 0 else v.clone()
 
 
 def layernorm_modulate(x, eps, weight=None, bias=None, scale=None, shift=None):
