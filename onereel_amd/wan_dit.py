@@ -95,6 +95,14 @@ class Linear:
     def __call__(self, x):
         return F.linear(x, self.weight, self.bias)
 
+    def gelu_tanh(self, x):
+        """GELU(x W^T + b, approximate='tanh') with the activation in the GEMM's epilogue (hipBLASLt through
+        torch._addmm_activation): the activation is applied to the fp32 accumulator and the [.., n_out] output is
+        written once, instead of a separate GELU pass over it"""
+        x2 = x.reshape(-1, x.shape[-1])
+        y = torch._addmm_activation(self.bias, x2, self.weight.t(), use_gelu=True)
+        return y.view(*x.shape[:-1], y.shape[-1])
+
 
 class RMSNorm:
     def __init__(self, n, eps, gen, device):
@@ -139,7 +147,7 @@ class Block:
         n = layernorm_modulate(x, eps, weight=self.norm2_w, bias=self.norm2_b)
         gated_residual_(x, p_cross(self.attn2, n, encoder_hidden_states=text))
         n = layernorm_modulate(x, eps, scale=c_scale, shift=c_shift)
-        f = self.ffn_out(F.gelu(self.ffn_in(n), approximate='tanh'))
+        f = self.ffn_out(self.ffn_in.gelu_tanh(n))
         return gated_residual_(x, f, c_gate)
 
 

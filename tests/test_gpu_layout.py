@@ -91,6 +91,19 @@ def test_layout_kernel_max_scenes():
         _check_plan(plan, sc, adjacent)
 
 
+def test_layout_kernel_more_runs_than_blocks():
+    """64 scenes of 40 frames with T = 3: over 8000 (segment, frame) runs, more than the kernel's 2048 blocks, so
+    blocks take several runs each"""
+    lengths = [40] * 64
+    F = sum(lengths)
+    case = dict(lengths=lengths, halo=2, sides='adj', extra={j: [(97 * j) % F] for j in range(0, 64, 3)}, T=3,
+                counts=[(5 * j) % 7 for j in range(64)], Le=250, scene_rope=True, rope_lengths=None)
+    for adjacent in (False, True):
+        print(f'layout 64 x 40 frames adjacent={adjacent}', flush=True)
+        plan, sc = _plans(case, adjacent)
+        _check_plan(plan, sc, adjacent)
+
+
 def _tables(case):
     F, Hh, Ww = case['table']
     assert Hh * Ww == case['T']

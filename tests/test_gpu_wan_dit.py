@@ -121,3 +121,20 @@ def test_fused_layernorm_modulate_and_residual_match_torch(S, C):
         y = x.clone()
         WD.gated_residual_(y, a, gt)
         assert torch.equal(y.view(torch.int16), ref.view(torch.int16))
+
+
+def test_linear_gelu_epilogue_matches_unfused():
+    """the feed-forward's GEMM with GELU (tanh) in the epilogue against linear then GELU: as close to the fp32
+    result as the unfused bf16 path, and within two bf16 steps of it"""
+    print('linear gelu epilogue', flush=True)
+    g = torch.Generator(device=DEV).manual_seed(11)
+    lin = WD.Linear(512, 1024, 0.05, g, DEV)
+    x = torch.randn(2, 300, 512, generator=g, device=DEV).to(torch.bfloat16)
+    got = lin.gelu_tanh(x)
+    ref = torch.nn.functional.gelu(lin(x), approximate='tanh')
+    assert got.shape == ref.shape == (2, 300, 1024) and got.dtype == torch.bfloat16
+    exact = torch.nn.functional.gelu(x.float() @ lin.weight.float().t() + lin.bias.float(), approximate='tanh')
+    err_got, err_ref = (got.float() - exact).abs().max().item(), (ref.float() - exact).abs().max().item()
+    assert err_got <= 1.5 * err_ref + 1e-3, (err_got, err_ref)
+    assert ((got.float() - ref.float()).abs() <= ref.float().abs() * 2 ** -6 + 2e-3).all()
+
