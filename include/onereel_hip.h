@@ -148,7 +148,9 @@ typedef struct or_varlen_args {
   int64_t workspace_bytes;
 } or_varlen_args;
 
-/* Bytes of device workspace or_varlen_fwd needs for this many segments, packed queries and heads. */
+/* Bytes of device workspace or_varlen_fwd needs for this many segments, packed queries and heads: the work-item
+ * queues, plus, for head_dim 128 calls with few query tiles, room for the fp32 partial results of items split by
+ * keys (up to 135 MB). */
 int64_t or_varlen_workspace_size(int32_t n_seg, int32_t sum_q, int32_t H, int32_t D);
 
 /* Replaces attention.varlen / flash_attn_varlen_func (src/onereel/attention.py:39-43), varlen_lse (:46-53) and

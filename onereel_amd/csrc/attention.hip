@@ -34,8 +34,13 @@ constexpr int kMinBQ = 128;     // smallest work-item query tile of the two kern
 constexpr int kQueues = 8;      // item queues: one per XCD
 constexpr int kQueueWords = 32; // words per queue header (head counter, item count, first item), one 128-byte line
 constexpr int kWsHeader = kQueues * kQueueWords;   // int32 words before the item list
+constexpr int kItemWords = 4;   // segment, tile << 8 | head, part | ways << 8 (0: whole item), split index
 constexpr int kPlanThreads = 1024;
 constexpr int kMaxPlanSeg = 4096;
+constexpr int kMaxSplitWays = 8;      // key parts of a split work item
+constexpr int kMaxSplitParts = 1024;  // parts of all split items of one call (sizes their partial results)
+constexpr int kSplitRows = 256;       // query rows of a split item (the 64-query kernel's tile)
+constexpr int kSplitMaxRounds = 4;    // items are split only when there are fewer than this many rounds of them
 
 struct AttnArgs {
   const uint16_t* q;
@@ -59,6 +64,11 @@ struct AttnArgs {
   int32_t sum_q, H;
   float c;              // scale * log2(e)
   float scale;
+  // key-split work items (workspace regions after the item list): per split item its segment, tile << 8 | head and
+  // part count; per part the lse [kSplitRows] and O / l in fp32 [kSplitRows][128] of its key range
+  int32_t* split_tab;
+  float* split_lse;
+  float* split_o;
 };
 
 __device__ __forceinline__ int seg_k_begin(const AttnArgs& a, int s) { return a.k_off ? a.k_off[s] : a.cu_k[s]; }
@@ -73,6 +83,12 @@ __device__ __forceinline__ int pi32(int i) { return ((i >> 2) & 1) * 16 + (i >> 
 // planner: one block. Segments sorted by key count (descending), then index. Queue q holds the heads h with
 // h % 8 == q: for every sorted segment, those heads in order, each head's query tiles in order. Queue q's header at
 // ws[32 q]: [0] head counter, [1] item count, [2] index of its first item in the item list.
+//
+// Last round: with `slots` persistent blocks, the rem = items % slots items past the last full round would leave
+// blocks idle at the end. When split_keys is set, the last items of every queue (rem in all, in proportion to the
+// queue sizes) are each cut into W parts by key blocks, W minimising ceil(rem W / slots) / W: the parts of an item
+// run on different blocks, each writes O / l and lse of its keys, and merge_kernel combines them afterwards
+// (log-sum-exp weights). ws[3] holds the number of split items, the split table their (segment, tile, head, W).
 __device__ inline int plan_upper_bound(const int* a, int n, int x) {
   int lo = 0, hi = n;
   while (lo < hi) {
@@ -85,11 +101,15 @@ __device__ inline int plan_upper_bound(const int* a, int n, int x) {
 
 __global__ __launch_bounds__(kPlanThreads) void plan_kernel(const int32_t* cu_q, const int32_t* cu_k,
                                                             const int32_t* k_len, int n_seg, int H, int bq,
-                                                            int max_items, int32_t* ws) {
+                                                            int max_items, int slots, int split_keys, int parts_cap,
+                                                            int32_t* ws) {
   __shared__ unsigned long long key[kMaxPlanSeg];
   __shared__ int off[kMaxPlanSeg + 1];
   __shared__ int part[kPlanThreads];
+  __shared__ int min_nb, split_w;
+  __shared__ int q_n[kQueues], q_s[kQueues], q_first[kQueues], q_sb[kQueues];
   const int tid = threadIdx.x;
+  if (tid == 0) min_nb = 0x7fffffff;
   int n2 = 1;
   while (n2 < n_seg) n2 <<= 1;
   for (int i = tid; i < n2; i += kPlanThreads) {
@@ -129,6 +149,7 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(const int32_t* cu_q,
       int tiles = lq > 0 ? (lq + bq - 1) / bq : 0;
       off[i] = tiles * H;
       local += tiles * H;
+      if (tiles > 0) atomicMin(&min_nb, (int)((0x7fffffffu - (unsigned)(key[i] >> 32) + 31) / 32));
     }
   }
   part[tid] = local;
@@ -156,16 +177,44 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(const int32_t* cu_q,
   // off[i] / H: query tiles of the sorted segments before i, each counted once
   const int all_tiles = total / H;
   auto heads_of = [&](int q) { return (H - q + kQueues - 1) / kQueues; };   // heads h < H with h % 8 == q
-  auto first_of = [&](int q) {
-    int b = 0;
-    for (int r = 0; r < q; ++r) b += all_tiles * heads_of(r);
-    return b;
-  };
+  if (tid == 0) {
+    int W = 1;
+    const int rem = slots > 0 ? total % slots : 0;
+    // with many rounds of items the GPU is at its power limit through the last one too, and blocks left idle at the
+    // end let the busy ones clock higher: splitting pays only for a few rounds (measured: none at 12.75 rounds,
+    // 7% at 3 rounds, 2.5-3x below one round)
+    if (split_keys && rem > 0 && total < kSplitMaxRounds * slots) {
+      float best = 1.0f;   // length of the last round in items: ceil(rem W / slots) / W
+      for (int w = 2; w <= kMaxSplitWays && w <= min_nb && (rem + kQueues) * w <= parts_cap; ++w) {
+        const float v = (float)((rem * w + slots - 1) / slots) / (float)w;
+        if (v < best - 1e-6f) {
+          best = v;
+          W = w;
+        }
+      }
+    }
+    int first = 0, sb = 0;
+    for (int q = 0; q < kQueues; ++q) {
+      const int n = all_tiles * heads_of(q);
+      const int sq = W > 1 ? min(n, (int)(((int64_t)rem * n + total - 1) / total)) : 0;
+      q_n[q] = n;
+      q_s[q] = sq;
+      q_first[q] = first;
+      q_sb[q] = sb;
+      first += n + sq * (W - 1);
+      sb += sq;
+    }
+    split_w = W;
+  }
+  __syncthreads();
+  const int W = split_w;
   if (tid < kQueues) {
     ws[kQueueWords * tid] = 0;
-    ws[kQueueWords * tid + 1] = all_tiles * heads_of(tid);
-    ws[kQueueWords * tid + 2] = first_of(tid);
+    ws[kQueueWords * tid + 1] = q_n[tid] + q_s[tid] * (W - 1);
+    ws[kQueueWords * tid + 2] = q_first[tid];
   }
+  int32_t* tab = ws + kWsHeader + (int64_t)kItemWords * (max_items + parts_cap);
+  if (tid == 0) ws[3] = W > 1 ? q_sb[kQueues - 1] + q_s[kQueues - 1] : 0;
   for (int it = tid; it < total; it += kPlanThreads) {
     int i = plan_upper_bound(off, n_seg + 1, it) - 1;
     int s = (int)(key[i] & 0xffffffffu);
@@ -174,9 +223,27 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(const int32_t* cu_q,
     int local_it = it - off[i];
     int head = local_it / tiles, t = local_it - head * tiles;
     const int q = head % kQueues;
-    const int pos = first_of(q) + (off[i] / H) * heads_of(q) + (head / kQueues) * tiles + t;
-    ws[kWsHeader + 2 * pos] = s;
-    ws[kWsHeader + 2 * pos + 1] = (t << 8) | head;
+    const int pos = (off[i] / H) * heads_of(q) + (head / kQueues) * tiles + t;   // position within queue q
+    const int keep = q_n[q] - q_s[q];
+    if (pos < keep) {
+      int32_t* e = ws + kWsHeader + kItemWords * (q_first[q] + pos);
+      e[0] = s;
+      e[1] = (t << 8) | head;
+      e[2] = 0;
+      e[3] = 0;
+    } else {
+      const int k = pos - keep, sidx = q_sb[q] + k;
+      for (int p = 0; p < W; ++p) {
+        int32_t* e = ws + kWsHeader + kItemWords * (q_first[q] + keep + k * W + p);
+        e[0] = s;
+        e[1] = (t << 8) | head;
+        e[2] = p | (W << 8);
+        e[3] = sidx;
+      }
+      tab[3 * sidx] = s;
+      tab[3 * sidx + 1] = (t << 8) | head;
+      tab[3 * sidx + 2] = W;
+    }
   }
 }
 
@@ -466,8 +533,8 @@ void attn4_kernel(AttnArgs a, int32_t* ws) {
     const int it = item_sh;
     __syncthreads();
     if (it < 0) break;
-    const int seg = ws[kWsHeader + 2 * it];
-    const int packed_ht = ws[kWsHeader + 2 * it + 1];
+    const int seg = ws[kWsHeader + kItemWords * it];
+    const int packed_ht = ws[kWsHeader + kItemWords * it + 1];
     const int head = packed_ht & 255, qt = packed_ht >> 8;
     const int q_beg = a.cu_q[seg];
     const int Lq = a.cu_q[seg + 1] - q_beg;
@@ -621,39 +688,51 @@ void attn8_kernel(AttnArgs a, int32_t* ws) {
     const int it = item_sh;
     __syncthreads();
     if (it < 0) break;
-    const int seg = ws[kWsHeader + 2 * it];
-    const int packed_ht = ws[kWsHeader + 2 * it + 1];
+    const int32_t* e = ws + kWsHeader + kItemWords * it;
+    const int seg = e[0], packed_ht = e[1], part = e[2] & 255, ways = e[2] >> 8, sidx = e[3];
     const int head = packed_ht & 255, qt = packed_ht >> 8;
     const int q_beg = a.cu_q[seg];
     const int Lq = a.cu_q[seg + 1] - q_beg;
-    const int k_beg = seg_k_begin(a, seg);
-    const int Lk = max(seg_k_len(a, seg), 0);
+    int k_beg = seg_k_begin(a, seg);
+    int Lk = max(seg_k_len(a, seg), 0);
+    if (ways > 1) {
+      // part `part` of `ways`: key blocks [nb_all part / ways, nb_all (part + 1) / ways), at least one each
+      const int nb_all = (Lk + kBKB - 1) / kBKB;
+      const int b0 = nb_all * part / ways, b1 = nb_all * (part + 1) / ways;
+      k_beg += kBKB * b0;
+      Lk = min(kBKB * b1, Lk) - kBKB * b0;
+    }
     const int q_src0 = a.seg_q_src ? a.seg_q_src[seg] : q_beg;
     const int q0 = qt * BQ + w * WQ;
     const int nb = (Lk + kBKB - 1) / kBKB;
+    float* part_o = ways > 1 ? a.split_o + (int64_t)(sidx * ways + part) * kSplitRows * D : nullptr;
 
-    // Q operands (rows past the segment repeat its last row; their outputs are not stored) and output rows
+    // Q operands and output rows. Rows past the segment get zero queries: their scores are 0 and their outputs are
+    // not stored, and zero operands cost the MFMA unit less power than real data (the GPU is power-limited here).
     bf16x8 q[2][KS];
     uint64_t op[2];
     int ok[2];
 #pragma unroll
     for (int qb = 0; qb < 2; ++qb) {
       const int i0 = q0 + qb * 32 + l32;
+      const bool live = i0 < Lq;
       const int i = min(i0, Lq - 1);
       const int64_t row = q_src0 + i;
       const uint16_t* qp = (row < a.n_q_video ? a.q + row * a.qs : a.q_text + (row - a.n_q_video) * a.qs) + head * D;
-      int rr = a.q_rope ? a.q_rope[q_beg + i] : -1;
+      int rr = live && a.q_rope ? a.q_rope[q_beg + i] : -1;
       if (rr >= a.n_rope_rows) rr = -1;
 #pragma unroll
       for (int k = 0; k < KS; ++k) {
         const int d = 16 * k + 8 * h;
-        u32x4 x = *(const u32x4*)(qp + d);
+        u32x4 x = {0u, 0u, 0u, 0u};
+        if (live) x = *(const u32x4*)(qp + d);
         if (rr >= 0) x = rotate8(x, a.cos_t, a.sin_t, (int64_t)rr * D + d, 1.0f);
         q[qb][k] = as_bf16x8(x);
       }
       uint16_t* o = (row < a.n_q_video ? a.o + row * a.os : a.o_text + (row - a.n_q_video) * a.os) + head * D + 4 * h;
-      op[qb] = (uint64_t)o;
-      ok[qb] = i0 < Lq;
+      // a split item's part writes O / l of its keys in fp32 to its partial rows instead
+      op[qb] = part_o ? (uint64_t)(part_o + (w * WQ + qb * 32 + l32) * D + 4 * h) : (uint64_t)o;
+      ok[qb] = live;
     }
     if (nb == 0) {
       // no keys: O = 0 and lse = -inf, as attn4_kernel
@@ -686,12 +765,56 @@ void attn8_kernel(AttnArgs a, int32_t* ws) {
                    [vk0] "v"(voff[0]), [vk1] "v"(voff[1]), [vv0] "v"(voff[2]), [vv1] "v"(voff[3]),
                    [sbase] "s"(sbase), [bb] "s"(bb), [kb_lo] "s"((uint32_t)kaddr), [kb_hi] "s"((uint32_t)(kaddr >> 32)),
                    [vb_lo] "s"((uint32_t)vaddr), [vb_hi] "s"((uint32_t)(vaddr >> 32)), [rem0] "s"(rem0),
-                   [op0] "v"(op[0]), [op1] "v"(op[1]), [ok0] "v"(ok[0]), [ok1] "v"(ok[1])
+                   [op0] "v"(op[0]), [op1] "v"(op[1]), [ok0] "v"(ok[0]), [ok1] "v"(ok[1]),
+                   [f32] "s"(__builtin_amdgcn_readfirstlane(ways > 1 ? 1 : 0))
                  : ONEREEL_RING64_CLOBBERS);
-    if (a.lse && h == 0) {
-      if (ok[0]) a.lse[(int64_t)head * a.sum_q + q_beg + q0 + l32] = mo0 * a.scale + logf(lo0);
-      if (ok[1]) a.lse[(int64_t)head * a.sum_q + q_beg + q0 + 32 + l32] = mo1 * a.scale + logf(lo1);
+    if (ways <= 1) {
+      if (a.lse && h == 0) {
+        if (ok[0]) a.lse[(int64_t)head * a.sum_q + q_beg + q0 + l32] = mo0 * a.scale + logf(lo0);
+        if (ok[1]) a.lse[(int64_t)head * a.sum_q + q_beg + q0 + 32 + l32] = mo1 * a.scale + logf(lo1);
+      }
+      continue;
     }
+    // a part of a split item: its lse next to its O / l (merge_kernel combines the parts)
+    float* part_lse = a.split_lse + (int64_t)(sidx * ways + part) * kSplitRows;
+    if (h == 0) {
+      if (ok[0]) part_lse[w * WQ + l32] = mo0 * a.scale + logf(lo0);
+      if (ok[1]) part_lse[w * WQ + 32 + l32] = mo1 * a.scale + logf(lo1);
+    }
+  }
+}
+
+// Merge of the key-split items, one block per split item (blocks past the count in ws[3] return): query r of the
+// item gets O = sum_p e^(lse_p - M) O_p / sum_p e^(lse_p - M) over its parts p, M = max_p lse_p, and
+// lse = M + log(sum_p e^(lse_p - M)); 4 dims per thread.
+__global__ __launch_bounds__(kThreads) void merge_kernel(AttnArgs a, const int32_t* ws) {
+  constexpr int D = 128;
+  const int sidx = blockIdx.x;
+  if (sidx >= ws[3]) return;
+  const int32_t* tab = a.split_tab + 3 * sidx;
+  const int seg = tab[0], head = tab[1] & 255, qt = tab[1] >> 8, ways = tab[2];
+  const int q_beg = a.cu_q[seg], i_beg = qt * kSplitRows;
+  const int n_rows = min(kSplitRows, a.cu_q[seg + 1] - q_beg - i_beg);
+  const int q_src0 = a.seg_q_src ? a.seg_q_src[seg] : q_beg;
+  const float* lse0 = a.split_lse + (int64_t)sidx * ways * kSplitRows;
+  const float* o0 = a.split_o + (int64_t)sidx * ways * kSplitRows * D;
+  for (int idx = threadIdx.x; idx < n_rows * (D / 4); idx += kThreads) {
+    const int r = idx / (D / 4), d = 4 * (idx % (D / 4));
+    float m = -__builtin_inff();
+    for (int p = 0; p < ways; ++p) m = fmaxf(m, lse0[p * kSplitRows + r]);
+    float wsum = 0.0f, acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int p = 0; p < ways; ++p) {
+      const float wt = expf(lse0[p * kSplitRows + r] - m);
+      const f32x4 o = *(const f32x4*)(o0 + ((int64_t)p * kSplitRows + r) * D + d);
+      wsum += wt;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) acc[t] += wt * o[t];
+    }
+    const float inv = 1.0f / wsum;
+    const int64_t row = q_src0 + i_beg + r;
+    uint16_t* out = (row < a.n_q_video ? a.o + row * a.os : a.o_text + (row - a.n_q_video) * a.os) + head * D + d;
+    *(uint2*)out = make_uint2(pack2(acc[0] * inv, acc[1] * inv), pack2(acc[2] * inv, acc[3] * inv));
+    if (a.lse && d == 0) a.lse[(int64_t)head * a.sum_q + q_beg + i_beg + r] = m + logf(wsum);
   }
 }
 
@@ -731,6 +854,36 @@ int64_t max_items_of(int32_t n_seg, int32_t sum_q, int32_t H) {
   return ((int64_t)(sum_q + kMinBQ - 1) / kMinBQ + n_seg) * H;
 }
 
+// fewest work items a call can have: every query in one segment
+int64_t min_items_of(int32_t sum_q, int32_t H, int32_t D) {
+  return (int64_t)H * ((sum_q + item_bq(D) - 1) / item_bq(D));
+}
+
+// parts of key-split items a call may hold: only the 64-query kernel (head_dim 128) splits items, and only calls that
+// can have fewer than kSplitMaxRounds rounds of items on kSplitSlots blocks get room for them
+constexpr int kSplitSlots = 256;   // persistent blocks of the 64-query kernel on MI355X (256 CUs, one block each)
+int64_t split_parts_cap(int32_t n_seg, int32_t sum_q, int32_t H, int32_t D) {
+  if (D != 128 || min_items_of(sum_q, H, D) >= (int64_t)kSplitMaxRounds * kSplitSlots) return 0;
+  const int64_t mi = max_items_of(n_seg, sum_q, H);
+  return mi * kMaxSplitWays < kMaxSplitParts ? mi * kMaxSplitWays : kMaxSplitParts;
+}
+
+// workspace layout (bytes): queue headers and the item list, the split table (3 words per split item, at most cap / 2
+// of them), then (16-byte aligned) the parts' lse and O / l
+struct WsLayout {
+  int64_t tab, lse, o, total;
+};
+
+WsLayout ws_layout(int32_t n_seg, int32_t sum_q, int32_t H, int32_t D) {
+  const int64_t mi = max_items_of(n_seg, sum_q, H), cap = split_parts_cap(n_seg, sum_q, H, D);
+  WsLayout l;
+  l.tab = (kWsHeader + kItemWords * (mi + cap)) * 4;
+  l.lse = (l.tab + (cap / 2) * 3 * 4 + 15) / 16 * 16;
+  l.o = l.lse + cap * kSplitRows * 4;
+  l.total = l.o + cap * kSplitRows * 128 * 4;
+  return l;
+}
+
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
 }  // namespace
@@ -739,9 +892,8 @@ bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 using namespace onereel;
 
 extern "C" int64_t or_varlen_workspace_size(int32_t n_seg, int32_t sum_q, int32_t H, int32_t D) {
-  (void)D;
   if (n_seg < 0 || sum_q < 0 || H < 1) return -1;
-  return (int64_t)(kWsHeader + 2 * max_items_of(n_seg, sum_q, H)) * 4;
+  return ws_layout(n_seg, sum_q, H, D).total;
 }
 
 extern "C" int or_varlen_fwd(const or_varlen_args* p, void* stream) {
@@ -775,8 +927,13 @@ extern "C" int or_varlen_fwd(const or_varlen_args* p, void* stream) {
   const int occ = di.occ[x.D == 128];
   if (occ < 1) return fail_arg("or_varlen_fwd: attention kernel cannot be resident (occupancy 0)");
   const int64_t max_items = max_items_of(x.n_seg, x.sum_q, x.H);
+  // persistent blocks: one per resident slot, but no more than the work entries (items, or their key parts when
+  // the planner may split items: only when even the fewest items the call can have come in few rounds)
   int64_t grid = (int64_t)di.cus * occ;
-  if (grid > max_items) grid = max_items;
+  const int64_t cap = split_parts_cap(x.n_seg, x.sum_q, x.H, x.D);
+  const bool may_split = cap > 0 && min_items_of(x.sum_q, x.H, x.D) < kSplitMaxRounds * grid;
+  const int64_t entries = max_items * (may_split ? kMaxSplitWays : 1);
+  if (grid > entries) grid = entries;
   AttnArgs a;
   a.q = (const uint16_t*)x.q;
   a.q_text = (const uint16_t*)(x.q_text ? x.q_text : x.q);
@@ -803,11 +960,23 @@ extern "C" int or_varlen_fwd(const or_varlen_args* p, void* stream) {
   a.scale = x.scale;
   a.c = x.scale * 1.4426950408889634f;
   int32_t* ws = (int32_t*)x.workspace;
+  const WsLayout wl = ws_layout(x.n_seg, x.sum_q, x.H, x.D);
+  a.split_tab = (int32_t*)((char*)x.workspace + wl.tab);
+  a.split_lse = (float*)((char*)x.workspace + wl.lse);
+  a.split_o = (float*)((char*)x.workspace + wl.o);
   hipStream_t st = (hipStream_t)stream;
   // the planner needs key counts only: k_len when given, else the cu_k differences
   hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(kPlanThreads), 0, st, x.cu_q, x.k_len ? nullptr : x.cu_k,
-                     x.k_len, x.n_seg, x.H, item_bq(x.D), (int)max_items, ws);
+                     x.k_len, x.n_seg, x.H, item_bq(x.D), (int)max_items, (int)grid, may_split ? 1 : 0,
+                     (int)cap, ws);
   if (int rc = check_hip(hipGetLastError(), "plan_kernel launch")) return rc;
   hipLaunchKernelGGL(attn_fn(x.D), dim3((unsigned)grid), dim3(kThreads), 0, st, a, ws);
-  return check_hip(hipGetLastError(), "attn_kernel launch");
+  if (int rc = check_hip(hipGetLastError(), "attn_kernel launch")) return rc;
+  // at most rem + 8 < grid + 8 items are split (the planner's rule), and at most cap / 2
+  const int64_t n_merge = cap / 2 < grid + kQueues ? cap / 2 : grid + kQueues;
+  if (may_split && n_merge > 0) {
+    hipLaunchKernelGGL(merge_kernel, dim3((unsigned)n_merge), dim3(kThreads), 0, st, a, ws);
+    return check_hip(hipGetLastError(), "merge_kernel launch");
+  }
+  return 0;
 }

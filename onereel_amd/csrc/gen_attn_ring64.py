@@ -485,8 +485,9 @@ class Kernel:
         return regs
 
     def store_block(self):
-        """O / l as bf16 to the output rows (rows past the segment masked off); 16 wait states after the last MFMA.
-        Temporaries live in the S registers, which are dead here."""
+        """O / l to the output rows (rows past the segment masked off): bf16, or fp32 when %[f32] is non-zero (the
+        partial results of a work item split by keys); 16 wait states after the last MFMA. Temporaries live in the
+        S registers, which are dead here."""
         e = Emitter()
         e.label('.Lstore_%=')
         e.nop_to(16)
@@ -503,17 +504,31 @@ class Kernel:
             e.valu(f'v_rcp_f32_e32 v{x[2]}, v{x[0]}', [v(x[0])], [v(x[2])], trans=True)
             e.valu(f'v_cmp_ne_u32_e32 vcc, 0, %[ok{qb}]', [], [])
             e.raw(f's_and_saveexec_b64 s[{SEX}:{SEX + 1}], vcc')
-            for db in range(4):
-                for g in range(4):
-                    acc = 64 * qb + 16 * db + 4 * g
-                    for i in range(4):
-                        e.valu(f'v_accvgpr_read_b32 v{x[3 + i]}, a{acc + i}', [], [v(x[3 + i])])
-                    for i in range(4):
-                        e.valu(f'v_mul_f32_e32 v{x[3 + i]}, v{x[3 + i]}, v{x[2]}', [v(x[3 + i]), v(x[2])],
-                               [v(x[3 + i])])
-                    e.valu(f'v_cvt_pk_bf16_f32 v{x[3]}, v{x[3]}, v{x[4]}', [v(x[3]), v(x[4])], [v(x[3])])
-                    e.valu(f'v_cvt_pk_bf16_f32 v{x[4]}, v{x[5]}, v{x[6]}', [v(x[5]), v(x[6])], [v(x[4])])
-                    e.raw(f'global_store_dwordx2 %[op{qb}], v[{x[3]}:{x[4]}], off offset:{db * 64 + 16 * g}')
+            e.raw('s_cmp_eq_u32 %[f32], 0')
+            e.raw(f's_cbranch_scc0 .Lst32_{qb}_%=')
+            for f32 in (False, True):
+                if f32:
+                    e.raw(f's_branch .Lstdone_{qb}_%=')
+                    e.label(f'.Lst32_{qb}_%=')
+                for db in range(4):
+                    for g in range(4):
+                        acc = 64 * qb + 16 * db + 4 * g
+                        for i in range(4):
+                            e.valu(f'v_accvgpr_read_b32 v{x[3 + i]}, a{acc + i}', [], [v(x[3 + i])])
+                        for i in range(4):
+                            e.valu(f'v_mul_f32_e32 v{x[3 + i]}, v{x[3 + i]}, v{x[2]}', [v(x[3 + i]), v(x[2])],
+                                   [v(x[3 + i])])
+                        if f32:
+                            # lane half h: dims 32 db + 8 g + 4 h .. + 3 of its query, 16 bytes. A store of more
+                            # than 8 bytes reads its data registers after issue: one wait state before they are
+                            # rewritten (gfx9 VMEM store-data hazard)
+                            e.raw(f'global_store_dwordx4 %[op{qb}], v[{x[3]}:{x[6]}], off offset:{db * 128 + 32 * g}')
+                            e.raw('s_nop 0')
+                        else:
+                            e.valu(f'v_cvt_pk_bf16_f32 v{x[3]}, v{x[3]}, v{x[4]}', [v(x[3]), v(x[4])], [v(x[3])])
+                            e.valu(f'v_cvt_pk_bf16_f32 v{x[4]}, v{x[5]}, v{x[6]}', [v(x[5]), v(x[6])], [v(x[4])])
+                            e.raw(f'global_store_dwordx2 %[op{qb}], v[{x[3]}:{x[4]}], off offset:{db * 64 + 16 * g}')
+            e.label(f'.Lstdone_{qb}_%=')
             e.raw(f's_mov_b64 exec, s[{SEX}:{SEX + 1}]')
         return e.lines
 

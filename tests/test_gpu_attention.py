@@ -67,6 +67,46 @@ def test_varlen_running_max_moves(growth, D):
         assert (lse[:, cq[s]:cq[s + 1]].cpu() - lref).abs().max() < 2e-3
 
 
+@pytest.mark.parametrize('lq,lk,H', [([1000], [20000], 4), ([300, 7], [5000, 3000], 3),
+                                     ([40, 0, 600], [9000, 50, 2500], 2)])
+def test_varlen_key_split_of_few_items(lq, lk, H):
+    """few work items over long key ranges: the planner cuts each item into up to 8 parts by key blocks (one part per
+    block) and merge_kernel combines the parts by their lse. O (O-only and lse calls) and lse against the fp32
+    oracle; the workspace's split count shows that the items were split."""
+    D = 128
+    print(f'key split lq={lq} lk={lk} H={H}', flush=True)
+    q, k, v, cq, ck = _segments_case(lq, lk, H, D, 51)
+    dq, dk, dv = q.to(DEV), k.to(DEV), v.to(DEV)
+    tq, tk = torch.tensor(cq, dtype=torch.int32, device=DEV), torch.tensor(ck, dtype=torch.int32, device=DEV)
+    ref = OA.packed_attention(q, k, v, cq, ck)
+    ws = torch.zeros(int(L.lib().or_varlen_workspace_size(len(lq), sum(lq), H, D)), dtype=torch.uint8, device=DEV)
+    o = scene.varlen(dq, dk, dv, tq, tk, max(lq), max(lk), workspace=ws)
+    assert_close(o.cpu(), ref, what='key-split varlen')
+    assert int(ws.view(torch.int32)[3]) > 0
+    o, lse = A.varlen_lse(dq, dk, dv, tq, tk, max(lq), max(lk))
+    assert_close(o.cpu(), ref, what='key-split varlen_lse')
+    for s in range(len(lq)):
+        if lq[s] == 0:
+            continue
+        qs, ks = q[cq[s]:cq[s + 1]].float(), k[ck[s]:ck[s + 1]].float()
+        lref = torch.logsumexp(torch.einsum('qhd,khd->hqk', qs, ks) * D ** -0.5, -1)
+        assert (lse[:, cq[s]:cq[s + 1]].cpu() - lref).abs().max() < 2e-3
+
+
+def test_key_split_of_overlapping_ranges():
+    """Wan-style in-place key ranges with few work items (3 scenes x 400 tokens per frame, 2 heads): the split parts
+    take their key blocks from inside each scene's range"""
+    H, D, T = 2, 128, 400
+    lay = OL.SceneLayout([3, 4, 2], halo=2, sides='next')
+    S = lay.n_frames * T
+    qq, kk, vv = (rand_bf16((S, H, D), s) for s in (61, 62, 63))
+    qr, kr = OL.wan_ranges(lay, T)
+    o = A.overlapping_ranges(qq.to(DEV), kk.to(DEV), vv.to(DEV), qr, kr).cpu()
+    cq = [0] + [b for _, b in qr]
+    ref = OA.packed_attention(qq, kk, vv, cq, None, k_off=[a for a, _ in kr], k_len=[b - a for a, b in kr])
+    assert_close(o, ref, what='key-split overlapping_ranges')
+
+
 def test_varlen_lse_and_packed_api():
     lq, lk, H, D = [70, 3, 129], [90, 300, 5], 2, 128
     q, k, v, cq, ck = _segments_case(lq, lk, H, D, 21)
