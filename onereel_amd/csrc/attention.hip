@@ -285,8 +285,8 @@ __device__ __forceinline__ float pair_sum(float x) {
 }
 
 // ------------------------------------------------------------------------------------------------------------------
-// Ring kernel (the default): software-pipelined over blocks of 32 keys. K and V blocks stream through two rings of
-// four LDS slots each, filled by buffer loads straight into LDS (LDS DMA) three iterations ahead; rows past a
+// Ring kernel with 32 queries per wavefront (attn4_kernel, run for head_dim 64): software-pipelined over blocks of
+// 32 keys. K and V blocks stream through two rings of four LDS slots each, filled by buffer loads straight into LDS (LDS DMA) three iterations ahead; rows past a
 // segment's end read as zeros. Iteration j of a wavefront runs the softmax of block j on the VALU while the MFMA unit
 // computes S of block j + 1 (QK^T) and O += V P^T of block j - 1, so the exponentials overlap the matrix work inside
 // one wavefront as well as across the two wavefronts that share a SIMD.
