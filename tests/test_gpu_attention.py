@@ -93,6 +93,37 @@ def test_varlen_key_split_of_few_items(lq, lk, H):
         assert (lse[:, cq[s]:cq[s + 1]].cpu() - lref).abs().max() < 2e-3
 
 
+def test_varlen_random_shapes():
+    """random segment counts, query / key lengths (empty segments included), head counts and head dims, O-only and
+    with lse, against the fp32 oracle: covers whole items and key-split items with every part count the planner
+    picks (the shortest segment bounds it)"""
+    rng = np.random.default_rng(2024)
+    for case in range(12):
+        n = int(rng.integers(1, 6))
+        lq = rng.integers(0, 300, n).tolist()
+        if sum(lq) == 0:
+            lq[0] = 1
+        lk = rng.integers(1, 2000, n).tolist()
+        H, D = int(rng.integers(1, 7)), int(rng.choice([64, 128]))
+        with_lse = bool(rng.integers(2))
+        print(f'random varlen case {case}: lq={lq} lk={lk} H={H} D={D} lse={with_lse}', flush=True)
+        q, k, v, cq, ck = _segments_case(lq, lk, H, D, 100 + case)
+        args = (q.to(DEV), k.to(DEV), v.to(DEV), torch.tensor(cq, dtype=torch.int32, device=DEV),
+                torch.tensor(ck, dtype=torch.int32, device=DEV), max(lq), max(lk))
+        ref = OA.packed_attention(q, k, v, cq, ck)
+        if not with_lse:
+            assert_close(A.varlen(*args).cpu(), ref, what=f'random varlen case {case}')
+            continue
+        o, lse = A.varlen_lse(*args)
+        assert_close(o.cpu(), ref, what=f'random varlen_lse case {case}')
+        for s in range(n):
+            if lq[s] == 0:
+                continue
+            qs, ks = q[cq[s]:cq[s + 1]].float(), k[ck[s]:ck[s + 1]].float()
+            lref = torch.logsumexp(torch.einsum('qhd,khd->hqk', qs, ks) * D ** -0.5, -1)
+            assert (lse[:, cq[s]:cq[s + 1]].cpu() - lref).abs().max() < 2e-3
+
+
 def test_key_split_of_overlapping_ranges():
     """Wan-style in-place key ranges with few work items (3 scenes x 400 tokens per frame, 2 heads): the split parts
     take their key blocks from inside each scene's range"""
