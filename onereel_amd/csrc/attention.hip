@@ -766,7 +766,8 @@ void attn8_kernel(AttnArgs a, int32_t* ws) {
                    [sbase] "s"(sbase), [bb] "s"(bb), [kb_lo] "s"((uint32_t)kaddr), [kb_hi] "s"((uint32_t)(kaddr >> 32)),
                    [vb_lo] "s"((uint32_t)vaddr), [vb_hi] "s"((uint32_t)(vaddr >> 32)), [rem0] "s"(rem0),
                    [op0] "v"(op[0]), [op1] "v"(op[1]), [ok0] "v"(ok[0]), [ok1] "v"(ok[1]),
-                   [f32] "s"(__builtin_amdgcn_readfirstlane(ways > 1 ? 1 : 0))
+                   [f32] "s"(__builtin_amdgcn_readfirstlane(ways > 1 ? 1 : 0)),
+                   [dead] "s"(__builtin_amdgcn_readfirstlane(q0 >= Lq ? 1 : 0))
                  : ONEREEL_RING64_CLOBBERS);
     if (ways <= 1) {
       if (a.lse && h == 0) {

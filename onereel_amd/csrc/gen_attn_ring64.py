@@ -566,6 +566,9 @@ class Kernel:
             self.dma_v(e, b)
         e.raw(f's_waitcnt vmcnt({4 * (R - 2)})')     # K0, K1 and V(-1) landed
         e.raw('s_barrier')
+        # a wavefront whose 64 queries all lie past the segment only keeps up the block's K/V stream
+        e.raw('s_cmp_eq_u32 %[dead], 0')
+        e.raw('s_cbranch_scc0 .Ldead_%=')
         # S(0) = K(0) Q^T (no offset yet); the operands of iteration 0's steps 0..3 (K(1), V(-1)) are read behind it
         for k in range(8):
             self.read_k(e, k, 0)
@@ -590,6 +593,23 @@ class Kernel:
                 e.valu(f'v_sub_f32_e32 v{S(0, qb, r)}, v{S(0, qb, r)}, v{M0 + qb}', [v(S(0, qb, r)), v(M0 + qb)],
                        [v(S(0, qb, r))])
                 e.valu(f'v_sub_f32_e32 v{MCV(qb) + r}, 0, v{M0 + qb}', [v(M0 + qb)], [v(MCV(qb) + r)])
+
+    def dead_loop(self):
+        """the key loop of a wavefront without live queries: per iteration only the barrier and its share of the
+        K/V refill, the same as a body's, so that the block's barriers and LDS DMA stay in step; no MFMA, softmax or
+        LDS read. Exits to the end of the asm block once every DMA has landed (no output is written)."""
+        R = self.R
+        lines = ['.Ldead_%=:']
+        for J in range(R):
+            lines.append(f's_waitcnt vmcnt({4 * (R - 3)})')
+            lines.append('s_barrier')
+            for op in self.dma_ops(J):
+                lines.append(op[1])
+                if op[0] == 'm0':
+                    lines.append('s_nop 0')          # an SALU write of M0 and the LDS DMA reading it
+            lines += [f's_add_u32 s{SJ}, s{SJ}, 1', f's_cmp_ge_u32 s{SJ}, %[nb]', 's_cbranch_scc1 .Ldeadexit_%=']
+        lines += ['s_branch .Ldead_%=', '.Ldeadexit_%=:', 's_waitcnt vmcnt(0)', 's_branch .Ldone_%=']
+        return lines
 
     def generate(self):
         R = self.R
@@ -626,7 +646,9 @@ class Kernel:
             lines += self.rescale_block(par)
         for par in range(2):
             lines += self.epilogue(par)
+        lines += self.dead_loop()
         lines += self.store_block()
+        lines.append('.Ldone_%=:')
         return lines
 
 
