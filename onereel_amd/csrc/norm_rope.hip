@@ -44,53 +44,80 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+// One row's inputs: its bf16 words, and this lane's cos / sin entries (d0 = 8 lane mod D, pairs 2p, 2p + 1).
 template <int NCH>
-__device__ __forceinline__ void norm_rope_row(const NormRopeArgs& g, int which, int64_t r, int lane) {
+struct RowIn {
+  u32x4 x[NCH];
+  float c[4], s[4];
+};
+
+template <int NCH>
+__device__ __forceinline__ void load_row(const NormRopeArgs& g, int which, int64_t r, int lane, RowIn<NCH>& in) {
   const uint16_t* xp = g.x[which] + r * g.x_stride[which];
-  u32x4 v[NCH];
+#pragma unroll
+  for (int i = 0; i < NCH; ++i) in.x[i] = *(const u32x4*)(xp + 8 * (lane + 64 * i));
+  const int rr = g.rope_row ? g.rope_row[r] : (int)r;
+  const int d0 = (8 * lane) % g.D;
+  const bool rot = rr >= 0 && rr < g.n_rope_rows;   // rows outside the table (or no table) are not rotated
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    in.c[p] = rot ? g.cos_t[(int64_t)rr * g.D + d0 + 2 * p] : 1.0f;
+    in.s[p] = rot ? g.sin_t[(int64_t)rr * g.D + d0 + 2 * p + 1] : 0.0f;
+  }
+}
+
+template <int NCH>
+__device__ __forceinline__ void norm_rope_row(const NormRopeArgs& g, int which, int64_t r, int lane,
+                                              const RowIn<NCH>& in, const uint16_t* w) {
   float ss = 0.0f;
 #pragma unroll
   for (int i = 0; i < NCH; ++i) {
-    v[i] = *(const u32x4*)(xp + 8 * (lane + 64 * i));
 #pragma unroll
     for (int p = 0; p < 4; ++p) {
-      const float a = bf2f((uint16_t)(v[i][p] & 0xffffu)), b = bf2f((uint16_t)(v[i][p] >> 16));
+      const float a = bf2f((uint16_t)(in.x[i][p] & 0xffffu)), b = bf2f((uint16_t)(in.x[i][p] >> 16));
       ss += a * a + b * b;
     }
   }
   const float inv = 1.0f / sqrtf(wave_sum(ss) / (float)g.C + g.eps);
-  int rr = g.rope_row ? g.rope_row[r] : (int)r;
-  const int d0 = (8 * lane) % g.D;
-  float c[4], s[4];
-  const bool rot = rr >= 0 && rr < g.n_rope_rows;
-#pragma unroll
-  for (int p = 0; p < 4; ++p) {
-    c[p] = rot ? g.cos_t[(int64_t)rr * g.D + d0 + 2 * p] : 1.0f;
-    s[p] = rot ? g.sin_t[(int64_t)rr * g.D + d0 + 2 * p + 1] : 0.0f;
-  }
   uint16_t* op = g.out[which] + r * g.out_stride[which];
 #pragma unroll
   for (int i = 0; i < NCH; ++i) {
     const int e = 8 * (lane + 64 * i);
-    const u32x4 wv = *(const u32x4*)(g.w[which] + e);
+    const u32x4 wv = *(const u32x4*)(w + e);
     u32x4 o;
 #pragma unroll
     for (int p = 0; p < 4; ++p) {
 #pragma clang fp contract(off)
-      const float y0 = bf2f((uint16_t)(v[i][p] & 0xffffu)) * inv * bf2f((uint16_t)(wv[p] & 0xffffu));
-      const float y1 = bf2f((uint16_t)(v[i][p] >> 16)) * inv * bf2f((uint16_t)(wv[p] >> 16));
-      o[p] = pack2(y0 * c[p] - y1 * s[p], y0 * s[p] + y1 * c[p]);
+      const float y0 = bf2f((uint16_t)(in.x[i][p] & 0xffffu)) * inv * bf2f((uint16_t)(wv[p] & 0xffffu));
+      const float y1 = bf2f((uint16_t)(in.x[i][p] >> 16)) * inv * bf2f((uint16_t)(wv[p] >> 16));
+      o[p] = pack2(y0 * in.c[p] - y1 * in.s[p], y0 * in.s[p] + y1 * in.c[p]);
     }
     *(u32x4*)(op + e) = o;
   }
 }
 
+// blockIdx.y picks q or k. The block stages its weight row in LDS; each wavefront loads its next row while it
+// normalises and writes the current one.
 template <int NCH>
 __global__ __launch_bounds__(kThreads) void norm_rope_kernel(NormRopeArgs g) {
+  __shared__ __attribute__((aligned(16))) uint16_t wl[64 * 8 * NCH];
   const int lane = threadIdx.x & 63;
   const int which = blockIdx.y;
-  const int64_t wave = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6);
-  for (int64_t r = wave; r < g.n_rows; r += (int64_t)gridDim.x * kWaves) norm_rope_row<NCH>(g, which, r, lane);
+  for (int e = 8 * threadIdx.x; e < g.C; e += 8 * kThreads) *(u32x4*)(wl + e) = *(const u32x4*)(g.w[which] + e);
+  __syncthreads();
+  const int64_t stride = (int64_t)gridDim.x * kWaves;
+  int64_t r = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6);
+  RowIn<NCH> a, b;
+  if (r < g.n_rows) load_row<NCH>(g, which, r, lane, a);
+  while (r < g.n_rows) {
+    if (r + stride < g.n_rows) load_row<NCH>(g, which, r + stride, lane, b);
+    norm_rope_row<NCH>(g, which, r, lane, a, wl);
+    r += stride;
+    if (r >= g.n_rows) break;
+    if (r + stride < g.n_rows) load_row<NCH>(g, which, r + stride, lane, a);
+    norm_rope_row<NCH>(g, which, r, lane, b, wl);
+    r += stride;
+  }
 }
 
 }  // namespace
@@ -108,8 +135,10 @@ extern "C" int or_rmsnorm_rope(const void* q, const void* k, const void* wq, con
     return fail_arg("or_rmsnorm_rope: need D a multiple of 8 dividing 512 and C a multiple of 512 up to %d "
                     "(C=%d D=%d)", 64 * 8 * kMaxChunks, C, D);
   if (n_rows == 0) return 0;
-  if (!q || !wq || !q_out || !cos_table || !sin_table || n_rope_rows < 1)
-    return fail_arg("or_rmsnorm_rope: q, wq, q_out and the cos / sin tables are required");
+  if (!q || !wq || !q_out) return fail_arg("or_rmsnorm_rope: q, wq and q_out are required");
+  if (n_rope_rows > 0 && (!cos_table || !sin_table))
+    return fail_arg("or_rmsnorm_rope: n_rope_rows > 0 needs the cos / sin tables");
+  if (n_rope_rows < 0) return fail_arg("or_rmsnorm_rope: n_rope_rows < 0");
   if (k && (!wk || !k_out)) return fail_arg("or_rmsnorm_rope: k needs wk and k_out");
   if (q_row_stride < C || qo_row_stride < C || (k && (k_row_stride < C || ko_row_stride < C)))
     return fail_arg("or_rmsnorm_rope: row strides must cover C elements");

@@ -110,7 +110,7 @@ class RMSNorm:
         self.eps = eps
 
     def __call__(self, x):
-        return F.rms_norm(x, (x.shape[-1],), self.weight, self.eps)
+        return wan.rms_norm(x, self.weight, self.eps)
 
 
 class Attention:

@@ -138,3 +138,19 @@ def test_linear_gelu_epilogue_matches_unfused():
     assert err_got <= 1.5 * err_ref + 1e-3, (err_got, err_ref)
     assert ((got.float() - ref.float()).abs() <= ref.float().abs() * 2 ** -6 + 2e-3).all()
 
+
+@pytest.mark.parametrize('S,C', [(300, 3072), (17, 512)])
+def test_rms_norm_matches_torch(S, C):
+    """the cross-attention's RMSNorm (or_rmsnorm_rope without tables) against torch's rms_norm: within one bf16 step
+    and > 99% bit-equal"""
+    print(f'rms_norm S={S} C={C}', flush=True)
+    from onereel_amd import wan
+    g = torch.Generator(device=DEV).manual_seed(C + S)
+    x = (torch.randn(S, C, generator=g, device=DEV) * 3).to(torch.bfloat16)
+    w = (1 + 0.1 * torch.randn(C, generator=g, device=DEV)).to(torch.bfloat16)
+    got = wan.rms_norm(x, w, 1e-6)
+    ref = torch.nn.functional.rms_norm(x.float(), (C,), w.float(), 1e-6).to(torch.bfloat16)
+    diff = (got.float() - ref.float()).abs()
+    assert (diff <= ref.float().abs() * 2 ** -7 + 1e-6).all(), diff.max()
+    assert (got.view(torch.int16) == ref.view(torch.int16)).float().mean() > 0.99
+
