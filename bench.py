@@ -251,6 +251,85 @@ def run_dit(args):
     print(json.dumps(out), flush=True)
 
 
+def run_lse_merge(args):
+    """the log-sum-exp merge of a partial attention result into a running one at the HunyuanVideo-1.5 480p layer's
+    packed shape (51 392 rows x 16 heads x 128): o fp32 read and written, o_s bf16 read, lse / lse_s fp32; each call
+    timed alone with the caches evicted before it"""
+    import torch
+    from onereel_amd import attention as A
+    dev = torch.device('cuda:0')
+    torch.cuda.set_device(dev)
+    N, H_, D_ = 51392, 16, 128
+    g = torch.Generator(device=dev).manual_seed(0)
+    o = torch.randn(N, H_, D_, generator=g, device=dev)
+    o_s = torch.randn(N, H_, D_, generator=g, device=dev).to(torch.bfloat16)
+    lse = torch.randn(H_, N, generator=g, device=dev) + 9.0
+    lse_s = torch.randn(H_, N, generator=g, device=dev) + 9.0
+    st = torch.cuda.current_stream(dev)
+    evict = torch.ones(128 << 20, dtype=torch.int32, device=dev)
+    flush = lambda: evict.sum()
+    A.merge_lse(o, lse, o_s, lse_s)
+    torch.cuda.synchronize()
+    t = time_cold(lambda: A.merge_lse(o, lse, o_s, lse_s), args.kernel_reps, st, flush)
+    nbytes = N * H_ * D_ * (4 + 4 + 2) + N * H_ * 4 * 3
+    gbs = nbytes / t / 1e6
+    out = dict(metric='LSE merge of a partial attention result: GB/s and % of HBM peak', value=round(gbs, 1),
+               unit='GB/s', n_gpus=1, steps=args.kernel_reps, warmup=1, ms_per_step=round(t, 4), higher_is_better=True,
+               scaling='weak', vs_baseline=None, dtype='fp32', data='synthetic',
+               config=dict(workload='lse-merge-hunyuan15-480p-packed-rows', rows=N, heads=H_, head_dim=D_),
+               roofline=dict(bound='hbm', achieved=round(gbs, 1), peak=PEAK_HBM_GBS, unit='GB/s',
+                             frac=round(gbs / PEAK_HBM_GBS, 4), traffic=None, kernel='lse_merge_kernel + lse_update_kernel'),
+               bytes=nbytes, timing='cold caches, single calls')
+    print(json.dumps(out), flush=True)
+
+
+def run_bounded_memory(args):
+    """the head-major bounded memory (per-head boundary-frame representatives, M = 128) at the HunyuanVideo-1.5 480p
+    layer's shape: one layer call = representative choice (warm-started k-means) + per-head index arrays + pack +
+    single-head varlen + scatter, timed in steady state (after the first call, whose k-means runs 50 iterations)"""
+    import torch
+    import torch.nn.functional as F
+    from onereel_amd.layout import SceneLayout
+    from onereel_amd.memory import BoundaryMemory, MemoryAttention, frame_plan
+    dev = torch.device('cuda:0')
+    torch.cuda.set_device(dev)
+    lay = SceneLayout(LENGTHS, halo=0)
+    S, Le = lay.n_frames * T, sum(COUNTS)
+    g = torch.Generator(device=dev).manual_seed(0)
+    q, k, v = (torch.randn(S + Le, H, D, generator=g, device=dev).to(torch.bfloat16) for _ in range(3))
+    tr, c = [], 0
+    for n in COUNTS:
+        tr.append((c, c + n))
+        c += n
+    plan = frame_plan(lay, T, torch.arange(S), S, [(j, lo * T, hi * T) for j, (lo, hi) in enumerate(lay.ranges)], tr,
+                      set(range(lay.n_scenes)), S, dev)
+    M = 128
+    mem = MemoryAttention(BoundaryMemory(M))
+    key = ('layer', True)
+    st = torch.cuda.current_stream(dev)
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record(st)
+    mem(key, q, k, v, plan)
+    b.record(st)
+    b.synchronize()
+    t_first = a.elapsed_time(b)
+    reps = max(3, args.kernel_reps)
+    t_call = time_events(lambda: mem(key, q, k, v, plan), reps, st)
+    # useful FLOPs of the attention: each piece and head reads its local keys plus the foreign representatives
+    rep, valid = BoundaryMemory(M).select(key, k[plan.cand])
+    rep_scene = plan.owner[rep]
+    foreign = valid[:, None, :] & (rep_scene[:, None, :] != plan.scene[None, :, None]) & plan.mem[None, :, None]
+    lk = (plan.lens[None] + foreign.sum(-1)).double()
+    flops = float((4.0 * plan.qlen[None].double() * lk * D).sum())
+    out = dict(metric='bounded memory layer: ms per call and attention TFLOP/s', value=round(t_call, 4), unit='ms',
+               n_gpus=1, steps=reps, warmup=1, ms_per_step=round(t_call, 4), higher_is_better=False, scaling='weak',
+               vs_baseline=None, dtype='bf16', data='synthetic',
+               config=dict(workload='bounded-memory-hunyuan15-480p-4scene', scenes=len(LENGTHS), tokens_per_frame=T,
+                           text_per_scene=COUNTS, heads=H, head_dim=D, representatives=M),
+               first_call_ms=round(t_first, 4), useful_flop=flops, tflops=round(flops / t_call / 1e9, 1))
+    print(json.dumps(out), flush=True)
+
+
 def run_frame_memory(args):
     """frame memory at the DiT-step shape: pooling of one observed layer (16 scenes x 15 frames x 880 tokens x 3072
     bf16, 1.3 GB) per frame, and the k-means choice of 4 representatives among the 240 frames; each call timed alone
@@ -310,13 +389,15 @@ def main():
     ap.add_argument('--kernel-reps', type=int, default=10)
     ap.add_argument('--no-gemm-ref', action='store_true', help='skip the bf16 GEMM reference')
     ap.add_argument('--workload', default='hunyuan480p',
-                    choices=['hunyuan480p', 'wan704'] + UNEVEN + ['wan-dit-step', 'frame-memory'],
+                    choices=['hunyuan480p', 'wan704'] + UNEVEN + ['wan-dit-step', 'frame-memory', 'lse-merge',
+                                                                   'bounded-memory'],
                     help='hunyuan480p (default, the headline): the HunyuanVideo-1.5 480p 4-scene layer; wan704 and '
                          'unevenK: the same layer at the Wan2.2 704x1280 shape and at the K-scene uneven sweep points '
                          '(K = 2, 4, 8, 12); wan-dit-step: '
                          'one forward of a random-init Wan2.2-TI2V-5B-shaped DiT over 16 scenes x 15 frames x 880 '
                          'tokens with frame memory 4 (end-to-end ms per step); frame-memory: the pooling and '
-                         'selection kernels at that shape')
+                         'selection kernels at that shape; lse-merge: the log-sum-exp merge at the 480p layer shape; '
+                         'bounded-memory: the head-major bounded memory layer at that shape')
     ap.add_argument('--once', action='store_true',
                     help='profiling mode: a 1 GiB device copy (counter calibration), then the layout, pack-gather, '
                          'attention and scatter kernels once each, then one bf16 16384^3 torch.matmul (the GEMM '
@@ -331,6 +412,10 @@ def main():
         return run_dit(args)
     if args.workload == 'frame-memory':
         return run_frame_memory(args)
+    if args.workload == 'lse-merge':
+        return run_lse_merge(args)
+    if args.workload == 'bounded-memory':
+        return run_bounded_memory(args)
     args.steps = 20 if args.steps is None else args.steps
     args.warmup = 3 if args.warmup is None else args.warmup
     W = workload(args.workload)
