@@ -405,7 +405,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get('WORLD_SIZE', '1')) != 1:
         print('bench.py measures the single-GPU scene-attention path only: run it with --gpus 1 '
-              '(the multi-GPU K/V gathering / Ulysses paths are not part of this build)', file=sys.stderr)
+              '(the multi-GPU K/V gathering and Ulysses paths are not implemented)', file=sys.stderr)
         sys.exit(2)
 
     if args.workload == 'wan-dit-step':

@@ -1,7 +1,7 @@
 """Token-interval helpers of the single-GPU path (src/onereel/parallel/comm.py:69-85,115-123).
 
-The multi-GPU exchange of the reference (HaloExchange, partitions, Ulysses all-to-all) is not part of this build;
-how the path shards over GPUs is described in DESIGN.md.
+The multi-GPU exchange of the reference (HaloExchange, partitions, Ulysses all-to-all) is not implemented: the path
+runs on one GPU.
 """
 from __future__ import annotations
 

@@ -3,8 +3,8 @@
 `Processor.__call__` keeps the diffusers processor signature (hunyuan15.py:177-210): the QKV projections and the
 RMSNorms run as the model's own torch modules; the scene-attention layer (RoPE, scope packing, varlen attention,
 write-back) runs as HIP kernels through `onereel_amd.scene`, with the scene RoPE fused into the K pack and the Q
-load. The multi-GPU modes of the reference (K/V gathering, Ulysses, ring), subject links and the bounded memory are
-not part of this build.
+load. The multi-GPU modes of the reference (K/V gathering, Ulysses, ring) and subject links are not implemented; the
+head-major bounded memory is `onereel_amd.memory`, called directly rather than through this processor.
 """
 from __future__ import annotations
 

@@ -1,4 +1,5 @@
-"""Shared test inputs: the BASELINE workload layouts and seeded bf16 tensors (identical bits on CPU and GPU)."""
+"""Shared test inputs: the benchmark workload layouts (CPU plumbing, HunyuanVideo-1.5 480p, Wan2.2 704x1280, uneven
+sweep) and seeded bf16 tensors (identical bits on CPU and GPU)."""
 from __future__ import annotations
 
 import numpy as np
@@ -9,18 +10,18 @@ from oracle import layout as OL
 
 def layout_case(name: str):
     """-> dict(lengths, halo, sides, extra, T, counts, Le, H, D, scene_rope, rope_lengths, table (F, Hh, Ww))"""
-    if name == 'config1':        # CPU plumbing: 2 scenes x 3 frames x 64 tokens + 16 text, 1 rep per scene
+    if name == 'cpu_plumbing':  # CPU plumbing: 2 scenes x 3 frames x 64 tokens + 16 text, 1 rep per scene
         return dict(lengths=[3, 3], halo=0, sides='adj', extra={0: [5], 1: [0]}, T=64, counts=[16, 16], Le=32, H=2,
                     D=64, scene_rope=True, rope_lengths=None, table=(6, 8, 8))
-    if name == 'config2':        # HunyuanVideo-1.5 480p: 4 x 8 frames x 1590 (30 x 53) + 128 text, memory 4
+    if name == 'hunyuan480p':  # HunyuanVideo-1.5 480p: 4 x 8 frames x 1590 (30 x 53) + 128 text, memory 4
         return dict(lengths=[8] * 4, halo=0, sides='adj', extra={0: [10, 21, 31], 1: [0, 21, 31], 2: [0, 10, 31],
                                                                   3: [0, 10, 21]},
                     T=1590, counts=[128] * 4, Le=512, H=16, D=128, scene_rope=True, rope_lengths=None,
                     table=(32, 30, 53))
-    if name == 'config3':        # Wan2.2 704x1280 joint scopes: 3 x 11 x 880 (22 x 40) + 128 text, sides=next
+    if name == 'wan704':  # Wan2.2 704x1280 joint scopes: 3 x 11 x 880 (22 x 40) + 128 text, sides=next
         return dict(lengths=[11] * 3, halo=2, sides='next', extra={}, T=880, counts=[128] * 3, Le=384, H=24, D=128,
                     scene_rope=False, rope_lengths=None, table=(33, 22, 40))
-    if name.startswith('config4_K'):  # uneven sweep, K scenes (seed K)
+    if name.startswith('uneven_K'):  # uneven sweep, K scenes (seed K)
         K = int(name.split('K')[1])
         rng = np.random.default_rng(K)
         lengths = rng.integers(2, 17, K).tolist()

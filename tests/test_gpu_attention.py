@@ -188,11 +188,11 @@ def _layer_inputs(case, seed=0):
     return q, k, v, eq, ek, ev, cos, sin
 
 
-@pytest.mark.parametrize('name,per_seg', [('config1', None), ('config2', 48), ('config3', 48), ('config4_K12', 24)])
+@pytest.mark.parametrize('name,per_seg', [('cpu_plumbing', None), ('hunyuan480p', 48), ('wan704', 48), ('uneven_K12', 24)])
 @pytest.mark.parametrize('adjacent', [False, True])
 def test_scene_layer_matches_oracle(name, per_seg, adjacent):
     """the fused layer (K/V pack with RoPE, Q RoPE on the load, in-place output) against the oracle's packing plus
-    per-scope fp32 attention; full outputs for config 1, sampled query rows (every segment's first / last rows
+    per-scope fp32 attention; full outputs for the CPU-plumbing layout, sampled query rows (every segment's first / last rows
     included) at the full-size configs"""
     case = layout_case(name)
     print(f'layer {name} adjacent={adjacent}', flush=True)
@@ -218,7 +218,7 @@ def test_scene_layer_matches_oracle(name, per_seg, adjacent):
 def test_scene_layer_reference_flow_and_rotated_inputs(adjacent):
     """fused=False (Q/K/V packed, varlen on packed tensors, scatter) and mode 'rotated' (already rotated q / k, shared
     keys re-rotated by _move_shared's two rotations) give the oracle's result; text padding rows stay zero"""
-    case = dict(layout_case('config1'), Le=40)
+    case = dict(layout_case('cpu_plumbing'), Le=40)
     q, k, v, eq, ek, ev, cos, sin = _layer_inputs(case, 5)
     lay = SceneLayout(case['lengths'], halo=0, extra=case['extra'])
     olay = OL.SceneLayout(case['lengths'], 0, 'adj', case['extra'])

@@ -1,5 +1,5 @@
 """GPU parity, bit-exact: the layout kernel, the K/V/Q pack-gather (with RoPE and _move_shared) and the scatter
-against the oracle, through the C ABI, at the BASELINE layouts' full sizes and on edge-case layouts."""
+against the oracle, through the C ABI, at the benchmark layouts' full sizes and on edge-case layouts."""
 import numpy as np
 import pytest
 import torch
@@ -42,15 +42,15 @@ def _check_plan(plan, sc, adjacent):
     assert (plan.n_seg, plan.sum_q, plan.sum_k) == (len(sc.lq), int(sc.cu_q[-1]), int(sc.cu_k[-1]))
 
 
-@pytest.mark.parametrize('name', ['config1', 'config2', 'config3', 'config4_K2', 'config4_K4', 'config4_K8',
-                                  'config4_K12'])
+@pytest.mark.parametrize('name', ['cpu_plumbing', 'hunyuan480p', 'wan704', 'uneven_K2', 'uneven_K4', 'uneven_K8',
+                                  'uneven_K12'])
 @pytest.mark.parametrize('adjacent', [False, True])
 def test_layout_kernel_bit_exact_configs(name, adjacent):
     case = layout_case(name)
     print(f'layout {name} adjacent={adjacent}', flush=True)
     plan, sc = _plans(case, adjacent)
     _check_plan(plan, sc, adjacent)
-    if name == 'config2':
+    if name == 'hunyuan480p':
         assert plan.cu_q.tolist() == [0, 12720, 12848, 25568, 25696, 38416, 38544, 51264, 51392]
         assert plan.cu_k.tolist() == [0, 17618, 30466, 48084, 60932, 78550, 91398, 109016, 121864]
 
@@ -110,7 +110,7 @@ def _tables(case):
     return OA.rope_table_3d(F, Hh, Ww, case['D'])
 
 
-@pytest.mark.parametrize('name', ['config1', 'config2', 'config3'])
+@pytest.mark.parametrize('name', ['cpu_plumbing', 'hunyuan480p', 'wan704'])
 @pytest.mark.parametrize('adjacent', [False, True])
 def test_pack_gather_bit_exact(name, adjacent):
     case = layout_case(name)
@@ -134,7 +134,7 @@ def test_pack_gather_bit_exact(name, adjacent):
         del kp, vp, qp
 
 
-@pytest.mark.parametrize('name', ['config1', 'config2'])
+@pytest.mark.parametrize('name', ['cpu_plumbing', 'hunyuan480p'])
 def test_scatter_bit_exact(name):
     case = layout_case(name)
     H, D, T = case['H'], case['D'], case['T']

@@ -79,8 +79,8 @@ def test_frame_memory_next_step_applies_reps():
         assert lay.extra[j] == [f for f in [1, 7] if not lo <= f < hi]
 
 
-def test_config2_extra_from_reps():
-    g = HD['config2_hunyuan480p']
+def test_hunyuan480p_extra_from_reps():
+    g = HD['hunyuan480p_4x8x1590']
     lay = OL.SceneLayout(g['lengths'], halo=0)
     fm = OL.FrameMemoryExtra(budget=4, fallback=(0, 'adj'))
     fm.reset(lay)
@@ -145,23 +145,23 @@ def test_tiny_scopes_hand_derived(variant):
 
 
 def test_config_scope_sizes():
-    g = HD['config1_cpu_plumbing']
+    g = HD['cpu_plumbing_2x3x64']
     sc = OL.hunyuan_scopes(OL.SceneLayout(g['lengths'], halo=0, extra=_extra(g['extra'])), g['T'], g['counts'])
     assert sc.lq == g['lq'] and sc.lk == g['lk']
     assert OA.useful_flops(sc.lq, sc.lk, 2, 64) == pytest.approx(g['useful_flop_H2_D64'], rel=1e-3)
-    g = HD['config2_hunyuan480p']
+    g = HD['hunyuan480p_4x8x1590']
     sc = OL.hunyuan_scopes(OL.SceneLayout(g['lengths'], halo=0, extra=_extra(g['extra'])), g['T'], g['counts'],
                            scene_rope=True, adjacent=True)
     assert sc.cu_q.tolist() == g['cu_q'] and sc.cu_k.tolist() == g['cu_k']
     assert (sc.max_q, sc.max_k) == (g['max_q'], g['max_k'])
     assert OA.useful_flops(sc.lq, sc.lk, 16, 128) == pytest.approx(g['useful_flop_H16_D128'], rel=1e-4)
-    g = HD['config3_wan704']
+    g = HD['wan704_3x11x880']
     lay = OL.SceneLayout(g['lengths'], halo=g['halo'], sides=g['sides'])
     sc = OL.hunyuan_scopes(lay, g['T'], g['counts'])
     assert sc.lq == g['lq'] and sc.lk == g['lk']
     _, kr = OL.wan_ranges(lay, g['T'])
     assert [[a // g['T'], b // g['T']] for a, b in kr] == g['wan_k_ranges_frames']
-    g = HD['config4_uneven_K12']
+    g = HD['uneven_K12']
     rng = np.random.default_rng(12)
     lengths = rng.integers(2, 17, 12).tolist()
     text = rng.integers(64, 257, 12).tolist()
