@@ -5,7 +5,8 @@
 // the write-back ov[lo:hi] = o / ot[t0:t1] = o after o.split (hunyuan15.py:226,231-235; attention.py:71).
 //
 // Both kernels are HBM-bound row copies: one wavefront moves one row of H*D bf16 (4 KiB at 16 x 128) per step in
-// 16-byte lanes (the scatter two rows per step), all loads issued before the stores. Stores are non-temporal: the
+// 16-byte lanes (the scatter two rows per step), all loads issued before the stores; rows under 1 KiB share a
+// wavefront. Stores are non-temporal: the
 // packed rows and the token-order outputs are written once and read by the next kernel from HBM, so they bypass
 // the caches (about 10% and 25% faster than cached stores for the pack and the scatter). The rotation is done in
 // fp32 as two rounded products and a rounded sum per element (no fused multiply-add), then rounded to bf16 to
@@ -41,13 +42,31 @@ struct GatherArgs {
   uint16_t* b_out;
 };
 
+// Rows narrower than 64 chunks (e.g. the single-head rows of the bounded memory, 16 chunks) share a wavefront: lane
+// group `sub` of `per` = 64 / cp lanes (cp: the chunk count rounded up to a power of two) moves row r0 + sub.
+struct RowLanes {
+  int cp, per, sub, cl;
+};
+
+template <bool NARROW>
+__device__ __forceinline__ RowLanes row_lanes(int chunks, int lane) {
+  if constexpr (!NARROW) return RowLanes{64, 1, 0, lane};
+  int cp = 1;
+  while (cp < chunks) cp <<= 1;
+  return RowLanes{cp, 64 / cp, lane / cp, lane % cp};
+}
+
+template <bool NARROW>
 __global__ __launch_bounds__(kThreads) void pack_gather_kernel(GatherArgs g) {
   const int lane = threadIdx.x & 63;
   const int64_t wave = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6);
   const int64_t n_waves = (int64_t)gridDim.x * kWaves;
   const int row_elems = g.H * g.D;
   const int chunks = row_elems >> 3;
-  for (int64_t r = wave; r < g.n_rows; r += n_waves) {
+  const RowLanes rl = row_lanes<NARROW>(chunks, lane);
+  for (int64_t r0 = wave * rl.per; r0 < g.n_rows; r0 += n_waves * rl.per) {
+    const int64_t r = r0 + rl.sub;
+    if (r >= g.n_rows) continue;
     const int src = g.src_idx[r];
     const bool text = src >= g.n_video;
     const int64_t off = text ? (int64_t)(src - g.n_video) * g.text_stride : (int64_t)src * g.src_stride;
@@ -60,7 +79,7 @@ __global__ __launch_bounds__(kThreads) void pack_gather_kernel(GatherArgs g) {
     u32x4 va[kMaxChunksPerLane], vb[kMaxChunksPerLane];
 #pragma unroll
     for (int i = 0; i < kMaxChunksPerLane; ++i) {
-      const int c = lane + 64 * i;
+      const int c = rl.cl + rl.cp * i;
       if (c < chunks) {
         va[i] = *(const u32x4*)(a + 8 * c);
         if (b) vb[i] = *(const u32x4*)(b + 8 * c);
@@ -70,7 +89,7 @@ __global__ __launch_bounds__(kThreads) void pack_gather_kernel(GatherArgs g) {
     uint16_t* bo = g.b_out ? g.b_out + r * (int64_t)row_elems : nullptr;
 #pragma unroll
     for (int i = 0; i < kMaxChunksPerLane; ++i) {
-      const int c = lane + 64 * i;
+      const int c = rl.cl + rl.cp * i;
       if (c < chunks) {
         u32x4 x = va[i];
         const int d0 = (8 * c) % g.D;
@@ -102,6 +121,7 @@ struct ScatterArgs {
 constexpr int kScatterRows = 2;   // rows per wavefront step (loads of both in flight before the stores)
 
 // rows r < n_rows: packed row r -> token-order row dst_idx[r]; rows n_rows .. n_rows + n_zero: zeroed text rows
+template <bool NARROW>
 __global__ __launch_bounds__(kThreads) void scatter_kernel(ScatterArgs g) {
   const int lane = threadIdx.x & 63;
   const int64_t wave = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6);
@@ -110,12 +130,14 @@ __global__ __launch_bounds__(kThreads) void scatter_kernel(ScatterArgs g) {
   const int chunks = row_elems >> 3;
   const int64_t n_zero = g.text_rows > g.zero_from ? g.text_rows - g.zero_from : 0;
   const int64_t total = g.n_rows + n_zero;
-  for (int64_t r0 = wave * kScatterRows; r0 < total; r0 += n_waves * kScatterRows) {
+  const RowLanes rl = row_lanes<NARROW>(chunks, lane);
+  const int64_t step = (int64_t)kScatterRows * rl.per;
+  for (int64_t r0 = wave * step; r0 < total; r0 += n_waves * step) {
     u32x4 v[kScatterRows][kMaxChunksPerLane];
     uint16_t* o[kScatterRows];
 #pragma unroll
     for (int k = 0; k < kScatterRows; ++k) {
-      const int64_t r = r0 + k;
+      const int64_t r = r0 + k * rl.per + rl.sub;
       o[k] = nullptr;
       if (r < g.n_rows) {
         const int dst = g.dst_idx[r];
@@ -124,7 +146,7 @@ __global__ __launch_bounds__(kThreads) void scatter_kernel(ScatterArgs g) {
         const uint16_t* p = g.packed + r * (int64_t)row_elems;
 #pragma unroll
         for (int i = 0; i < kMaxChunksPerLane; ++i) {
-          const int c = lane + 64 * i;
+          const int c = rl.cl + rl.cp * i;
           if (c < chunks) v[k][i] = *(const u32x4*)(p + 8 * c);
         }
       } else if (r < total) {
@@ -138,7 +160,7 @@ __global__ __launch_bounds__(kThreads) void scatter_kernel(ScatterArgs g) {
       if (o[k]) {
 #pragma unroll
         for (int i = 0; i < kMaxChunksPerLane; ++i) {
-          const int c = lane + 64 * i;
+          const int c = rl.cl + rl.cp * i;
           if (c < chunks) store_nt(o[k] + 8 * c, v[k][i]);
         }
       }
@@ -187,7 +209,10 @@ extern "C" int or_pack_gather(const void* a_video, const void* a_text, const voi
                (const uint16_t*)b_video, (const uint16_t*)(b_text ? b_text : b_video),
                src_row_stride, text_row_stride, n_video, src_idx, rope_row, move_from, cos_table, sin_table,
                n_rope_rows, n_rows, H, D, (uint16_t*)a_out, (uint16_t*)b_out};
-  hipLaunchKernelGGL(pack_gather_kernel, dim3(row_grid(n_rows)), dim3(kThreads), 0, (hipStream_t)stream, g);
+  if ((int64_t)H * D < 64 * 8)   // rows under 64 chunks share a wavefront
+    hipLaunchKernelGGL(pack_gather_kernel<true>, dim3(row_grid(n_rows)), dim3(kThreads), 0, (hipStream_t)stream, g);
+  else
+    hipLaunchKernelGGL(pack_gather_kernel<false>, dim3(row_grid(n_rows)), dim3(kThreads), 0, (hipStream_t)stream, g);
   return check_hip(hipGetLastError(), "pack_gather_kernel launch");
 }
 
@@ -207,6 +232,11 @@ extern "C" int or_scatter(const void* packed, const int32_t* dst_idx, int64_t n_
   ScatterArgs g{(const uint16_t*)packed, dst_idx, n_rows, n_video, (uint16_t*)o_video,
                 (uint16_t*)(o_text ? o_text : o_video), dst_row_stride, text_row_stride, text_zero_from, text_rows,
                 H, D};
-  hipLaunchKernelGGL(scatter_kernel, dim3(row_grid(n_rows + n_zero)), dim3(kThreads), 0, (hipStream_t)stream, g);
+  if ((int64_t)H * D < 64 * 8)
+    hipLaunchKernelGGL(scatter_kernel<true>, dim3(row_grid(n_rows + n_zero)), dim3(kThreads), 0, (hipStream_t)stream,
+                       g);
+  else
+    hipLaunchKernelGGL(scatter_kernel<false>, dim3(row_grid(n_rows + n_zero)), dim3(kThreads), 0, (hipStream_t)stream,
+                       g);
   return check_hip(hipGetLastError(), "scatter_kernel launch");
 }
