@@ -27,7 +27,12 @@ Schedule of iteration j (32 keys; R-slot rings of K and V blocks in LDS, 8 KiB p
     phase B  steps k = 4..7, P(j) of query block 1, and the LDS operands of steps 0..3 of iteration j+1
     tail     if a row-half sum of P(j) exceeds 2^20 (or is not finite): out-of-line rescale (m moves up by the block
              max d, O and l scale by 2^(-c d), S(j), S(j+1) and -m shift by -d, P(j) recomputed); then l += row sums
+Within a phase the eight S MFMAs go before the eight PV MFMAs, and the side work (softmax VALU, LDS reads, DMA) is
+spread between them in proportion to its issue cost (SIDE_COST).
 The running max starts at block 0's own maximum (prologue), so row sums never underflow and m only moves up.
+After the loop: the epilogue (O += V(nb-1) P(nb-1)) and the store of O / l, as bf16 output rows or, for the parts of
+a key-split work item, as fp32 partial rows (%[f32]). A wavefront whose queries all lie past the segment (%[dead])
+runs a loop of only the barriers and its share of the DMA, so that the block stays in step, and writes nothing.
 The generator inserts the LDS waits (lgkmcnt) from the order of the reads, and s_nop where gfx950 needs wait states
 between dependent instructions (see Emitter).
 """
