@@ -73,6 +73,15 @@ class HipPathError(RuntimeError):
     """a library call failed (bad argument or HIP error); the message is the library's"""
 
 
+class HipValueError(HipPathError, ValueError):
+    """an argument the host layer rejects before calling the library (shape, size, layout): a RuntimeError, as
+    FlashAttention's argument errors are, and a ValueError"""
+
+
+class HipTypeError(HipPathError, TypeError):
+    """a tensor of the wrong dtype or device: a RuntimeError, as FlashAttention's dtype errors are, and a TypeError"""
+
+
 def lib():
     """the loaded library; raises if it was not built (no CPU fallback exists)"""
     global _lib

@@ -154,7 +154,7 @@ class FrameMemory:
             return []
         n_frames, C = feats.shape
         if any(not 0 <= f < n_frames for f in cand):
-            raise ValueError(f'candidate frames outside [0, {n_frames})')
+            raise L.HipValueError(f'candidate frames outside [0, {n_frames})')
         x = feats.to(torch.float32).contiguous()
         dev = x.device
         ct = torch.tensor(cand, dtype=torch.int32, device=dev)

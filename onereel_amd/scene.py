@@ -29,7 +29,7 @@ def _desc(lay: SceneLayout, T: int, counts, text_rows: int, scene_rope: bool, ro
     d = L.LayoutDesc()
     n = lay.n_scenes
     if n > L.OR_MAX_SCENES:
-        raise ValueError(f'{n} scenes exceed the maximum {L.OR_MAX_SCENES}')
+        raise L.HipValueError(f'{n} scenes exceed the maximum {L.OR_MAX_SCENES}')
     d.n_scenes, d.T, d.halo = n, int(T), int(lay.halo)
     d.sides = ('adj', 'prev', 'next').index(lay.sides)
     d.with_text, d.scene_rope, d.adjacent = int(with_text), int(scene_rope), int(adjacent)
@@ -38,12 +38,12 @@ def _desc(lay: SceneLayout, T: int, counts, text_rows: int, scene_rope: bool, ro
         d.lengths[j] = int(x)
     counts = list(counts) if with_text else [0] * n
     if len(counts) != n:
-        raise ValueError(f'{len(counts)} sentence counts for {n} scenes')
+        raise L.HipValueError(f'{len(counts)} sentence counts for {n} scenes')
     for j, c in enumerate(counts):
         d.counts[j] = int(c)
     rl = list(rope_lengths) if rope_lengths else []
     if len(rl) > L.OR_MAX_SCENES:
-        raise ValueError('too many rope_lengths')
+        raise L.HipValueError('too many rope_lengths')
     d.n_rope_lengths = len(rl)
     for s, x in enumerate(rl):
         d.rope_lengths[s] = int(x)
@@ -52,7 +52,7 @@ def _desc(lay: SceneLayout, T: int, counts, text_rows: int, scene_rope: bool, ro
     for j in range(n):
         fr = list(lay.extra.get(j, ()))
         if e + len(fr) > L.OR_MAX_EXTRA:
-            raise ValueError(f'more than {L.OR_MAX_EXTRA} extra frames')
+            raise L.HipValueError(f'more than {L.OR_MAX_EXTRA} extra frames')
         for f in fr:
             d.extra[e] = int(f)
             e += 1
@@ -116,23 +116,23 @@ class ScopePlan:
 def _rows2d(x: torch.Tensor, H: int, D: int):
     """(tensor, row stride) of a [rows, H, D] view whose (H, D) part is contiguous"""
     if x.dim() != 3 or x.shape[1] != H or x.shape[2] != D:
-        raise ValueError(f'expected [rows, {H}, {D}], got {tuple(x.shape)}')
+        raise L.HipValueError(f'expected [rows, {H}, {D}], got {tuple(x.shape)}')
     if x.stride(2) != 1 or x.stride(1) != D:
-        raise ValueError('heads and head dims must be contiguous')
+        raise L.HipValueError('heads and head dims must be contiguous')
     return x, x.stride(0)
 
 
 def _check_bf16(*xs):
     for x in xs:
         if x is not None and (x.dtype != torch.bfloat16 or not x.is_cuda):
-            raise TypeError(f'expected a bf16 GPU tensor, got {x.dtype} on {x.device}')
+            raise L.HipTypeError(f'expected a bf16 GPU tensor, got {x.dtype} on {x.device}')
 
 
 def _tables(cos, sin, D):
     if cos is None:
         return None, None, 0
     if cos.dim() != 2 or cos.shape[1] != D or sin.shape != cos.shape:
-        raise ValueError(f'rotary tables must be [rows, {D}]')
+        raise L.HipValueError(f'rotary tables must be [rows, {D}]')
     cos = cos.to(torch.float32).contiguous()
     sin = sin.to(torch.float32).contiguous()
     return cos, sin, cos.shape[0]
@@ -148,7 +148,7 @@ def pack_rows(plan: ScopePlan, video: torch.Tensor, text: torch.Tensor | None, w
     ts = _rows2d(text, H, D)[1] if text is not None and text.shape[0] else vs
     if b_video is not None:
         if _rows2d(b_video, H, D)[1] != vs or (b_text is not None and b_text.shape[0] and b_text.stride(0) != ts):
-            raise ValueError('value rows must have the strides of the key rows')
+            raise L.HipValueError('value rows must have the strides of the key rows')
     n = plan.sum_q if which == 'q' else plan.sum_k
     src = plan.q_src if which == 'q' else plan.k_src
     rope = move = None
@@ -156,15 +156,15 @@ def pack_rows(plan: ScopePlan, video: torch.Tensor, text: torch.Tensor | None, w
         rope = plan.q_rope if which == 'q' else plan.k_rope
     elif mode == 'rotated' and which == 'k' and plan.adjacent:
         if plan.k_move_a is None:
-            raise ValueError('plan was built without move rows (moves=True)')
+            raise L.HipValueError('plan was built without move rows (moves=True)')
         rope, move = plan.k_move_b, plan.k_move_a
     elif mode not in MODES:
-        raise ValueError(mode)
+        raise L.HipValueError(mode)
     cos, sin, n_rows = _tables(cos, sin, D) if rope is not None else (None, None, 0)
     if rope is not None and cos is None:
-        raise ValueError('RoPE needs the (cos, sin) tables')
+        raise L.HipValueError('RoPE needs the (cos, sin) tables')
     if rope is not None and plan.max_rope_row >= n_rows:
-        raise ValueError(f'layout needs rotary row {plan.max_rope_row} but the table has {n_rows} rows')
+        raise L.HipValueError(f'layout needs rotary row {plan.max_rope_row} but the table has {n_rows} rows')
     out = out if out is not None else torch.empty(n, H, D, dtype=video.dtype, device=video.device)
     if b_video is not None and b_out is None:
         b_out = torch.empty(n, H, D, dtype=video.dtype, device=video.device)
@@ -183,9 +183,9 @@ def gather_rows(src: torch.Tensor, idx: torch.Tensor, b_src: torch.Tensor | None
     _check_bf16(src, b_src)
     _, ss = _rows2d(src, H, D)
     if b_src is not None and (b_src.shape != src.shape or _rows2d(b_src, H, D)[1] != ss):
-        raise ValueError('b_src must have the shape and row stride of src')
+        raise L.HipValueError('b_src must have the shape and row stride of src')
     if idx.dtype != torch.int32 or not idx.is_cuda or not idx.is_contiguous():
-        raise TypeError('idx must be a contiguous int32 GPU tensor')
+        raise L.HipTypeError('idx must be a contiguous int32 GPU tensor')
     n = idx.numel()
     out = torch.empty(n, H, D, dtype=src.dtype, device=src.device)
     b_out = torch.empty_like(out) if b_src is not None else None
@@ -201,7 +201,7 @@ def scatter_rows(packed: torch.Tensor, idx: torch.Tensor, out: torch.Tensor):
     _check_bf16(packed, out)
     _, os_ = _rows2d(out, H, D)
     if idx.dtype != torch.int32 or not idx.is_cuda or not idx.is_contiguous() or idx.numel() != n:
-        raise TypeError('idx must be a contiguous int32 GPU tensor with one entry per packed row')
+        raise L.HipTypeError('idx must be a contiguous int32 GPU tensor with one entry per packed row')
     L.check(L.lib().or_scatter(packed.data_ptr(), idx.data_ptr(), n, out.shape[0], out.data_ptr(), None, os_, os_, 0,
                                0, H, D, L.stream_handle(out.device)), 'or_scatter')
     return out
@@ -216,22 +216,22 @@ def varlen(q, k, v, cu_q, cu_k, max_q, max_k, *, k_off=None, k_len=None, out=Non
     _, qs = _rows2d(q, H, D)
     _, ks = _rows2d(k, H, D)
     if _rows2d(v, H, D)[1] != ks:
-        raise ValueError('k and v must have the same row stride')
+        raise L.HipValueError('k and v must have the same row stride')
     if q_text is not None and q_text.shape[0] and q_text.stride(0) != qs:
-        raise ValueError('q and q_text must have the same row stride')
+        raise L.HipValueError('q and q_text must have the same row stride')
     n_seg = (cu_q.numel() - 1)
     for t in (cu_q, cu_k, k_off, k_len, seg_q_src, q_rope):
         if t is not None and (t.dtype != torch.int32 or not t.is_cuda or not t.is_contiguous()):
-            raise TypeError('index arrays must be contiguous int32 GPU tensors')
+            raise L.HipTypeError('index arrays must be contiguous int32 GPU tensors')
     if sum_q is None:
         sum_q = q.shape[0] if seg_q_src is None else None
         if sum_q is None:
-            raise ValueError('sum_q is required with seg_q_src')
+            raise L.HipValueError('sum_q is required with seg_q_src')
     if out is None:
         out = torch.empty(q.shape[0], H, D, dtype=torch.bfloat16, device=q.device)
     _, os_ = _rows2d(out, H, D)
     if o_text is not None and o_text.shape[0] and o_text.stride(0) != os_:
-        raise ValueError('o and o_text must have the same row stride')
+        raise L.HipValueError('o and o_text must have the same row stride')
     cos, sin, n_rope_rows = _tables(cos, sin, D) if q_rope is not None else (None, None, 0)
     if workspace is None:
         nb = L.lib().or_varlen_workspace_size(int(n_seg), int(sum_q), int(H), int(D))
@@ -286,12 +286,12 @@ def scene_attention(plan: ScopePlan, q, k, v, eq, ek, ev, cos=None, sin=None, mo
     fused=True: K/V packed once, Q read in place, outputs written in place. fused=False: the reference's data flow
     (Q, K, V packed, one varlen call on packed tensors, write-back by the scatter kernel)."""
     if mode not in MODES:
-        raise ValueError(mode)
+        raise L.HipValueError(mode)
     H, D = q.shape[1], q.shape[2]
     if q.shape[0] != plan.n_video:
-        raise ValueError(f'{q.shape[0]} video rows, layout has {plan.n_video}')
+        raise L.HipValueError(f'{q.shape[0]} video rows, layout has {plan.n_video}')
     if plan.with_text and eq.shape[0] != plan.text_rows:
-        raise ValueError(f'{eq.shape[0]} text rows, layout has {plan.text_rows}')
+        raise L.HipValueError(f'{eq.shape[0]} text rows, layout has {plan.text_rows}')
     kp, vp = pack_rows(plan, k, ek, 'k', out=kbuf, b_video=v, b_text=ev, b_out=vbuf, cos=cos, sin=sin, mode=mode)
     ov = torch.empty_like(q)
     ot = torch.empty(eq.shape[0], H, D, dtype=q.dtype, device=q.device) if eq is not None else None

@@ -50,7 +50,7 @@ def _rows(x: torch.Tensor):
     C = x.shape[-1]
     x2 = x.reshape(-1, C)
     if x.dtype != torch.bfloat16 or x2.stride(1) != 1:
-        raise ValueError('expected bf16 rows with contiguous elements')
+        raise L.HipValueError('expected bf16 rows with contiguous elements')
     return x2, C
 
 
@@ -80,7 +80,7 @@ def gated_residual_(x, a, gate=None):
     x2, C = _rows(x)
     a2, Ca = _rows(a)
     if Ca != C or a2.shape[0] != x2.shape[0]:
-        raise ValueError('x and a must have the same rows')
+        raise L.HipValueError('x and a must have the same rows')
     g = _vec(gate, C)
     L.check(L.lib().or_gated_residual(x2.data_ptr(), a2.data_ptr(), L.ptr(g), x2.shape[0], C, x2.stride(0),
                                       a2.stride(0), L.stream_handle(x.device)), 'or_gated_residual')

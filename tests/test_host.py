@@ -167,3 +167,19 @@ def test_product_has_no_cpu_fallback():
     x = torch.zeros(4, 2, 64, dtype=torch.bfloat16)
     with pytest.raises(TypeError, match='GPU'):
         scene.varlen(x, x, x, torch.zeros(2, dtype=torch.int32), torch.zeros(2, dtype=torch.int32), 4, 4)
+
+
+def test_argument_errors_are_runtime_errors():
+    """as FlashAttention's argument and dtype errors are RuntimeErrors, so are the host layer's (they are also
+    ValueError / TypeError)"""
+    from onereel_amd import attention as A
+    from onereel_amd import scene
+    x = torch.zeros(4, 2, 64, dtype=torch.float32)
+    for call in (lambda: scene.varlen(x, x, x, torch.zeros(2, dtype=torch.int32), torch.zeros(2, dtype=torch.int32),
+                                      4, 4),
+                 lambda: A.merge_lse(torch.zeros(3, 2, 8, dtype=torch.bfloat16), torch.zeros(2, 3), x, x),
+                 lambda: A.overlapping_ranges(x, x, x, [(1, 4)], [(0, 4)])):
+        with pytest.raises(RuntimeError) as e:
+            call()
+        assert isinstance(e.value, (ValueError, TypeError)), type(e.value)
+
