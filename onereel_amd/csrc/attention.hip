@@ -34,7 +34,9 @@ constexpr int kMinBQ = 128;     // smallest work-item query tile of the two kern
 constexpr int kQueues = 8;      // item queues: one per XCD
 constexpr int kQueueWords = 32; // words per queue header (head counter, item count, first item), one 128-byte line
 constexpr int kWsHeader = kQueues * kQueueWords;   // int32 words before the item list
-constexpr int kItemWords = 4;   // segment, tile << 8 | head, part | ways << 8 (0: whole item), split index
+// an item record: tile << 8 | head, part | ways << 8 (0: whole item), split index, and the segment's first query,
+// query count, first source row, first key and key count (a kernel reads the record with two 16-byte loads)
+constexpr int kItemWords = 8;
 constexpr int kPlanThreads = 1024;
 constexpr int kMaxPlanSeg = 4096;
 constexpr int kMaxSplitWays = 8;      // key parts of a split work item
@@ -71,10 +73,6 @@ struct AttnArgs {
   float* split_o;
 };
 
-__device__ __forceinline__ int seg_k_begin(const AttnArgs& a, int s) { return a.k_off ? a.k_off[s] : a.cu_k[s]; }
-__device__ __forceinline__ int seg_k_len(const AttnArgs& a, int s) {
-  return a.k_len ? a.k_len[s] : a.cu_k[s + 1] - a.cu_k[s];
-}
 
 // A-operand row permutation of the S^T MFMA: row i = 8g + 4h + c reads key 16h + 4g + c
 __device__ __forceinline__ int pi32(int i) { return ((i >> 2) & 1) * 16 + (i >> 3) * 4 + (i & 3); }
@@ -82,7 +80,8 @@ __device__ __forceinline__ int pi32(int i) { return ((i >> 2) & 1) * 16 + (i >> 
 // ------------------------------------------------------------------------------------------------------------------
 // planner: one block. Segments sorted by key count (descending), then index. Queue q holds the heads h with
 // h % 8 == q: for every sorted segment, those heads in order, each head's query tiles in order. Queue q's header at
-// ws[32 q]: [0] head counter, [1] item count, [2] index of its first item in the item list.
+// ws[32 q]: [0] head counter, [1] item count, [2] index of its first item in the item list. Each item record carries
+// its segment's query and key ranges, so a kernel needs no further lookups to start an item.
 //
 // Last round: with `slots` persistent blocks, the rem = items % slots items past the last full round would leave
 // blocks idle at the end. When split_keys is set, the last items of every queue (rem in all, in proportion to the
@@ -100,7 +99,8 @@ __device__ inline int plan_upper_bound(const int* a, int n, int x) {
 }
 
 __global__ __launch_bounds__(kPlanThreads) void plan_kernel(const int32_t* cu_q, const int32_t* cu_k,
-                                                            const int32_t* k_len, int n_seg, int H, int bq,
+                                                            const int32_t* k_off, const int32_t* k_len,
+                                                            const int32_t* seg_q_src, int n_seg, int H, int bq,
                                                             int max_items, int slots, int split_keys, int parts_cap,
                                                             int32_t* ws) {
   __shared__ unsigned long long key[kMaxPlanSeg];
@@ -225,21 +225,20 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(const int32_t* cu_q,
     const int q = head % kQueues;
     const int pos = (off[i] / H) * heads_of(q) + (head / kQueues) * tiles + t;   // position within queue q
     const int keep = q_n[q] - q_s[q];
+    const int q_beg = cu_q[s];
+    const int k_beg = k_off ? k_off[s] : cu_k[s];
+    const int lk = k_len ? k_len[s] : cu_k[s + 1] - cu_k[s];
+    const int q_src0 = seg_q_src ? seg_q_src[s] : q_beg;
+    auto put = [&](int64_t entry, int pw, int sidx) {
+      int32_t* e = ws + kWsHeader + kItemWords * entry;
+      *(int4*)e = make_int4((t << 8) | head, pw, sidx, q_beg);
+      *(int4*)(e + 4) = make_int4(lq, q_src0, k_beg, lk < 0 ? 0 : lk);
+    };
     if (pos < keep) {
-      int32_t* e = ws + kWsHeader + kItemWords * (q_first[q] + pos);
-      e[0] = s;
-      e[1] = (t << 8) | head;
-      e[2] = 0;
-      e[3] = 0;
+      put(q_first[q] + pos, 0, 0);
     } else {
       const int k = pos - keep, sidx = q_sb[q] + k;
-      for (int p = 0; p < W; ++p) {
-        int32_t* e = ws + kWsHeader + kItemWords * (q_first[q] + keep + k * W + p);
-        e[0] = s;
-        e[1] = (t << 8) | head;
-        e[2] = p | (W << 8);
-        e[3] = sidx;
-      }
+      for (int p = 0; p < W; ++p) put(q_first[q] + keep + k * W + p, p | (W << 8), sidx);
       tab[3 * sidx] = s;
       tab[3 * sidx + 1] = (t << 8) | head;
       tab[3 * sidx + 2] = W;
@@ -533,14 +532,10 @@ void attn4_kernel(AttnArgs a, int32_t* ws) {
     const int it = item_sh;
     __syncthreads();
     if (it < 0) break;
-    const int seg = ws[kWsHeader + kItemWords * it];
-    const int packed_ht = ws[kWsHeader + kItemWords * it + 1];
-    const int head = packed_ht & 255, qt = packed_ht >> 8;
-    const int q_beg = a.cu_q[seg];
-    const int Lq = a.cu_q[seg + 1] - q_beg;
-    const int k_beg = seg_k_begin(a, seg);
-    const int Lk = max(seg_k_len(a, seg), 0);
-    const int q_src0 = a.seg_q_src ? a.seg_q_src[seg] : q_beg;
+    const int4 r0 = *(const int4*)(ws + kWsHeader + kItemWords * it);
+    const int4 r1 = *(const int4*)(ws + kWsHeader + kItemWords * it + 4);
+    const int head = r0.x & 255, qt = r0.x >> 8;
+    const int q_beg = r0.w, Lq = r1.x, q_src0 = r1.y, k_beg = r1.z, Lk = r1.w;
     const int q0 = qt * BQ + w * WQ;
     const bool active = q0 < Lq;
     const int nb = (Lk + kBKB - 1) / kBKB;
@@ -688,13 +683,11 @@ void attn8_kernel(AttnArgs a, int32_t* ws) {
     const int it = item_sh;
     __syncthreads();
     if (it < 0) break;
-    const int32_t* e = ws + kWsHeader + kItemWords * it;
-    const int seg = e[0], packed_ht = e[1], part = e[2] & 255, ways = e[2] >> 8, sidx = e[3];
-    const int head = packed_ht & 255, qt = packed_ht >> 8;
-    const int q_beg = a.cu_q[seg];
-    const int Lq = a.cu_q[seg + 1] - q_beg;
-    int k_beg = seg_k_begin(a, seg);
-    int Lk = max(seg_k_len(a, seg), 0);
+    const int4 r0 = *(const int4*)(ws + kWsHeader + kItemWords * it);
+    const int4 r1 = *(const int4*)(ws + kWsHeader + kItemWords * it + 4);
+    const int head = r0.x & 255, qt = r0.x >> 8, part = r0.y & 255, ways = r0.y >> 8, sidx = r0.z;
+    const int q_beg = r0.w, Lq = r1.x, q_src0 = r1.y;
+    int k_beg = r1.z, Lk = r1.w;
     if (ways > 1) {
       // part `part` of `ways`: key blocks [nb_all part / ways, nb_all (part + 1) / ways), at least one each
       const int nb_all = (Lk + kBKB - 1) / kBKB;
@@ -702,7 +695,6 @@ void attn8_kernel(AttnArgs a, int32_t* ws) {
       k_beg += kBKB * b0;
       Lk = min(kBKB * b1, Lk) - kBKB * b0;
     }
-    const int q_src0 = a.seg_q_src ? a.seg_q_src[seg] : q_beg;
     const int q0 = qt * BQ + w * WQ;
     const int nb = (Lk + kBKB - 1) / kBKB;
     float* part_o = ways > 1 ? a.split_o + (int64_t)(sidx * ways + part) * kSplitRows * D : nullptr;
@@ -920,8 +912,8 @@ extern "C" int or_varlen_fwd(const or_varlen_args* p, void* stream) {
     return fail_arg("or_varlen_fwd: a segment's keys span more than 2 GiB (max_k %d x row stride %lld)", x.max_k,
                     (long long)x.k_row_stride);
   const int64_t need = or_varlen_workspace_size(x.n_seg, x.sum_q, x.H, x.D);
-  if (!x.workspace || x.workspace_bytes < need)
-    return fail_arg("or_varlen_fwd: workspace of %lld bytes needed", (long long)need);
+  if (!x.workspace || x.workspace_bytes < need || !aligned16(x.workspace))
+    return fail_arg("or_varlen_fwd: a 16-byte aligned workspace of %lld bytes is needed", (long long)need);
   if (x.sum_q == 0) return 0;
   DevInfo di;
   if (int rc = dev_info(di)) return rc;
@@ -967,9 +959,9 @@ extern "C" int or_varlen_fwd(const or_varlen_args* p, void* stream) {
   a.split_o = (float*)((char*)x.workspace + wl.o);
   hipStream_t st = (hipStream_t)stream;
   // the planner needs key counts only: k_len when given, else the cu_k differences
-  hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(kPlanThreads), 0, st, x.cu_q, x.k_len ? nullptr : x.cu_k,
-                     x.k_len, x.n_seg, x.H, item_bq(x.D), (int)max_items, (int)grid, may_split ? 1 : 0,
-                     (int)cap, ws);
+  hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(kPlanThreads), 0, st, x.cu_q, x.cu_k, x.k_len ? x.k_off : nullptr,
+                     x.k_len, x.seg_q_src, x.n_seg, x.H, item_bq(x.D), (int)max_items, (int)grid,
+                     may_split ? 1 : 0, (int)cap, ws);
   if (int rc = check_hip(hipGetLastError(), "plan_kernel launch")) return rc;
   hipLaunchKernelGGL(attn_fn(x.D), dim3((unsigned)grid), dim3(kThreads), 0, st, a, ws);
   if (int rc = check_hip(hipGetLastError(), "attn_kernel launch")) return rc;
