@@ -342,12 +342,13 @@ struct Ring {
 // LDS byte m0 + n * 4096 + 16 * lane (m0: the slot plus this wavefront's 1 KiB). The buffer descriptor's record
 // count ends at the segment's last row, so rows past it read 0. Inline asm: the compiler does not see these LDS
 // writes, so it adds no waits on them before unrelated LDS reads; the kernel waits with vmcnt and a barrier itself.
+// gfx9 needs one wait state between an SALU write of M0 and the LDS DMA that reads it (the s_nop).
 template <int LPB>
 __device__ __forceinline__ void dma_block(uint64_t base, int32_t nrec, const uint32_t* voff, uint32_t m0) {
   const i32x4 r = {(int32_t)(uint32_t)base, (int32_t)(uint32_t)(base >> 32), nrec, 0x00020000};
 #pragma unroll
   for (int n = 0; n < LPB; ++n)
-    asm volatile("s_mov_b32 m0, %2\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voff[n]), "s"(r),
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voff[n]), "s"(r),
                  "s"(m0 + n * kThreads * 16)
                  : "memory");
 }
@@ -641,7 +642,8 @@ void attn4_kernel(AttnArgs a, int32_t* ws) {
 // live in AGPRs for the whole key loop, which is generated inline asm (gen_attn_ring64.py -> attn_ring64.inc): K and
 // V blocks of 32 keys stream through rings of ONEREEL_RING64 LDS slots each, the barrier sits in the middle of an
 // iteration so that the next iteration's operands are read during this one's MFMAs, and the epilogue normalises O and
-// stores it (rows past the segment masked off). The item queue, the Q load (with RoPE) and the lse store are C++.
+// stores it (rows past the segment masked off). The item queue, the first two K blocks of an item, the Q load
+// (with RoPE) and the lse store are C++.
 
 constexpr int kRing64 = ONEREEL_RING64;
 constexpr int kSlot64 = kBKB * 128;   // bf16 elements per slot
@@ -698,6 +700,20 @@ void attn8_kernel(AttnArgs a, int32_t* ws) {
     const int q0 = qt * BQ + w * WQ;
     const int nb = (Lk + kBKB - 1) / kBKB;
     float* part_o = ways > 1 ? a.split_o + (int64_t)(sidx * ways + part) * kSplitRows * D : nullptr;
+    const uint64_t kaddr = (uint64_t)(a.k + (int64_t)k_beg * rs + head * D);
+    const uint64_t vaddr = (uint64_t)(a.v + (int64_t)k_beg * rs + head * D);
+    const int32_t rb = (int32_t)rs * 2;
+    const int32_t rem0 = Lk * rb - rb + D * 2;
+    const int32_t bb = kBKB * rb;
+    if (nb > 0) {
+      // the head of the ring, ahead of the Q loads so that both latencies overlap: K blocks 0 and 1 into slots 0
+      // and 1, and zeros (record count 0) into the last V slot, the V operand of the key loop's first PV step; the
+      // generated prologue fetches the rest of the ring
+      const uint32_t vring = sbase + (uint32_t)(kRing64 * kSlot64 * 2);
+      dma_block<2>(kaddr, max(rem0, 0), voff, sbase);
+      dma_block<2>(kaddr + bb, max(rem0 - bb, 0), voff, sbase + kSlot64 * 2);
+      dma_block<2>(vaddr, 0, voff + 2, vring + (kRing64 - 1) * kSlot64 * 2);
+    }
 
     // Q operands and output rows. Rows past the segment get zero queries: their scores are 0 and their outputs are
     // not stored, and zero operands cost the MFMA unit less power than real data (the GPU is power-limited here).
@@ -740,12 +756,8 @@ void attn8_kernel(AttnArgs a, int32_t* ws) {
         }
       continue;
     }
-    const uint64_t kaddr = (uint64_t)(a.k + (int64_t)k_beg * rs + head * D);
-    const uint64_t vaddr = (uint64_t)(a.v + (int64_t)k_beg * rs + head * D);
-    const int32_t rb = (int32_t)rs * 2;
-    const int32_t rem0 = Lk * rb - rb + D * 2;
-    const int32_t bb = kBKB * rb;
     const int valid = Lk - (nb - 1) * kBKB - 16 * h;
+    const uint64_t kaddr2 = kaddr + 2 * (uint64_t)bb;   // K block 2, where the prologue's ring fill starts
     float mo0, mo1, lo0, lo1;   // per query: the running max of q k^T, and the row sum relative to it
     asm volatile(ONEREEL_RING64_ASM
                  : [mo0] "=&v"(mo0), [mo1] "=&v"(mo1), [lo0] "=&v"(lo0), [lo1] "=&v"(lo1)
@@ -755,8 +767,8 @@ void attn8_kernel(AttnArgs a, int32_t* ws) {
                    [q14] "a"(q[1][4]), [q15] "a"(q[1][5]), [q16] "a"(q[1][6]), [q17] "a"(q[1][7]),
                    [c] "s"(a.c), [nb] "s"(nb), [valid] "v"(valid), [kb] "v"(kb), [vb] "v"(vb),
                    [vk0] "v"(voff[0]), [vk1] "v"(voff[1]), [vv0] "v"(voff[2]), [vv1] "v"(voff[3]),
-                   [sbase] "s"(sbase), [bb] "s"(bb), [kb_lo] "s"((uint32_t)kaddr), [kb_hi] "s"((uint32_t)(kaddr >> 32)),
-                   [vb_lo] "s"((uint32_t)vaddr), [vb_hi] "s"((uint32_t)(vaddr >> 32)), [rem0] "s"(rem0),
+                   [sbase] "s"(sbase), [bb] "s"(bb), [kb_lo] "s"((uint32_t)kaddr2), [kb_hi] "s"((uint32_t)(kaddr2 >> 32)),
+                   [vb_lo] "s"((uint32_t)vaddr), [vb_hi] "s"((uint32_t)(vaddr >> 32)), [rem0] "s"(rem0), [remk] "s"(rem0 - 2 * bb),
                    [op0] "v"(op[0]), [op1] "v"(op[1]), [ok0] "v"(ok[0]), [ok1] "v"(ok[1]),
                    [f32] "s"(__builtin_amdgcn_readfirstlane(ways > 1 ? 1 : 0)),
                    [dead] "s"(__builtin_amdgcn_readfirstlane(q0 >= Lq ? 1 : 0))

@@ -215,26 +215,21 @@ class Kernel:
         self.VBASE = ring * SLOT      # V ring after the K ring
 
     # ---- pieces ------------------------------------------------------------------------------------------------
-    def dma(self, e, res, rem, vo, lds_off, zero=False, advance=True):
-        if zero:
-            e.raw(f's_mov_b32 s{res + 2}, 0')
+    def dma(self, e, res, rem, vo, lds_off):
         for n in range(2):
             e.raw(f's_add_u32 m0, %[sbase], {lds_off + n * 4096}')
             e.raw('s_nop 0')                      # gfx9: an SALU write of M0 and the LDS DMA reading it
             e.raw(f'buffer_load_dwordx4 %[{vo}{n}], s[{res}:{res + 3}], 0 offen lds')
-        if zero:
-            e.raw(f's_max_i32 s{res + 2}, s{rem}, 0')
-        if advance:
-            e.raw(f's_add_u32 s{res}, s{res}, %[bb]')
-            e.raw(f's_addc_u32 s{res + 1}, s{res + 1}, 0')
-            e.raw(f's_sub_i32 s{rem}, s{rem}, %[bb]')
-            e.raw(f's_max_i32 s{res + 2}, s{rem}, 0')
+        e.raw(f's_add_u32 s{res}, s{res}, %[bb]')
+        e.raw(f's_addc_u32 s{res + 1}, s{res + 1}, 0')
+        e.raw(f's_sub_i32 s{rem}, s{rem}, %[bb]')
+        e.raw(f's_max_i32 s{res + 2}, s{rem}, 0')
 
     def dma_k(self, e, slot):
         self.dma(e, KRES, KREM, 'vk', slot * SLOT)
 
-    def dma_v(self, e, slot, zero=False):
-        self.dma(e, VRES, VREM, 'vv', self.VBASE + slot * SLOT, zero=zero, advance=not zero)
+    def dma_v(self, e, slot):
+        self.dma(e, VRES, VREM, 'vv', self.VBASE + slot * SLOT)
 
     def dma_ops(self, J):
         """the mid-iteration refill as side ops: K(j+R) into slot J, V(j+R-2) into slot (J-2) % R"""
@@ -543,10 +538,11 @@ class Kernel:
         e.raw(f's_mov_b32 s{SRR}, 0x49800000')      # 2^20
         e.raw(f's_mov_b32 s{SJ}, 0')
         e.raw(f's_sub_u32 s{SNB1}, %[nb], 1')
-        for res, rem, lo, hi in ((KRES, KREM, 'kb_lo', 'kb_hi'), (VRES, VREM, 'vb_lo', 'vb_hi')):
+        # the K descriptor starts at block 2 (%[kb_lo], %[kb_hi], %[remk]): the kernel fetched the ring's head
+        for res, rem, lo, hi, r0 in ((KRES, KREM, 'kb_lo', 'kb_hi', 'remk'), (VRES, VREM, 'vb_lo', 'vb_hi', 'rem0')):
             e.raw(f's_mov_b32 s{res}, %[{lo}]')
             e.raw(f's_mov_b32 s{res + 1}, %[{hi}]')
-            e.raw(f's_mov_b32 s{rem}, %[rem0]')
+            e.raw(f's_mov_b32 s{rem}, %[{r0}]')
             e.raw(f's_max_i32 s{res + 2}, s{rem}, 0')
             e.raw(f's_mov_b32 s{res + 3}, 0x20000')
         e.valu(f'v_mov_b32_e32 v{KADDR0}, %[kb]', [], [v(KADDR0)])
@@ -562,14 +558,12 @@ class Kernel:
                     e.valu(f'v_mov_b32_e32 v{P(1, qb, half, i)}, 0', [], [v(P(1, qb, half, i))])
         for i in range(128):
             e.valu(f'v_accvgpr_write_b32 a{i}, 0', [], [f'a{i}'])
-        # ring fill: K0 K1 V(-1) then K(b+2) V(b) for b = 0 .. R-3 (block b of K in slot b, of V in slot b)
-        self.dma_k(e, 0)
-        self.dma_k(e, 1)
-        self.dma_v(e, R - 1, zero=True)
+        # ring fill: K(b+2) V(b) for b = 0 .. R-3 (block b of K in slot b, of V in slot b). The kernel issued the
+        # head (K0, K1, a zero V(-1) in slot R-1) before its Q loads, and this wavefront's part of it has landed
+        # (vmcnt(0) above); the barrier makes every wavefront's part visible.
         for b in range(R - 2):
             self.dma_k(e, b + 2)
             self.dma_v(e, b)
-        e.raw(f's_waitcnt vmcnt({4 * (R - 2)})')     # K0, K1 and V(-1) landed
         e.raw('s_barrier')
         # a wavefront whose 64 queries all lie past the segment only keeps up the block's K/V stream
         e.raw('s_cmp_eq_u32 %[dead], 0')
