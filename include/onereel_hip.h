@@ -10,7 +10,8 @@
  *   or_rmsnorm_rope   fused RMSNorm + interleaved RoPE of the Wan self-attention's queries and keys
  *   or_frame_pool     frame memory: per-frame sums of hidden states (deterministic)
  *   or_frame_select   frame memory: k-means (cosine) representatives and their medoids, one workgroup
- *   or_layernorm_modulate, or_gated_residual   the fused elementwise work of the Wan-shaped DiT block harness
+ *   or_layernorm_modulate, or_gated_residual,
+ *   or_residual_layernorm_modulate             the fused elementwise work of the Wan-shaped DiT block harness
  *
  * Conventions: every tensor is caller-owned device memory passed as a raw pointer; rows are [row][head][dim] with a
  * row stride in elements; bf16 is IEEE bfloat16 stored as uint16_t; index arrays are int32. Every launch goes on the
@@ -207,6 +208,14 @@ int or_layernorm_modulate(const void* x, void* out, int64_t n_rows, int32_t C, i
  * x = bf16(float(x) + float(a)) when gate is NULL; in place on x. */
 int or_gated_residual(void* x, const void* a, const float* gate, int64_t n_rows, int32_t C, int64_t x_row_stride,
                       int64_t a_row_stride, void* stream);
+
+/* Replaces a residual add of the block followed by the next LayerNorm + modulation (the same block, or the next
+ * block's first norm): or_gated_residual on x, then or_layernorm_modulate of the updated x into out, with the same
+ * results bit for bit, in one pass over the rows when C <= 4096 (two passes above). out must be neither x nor a. */
+int or_residual_layernorm_modulate(void* x, const void* a, const float* gate, void* out, int64_t n_rows, int32_t C,
+                                   int64_t x_row_stride, int64_t a_row_stride, int64_t out_row_stride, float eps,
+                                   const float* weight, const float* bias, const float* scale, const float* shift,
+                                   void* stream);
 
 /* Message of the calling thread's last failed call ("" if none). */
 const char* or_last_error(void);

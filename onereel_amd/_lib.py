@@ -62,6 +62,8 @@ SIGNATURES = {
     'or_frame_select': (i32, [vp, i32, i32, vp, i32, i32, i32, vp, vp, vp]),
     'or_layernorm_modulate': (i32, [vp, vp, i64, i32, i64, i64, ctypes.c_float, vp, vp, vp, vp, vp]),
     'or_gated_residual': (i32, [vp, vp, vp, i64, i32, i64, i64, vp]),
+    'or_residual_layernorm_modulate': (i32, [vp, vp, vp, vp, i64, i32, i64, i64, i64, ctypes.c_float, vp, vp, vp, vp,
+                                             vp]),
     'or_last_error': (ctypes.c_char_p, []),
     'or_version': (ctypes.c_char_p, []),
 }

@@ -14,8 +14,10 @@ It runs the attention through onereel_amd.wan's processors:
   scopes);
 - cross-attention: the varlen kernel's zero-copy key ranges.
 
-GEMMs stay torch ops (hipBLASLt). The block's LayerNorm + modulation and gated residual adds are one HIP pass each
-(`or_layernorm_modulate`, `or_gated_residual`) instead of chains of torch kernels over fp32 temporaries. Shapes of
+GEMMs stay torch ops (hipBLASLt). The block's LayerNorm + modulation and gated residual adds are HIP passes instead of
+chains of torch kernels over fp32 temporaries: every residual add runs in one pass with the LayerNorm that follows it
+(`or_residual_layernorm_modulate`: the next norm of the block, or the next block's first norm, or the output norm),
+and only the first norm runs alone (`or_layernorm_modulate`). Shapes of
 Wan2.2-TI2V-5B: hidden 3072 = 24 heads x 128, FFN 14336, 30 blocks, eps 1e-6, patch (1, 2, 2) over 48 latent
 channels, text width 4096 projected to 3072.
 """
@@ -87,6 +89,22 @@ def gated_residual_(x, a, gate=None):
     return x
 
 
+def residual_layernorm_modulate_(x, a, eps, gate=None, weight=None, bias=None, scale=None, shift=None):
+    """gated_residual_(x, a, gate), then layernorm_modulate of the updated x, in one HIP pass over the rows (the same
+    bits as the two calls); x is updated in place and the normalised rows are returned"""
+    x2, C = _rows(x)
+    a2, Ca = _rows(a)
+    if Ca != C or a2.shape[0] != x2.shape[0]:
+        raise L.HipValueError('x and a must have the same rows')
+    out = torch.empty(x2.shape, dtype=torch.bfloat16, device=x.device)
+    g, w, b, sc, sh = (_vec(t, C) for t in (gate, weight, bias, scale, shift))
+    L.check(L.lib().or_residual_layernorm_modulate(x2.data_ptr(), a2.data_ptr(), L.ptr(g), out.data_ptr(), x2.shape[0],
+                                                   C, x2.stride(0), a2.stride(0), C, float(eps), L.ptr(w), L.ptr(b),
+                                                   L.ptr(sc), L.ptr(sh), L.stream_handle(x.device)),
+            'or_residual_layernorm_modulate')
+    return out.view(x.shape)
+
+
 class Linear:
     def __init__(self, n_in, n_out, std, gen, device):
         self.weight = (torch.randn(n_out, n_in, generator=gen, device=device) * std).to(torch.bfloat16)
@@ -138,17 +156,21 @@ class Block:
         self.ffn_out = Linear(cfg.ffn, d, cfg.std, gen, device)
         self.scale_shift_table = torch.randn(6, d, generator=gen, device=device) / d ** 0.5
 
-    def __call__(self, x, text, temb6, rotary, p_self, p_cross):
-        """x [1, S, dim] bf16 (updated in place and returned), text [1, L, dim] bf16, temb6 [6, dim] fp32"""
+    def modulation(self, temb6):
+        """(shift, scale, gate, c_shift, c_scale, c_gate), each [1, dim] fp32"""
+        return (self.scale_shift_table + temb6).chunk(6, 0)
+
+    def __call__(self, x, n, mod, text, rotary, p_self, p_cross):
+        """x [1, S, dim] bf16, updated in place; n: LayerNorm(x) * (1 + scale) + shift of this block's modulation
+        `mod`; text [1, L, dim] bf16. Returns the feed forward's output and its gate: the caller adds them to x
+        together with the next LayerNorm (the block's own residual adds run with the norms that follow them)."""
         eps = self.cfg.eps
-        shift, scale, gate, c_shift, c_scale, c_gate = (self.scale_shift_table + temb6).chunk(6, 0)
-        n = layernorm_modulate(x, eps, scale=scale, shift=shift)
-        gated_residual_(x, p_self(self.attn1, n, rotary_emb=rotary), gate)
-        n = layernorm_modulate(x, eps, weight=self.norm2_w, bias=self.norm2_b)
-        gated_residual_(x, p_cross(self.attn2, n, encoder_hidden_states=text))
-        n = layernorm_modulate(x, eps, scale=c_scale, shift=c_shift)
-        f = self.ffn_out(self.ffn_in.gelu_tanh(n))
-        return gated_residual_(x, f, c_gate)
+        shift, scale, gate, c_shift, c_scale, c_gate = mod
+        n = residual_layernorm_modulate_(x, p_self(self.attn1, n, rotary_emb=rotary), eps, gate=gate,
+                                         weight=self.norm2_w, bias=self.norm2_b)
+        n = residual_layernorm_modulate_(x, p_cross(self.attn2, n, encoder_hidden_states=text), eps, scale=c_scale,
+                                         shift=c_shift)
+        return self.ffn_out(self.ffn_in.gelu_tanh(n)), c_gate
 
 
 def timestep_features(t: float, n: int, device) -> torch.Tensor:
@@ -184,11 +206,16 @@ class WanDiT:
                                                  .to(torch.bfloat16))))
         temb6 = self.time_proj(F.silu(temb)).float().view(6, d)
         ctx_text = self.text_out(F.gelu(self.text_in(text), approximate='tanh'))[None]
-        for blk in self.blocks:
-            x = blk(x, ctx_text, temb6, rotary, self.p_self, self.p_cross)
-        shift, scale = (self.scale_shift_table + temb.float()[None]).chunk(2, 0)
-        x = layernorm_modulate(x, self.cfg.eps, scale=scale, shift=shift)
-        return self.proj_out(x)[0]
+        eps = self.cfg.eps
+        mods = [blk.modulation(temb6) for blk in self.blocks]
+        out_shift, out_scale = (self.scale_shift_table + temb.float()[None]).chunk(2, 0)
+        n = layernorm_modulate(x, eps, scale=mods[0][1], shift=mods[0][0])
+        for i, blk in enumerate(self.blocks):
+            f, gate = blk(x, n, mods[i], ctx_text, rotary, self.p_self, self.p_cross)
+            # the feed forward's residual add, with the next block's first norm (the output norm after the last)
+            shift, scale = (mods[i + 1][0], mods[i + 1][1]) if i + 1 < len(self.blocks) else (out_shift, out_scale)
+            n = residual_layernorm_modulate_(x, f, eps, gate=gate, scale=scale, shift=shift)
+        return self.proj_out(n)[0]
 
     def flops(self, text_rows: int) -> dict:
         """useful FLOP of one forward: GEMMs (2 m n k each) and attention (4 Lq Lk H D per scope, self and cross)"""

@@ -32,6 +32,7 @@ def _segments_case(lq, lk, H, D, seed):
     ([63, 64, 65], [64, 63, 129], 3),
     ([256, 257, 300, 7], [1000, 64, 65, 2049], 2),
     ([0, 40, 0, 12], [5, 77, 9, 200], 4),          # empty query segments
+    ([7, 300, 20], [0, 50, 0], 2),                 # segments without keys (O = 0) beside one with keys
     ([300, 45, 129], [700, 130, 33], 11),          # more heads than item queues, not a multiple of them
 ])
 def test_varlen_matches_fp32_reference(lq, lk, H, D):

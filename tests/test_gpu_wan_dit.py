@@ -123,6 +123,27 @@ def test_fused_layernorm_modulate_and_residual_match_torch(S, C):
         assert torch.equal(y.view(torch.int16), ref.view(torch.int16))
 
 
+@pytest.mark.parametrize('S,C', [(257, 3072), (64, 512), (9, 1000), (5, 4096), (3, 5120)])
+def test_fused_residual_layernorm_matches_two_passes(S, C):
+    """x += a [* gate] with the following LayerNorm in one pass: x and the normalised rows bit-equal to
+    gated_residual_ then layernorm_modulate, with and without gate, modulation or affine weights; strided rows
+    (a view of a wider buffer); C over 4096 takes the two-pass path"""
+    print(f'fused residual + layernorm S={S} C={C}', flush=True)
+    g = torch.Generator(device=DEV).manual_seed(C + S)
+    x0 = (torch.randn(S, C + 64, generator=g, device=DEV) * 2 + 0.5).to(torch.bfloat16)
+    a = torch.randn(S, C, generator=g, device=DEV).to(torch.bfloat16)
+    scale, shift, gate = (0.3 * torch.randn(1, C, generator=g, device=DEV) for _ in range(3))
+    w, b = 1 + 0.1 * torch.randn(C, generator=g, device=DEV), 0.1 * torch.randn(C, generator=g, device=DEV)
+    for gt, prm in ((gate, dict(scale=scale, shift=shift)), (None, dict(weight=w, bias=b)), (gate, {})):
+        ref_buf, buf = x0.clone(), x0.clone()
+        x_ref, x = ref_buf[:, :C], buf[:, :C]          # rows of C inside rows of C + 64
+        WD.gated_residual_(x_ref, a, gt)
+        n_ref = WD.layernorm_modulate(x_ref, 1e-6, **prm)
+        n = WD.residual_layernorm_modulate_(x, a, 1e-6, gate=gt, **prm)
+        assert torch.equal(buf.view(torch.int16), ref_buf.view(torch.int16))    # the padding columns untouched too
+        assert torch.equal(n.view(torch.int16), n_ref.view(torch.int16))
+
+
 def test_linear_gelu_epilogue_matches_unfused():
     """the feed-forward's GEMM with GELU (tanh) in the epilogue against linear then GELU: as close to the fp32
     result as the unfused bf16 path, and within two bf16 steps of it"""
