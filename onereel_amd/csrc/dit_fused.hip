@@ -47,19 +47,6 @@ struct LnArgs {
   int64_t a_stride;
 };
 
-// sum over the 64 lanes, the same in every lane: DPP adds within rows of 16 (pairs, quads, halves, rows), then the
-// row pairs and the two halves through v_permlane16_swap / v_permlane32_swap (no LDS round trips)
-__device__ __forceinline__ float wave_sum(float v) {
-  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xf, 0xf, false));
-  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xf, 0xf, false));
-  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xf, 0xf, false));
-  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xf, 0xf, false));
-  auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  v = __uint_as_float(p[0]) + __uint_as_float(p[1]);
-  auto q = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  return __uint_as_float(q[0]) + __uint_as_float(q[1]);
-}
-
 __device__ __forceinline__ void unpack8(u32x4 v, float (&f)[8]) {
 #pragma unroll
   for (int p = 0; p < 4; ++p) {

@@ -38,12 +38,6 @@ struct NormRopeArgs {
   float eps;
 };
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
-}
-
 // One row's inputs: its bf16 words, and this lane's cos / sin entries (d0 = 8 lane mod D, pairs 2p, 2p + 1).
 template <int NCH>
 struct RowIn {
@@ -92,12 +86,12 @@ __device__ __forceinline__ void norm_rope_row(const NormRopeArgs& g, int which, 
       const float y1 = bf2f((uint16_t)(in.x[i][p] >> 16)) * inv * bf2f((uint16_t)(wv[p] >> 16));
       o[p] = pack2(y0 * in.c[p] - y1 * in.s[p], y0 * in.s[p] + y1 * in.c[p]);
     }
-    *(u32x4*)(op + e) = o;
+    __builtin_nontemporal_store(o, (u32x4*)(op + e));
   }
 }
 
-// blockIdx.y picks q or k. The block stages its weight row in LDS; each wavefront loads its next row while it
-// normalises and writes the current one.
+// blockIdx.y picks q or k. The block stages its weight row in LDS; each wavefront takes one row at a time, and the
+// other wavefronts of its SIMD cover the load latency.
 template <int NCH>
 __global__ __launch_bounds__(kThreads) void norm_rope_kernel(NormRopeArgs g) {
   __shared__ __attribute__((aligned(16))) uint16_t wl[64 * 8 * NCH];
@@ -106,17 +100,10 @@ __global__ __launch_bounds__(kThreads) void norm_rope_kernel(NormRopeArgs g) {
   for (int e = 8 * threadIdx.x; e < g.C; e += 8 * kThreads) *(u32x4*)(wl + e) = *(const u32x4*)(g.w[which] + e);
   __syncthreads();
   const int64_t stride = (int64_t)gridDim.x * kWaves;
-  int64_t r = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6);
-  RowIn<NCH> a, b;
-  if (r < g.n_rows) load_row<NCH>(g, which, r, lane, a);
-  while (r < g.n_rows) {
-    if (r + stride < g.n_rows) load_row<NCH>(g, which, r + stride, lane, b);
+  for (int64_t r = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6); r < g.n_rows; r += stride) {
+    RowIn<NCH> a;
+    load_row<NCH>(g, which, r, lane, a);
     norm_rope_row<NCH>(g, which, r, lane, a, wl);
-    r += stride;
-    if (r >= g.n_rows) break;
-    if (r + stride < g.n_rows) load_row<NCH>(g, which, r + stride, lane, a);
-    norm_rope_row<NCH>(g, which, r, lane, b, wl);
-    r += stride;
   }
 }
 
