@@ -181,7 +181,7 @@ def cpu_baseline(heads=16, runs=3):
     except OSError:
         pass
     return dict(value=round(flops / t / 1e12, 4), unit='TFLOP/s', cores=torch.get_num_threads(), kind='port',
-                sample=f'full config-2 layer (layout, packing with RoPE, fp32 SDPA per scope) for {heads} of {H} heads; '
+                sample=f'the full HunyuanVideo-1.5 480p 4-scene layer (layout, packing with RoPE, fp32 SDPA per scope) for {heads} of {H} heads; '
                        f'median of {runs} runs after 1 warm-up: {t:.2f} s on {os.cpu_count()} logical CPUs ({cpu})',
                 seconds=round(t, 3))
 

@@ -247,7 +247,7 @@ def test_packed_attention_matches_explicit_softmax():
 
 
 @pytest.mark.parametrize('case', [
-    dict(lengths=[3, 3], halo=0, extra={0: [5], 1: [0]}, T=8, counts=[4, 4], Le=8),     # config-1 shape, smaller T
+    dict(lengths=[3, 3], halo=0, extra={0: [5], 1: [0]}, T=8, counts=[4, 4], Le=8),     # the 2-scene CPU-plumbing shape, smaller T
     dict(lengths=[2, 3, 2], halo=1, extra={}, T=4, counts=[3, 0, 2], Le=7),             # halo, empty sentence, padding
     dict(lengths=[4, 2], halo=2, sides='next', extra={}, T=5, counts=[2, 2], Le=4),
 ])
