@@ -183,3 +183,19 @@ def test_argument_errors_are_runtime_errors():
             call()
         assert isinstance(e.value, (ValueError, TypeError)), type(e.value)
 
+
+
+def test_fused_residual_layernorm_argument_errors_without_gpu():
+    """or_residual_layernorm_modulate refuses bad widths, a missing or misaligned addend and an output that is x or
+    a before it launches anything (device pointers are never dereferenced on the host)"""
+    f = L.lib().or_residual_layernorm_modulate
+    x, a, out = 0x10000, 0x20000, 0x30000
+
+    def call(x=x, a=a, out=out, C=512, a_stride=512):
+        return L.check(f(x, a, None, out, 4, C, C, a_stride, C, 1e-6, None, None, None, None, None),
+                       'or_residual_layernorm_modulate')
+    for kw, msg in ((dict(C=100), 'multiple of 8'), (dict(C=9000), 'multiple of 8'), (dict(a=None), 'a must be'),
+                    (dict(a=a + 8), 'a must be'), (dict(a_stride=256), 'a must be'), (dict(out=x), 'must not be'),
+                    (dict(out=a), 'must not be'), (dict(x=x + 4), '16-byte aligned')):
+        with pytest.raises(L.HipPathError, match=msg):
+            call(**kw)
