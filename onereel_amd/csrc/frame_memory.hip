@@ -83,7 +83,8 @@ struct SelectArgs {
   float* work;             // [8, C] workspace
 };
 
-__device__ __forceinline__ float wave_sum(float v) {
+// butterfly sum over the 64 lanes by xor shuffles, the same in every lane
+__device__ __forceinline__ float wave_sum_xor(float v) {
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
   return v;
@@ -123,7 +124,7 @@ __device__ __forceinline__ float row_dot(const SelectArgs& g, int n, const float
   const float* x = g.feats + (int64_t)g.cand[n] * g.C;
   float acc = 0.0f;
   for (int e = lane; e < g.C; e += 64) acc += x[e] * cv[e];
-  return wave_sum(acc);
+  return wave_sum_xor(acc);
 }
 
 __global__ __launch_bounds__(kSelThreads) void frame_select_kernel(SelectArgs g) {
@@ -179,7 +180,7 @@ __global__ __launch_bounds__(kSelThreads) void frame_select_kernel(SelectArgs g)
 #pragma unroll
         for (int q = 0; q < 8; ++q) {
           if (i0 + q >= k) break;
-          const float d = wave_sum(acc[q]);
+          const float d = wave_sum_xor(acc[q]);
           if (i0 + q == 0 || d > best) {
             best = d;
             bi = i0 + q;
@@ -216,7 +217,7 @@ __global__ __launch_bounds__(kSelThreads) void frame_select_kernel(SelectArgs g)
       }
 #pragma unroll
       for (int q = 0; q < 8; ++q) {
-        const float p = wave_sum(part[q]);
+        const float p = wave_sum_xor(part[q]);
         if (lane == 0) sv[q * kSelWaves + w] = p;
       }
       __syncthreads();
