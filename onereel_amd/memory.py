@@ -80,7 +80,9 @@ class BoundaryMemory:
             s, n = oh.transpose(1, 2) @ x, oh.sum(1)
             prev = c
             c = torch.where((n > 0)[..., None], s / n.clamp_min(1)[..., None], c)
-            if torch.equal(c, prev):
+            # the first clustering stops once the centroids stand still; the warm updates run their few iterations
+            # without that host read (an iteration after convergence changes nothing, so the result is the same)
+            if iters == ITERS_INIT and torch.equal(c, prev):
                 break
         self.centroids[key] = c
         dist = d.gather(-1, z[..., None])[..., 0]
@@ -91,11 +93,11 @@ class BoundaryMemory:
         first = torch.ones_like(zs, dtype=torch.bool)
         first[:, 1:] = zs[:, 1:] != zs[:, :-1]
         rank = first.cumsum(-1) - 1
-        rep = torch.zeros(H, M, dtype=torch.long, device=x.device)
-        valid = torch.zeros(H, M, dtype=torch.bool, device=x.device)
-        hh = torch.arange(H, device=x.device)[:, None].expand_as(order)
-        rep[hh[first], rank[first]] = order[first]
-        valid[hh[first], rank[first]] = True
+        # each cluster's first member goes to column rank; the other members to a spare column M, dropped after
+        # (scatters instead of boolean indexing, which would read the selection's size back to the host)
+        col = torch.where(first, rank, M)
+        rep = torch.zeros(H, M + 1, dtype=torch.long, device=x.device).scatter_(1, col, order)[:, :M]
+        valid = torch.zeros(H, M + 1, dtype=torch.bool, device=x.device).scatter_(1, col, first)[:, :M]
         return rep, valid
 
 
@@ -111,6 +113,9 @@ class Plan:
     mem: torch.Tensor                    # [n] the piece reads the memory
     cand: torch.Tensor                   # [B] key-buffer rows of the boundary candidates
     owner: torch.Tensor                  # [B] their scene
+    max_qlen: int = 0                    # host copies: the longest piece's queries, local keys, and all local keys
+    max_len: int = 0
+    sum_len: int = 0
 
 
 def make_plan(pieces, cand, owner, device) -> Plan:
@@ -127,7 +132,7 @@ def make_plan(pieces, cand, owner, device) -> Plan:
     return Plan(qrows=torch.cat([q for _, q, _, _ in pieces]), qlen=t([len(q) for _, q, _, _ in pieces]), pad=pad,
                 pmask=pmask, lens=t(lens), scene=t([j for j, _, _, _ in pieces]),
                 mem=torch.tensor([m for *_, m in pieces], dtype=torch.bool, device=device), cand=t(cand),
-                owner=t(owner))
+                owner=t(owner), max_qlen=max(len(q) for _, q, _, _ in pieces), max_len=max(lens), sum_len=sum(lens))
 
 
 def frame_plan(layout: SceneLayout, T: int, token_row, Lv: int, q_pieces, text_ranges=None, text_for=(), Sq: int = 0,
@@ -165,7 +170,15 @@ class MemoryAttention:
         hh = torch.arange(H, device=dev)[:, None, None]
         foreign = valid[:, None, :] & (rep_scene[:, None, :] != p.scene[None, :, None]) & p.mem[None, :, None]
         idx = torch.cat([p.pad[None].expand(H, -1, -1), rep_row[:, None, :].expand(-1, n, -1)], -1) * H + hh
-        kidx = idx[torch.cat([p.pmask[None].expand(H, -1, -1), foreign], -1)].to(torch.int32)
+        keep = torch.cat([p.pmask[None].expand(H, -1, -1), foreign], -1).flatten()
+        # the kept key rows, compacted in (head, piece, position) order without reading their count back: kidx is
+        # sized for every representative kept (host-known bound); rows past the last segment are row 0, packed but
+        # never read (each segment reads its cu_k range)
+        Mr = rep.shape[1]
+        bound = H * (p.sum_len + n * Mr)
+        at = torch.where(keep, keep.cumsum(0) - 1, bound)
+        kidx = torch.zeros(bound + 1, dtype=torch.int32, device=dev).scatter_(0, at, idx.flatten().to(torch.int32))
+        kidx = kidx[:bound]
         qidx = (p.qrows[None] * H + hh[:, 0]).flatten().to(torch.int32)
         lq = p.qlen.repeat(H)
         lk = (p.lens[None] + foreign.sum(-1)).flatten()
@@ -174,7 +187,8 @@ class MemoryAttention:
         # single-head rows: row * H + head of the [rows, H, D] buffers
         qp = gather_rows(q.reshape(Sq * H, 1, D), qidx)
         kp, vp = gather_rows(k.reshape(L * H, 1, D), kidx, v.reshape(L * H, 1, D))
-        o = varlen(qp, kp, vp, cu_q, cu_k, int(lq.max()), int(lk.max()))
+        # max_q / max_k as host bounds (the kernel checks only that a segment's keys span under 2 GiB)
+        o = varlen(qp, kp, vp, cu_q, cu_k, p.max_qlen, p.max_len + Mr)
         out = q.new_zeros(Sq * H, 1, D)
         scatter_rows(o, qidx, out)
         return out.view(Sq, H, D)
