@@ -360,7 +360,7 @@ def run_frame_memory(args):
     # the sums buffers are allocated inside collect; time the kernel on preallocated buffers
     sums, counts = fm.sums[15], fm.counts[15]
     from onereel_amd import _lib as L
-    row0, T_ = fm._rows[next(iter(fm._rows))]
+    row0, T_ = fm.frame_layout(frame)
     call = lambda: L.check(L.lib().or_frame_pool(hs.data_ptr(), S, C, hs.stride(0), row0, T_, lay.n_frames,
                                                  sums.data_ptr(), counts.data_ptr(), st.cuda_stream), 'or_frame_pool')
     t_pool = time_cold(call, reps, st, flush)

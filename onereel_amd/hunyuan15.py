@@ -8,7 +8,9 @@ head-major bounded memory is `onereel_amd.memory`, called directly rather than t
 """
 from __future__ import annotations
 
+from bisect import bisect_right
 from dataclasses import dataclass, field
+from itertools import accumulate
 
 import torch
 
@@ -36,10 +38,12 @@ class Context:
     _rot_full: tuple = None
 
     def step(self) -> int:
-        return (self.fwd - 1) // 2 if self.cfg else self.fwd - 1
+        """denoising step of the current forward (forwards count from 1; with CFG a step takes two forwards)"""
+        return (self.fwd - 1) // (2 if self.cfg else 1)
 
     def cond(self) -> bool:
-        return (self.fwd - 1) % 2 == 0 if self.cfg else True
+        """the current forward is the conditional branch (the first of each CFG pair; always without CFG)"""
+        return not self.cfg or (self.fwd - 1) % 2 == 0
 
     def text_ranges(self) -> list:
         c, out = 0, []
@@ -54,36 +58,41 @@ class Context:
 
 
 def adjacent_positions(lay: SceneLayout, j: int) -> list:
-    """shared_pos = 'adjacent' (global RoPE): per shared frame of scene j, its temporal position (hunyuan15.py:92-100)"""
-    lo, hi = lay.ranges[j]
+    """shared_pos 'adjacent' under global RoPE (hunyuan15.py:92-100): per shared frame of scene j, in shared_frames
+    order, its temporal position. Frames before the scene occupy the slots just before its first frame and frames
+    after it the slots from its end on, each group in time order; a frame listed twice takes its later slot."""
+    first, end = lay.ranges[j]
     shared = lay.shared_frames(j)
-    before, after = sorted(f for f in shared if f < lo), sorted(f for f in shared if f >= hi)
-    pos = {f: lo - len(before) + i for i, f in enumerate(before)}
-    pos.update({f: hi + i for i, f in enumerate(after)})
-    return [pos[f] for f in shared]
+    early = [f for f in shared if f < first]
+    late = [f for f in shared if f >= end]
+    return [first - 1 - sum(e > f for e in early) if f < first else end - 1 + sum(x <= f for x in late)
+            for f in shared]
 
 
 def frame_position(ctx: Context, f: int) -> int:
-    """temporal RoPE index of latent frame f (hunyuan15.py:103-113)"""
+    """temporal RoPE index of latent frame f (hunyuan15.py:103-113): f itself, or with scene_rope its offset inside
+    its rope scene plus one in every scene after the first; IndexError past the rope scenes"""
     if not ctx.scene_rope:
         return f
-    start = 0
-    for n in list(ctx.rope_lengths or ctx.layout.lengths):
-        if f < start + n:
-            return f - start + (start > 0)
-        start += n
-    raise IndexError(f)
+    ends = list(accumulate(ctx.rope_lengths or ctx.layout.lengths))
+    s = bisect_right(ends, f)
+    if s == len(ends):
+        raise IndexError(f)
+    start = ends[s - 1] if s else 0
+    return f - start + (start > 0)
 
 
 def shared_positions(ctx: Context, j: int) -> list:
-    """per shared frame of scene j, its temporal RoPE index under shared_pos = 'adjacent' (hunyuan15.py:116-124)"""
+    """per shared frame of scene j, in shared_frames order, its temporal RoPE index under shared_pos 'adjacent'
+    (hunyuan15.py:116-124): with scene_rope the shared frames follow the scene's last position in time order (a frame
+    listed twice takes its later slot); with global RoPE `adjacent_positions`"""
     lay = ctx.layout
     if not ctx.scene_rope:
         return adjacent_positions(lay, j)
+    first, end = lay.ranges[j]
+    top = max(frame_position(ctx, f) for f in range(first, end))
     shared = lay.shared_frames(j)
-    last = max(frame_position(ctx, f) for f in lay.frames[j])
-    pos = {f: last + 1 + i for i, f in enumerate(sorted(shared))}
-    return [pos[f] for f in shared]
+    return [top + sum(x <= f for x in shared) for f in shared]
 
 
 def _key(ctx: Context, Le: int, adjacent: bool, moves: bool, device):

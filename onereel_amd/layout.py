@@ -1,34 +1,46 @@
-"""Scene layout over the latent frames of one video: the drop-in `SceneLayout` (src/onereel/layout.py:10-78).
+"""`SceneLayout`, the drop-in for src/onereel/layout.py:10-78: the same constructor, fields, methods and results.
 
-Host-side API object. The per-token index arrays of a layout are never built here: `onereel_amd.scene` hands the
-layout to the device layout kernel (`or_layout_build`), which derives the same frame lists on the GPU.
+The object answers frame-list questions on the host (which frames a scene owns, which frames of other scenes it also
+reads, in which order). The per-token index arrays of a layer are never built here: `onereel_amd.scene` copies the
+fields into an `or_layout_desc`, and the device layout kernel derives every scene's shared frames by the same rules
+(csrc/common.h, `scene_shared_frames`). Frame lists are computed arithmetically from the scene boundaries.
 """
 from __future__ import annotations
 
 from dataclasses import dataclass, field
+from itertools import accumulate
 
 import torch
+
+SIDES = ('adj', 'prev', 'next')
 
 
 @dataclass
 class SceneLayout:
-    """lengths: latent frames per scene, in order. A scene also reads `halo` frames of the neighbouring scenes nearest
-    to it: both neighbours ('adj'), only the previous ('prev') or only the next ('next'), and the frames in extra[j]
-    (frame memory: representative frames of other scenes, replaced every denoising step). layout.py:10-22"""
+    """Latent frames 0 .. n_frames-1 cut into consecutive scenes.
+
+    lengths: frame count of every scene, in order, each positive.
+    halo:    frames of each neighbouring scene that a scene also reads (context across the cut).
+    sides:   which neighbours give them: 'adj' the previous and the next scene, 'prev' or 'next' only that one.
+    extra:   scene index -> further frames it reads, e.g. the frame memory's representatives (reassigned per step).
+    """
     lengths: list
     halo: int = 2
     sides: str = 'adj'
     extra: dict = field(default_factory=dict)
 
     def __post_init__(self):
-        assert self.sides in ('adj', 'prev', 'next'), self.sides
-        assert all(n > 0 for n in self.lengths), self.lengths
+        if self.sides not in SIDES:
+            raise AssertionError(f'sides must be one of {SIDES}, got {self.sides!r}')
+        if not all(n > 0 for n in self.lengths):
+            raise AssertionError(f'every scene needs at least one frame: {self.lengths}')
 
     @classmethod
     def even(cls, n_frames: int, n_scenes: int, **kw) -> 'SceneLayout':
-        """scene of frame f = f * n_scenes // n_frames (layout.py:25-28)"""
-        sc = [f * n_scenes // n_frames for f in range(n_frames)]
-        return cls([sc.count(j) for j in range(n_scenes)], **kw)
+        """n_scenes scenes over n_frames frames where frame f falls in scene floor(f * n_scenes / n_frames): scene j
+        then starts at frame ceil(j * n_frames / n_scenes)"""
+        starts = [-(-j * n_frames // n_scenes) for j in range(n_scenes + 1)]
+        return cls([b - a for a, b in zip(starts, starts[1:])], **kw)
 
     @property
     def n_frames(self) -> int:
@@ -44,41 +56,48 @@ class SceneLayout:
 
     @property
     def ranges(self) -> list:
-        out, s = [], 0
-        for n in self.lengths:
-            out.append((s, s + n))
-            s += n
-        return out
+        """per scene (first frame, one past its last frame)"""
+        return [(int(end - n), int(end)) for n, end in zip(self.lengths, accumulate(self.lengths))]
 
     @property
     def frames(self) -> list:
-        return [list(range(lo, hi)) for lo, hi in self.ranges]
+        return [list(range(a, b)) for a, b in self.ranges]
 
     def scene_of_frame(self) -> torch.Tensor:
-        return torch.repeat_interleave(torch.arange(self.n_scenes), torch.tensor(self.lengths))
+        """scene index of every frame (int64 [n_frames])"""
+        return torch.arange(self.n_scenes).repeat_interleave(torch.tensor(self.lengths))
 
     def halo_frames(self, j: int) -> list:
-        """frames of other scenes that scene j reads: the previous neighbour's last frames, then the next one's first"""
-        fr, k, out = self.frames, self.halo, []
-        if k == 0:
-            return out
-        if j > 0 and self.sides in ('adj', 'prev'):
-            out += fr[j - 1][-k:]
-        if j + 1 < self.n_scenes and self.sides in ('adj', 'next'):
-            out += fr[j + 1][:k]
+        """neighbour frames scene j reads: the last `halo` frames before its first frame (sides 'adj' / 'prev'), then
+        the first `halo` frames after its last one (sides 'adj' / 'next'), each clipped to that neighbour's frames"""
+        if self.halo <= 0:
+            return []
+        bounds = self.ranges
+        out = []
+        if j > 0 and self.sides != 'next':
+            a, b = bounds[j - 1]
+            out.extend(range(max(a, b - self.halo), b))
+        if j + 1 < len(bounds) and self.sides != 'prev':
+            a, b = bounds[j + 1]
+            out.extend(range(a, min(b, a + self.halo)))
         return out
 
     def shared_frames(self, j: int) -> list:
-        """frames of other scenes that scene j reads: its halo frames, then its extra frames in order"""
-        lo, hi = self.ranges[j]
-        out = self.halo_frames(j)
-        return out + [f for f in sorted(self.extra.get(j, ())) if not lo <= f < hi and f not in out]
+        """frames scene j reads beyond its own: the halo frames, then extra[j] in ascending order without scene j's
+        own frames and without frames the halo already gave (a frame that extra[j] lists twice is read twice)"""
+        first, end = self.ranges[j]
+        halo = self.halo_frames(j)
+        taken = set(halo).union(range(first, end))
+        return halo + [f for f in sorted(self.extra.get(j, ())) if f not in taken]
 
     def key_frames(self, j: int) -> list:
-        """scene j's own frames, then its shared frames (the key order of the packed varlen layout)"""
-        return self.frames[j] + self.shared_frames(j)
+        """scene j's own frames, then its shared frames: the key order of its packed scope"""
+        first, end = self.ranges[j]
+        return list(range(first, end)) + self.shared_frames(j)
 
     def key_range(self, j: int) -> tuple:
-        """scene j's keys as one contiguous frame range (scene plus halo are adjacent)"""
-        kf = self.key_frames(j)
-        return min(kf), max(kf) + 1
+        """(lowest, one past the highest) key frame of scene j; one contiguous range when its shared frames are
+        adjacent to it (halo only)"""
+        first, end = self.ranges[j]
+        shared = self.shared_frames(j)
+        return min([first] + shared), max([end - 1] + shared) + 1

@@ -100,10 +100,12 @@ class ScopePlan:
         return self
 
     def workspace(self, H: int, D: int) -> torch.Tensor:
-        if H not in self._ws:
+        """the attention workspace of this plan's calls with H heads of D dims (its size depends on both), kept"""
+        key = (int(H), int(D))
+        if key not in self._ws:
             n = L.lib().or_varlen_workspace_size(int(self.n_seg), int(self.sum_q), int(H), int(D))
-            self._ws[H] = torch.empty(int(n), dtype=torch.uint8, device=self.device)
-        return self._ws[H]
+            self._ws[key] = torch.empty(int(n), dtype=torch.uint8, device=self.device)
+        return self._ws[key]
 
     def index_bytes(self) -> int:
         """bytes the layout kernel writes"""

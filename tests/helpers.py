@@ -88,3 +88,72 @@ def assert_close(got, ref, max_abs=2e-2, mean_abs=2e-3, what=''):
     assert torch.isfinite(got.float()).all(), f'{what}: non-finite output'
     assert d.max().item() <= max_abs, f'{what}: max-abs {d.max().item():.3e} > {max_abs}'
     assert d.mean().item() <= mean_abs, f'{what}: mean-abs {d.mean().item():.3e} > {mean_abs}'
+
+
+def gather_src(video, text, src):
+    """rows `src` of the virtual concatenation [video ; text] (text row t encoded as len(video) + t), without
+    materialising the concatenation"""
+    src = torch.as_tensor(np.asarray(src, dtype=np.int64))
+    nv = video.shape[0]
+    out = torch.empty((len(src),) + tuple(video.shape[1:]), dtype=video.dtype)
+    vid = src < nv
+    out[vid] = video[src[vid]]
+    if bool((~vid).any()):
+        out[~vid] = text[src[~vid] - nv]
+    return out
+
+
+def scope_rows_reference(sc, q, k, v, eq, ek, ev, rows, cos=None, sin=None, mode='raw'):
+    """fp32 softmax(q k^T / sqrt(D)) v of the packed query rows `rows` of the oracle's scopes `sc`, each segment's
+    queries and keys gathered (and rotated per `mode`, as the oracle's pack does: 'raw' RoPE at the layout's rotary
+    rows, 'rotated' the _move_shared re-rotation of shared keys, 'none') from the token-order tensors for that
+    segment alone. Returns [len(rows), H, D] in the order of `rows`."""
+    from oracle import attention as OA
+    rows = np.asarray(rows)
+    cu_q, cu_k = np.asarray(sc.cu_q), np.asarray(sc.cu_k)
+    seg = np.searchsorted(cu_q, rows, side='right') - 1
+    D = q.shape[-1]
+    out = torch.empty(len(rows), q.shape[1], D)
+    for s in np.unique(seg):
+        m = seg == s
+        r = rows[m]
+        a, b = int(cu_k[s]), int(cu_k[s + 1])
+        qs = gather_src(q, eq, np.asarray(sc.q_src)[r])
+        ks = gather_src(k, ek, np.asarray(sc.k_src)[a:b])
+        vs = gather_src(v, ev, np.asarray(sc.k_src)[a:b])
+        if mode == 'raw':
+            qs = OA.rotate_rows(qs, np.asarray(sc.q_rope)[r], cos, sin)
+            ks = OA.rotate_rows(ks, np.asarray(sc.k_rope)[a:b], cos, sin)
+        elif mode == 'rotated':
+            ks = OA.move_shared(ks, np.asarray(sc.k_move_a)[a:b], np.asarray(sc.k_move_b)[a:b], cos, sin)
+        else:
+            assert mode == 'none', mode
+        qh, kh, vh = (x.float().transpose(0, 1) for x in (qs, ks, vs))
+        p = torch.softmax(qh @ kh.transpose(1, 2) * D ** -0.5, -1)
+        out[torch.as_tensor(m)] = (p @ vh).transpose(0, 1)
+    return out
+
+
+def packed_rows_reference(sc, k, ek, v, ev, sel, cos=None, sin=None, mode='raw', which='k', q=None, eq=None):
+    """the oracle's packed rows `sel` (bf16, bit for bit what its pack writes) without packing the others: keys and
+    values (which='k', rotated per `mode`), or queries (which='q', rotated when mode == 'raw')"""
+    from oracle import attention as OA
+    sel = np.asarray(sel)
+    if which == 'q':
+        qs = gather_src(q, eq, np.asarray(sc.q_src)[sel])
+        return OA.rotate_rows(qs, np.asarray(sc.q_rope)[sel], cos, sin) if mode == 'raw' else qs
+    src = np.asarray(sc.k_src)[sel]
+    ks, vs = gather_src(k, ek, src), gather_src(v, ev, src)
+    if mode == 'raw':
+        ks = OA.rotate_rows(ks, np.asarray(sc.k_rope)[sel], cos, sin)
+    elif mode == 'rotated':
+        ks = OA.move_shared(ks, np.asarray(sc.k_move_a)[sel], np.asarray(sc.k_move_b)[sel], cos, sin)
+    return ks, vs
+
+
+def sample_packed(cu, n, seed=0):
+    """n random packed rows plus the first and last row of every non-empty segment, sorted"""
+    cu = np.asarray(cu)
+    g = np.random.default_rng(seed)
+    edges = [x for a, b in zip(cu[:-1], cu[1:]) if b > a for x in (a, b - 1)]
+    return np.unique(np.concatenate([g.integers(0, int(cu[-1]), n), np.asarray(edges, dtype=np.int64)]))

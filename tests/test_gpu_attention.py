@@ -4,7 +4,7 @@ import numpy as np
 import pytest
 import torch
 
-from helpers import assert_close, attn_rows_reference, layout_case, rand_bf16, sample_rows
+from helpers import assert_close, attn_rows_reference, layout_case, rand_bf16, sample_rows, scope_rows_reference
 from onereel_amd import _lib as L
 from onereel_amd import attention as A
 from onereel_amd import hunyuan15 as HY
@@ -189,12 +189,13 @@ def _layer_inputs(case, seed=0):
     return q, k, v, eq, ek, ev, cos, sin
 
 
-@pytest.mark.parametrize('name,per_seg', [('cpu_plumbing', None), ('hunyuan480p', 48), ('wan704', 48), ('uneven_K12', 24)])
+@pytest.mark.parametrize('name,per_seg', [('cpu_plumbing', None), ('hunyuan480p', 48), ('wan704', 48),
+                                          ('uneven_K2', 32), ('uneven_K4', 24), ('uneven_K8', 24), ('uneven_K12', 24)])
 @pytest.mark.parametrize('adjacent', [False, True])
 def test_scene_layer_matches_oracle(name, per_seg, adjacent):
     """the fused layer (K/V pack with RoPE, Q RoPE on the load, in-place output) against the oracle's packing plus
-    per-scope fp32 attention; full outputs for the CPU-plumbing layout, sampled query rows (every segment's first / last rows
-    included) at the full-size configs"""
+    per-scope fp32 attention; full outputs for the CPU-plumbing layout, sampled query rows (every segment's first / last
+    rows included) at the full-size configs, each segment's reference built from that segment's keys alone"""
     case = layout_case(name)
     print(f'layer {name} adjacent={adjacent}', flush=True)
     q, k, v, eq, ek, ev, cos, sin = _layer_inputs(case)
@@ -205,9 +206,8 @@ def test_scene_layer_matches_oracle(name, per_seg, adjacent):
     olay = OL.SceneLayout(case['lengths'], case['halo'], case['sides'], case['extra'])
     sc = OL.hunyuan_scopes(olay, case['T'], case['counts'], case['Le'], scene_rope=case['scene_rope'],
                            adjacent=adjacent)
-    qp, kp, vp = OA.pack(sc, q, k, v, eq, ek, ev, cos, sin, mode='raw')
     rows = np.arange(int(sc.cu_q[-1])) if per_seg is None else sample_rows(sc.cu_q, per_seg)
-    ref = attn_rows_reference(qp, kp, vp, sc.cu_q, sc.cu_k, rows)
+    ref = scope_rows_reference(sc, q, k, v, eq, ek, ev, rows, cos, sin, mode='raw')
     got = torch.cat([ov, ot]).cpu()[torch.as_tensor(sc.q_src[rows])]
     assert_close(got, ref, what=f'{name} layer')
     valid = sum(case['counts'])
@@ -240,6 +240,45 @@ def test_scene_layer_reference_flow_and_rotated_inputs(adjacent):
         ov2, ot2 = scene.scene_attention(plan, qr.to(DEV), kr.to(DEV), *g[2:], mode='rotated', fused=fused)
         assert_close(ov2.cpu(), rv2, what=f'rotated video fused={fused}')
         assert_close(ot2.cpu(), rt2, what=f'rotated text fused={fused}')
+
+
+@pytest.mark.parametrize('adjacent', [False, True])
+def test_reference_flow_and_processor_scene_at_480p(adjacent):
+    """at the HunyuanVideo-1.5 480p shape (4 x 8 frames x 1590 + 128 text, frame memory 4, 16 x 128), before
+    (step 0, 'source') and after (step 5, 'adjacent') the shared-position switch: the reference's packed flow
+    (Q / K / V packed, varlen on packed tensors, scatter) on raw inputs, and the reference's own entry
+    Processor.scene on already-rotated q / k (shared keys re-rotated by _move_shared's two rotations through the full
+    rotary table), fused and packed, on sampled query rows against the oracle"""
+    case = layout_case('hunyuan480p')
+    T = case['T']
+    print(f'480p reference flow adjacent={adjacent}', flush=True)
+    q, k, v, eq, ek, ev, cos, sin = _layer_inputs(case, 7)
+    lay = SceneLayout(case['lengths'], halo=0, extra=case['extra'])
+    olay = OL.SceneLayout(case['lengths'], 0, 'adj', case['extra'])
+    sc = OL.hunyuan_scopes(olay, T, case['counts'], case['Le'], scene_rope=True, adjacent=adjacent)
+    rows = sample_rows(sc.cu_q, 24, seed=3)
+    src = torch.as_tensor(sc.q_src[rows])
+    g = [x.to(DEV) for x in (q, k, v, eq, ek, ev, cos, sin)]
+    plan = scene.ScopePlan(lay, T, case['counts'], case['Le'], True, None, adjacent, True, DEV, moves=True)
+    ov, ot = scene.scene_attention(plan, *g, mode='raw', fused=False)
+    ref = scope_rows_reference(sc, q, k, v, eq, ek, ev, rows, cos, sin, mode='raw')
+    assert_close(torch.cat([ov, ot]).cpu()[src], ref, what='480p packed flow, raw inputs')
+    del ov, ot
+    rr = torch.as_tensor(OL.scene_rope_rows(olay, T))
+    qr = OA.apply_rotary_emb(q, cos[rr], sin[rr])
+    kr = OA.apply_rotary_emb(k, cos[rr], sin[rr])
+    ref = scope_rows_reference(sc, qr, kr, v, eq, ek, ev, rows, cos, sin, mode='rotated')
+    ctx = HY.Context(lay, T=T, scene_rope=True, shared_pos='switch', shared_switch=5, cfg=True)
+    ctx.counts = {True: case['counts']}
+    ctx.fwd = 11 if adjacent else 1                       # step 5 or step 0, conditional branch
+    ctx._rot_full = (g[6], g[7])
+    assert ctx.adjacent() == adjacent
+    gqr, gkr = qr.to(DEV), kr.to(DEV)
+    for fused in (True, False):
+        ctx.fused = fused
+        ov, ot = HY.Processor(ctx, 0).scene(gqr, gkr, g[2], g[3], g[4], g[5])
+        assert_close(torch.cat([ov, ot]).cpu()[src], ref, what=f'480p Processor.scene fused={fused}')
+        del ov, ot
 
 
 class _Attn(torch.nn.Module):

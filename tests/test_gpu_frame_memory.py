@@ -32,8 +32,9 @@ def test_frame_pool_matches_index_add_and_is_deterministic(N, C, row0, T):
     for _ in range(2):
         fm = FrameMemory(budget=2)
         fm.reset(lay, 2)
-        fm.collect(frame.to(DEV), hs.to(DEV), layer=0)
-        assert fm._rows[next(iter(fm._rows))] == (row0, T)
+        gframe = frame.to(DEV)
+        fm.collect(gframe, hs.to(DEV), layer=0)
+        assert fm.frame_layout(gframe) == (row0, T)
         outs.append((fm.sums[0].cpu(), fm.counts[0].cpu()))
     s_ref, c_ref = OF.pool(frame, hs, n_frames)
     assert torch.equal(outs[0][0], outs[1][0])
@@ -48,8 +49,9 @@ def test_frame_pool_general_frame_map_uses_index_add():
     frame[3] = -1
     fm = FrameMemory(budget=2)
     fm.reset(SceneLayout([7], halo=0), 2)
-    fm.collect(frame.to(DEV), hs.to(DEV), layer=0)
-    assert fm._rows[next(iter(fm._rows))] is None
+    gframe = frame.to(DEV)
+    fm.collect(gframe, hs.to(DEV), layer=0)
+    assert fm.frame_layout(gframe) is None
     s_ref, c_ref = OF.pool(frame, hs, 7)
     assert (fm.sums[0].cpu().double() - s_ref).abs().max() < 1e-4 and torch.equal(fm.counts[0].cpu(), c_ref.float())
 
@@ -103,3 +105,29 @@ def test_frame_memory_step_cycle():
     assert len(reps) == 2 and min(reps) < 5 <= max(reps)
     for j, (lo, hi) in enumerate(lay.ranges):
         assert lay.extra[j] == [f for f in reps if not lo <= f < hi]
+
+
+def test_frame_map_cache_follows_new_and_changed_maps():
+    """collect with one frame map, drop it, then collect a map of the same length but another T (the caching
+    allocator may give it the old map's memory), then change that map in place: the pooled sums follow the map of
+    each call"""
+    N, C = 60, 64
+    g = torch.Generator().manual_seed(5)
+    hs = torch.randn(N, C, generator=g).to(torch.bfloat16)
+    ghs = hs.to(DEV)
+    fm = FrameMemory(budget=2)
+    fm.reset(SceneLayout([20], halo=0), 2)
+    f1 = (torch.arange(N) // 6).to(DEV)
+    fm.collect(f1, ghs, layer=0)
+    del f1
+    for T, inplace in ((4, False), (3, True)):
+        fm.sums, fm.counts = {}, {}
+        if inplace:
+            f2.copy_((torch.arange(N) // T).to(DEV))
+        else:
+            f2 = (torch.arange(N) // T).to(DEV)
+        fm.collect(f2, ghs, layer=0)
+        assert fm.frame_layout(f2) == (0, T)
+        s_ref, c_ref = OF.pool(f2.cpu(), hs, 20)
+        assert torch.equal(fm.counts[0].cpu(), c_ref.float())
+        assert (fm.sums[0].cpu().double() - s_ref).abs().max() < 1e-4

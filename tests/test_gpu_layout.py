@@ -4,7 +4,7 @@ import numpy as np
 import pytest
 import torch
 
-from helpers import bits, layout_case, rand_bf16
+from helpers import bits, layout_case, packed_rows_reference, rand_bf16, sample_packed
 from onereel_amd.layout import SceneLayout
 from onereel_amd.scene import ScopePlan, pack_rows, scatter
 from oracle import attention as OA
@@ -131,6 +131,36 @@ def test_pack_gather_bit_exact(name, adjacent):
         assert torch.equal(bits(vp.cpu()), bits(rv)), mode
         assert torch.equal(bits(kp.cpu()), bits(rk)), mode
         assert torch.equal(bits(qp.cpu()), bits(rq)), mode
+        del kp, vp, qp
+
+
+@pytest.mark.parametrize('name', ['uneven_K2', 'uneven_K4', 'uneven_K8', 'uneven_K12'])
+@pytest.mark.parametrize('adjacent', [False, True])
+def test_pack_gather_bit_exact_uneven_sweep(name, adjacent):
+    """the uneven scene-count sweep (2-12 scenes of 2-16 frames x 1590 tokens, 64-256 text rows, frame memory 4):
+    every packed K / V / Q row the GPU writes, for 4000 sampled rows plus every segment's first and last row, equals
+    the oracle's row bit for bit in all three RoPE modes"""
+    case = layout_case(name)
+    print(f'pack {name} adjacent={adjacent}', flush=True)
+    H, D, T = case['H'], case['D'], case['T']
+    S = sum(case['lengths']) * T
+    plan, sc = _plans(case, adjacent)
+    cos, sin = _tables(case)
+    q, k, v = (rand_bf16((S, H, D), s) for s in (1, 2, 3))
+    eq, ek, ev = (rand_bf16((case['Le'], H, D), s) for s in (4, 5, 6))
+    gq, gk, gv, geq, gek, gev = (x.to(DEV) for x in (q, k, v, eq, ek, ev))
+    gcos, gsin = cos.to(DEV), sin.to(DEV)
+    sel_k, sel_q = sample_packed(sc.cu_k, 4000, 1), sample_packed(sc.cu_q, 4000, 2)
+    for mode in ('raw', 'rotated', 'none'):
+        kp, vp = pack_rows(plan, gk, gek, 'k', b_video=gv, b_text=gev, cos=gcos, sin=gsin, mode=mode)
+        qmode = 'raw' if mode == 'raw' else 'none'
+        qp = pack_rows(plan, gq, geq, 'q', cos=gcos, sin=gsin, mode=qmode)
+        rk, rv = packed_rows_reference(sc, k, ek, v, ev, sel_k, cos, sin, mode=mode)
+        rq = packed_rows_reference(sc, k, ek, v, ev, sel_q, cos, sin, mode=qmode, which='q', q=q, eq=eq)
+        tk, tq = torch.as_tensor(sel_k).to(DEV), torch.as_tensor(sel_q).to(DEV)
+        assert torch.equal(bits(kp[tk].cpu()), bits(rk)), mode
+        assert torch.equal(bits(vp[tk].cpu()), bits(rv)), mode
+        assert torch.equal(bits(qp[tq].cpu()), bits(rq)), mode
         del kp, vp, qp
 
 

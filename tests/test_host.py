@@ -90,7 +90,6 @@ def _header_symbols():
 
 def test_library_exports_every_declared_symbol():
     syms = _header_symbols()
-    assert len(syms) == 15, syms
     h = ctypes.CDLL(str(L.LIB_PATH))
     for s in syms:
         assert hasattr(h, s), s
@@ -199,3 +198,78 @@ def test_fused_residual_layernorm_argument_errors_without_gpu():
                     (dict(out=a), 'must not be'), (dict(x=x + 4), '16-byte aligned')):
         with pytest.raises(L.HipPathError, match=msg):
             call(**kw)
+
+
+def test_generated_key_loop_is_current(tmp_path):
+    """the tracked asm key loop of the 64-query attention kernel is exactly what its generator writes (the build
+    regenerates it; a stale tracked copy would differ from the code that runs)"""
+    import subprocess
+    import sys
+    csrc = ROOT / 'onereel_amd' / 'csrc'
+    out = tmp_path / 'attn_ring64.inc'
+    subprocess.run([sys.executable, str(csrc / 'gen_attn_ring64.py'), '--out', str(out)], check=True)
+    assert out.read_bytes() == (csrc / 'attn_ring64.inc').read_bytes()
+
+
+def test_plan_workspace_is_per_head_count_and_head_dim():
+    """ScopePlan.workspace keys its buffer on (heads, head_dim): the size or_varlen_fwd needs depends on both, so a
+    plan reused at another head_dim gets a buffer of that size (no GPU: the buffer is allocated on the CPU here)"""
+    from onereel_amd.scene import ScopePlan
+    plan = ScopePlan.__new__(ScopePlan)
+    plan.n_seg, plan.sum_q, plan.device, plan._ws = 8, 700, torch.device('cpu'), {}
+    sizes = {(H, D): int(L.lib().or_varlen_workspace_size(8, 700, H, D)) for H, D in ((16, 64), (16, 128), (4, 128))}
+    assert sizes[(16, 64)] != sizes[(16, 128)]
+    for (H, D), n in sizes.items():
+        assert plan.workspace(H, D).numel() == n
+    assert plan.workspace(16, 64) is plan.workspace(16, 64)
+
+
+def test_host_api_agrees_with_oracle_on_random_layouts():
+    """the product's host API (SceneLayout frame lists, comm runs, RoPE position helpers, FrameMemory extras) against
+    the oracle on random layouts: repeated and out-of-range-of-scene extra frames, every halo side, scene RoPE over
+    other scene lengths"""
+    rng = np.random.default_rng(11)
+    for _ in range(400):
+        n = int(rng.integers(1, 7))
+        lengths = rng.integers(1, 6, n).tolist()
+        F = sum(lengths)
+        extra = {j: rng.integers(0, F, int(rng.integers(0, 6))).tolist() for j in range(n) if rng.random() < 0.8}
+        halo, sides = int(rng.integers(0, 4)), ['adj', 'prev', 'next'][int(rng.integers(3))]
+        rl = None
+        if rng.random() < 0.3:
+            rl, left = [], F
+            while left > 0:
+                rl.append(int(rng.integers(1, left + 1)))
+                left -= rl[-1]
+        lay, olay = SceneLayout(lengths, halo, sides, extra), OL.SceneLayout(lengths, halo, sides, extra)
+        assert lay.ranges == olay.ranges and lay.frames == olay.frames
+        for j in range(n):
+            assert lay.halo_frames(j) == olay.halo_frames(j) and lay.shared_frames(j) == olay.shared_frames(j)
+            assert lay.key_frames(j) == olay.key_frames(j)
+            kf = olay.key_frames(j)
+            assert lay.key_range(j) == (min(kf), max(kf) + 1)
+            assert [tuple(r) for r in comm.runs(kf)] == [tuple(r) for r in OL.runs(kf)]
+        for scene_rope in (False, True):
+            ctx = HY.Context(lay, scene_rope=scene_rope, rope_lengths=rl)
+            for j in range(n):
+                assert HY.adjacent_positions(lay, j) == OL.adjacent_positions(olay, j)
+                assert HY.shared_positions(ctx, j) == OL.shared_positions(olay, j, scene_rope, rl)
+            assert [HY.frame_position(ctx, f) for f in range(F)] == [OL.frame_position(olay, f, scene_rope, rl)
+                                                                     for f in range(F)]
+        reps = sorted(set(rng.integers(0, F, 3).tolist()))
+        sink = tuple(sorted(set(rng.integers(0, F, int(rng.integers(0, 2))).tolist())))
+        fm = FrameMemory(budget=4, fallback=(int(rng.integers(0, 3)), sides), sink=sink)
+        fm.reset(SceneLayout(lengths, halo=0), 4)
+        om = OL.FrameMemoryExtra(budget=4, fallback=fm.fallback, sink=sink)
+        olay0 = OL.SceneLayout(lengths, 0)
+        om.reset(olay0)
+        assert fm.layout.extra == olay0.extra
+        fm.set_representatives(reps)
+        fm.begin_step(1)
+        om.propose(reps)
+        om.begin_step(1)
+        assert fm.layout.extra == olay0.extra
+    for F in range(1, 30):
+        for k in range(1, F + 1):
+            sc = [f * k // F for f in range(F)]
+            assert SceneLayout.even(F, k).lengths == [sc.count(j) for j in range(k)]

@@ -407,3 +407,32 @@ def test_memory_select_one_representative_per_separated_group():
     rep, valid = OM.select(x, 4)
     for h in range(2):
         assert sorted(r // 10 for r in rep[h][valid[h]].tolist()) == [0, 1, 2, 3]
+
+
+@pytest.mark.parametrize('mode', ['raw', 'rotated', 'none'])
+@pytest.mark.parametrize('adjacent', [False, True])
+def test_sampled_row_references_match_the_full_pack(mode, adjacent):
+    """the GPU tests' sampled-row references (per-segment gathers) give exactly the rows of the oracle's full pack
+    and of its packed attention, on the CPU-plumbing layout"""
+    import helpers as Hp
+    case = Hp.layout_case('cpu_plumbing')
+    H, D, T = case['H'], case['D'], case['T']
+    S = sum(case['lengths']) * T
+    q, k, v = (Hp.rand_bf16((S, H, D), s) for s in (1, 2, 3))
+    eq, ek, ev = (Hp.rand_bf16((case['Le'], H, D), s) for s in (4, 5, 6))
+    cos, sin = OA.rope_table_3d(*case['table'], D)
+    sc = OL.hunyuan_scopes(OL.SceneLayout(case['lengths'], 0, 'adj', case['extra']), T, case['counts'], case['Le'],
+                           scene_rope=True, adjacent=adjacent)
+    qp, kp, vp = OA.pack(sc, q, k, v, eq, ek, ev, cos, sin, mode=mode)
+    sel = Hp.sample_packed(sc.cu_k, 50)
+    ks, vs = Hp.packed_rows_reference(sc, k, ek, v, ev, sel, cos, sin, mode=mode)
+    assert torch.equal(ks.view(torch.int16), kp[sel].view(torch.int16))
+    assert torch.equal(vs.view(torch.int16), vp[sel].view(torch.int16))
+    qmode = 'raw' if mode == 'raw' else 'none'
+    selq = Hp.sample_packed(sc.cu_q, 30)
+    qs = Hp.packed_rows_reference(sc, k, ek, v, ev, selq, cos, sin, mode=qmode, which='q', q=q, eq=eq)
+    assert torch.equal(qs.view(torch.int16), OA.pack(sc, q, k, v, eq, ek, ev, cos, sin, mode=qmode)[0][selq]
+                       .view(torch.int16))
+    rows = Hp.sample_rows(sc.cu_q, 20)
+    full = OA.packed_attention(qp, kp, vp, sc.cu_q, sc.cu_k)[rows]
+    assert (Hp.scope_rows_reference(sc, q, k, v, eq, ek, ev, rows, cos, sin, mode=mode) - full).abs().max() < 1e-5
