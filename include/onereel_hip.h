@@ -160,6 +160,19 @@ int64_t or_varlen_workspace_size(int32_t n_seg, int32_t sum_q, int32_t H, int32_
  * D = 128, 32 at D = 64). */
 int or_varlen_fwd(const or_varlen_args* args, void* stream);
 
+/* Bytes of the device array that or_varlen_fwd_noalloc uses in place of a caller workspace (one per GPU). */
+#define OR_NOALLOC_SCRATCH_BYTES (32ll << 20)
+
+/* No counterpart in the reference: or_varlen_fwd for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc). Same arguments and results; args->workspace and
+ * args->workspace_bytes are ignored. The work-item queue (and the key-split partials) live in a fixed array of
+ * OR_NOALLOC_SCRATCH_BYTES bytes inside the library, one per GPU, held until the process ends; no call allocates or
+ * frees memory. A call whose queue alone exceeds the array is rejected (-1). Calls with few work items split fewer
+ * of them by keys when the partials would not fit (the same results within the kernel's rounding). Every call on a
+ * GPU shares that GPU's array: calls that overlap on one GPU (other streams, other threads) race and must be
+ * serialised by the caller; calls on one stream are ordered. */
+int or_varlen_fwd_noalloc(const or_varlen_args* args, void* stream);
+
 /* Replaces the log-sum-exp merge of partial attention results: ring._merge (src/onereel/parallel/ring.py:63-70) and
  * the merge in Processor._far_lse (src/onereel/models/hunyuan15.py:270-275). o: fp32 [n_rows, H, D] (row stride
  * o_row_stride elements), lse: fp32 [H, n_rows], both updated in place with the partial result o_s: bf16

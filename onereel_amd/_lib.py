@@ -55,6 +55,7 @@ SIGNATURES = {
     'or_scatter': (i32, [vp, vp, i64, i64, vp, vp, i64, i64, i64, i64, i32, i32, vp]),
     'or_varlen_workspace_size': (i64, [i32, i32, i32, i32]),
     'or_varlen_fwd': (i32, [ctypes.POINTER(VarlenArgs), vp]),
+    'or_varlen_fwd_noalloc': (i32, [ctypes.POINTER(VarlenArgs), vp]),
     'or_lse_merge': (i32, [vp, vp, vp, vp, i64, i32, i32, i64, i64, vp]),
     'or_rmsnorm_rope': (i32, [vp, vp, vp, vp, i64, i64, i64, i32, i32, ctypes.c_float, vp, vp, vp, i64, vp, vp, i64,
                               i64, vp]),

@@ -19,8 +19,13 @@
 // - Optional RoPE on the Q load (table row per packed query), with the rounding of diffusers apply_rotary_emb.
 #include <math.h>
 
+#include <mutex>
+
 #include "common.h"
 #include "attn_ring64.inc"
+
+// work-item queue and key-split partials of or_varlen_fwd_noalloc (see scratch_of_current_device)
+static __device__ __align__(256) unsigned char scratch[OR_NOALLOC_SCRATCH_BYTES];
 
 namespace onereel {
 
@@ -874,13 +879,13 @@ int64_t split_parts_cap(int32_t n_seg, int32_t sum_q, int32_t H, int32_t D) {
 }
 
 // workspace layout (bytes): queue headers and the item list, the split table (3 words per split item, at most cap / 2
-// of them), then (16-byte aligned) the parts' lse and O / l
+// of them), then (16-byte aligned) the parts' lse and O / l, for at most `cap` key-split parts
 struct WsLayout {
   int64_t tab, lse, o, total;
 };
 
-WsLayout ws_layout(int32_t n_seg, int32_t sum_q, int32_t H, int32_t D) {
-  const int64_t mi = max_items_of(n_seg, sum_q, H), cap = split_parts_cap(n_seg, sum_q, H, D);
+WsLayout ws_layout(int32_t n_seg, int32_t sum_q, int32_t H, int64_t cap) {
+  const int64_t mi = max_items_of(n_seg, sum_q, H);
   WsLayout l;
   l.tab = (kWsHeader + kItemWords * (mi + cap)) * 4;
   l.lse = (l.tab + (cap / 2) * 3 * 4 + 15) / 16 * 16;
@@ -891,41 +896,32 @@ WsLayout ws_layout(int32_t n_seg, int32_t sum_q, int32_t H, int32_t D) {
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
-}  // namespace
-}  // namespace onereel
-
-using namespace onereel;
-
-extern "C" int64_t or_varlen_workspace_size(int32_t n_seg, int32_t sum_q, int32_t H, int32_t D) {
-  if (n_seg < 0 || sum_q < 0 || H < 1) return -1;
-  return ws_layout(n_seg, sum_q, H, D).total;
-}
-
-extern "C" int or_varlen_fwd(const or_varlen_args* p, void* stream) {
-  if (!p) return fail_arg("or_varlen_fwd: args is NULL");
-  const or_varlen_args& x = *p;
-  if (x.D != 64 && x.D != 128) return fail_arg("or_varlen_fwd: head_dim %d not supported (64 or 128)", x.D);
-  if (x.H < 1 || x.H > 256) return fail_arg("or_varlen_fwd: H=%d outside [1, 256]", x.H);
-  if (x.n_seg < 1 || x.n_seg > kMaxPlanSeg) return fail_arg("or_varlen_fwd: n_seg=%d outside [1, %d]", x.n_seg, kMaxPlanSeg);
-  if (x.sum_q < 0) return fail_arg("or_varlen_fwd: sum_q < 0");
-  if (!x.q || !x.k || !x.v || !x.o || !x.cu_q) return fail_arg("or_varlen_fwd: q, k, v, o and cu_q are required");
-  if (!x.cu_k && !(x.k_off && x.k_len)) return fail_arg("or_varlen_fwd: need cu_k, or k_off with k_len");
-  if (x.k_off && !x.k_len) return fail_arg("or_varlen_fwd: k_off needs k_len (the per-segment key counts)");
+// argument checks shared by both entry points (everything but the workspace)
+int check_args(const or_varlen_args& x, const char* fn) {
+  if (x.D != 64 && x.D != 128) return fail_arg("%s: head_dim %d not supported (64 or 128)", fn, x.D);
+  if (x.H < 1 || x.H > 256) return fail_arg("%s: H=%d outside [1, 256]", fn, x.H);
+  if (x.n_seg < 1 || x.n_seg > kMaxPlanSeg) return fail_arg("%s: n_seg=%d outside [1, %d]", fn, x.n_seg, kMaxPlanSeg);
+  if (x.sum_q < 0) return fail_arg("%s: sum_q < 0", fn);
+  if (!x.q || !x.k || !x.v || !x.o || !x.cu_q) return fail_arg("%s: q, k, v, o and cu_q are required", fn);
+  if (!x.cu_k && !(x.k_off && x.k_len)) return fail_arg("%s: need cu_k, or k_off with k_len", fn);
+  if (x.k_off && !x.k_len) return fail_arg("%s: k_off needs k_len (the per-segment key counts)", fn);
   if (x.q_rope && (!x.cos_table || !x.sin_table || x.n_rope_rows < 1))
-    return fail_arg("or_varlen_fwd: q_rope needs cos / sin tables");
+    return fail_arg("%s: q_rope needs cos / sin tables", fn);
   if (x.q_row_stride < (int64_t)x.H * x.D || x.k_row_stride < (int64_t)x.H * x.D || x.o_row_stride < (int64_t)x.H * x.D)
-    return fail_arg("or_varlen_fwd: row strides must cover H * D elements");
+    return fail_arg("%s: row strides must cover H * D elements", fn);
   if (x.q_row_stride % 8 || x.k_row_stride % 8 || x.o_row_stride % 8 || !aligned16(x.q) || !aligned16(x.k) ||
       !aligned16(x.v) || !aligned16(x.o) || (x.q_text && !aligned16(x.q_text)) || (x.o_text && !aligned16(x.o_text)))
-    return fail_arg("or_varlen_fwd: pointers must be 16-byte aligned and row strides multiples of 8 elements");
+    return fail_arg("%s: pointers must be 16-byte aligned and row strides multiples of 8 elements", fn);
   if (x.cos_table && (((uintptr_t)x.cos_table | (uintptr_t)x.sin_table) & 15u))
-    return fail_arg("or_varlen_fwd: rotary tables must be 16-byte aligned");
+    return fail_arg("%s: rotary tables must be 16-byte aligned", fn);
   if ((int64_t)(x.max_k + 8 * 32) * x.k_row_stride * 2 > 0x7fffffffLL)
-    return fail_arg("or_varlen_fwd: a segment's keys span more than 2 GiB (max_k %d x row stride %lld)", x.max_k,
+    return fail_arg("%s: a segment's keys span more than 2 GiB (max_k %d x row stride %lld)", fn, x.max_k,
                     (long long)x.k_row_stride);
-  const int64_t need = or_varlen_workspace_size(x.n_seg, x.sum_q, x.H, x.D);
-  if (!x.workspace || x.workspace_bytes < need || !aligned16(x.workspace))
-    return fail_arg("or_varlen_fwd: a 16-byte aligned workspace of %lld bytes is needed", (long long)need);
+  return 0;
+}
+
+// planner + attention kernel (+ merge of key-split parts) on workspace `wsp`, laid out by ws_layout(..., cap)
+int launch_varlen(const or_varlen_args& x, void* wsp, int64_t cap, hipStream_t st) {
   if (x.sum_q == 0) return 0;
   DevInfo di;
   if (int rc = dev_info(di)) return rc;
@@ -935,7 +931,6 @@ extern "C" int or_varlen_fwd(const or_varlen_args* p, void* stream) {
   // persistent blocks: one per resident slot, but no more than the work entries (items, or their key parts when
   // the planner may split items: only when even the fewest items the call can have come in few rounds)
   int64_t grid = (int64_t)di.cus * occ;
-  const int64_t cap = split_parts_cap(x.n_seg, x.sum_q, x.H, x.D);
   const bool may_split = cap > 0 && min_items_of(x.sum_q, x.H, x.D) < kSplitMaxRounds * grid;
   const int64_t entries = max_items * (may_split ? kMaxSplitWays : 1);
   if (grid > entries) grid = entries;
@@ -964,13 +959,13 @@ extern "C" int or_varlen_fwd(const or_varlen_args* p, void* stream) {
   a.H = x.H;
   a.scale = x.scale;
   a.c = x.scale * 1.4426950408889634f;
-  int32_t* ws = (int32_t*)x.workspace;
-  const WsLayout wl = ws_layout(x.n_seg, x.sum_q, x.H, x.D);
-  a.split_tab = (int32_t*)((char*)x.workspace + wl.tab);
-  a.split_lse = (float*)((char*)x.workspace + wl.lse);
-  a.split_o = (float*)((char*)x.workspace + wl.o);
-  hipStream_t st = (hipStream_t)stream;
-  // the planner needs key counts only: k_len when given, else the cu_k differences
+  int32_t* ws = (int32_t*)wsp;
+  const WsLayout wl = ws_layout(x.n_seg, x.sum_q, x.H, cap);
+  a.split_tab = (int32_t*)((char*)wsp + wl.tab);
+  a.split_lse = (float*)((char*)wsp + wl.lse);
+  a.split_o = (float*)((char*)wsp + wl.o);
+  // the planner needs key counts only: k_len when given, else the cu_k differences. It writes every word of the
+  // workspace the other kernels read (queue headers, item list, split table) before they run.
   hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(kPlanThreads), 0, st, x.cu_q, x.cu_k, x.k_len ? x.k_off : nullptr,
                      x.k_len, x.seg_q_src, x.n_seg, x.H, item_bq(x.D), (int)max_items, (int)grid,
                      may_split ? 1 : 0, (int)cap, ws);
@@ -984,4 +979,67 @@ extern "C" int or_varlen_fwd(const or_varlen_args* p, void* stream) {
     return check_hip(hipGetLastError(), "merge_kernel launch");
   }
   return 0;
+}
+
+// ------------------------------------------------------------------------------------------------------------------
+// Library-held workspace of or_varlen_fwd_noalloc: one array per GPU, created with the code object on that GPU and
+// held until the process ends. The host name `scratch` is only a stand-in for the symbol: its device address on the
+// current GPU comes from hipGetSymbolAddress, once per device, and only that address is passed to kernels.
+constexpr int64_t kScratchBytes = OR_NOALLOC_SCRATCH_BYTES;
+constexpr int kMaxDevices = 64;
+
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+int scratch_of_current_device(void** out) {
+  int dev = 0;
+  if (int rc = check_hip(hipGetDevice(&dev), "hipGetDevice")) return rc;
+  if (dev < 0 || dev >= kMaxDevices) return fail_arg("or_varlen_fwd_noalloc: device %d beyond %d", dev, kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    if (int rc = check_hip(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)")) return rc;
+    if (!p) return fail_arg("or_varlen_fwd_noalloc: no device address for the scratch array");
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return 0;
+}
+
+}  // namespace
+}  // namespace onereel
+
+using namespace onereel;
+
+extern "C" int64_t or_varlen_workspace_size(int32_t n_seg, int32_t sum_q, int32_t H, int32_t D) {
+  if (n_seg < 0 || sum_q < 0 || H < 1) return -1;
+  return ws_layout(n_seg, sum_q, H, split_parts_cap(n_seg, sum_q, H, D)).total;
+}
+
+extern "C" int or_varlen_fwd(const or_varlen_args* p, void* stream) {
+  if (!p) return fail_arg("or_varlen_fwd: args is NULL");
+  const or_varlen_args& x = *p;
+  if (int rc = check_args(x, "or_varlen_fwd")) return rc;
+  const int64_t need = or_varlen_workspace_size(x.n_seg, x.sum_q, x.H, x.D);
+  if (!x.workspace || x.workspace_bytes < need || !aligned16(x.workspace))
+    return fail_arg("or_varlen_fwd: a 16-byte aligned workspace of %lld bytes is needed", (long long)need);
+  return launch_varlen(x, x.workspace, split_parts_cap(x.n_seg, x.sum_q, x.H, x.D), (hipStream_t)stream);
+}
+
+extern "C" int or_varlen_fwd_noalloc(const or_varlen_args* p, void* stream) {
+  if (!p) return fail_arg("or_varlen_fwd_noalloc: args is NULL");
+  const or_varlen_args& x = *p;
+  if (int rc = check_args(x, "or_varlen_fwd_noalloc")) return rc;
+  // key-split parts: as many as or_varlen_fwd would use, fewer when their partial results do not fit the array
+  int64_t cap = split_parts_cap(x.n_seg, x.sum_q, x.H, x.D);
+  const int64_t base = ws_layout(x.n_seg, x.sum_q, x.H, 0).total;
+  if (base > kScratchBytes)
+    return fail_arg("or_varlen_fwd_noalloc: the call needs %lld bytes of work-item queue, more than the %lld-byte "
+                    "library array (fewer packed queries, segments or heads per call, or or_varlen_fwd with a "
+                    "caller workspace)", (long long)base, (long long)kScratchBytes);
+  while (cap > 0 && ws_layout(x.n_seg, x.sum_q, x.H, cap).total > kScratchBytes) cap = cap * 3 / 4;
+  if (x.sum_q == 0) return 0;
+  void* ws = nullptr;
+  if (int rc = scratch_of_current_device(&ws)) return rc;
+  return launch_varlen(x, ws, cap, (hipStream_t)stream);
 }

@@ -211,8 +211,9 @@ def scatter_rows(packed: torch.Tensor, idx: torch.Tensor, out: torch.Tensor):
 
 def varlen(q, k, v, cu_q, cu_k, max_q, max_k, *, k_off=None, k_len=None, out=None, lse=None, seg_q_src=None,
            q_text=None, o_text=None, n_q_video=None, q_rope=None, cos=None, sin=None, sum_q=None, workspace=None,
-           scale=None):
-    """or_varlen_fwd on torch tensors. Returns out (allocated [Nq, H, D] when not given)."""
+           scale=None, noalloc=False):
+    """or_varlen_fwd on torch tensors. Returns out (allocated [Nq, H, D] when not given). noalloc=True calls
+    or_varlen_fwd_noalloc instead: no workspace, the library's fixed per-GPU array (calls must not overlap on a GPU)."""
     H, D = k.shape[1], k.shape[2]
     _check_bf16(q, k, v, q_text, out, o_text)
     _, qs = _rows2d(q, H, D)
@@ -235,7 +236,7 @@ def varlen(q, k, v, cu_q, cu_k, max_q, max_k, *, k_off=None, k_len=None, out=Non
     if o_text is not None and o_text.shape[0] and o_text.stride(0) != os_:
         raise L.HipValueError('o and o_text must have the same row stride')
     cos, sin, n_rope_rows = _tables(cos, sin, D) if q_rope is not None else (None, None, 0)
-    if workspace is None:
+    if workspace is None and not noalloc:
         nb = L.lib().or_varlen_workspace_size(int(n_seg), int(sum_q), int(H), int(D))
         workspace = torch.empty(int(nb), dtype=torch.uint8, device=q.device)
     a = L.VarlenArgs()
@@ -250,6 +251,11 @@ def varlen(q, k, v, cu_q, cu_k, max_q, max_k, *, k_off=None, k_len=None, out=Non
     a.q_row_stride, a.k_row_stride, a.o_row_stride = qs, ks, os_
     a.n_seg, a.sum_q, a.max_q, a.max_k, a.H, a.D = int(n_seg), int(sum_q), int(max_q), int(max_k), H, D
     a.scale = float(D ** -0.5 if scale is None else scale)
+    if noalloc:
+        a.workspace, a.workspace_bytes = None, 0
+        with torch.cuda.device(q.device):
+            L.check(L.lib().or_varlen_fwd_noalloc(ctypes.byref(a), L.stream_handle(q.device)), 'or_varlen_fwd_noalloc')
+        return out
     a.workspace, a.workspace_bytes = workspace.data_ptr(), workspace.numel()
     L.check(L.lib().or_varlen_fwd(ctypes.byref(a), L.stream_handle(q.device)), 'or_varlen_fwd')
     return out
