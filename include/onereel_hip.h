@@ -10,6 +10,7 @@
  *   or_rmsnorm_rope   fused RMSNorm + interleaved RoPE of the Wan self-attention's queries and keys
  *   or_frame_pool     frame memory: per-frame sums of hidden states (deterministic)
  *   or_frame_select   frame memory: k-means (cosine) representatives and their medoids, one workgroup
+ *   or_memory_select, or_memory_index         bounded memory: per-head k-means representatives, per-piece key lists
  *   or_layernorm_modulate, or_gated_residual,
  *   or_residual_layernorm_modulate             the fused elementwise work of the Wan-shaped DiT block harness
  *
@@ -116,7 +117,8 @@ int or_scatter(const void* packed, const int32_t* dst_idx, int64_t n_rows, int64
 /* Arguments of or_varlen_fwd. Segment s has queries [cu_q[s], cu_q[s+1]) of the packed query space and keys
  * k[k_start .. k_start + k_len) with k_start = k_off ? k_off[s] : cu_k[s] and k_len = k_len ? k_len[s] :
  * cu_k[s+1] - cu_k[s]. Query i of segment s is read from (and its output written to) source row
- * (seg_q_src ? seg_q_src[s] : cu_q[s]) + i, a row of q / o when below n_q_video, else of q_text / o_text. */
+ * (seg_q_src ? seg_q_src[s] : cu_q[s]) + i * max(q_row_step, 1), a row of q / o when below n_q_video, else of
+ * q_text / o_text. */
 typedef struct or_varlen_args {
   const void* q;            /* bf16 [.., H, D] rows with stride q_row_stride */
   const void* q_text;       /* bf16 text query rows (may equal q when n_q_video covers every row) */
@@ -147,6 +149,9 @@ typedef struct or_varlen_args {
   float scale;              /* softmax scale, D^-0.5 in the reference */
   void* workspace;          /* device scratch of or_varlen_workspace_size() bytes */
   int64_t workspace_bytes;
+  int32_t q_row_step;       /* 0 or 1: a segment's queries are consecutive source rows; s > 1 (with seg_q_src):
+                               query i of segment s is source row seg_q_src[s] + i * s, and its output row too
+                               (e.g. one head of [tokens, H, D] rows viewed as [tokens * H, 1, D]: s = H) */
 } or_varlen_args;
 
 /* Bytes of device workspace or_varlen_fwd needs for this many segments, packed queries and heads: the work-item
@@ -229,6 +234,33 @@ int or_residual_layernorm_modulate(void* x, const void* a, const float* gate, vo
                                    int64_t x_row_stride, int64_t a_row_stride, int64_t out_row_stride, float eps,
                                    const float* weight, const float* bias, const float* scale, const float* shift,
                                    void* stream);
+
+/* Bytes of device workspace or_memory_select needs: the normalised keys [H, B, D] fp32 and per-candidate arrays. */
+int64_t or_memory_select_workspace_size(int32_t B, int32_t H, int32_t D, int32_t M, int32_t iters);
+
+/* Replaces BoundaryMemory.select (src/onereel/memory.py:58-93): per head h, k-means over the B candidate keys
+ * x_b = key_b / max(|key_b|, 1e-12) (key_b: row rows[b] (or b) of keys, head h, D elements; bf16, or fp32 when
+ * fp32_keys) into M clusters with squared Euclidean distance |x|^2 - 2 x.c + |c|^2 (fp32; the nearest centroid, the
+ * lowest index on equal distances), centroids (fp32 [H, M, D], 16-byte aligned) updated in place: from the
+ * candidates init[i] (int32 [M]) when init != NULL, else from their current values; `iters` update passes, an empty
+ * cluster keeping its centroid, stopping early once no centroid moves (device-side: no host read). Then per head,
+ * for every non-empty cluster in cluster order, the member nearest its centroid (the lowest candidate on equal
+ * distances): rep (int64 [H, M]) = those candidates, valid (uint8 [H, M]) = 1, zeros after them. M <= min(B, 1024),
+ * D 64 or 128; keys and centroids 16-byte aligned, key rows a multiple of 16 bytes apart. Sums are taken in a fixed
+ * order (deterministic). */
+int or_memory_select(const void* keys, int32_t fp32_keys, const int32_t* rows, int64_t key_row_stride, int32_t B,
+                     int32_t H, int32_t D, int32_t M, float* centroids, const int32_t* init, int32_t iters,
+                     int64_t* rep, uint8_t* valid, void* workspace, int64_t workspace_bytes, void* stream);
+
+/* Replaces the key-list building of MemoryAttention.__call__ (src/onereel/memory.py:152-168), the per-call part: for
+ * every piece i and head h (segment h * n_pieces + i), after the piece's piece_len[i] local keys at
+ * kidx[k_off[seg] ..], the single-head rows cand_row[rep[h, r]] * H + h of head h's valid representatives r (in
+ * order) whose scene cand_scene[rep[h, r]] differs from piece_scene[i], when piece_mem[i]; k_len[seg] = piece_len[i]
+ * + their count. kidx must hold piece_len[i] + M entries from k_off[seg]. One launch. */
+int or_memory_index(const int64_t* rep, const uint8_t* valid, const int64_t* cand_row, const int64_t* cand_scene,
+                    const int64_t* piece_scene, const uint8_t* piece_mem, const int32_t* piece_len,
+                    const int32_t* k_off, int32_t n_pieces, int32_t H, int32_t M, int32_t* kidx, int32_t* k_len,
+                    void* stream);
 
 /* Message of the calling thread's last failed call ("" if none). */
 const char* or_last_error(void);

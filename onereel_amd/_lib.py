@@ -44,7 +44,7 @@ class VarlenArgs(ctypes.Structure):
                 ('cos_table', vp), ('sin_table', vp), ('n_rope_rows', i64), ('n_q_video', i64),
                 ('q_row_stride', i64), ('k_row_stride', i64), ('o_row_stride', i64), ('n_seg', i32), ('sum_q', i32),
                 ('max_q', i32), ('max_k', i32), ('H', i32), ('D', i32), ('scale', ctypes.c_float),
-                ('workspace', vp), ('workspace_bytes', i64)]
+                ('workspace', vp), ('workspace_bytes', i64), ('q_row_step', i32)]
 
 
 # every exported symbol with its ctypes signature: include/onereel_hip.h
@@ -61,6 +61,9 @@ SIGNATURES = {
                               i64, vp]),
     'or_frame_pool': (i32, [vp, i64, i32, i64, i64, i32, i32, vp, vp, vp]),
     'or_frame_select': (i32, [vp, i32, i32, vp, i32, i32, i32, vp, vp, vp]),
+    'or_memory_select_workspace_size': (i64, [i32, i32, i32, i32, i32]),
+    'or_memory_select': (i32, [vp, i32, vp, i64, i32, i32, i32, i32, vp, vp, i32, vp, vp, vp, i64, vp]),
+    'or_memory_index': (i32, [vp, vp, vp, vp, vp, vp, vp, vp, i32, i32, i32, vp, vp, vp]),
     'or_layernorm_modulate': (i32, [vp, vp, i64, i32, i64, i64, ctypes.c_float, vp, vp, vp, vp, vp]),
     'or_gated_residual': (i32, [vp, vp, vp, i64, i32, i64, i64, vp]),
     'or_residual_layernorm_modulate': (i32, [vp, vp, vp, vp, i64, i32, i64, i64, i64, ctypes.c_float, vp, vp, vp, vp,

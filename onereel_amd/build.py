@@ -15,7 +15,7 @@ CSRC = PKG / 'csrc'
 INCLUDE = PKG.parent / 'include'
 LIB = PKG / 'libonereel_hip.so'
 OBJ = PKG / 'csrc' / '_obj'
-SOURCES = ['layout.hip', 'gather.hip', 'attention.hip', 'merge.hip', 'norm_rope.hip', 'frame_memory.hip',
+SOURCES = ['layout.hip', 'gather.hip', 'attention.hip', 'merge.hip', 'norm_rope.hip', 'frame_memory.hip', 'memory.hip',
            'dit_fused.hip']
 # attention: no NaN operands reach the softmax max, so fmax needs no quieting of its inputs (v_max3_f32 directly)
 SOURCE_FLAGS = {'attention.hip': ['-fno-honor-nans']}

@@ -68,6 +68,7 @@ struct AttnArgs {
   int64_t n_rope_rows;
   int64_t n_q_video;
   int64_t qs, ks, os;   // row strides (elements)
+  int64_t qstep;        // query i of a segment is source row (first source row) + i * qstep
   int32_t sum_q, H;
   float c;              // scale * log2(e)
   float scale;
@@ -557,7 +558,7 @@ void attn4_kernel(AttnArgs a, int32_t* ws) {
     dma_block<C::LPB>(vs.at(0), 0, voffv, lds_addr(rg.v[3]) + m0w);
     if (active) {
       const int i = q0 + l32 < Lq ? q0 + l32 : Lq - 1;
-      const int64_t row = q_src0 + i;
+      const int64_t row = q_src0 + (int64_t)i * a.qstep;
       const uint16_t* qp = (row < a.n_q_video ? a.q + row * a.qs : a.q_text + (row - a.n_q_video) * a.qs) + head * D;
       int rr = a.q_rope ? a.q_rope[q_beg + i] : -1;
       if (rr >= a.n_rope_rows) rr = -1;
@@ -622,7 +623,7 @@ void attn4_kernel(AttnArgs a, int32_t* ws) {
       const int i = q0 + l32;
       if (i < Lq) {
         const float inv = nb > 0 ? 1.0f / ltot : 0.0f;
-        const int64_t row = q_src0 + i;
+        const int64_t row = q_src0 + (int64_t)i * a.qstep;
         uint16_t* op = (row < a.n_q_video ? a.o + row * a.os : a.o_text + (row - a.n_q_video) * a.os) + head * D;
 #pragma unroll
         for (int db = 0; db < C::DB; ++db)
@@ -730,7 +731,7 @@ void attn8_kernel(AttnArgs a, int32_t* ws) {
       const int i0 = q0 + qb * 32 + l32;
       const bool live = i0 < Lq;
       const int i = min(i0, Lq - 1);
-      const int64_t row = q_src0 + i;
+      const int64_t row = q_src0 + (int64_t)i * a.qstep;
       const uint16_t* qp = (row < a.n_q_video ? a.q + row * a.qs : a.q_text + (row - a.n_q_video) * a.qs) + head * D;
       int rr = live && a.q_rope ? a.q_rope[q_beg + i] : -1;
       if (rr >= a.n_rope_rows) rr = -1;
@@ -821,7 +822,7 @@ __global__ __launch_bounds__(kThreads) void merge_kernel(AttnArgs a, const int32
       for (int t = 0; t < 4; ++t) acc[t] += wt * o[t];
     }
     const float inv = 1.0f / wsum;
-    const int64_t row = q_src0 + i_beg + r;
+    const int64_t row = q_src0 + (int64_t)(i_beg + r) * a.qstep;
     uint16_t* out = (row < a.n_q_video ? a.o + row * a.os : a.o_text + (row - a.n_q_video) * a.os) + head * D + d;
     *(uint2*)out = make_uint2(pack2(acc[0] * inv, acc[1] * inv), pack2(acc[2] * inv, acc[3] * inv));
     if (a.lse && d == 0) a.lse[(int64_t)head * a.sum_q + q_beg + i_beg + r] = m + logf(wsum);
@@ -905,6 +906,8 @@ int check_args(const or_varlen_args& x, const char* fn) {
   if (!x.q || !x.k || !x.v || !x.o || !x.cu_q) return fail_arg("%s: q, k, v, o and cu_q are required", fn);
   if (!x.cu_k && !(x.k_off && x.k_len)) return fail_arg("%s: need cu_k, or k_off with k_len", fn);
   if (x.k_off && !x.k_len) return fail_arg("%s: k_off needs k_len (the per-segment key counts)", fn);
+  if (x.q_row_step < 0 || (x.q_row_step > 1 && !x.seg_q_src))
+    return fail_arg("%s: q_row_step %d needs seg_q_src (and must not be negative)", fn, x.q_row_step);
   if (x.q_rope && (!x.cos_table || !x.sin_table || x.n_rope_rows < 1))
     return fail_arg("%s: q_rope needs cos / sin tables", fn);
   if (x.q_row_stride < (int64_t)x.H * x.D || x.k_row_stride < (int64_t)x.H * x.D || x.o_row_stride < (int64_t)x.H * x.D)
@@ -955,6 +958,7 @@ int launch_varlen(const or_varlen_args& x, void* wsp, int64_t cap, hipStream_t s
   a.qs = x.q_row_stride;
   a.ks = x.k_row_stride;
   a.os = x.o_row_stride;
+  a.qstep = x.q_row_step > 1 ? x.q_row_step : 1;
   a.sum_q = x.sum_q;
   a.H = x.H;
   a.scale = x.scale;

@@ -118,7 +118,7 @@ struct ScatterArgs {
   int H, D;
 };
 
-constexpr int kScatterRows = 2;   // rows per wavefront step (loads of both in flight before the stores)
+constexpr int kScatterRows = 1;   // rows per wavefront step: one 4 KiB row per wavefront, one step per wavefront
 
 // rows r < n_rows: packed row r -> token-order row dst_idx[r]; rows n_rows .. n_rows + n_zero: zeroed text rows
 template <bool NARROW>
@@ -172,6 +172,14 @@ int row_grid(int64_t rows) {
   // enough waves to keep every CU's memory pipes busy; the kernels loop over the rest
   int64_t blocks = (rows + kWaves - 1) / kWaves;
   if (blocks > 256 * 16) blocks = 256 * 16;
+  return (int)(blocks < 1 ? 1 : blocks);
+}
+
+// the scatter: one wavefront per row (group of narrow rows), no loop; a cold 421 MB scatter measured 0.073 ms this
+// way against 0.078 ms with two rows per step on a grid capped at 4096 blocks
+int scatter_grid(int64_t rows, int rows_per_wave) {
+  int64_t blocks = (rows + (int64_t)kWaves * rows_per_wave - 1) / ((int64_t)kWaves * rows_per_wave);
+  if (blocks > 0x7fffffffLL) blocks = 0x7fffffffLL;
   return (int)(blocks < 1 ? 1 : blocks);
 }
 
@@ -232,11 +240,14 @@ extern "C" int or_scatter(const void* packed, const int32_t* dst_idx, int64_t n_
   ScatterArgs g{(const uint16_t*)packed, dst_idx, n_rows, n_video, (uint16_t*)o_video,
                 (uint16_t*)(o_text ? o_text : o_video), dst_row_stride, text_row_stride, text_zero_from, text_rows,
                 H, D};
-  if ((int64_t)H * D < 64 * 8)
-    hipLaunchKernelGGL(scatter_kernel<true>, dim3(row_grid(n_rows + n_zero)), dim3(kThreads), 0, (hipStream_t)stream,
-                       g);
-  else
-    hipLaunchKernelGGL(scatter_kernel<false>, dim3(row_grid(n_rows + n_zero)), dim3(kThreads), 0, (hipStream_t)stream,
-                       g);
+  if ((int64_t)H * D < 64 * 8) {
+    int cp = 1;   // lanes per narrow row (as row_lanes), so 64 / cp rows per wavefront
+    while (cp < H * D / 8) cp <<= 1;
+    hipLaunchKernelGGL(scatter_kernel<true>, dim3(scatter_grid(n_rows + n_zero, kScatterRows * (64 / cp))),
+                       dim3(kThreads), 0, (hipStream_t)stream, g);
+  } else {
+    hipLaunchKernelGGL(scatter_kernel<false>, dim3(scatter_grid(n_rows + n_zero, kScatterRows)), dim3(kThreads), 0,
+                       (hipStream_t)stream, g);
+  }
   return check_hip(hipGetLastError(), "scatter_kernel launch");
 }

@@ -1,28 +1,29 @@
-"""Bounded cross-scene memory with per-head representatives (src/onereel/memory.py), on the HIP kernels.
+"""Bounded cross-scene memory with per-head representatives: the drop-in for src/onereel/memory.py (the same names,
+fields and results), on HIP kernels.
 
-The candidates are the boundary frames of every scene (first and last frame, each once). Per layer, CFG branch and
-head, the L2-normalised candidate keys are clustered into at most M groups (k-means; warm-started from the previous
-centroids after the first call), and each non-empty cluster keeps the candidate nearest its centroid. A scene's
-queries then read their local keys plus the other scenes' representatives of their head, in one softmax.
+Every scene reads its own context (its frames and sentence) plus, per head, at most M representative keys of the
+other scenes, chosen among the boundary frames' keys (the first and last frame of every scene) by k-means over the
+L2-normalised keys: 50 passes the first time a (layer, branch) key is seen, 2 warm passes from the stored centroids
+after that, one medoid per non-empty cluster. Representatives differ per head, so the attention runs head-major: each
+(head, query piece) pair is one single-head segment over rows of D elements, row = token * H + head.
 
-Representatives differ per head, so the attention is head-major: every (head, query piece) pair is one single-head
-segment of one varlen launch over rows of D elements, row = token * H + head. The reference gathers and scatters those
-rows with torch indexing around FlashAttention (memory.py:145-174); here the same per-head index arrays drive:
+Per call, all on the caller's stream and without host reads:
 
-- the pack kernel (queries; keys and values in one pass);
-- the varlen kernel with one head;
-- the scatter kernel.
+    or_memory_select   k-means + medoids for every head (fp32 MFMA distances, fixed-order sums, device-side stop)
+    or_memory_index    each (head, piece)'s foreign representatives appended after its local keys
+    or_pack_gather     the K / V rows of every segment (local rows from a per-plan table, then the foreign ones)
+    or_varlen_fwd      single-head attention; queries read and outputs written in place, query i of piece p at row
+                       (first row of p + i) * H + head (q_row_step = H), when every piece's query rows are contiguous
 
-The clustering (`BoundaryMemory.select`) keeps the reference's torch formulation on the GPU: batched matmuls for the
-distances (hipBLASLt) and stable sorts for the deterministic choice (memory.py:48-93).
+A plan's static parts (segment offsets, the local key rows, the query rows) are built once per (plan, H) and kept.
 """
 from __future__ import annotations
 
 from dataclasses import dataclass
 
 import torch
-import torch.nn.functional as F
 
+from . import _lib as L
 from .layout import SceneLayout
 from .scene import gather_rows, scatter_rows, varlen
 
@@ -30,80 +31,96 @@ ITERS_INIT, ITERS_UPDATE = 50, 2
 
 
 def candidate_frames(layout: SceneLayout):
-    """boundary frames (first and last frame of every scene, each frame once) and their scene (memory.py:30-37)"""
+    """(frames, owner): each scene's first and last frame, a one-frame scene's frame once, and the scene of each"""
     frames, owner = [], []
-    for j, (lo, hi) in enumerate(layout.ranges):
-        for f in dict.fromkeys((lo, hi - 1)):
-            frames.append(f)
-            owner.append(j)
+    for j, (first, end) in enumerate(layout.ranges):
+        ends = [first] if end - first == 1 else [first, end - 1]
+        frames += ends
+        owner += [j] * len(ends)
     return frames, owner
 
 
 def candidates(layout: SceneLayout, T: int, device):
-    """video rows (frame-major, all tokens) of the boundary frames and their scene (memory.py:40-45)"""
+    """(rows, scene): the token rows (frame-major, T per frame) of the boundary frames and the scene of each row"""
     frames, owner = candidate_frames(layout)
-    rows = torch.cat([torch.arange(f * T, (f + 1) * T, device=device) for f in frames])
-    scene = torch.tensor(owner, device=device).repeat_interleave(T)
-    return rows, scene
+    f = torch.tensor(frames, dtype=torch.long)
+    rows = (f[:, None] * T + torch.arange(T)).flatten()
+    scene = torch.tensor(owner, dtype=torch.long).repeat_interleave(T)
+    return rows.to(device), scene.to(device)
 
 
 class BoundaryMemory:
-    """per (layer, branch) key: centroids [H, M, D] carried across steps (memory.py:48-56)"""
+    """M representatives per head; `centroids` maps a (layer, CFG branch) key to that key's fp32 [H, M, D]
+    centroids, carried from one denoising step to the next"""
 
     def __init__(self, M: int = 128):
         self.M = M
         self.centroids = {}
+        self._init_cols = {}
+        self._ws = {}
 
     def reset(self):
         self.centroids = {}
 
+    def _start_columns(self, B: int, M: int, device):
+        """the cold start's candidates: M evenly spaced over [0, B - 1], rounded half to even (torch.linspace)"""
+        key = (B, M, str(device))
+        if key not in self._init_cols:
+            cols = torch.linspace(0, B - 1, M).round().to(torch.int32)
+            self._init_cols[key] = cols.to(device)
+        return self._init_cols[key]
+
+    def _workspace(self, B, H, D, M, iters, device):
+        n = int(L.lib().or_memory_select_workspace_size(B, H, D, M, iters))
+        if n < 0:
+            raise L.HipValueError(f'no k-means workspace for B={B} H={H} D={D} M={M}')
+        ws = self._ws.get(str(device))
+        if ws is None or ws.numel() < n:
+            ws = torch.empty(n + 256, dtype=torch.uint8, device=device)
+            self._ws[str(device)] = ws
+        off = (-ws.data_ptr()) % 256
+        return ws[off:off + n]
+
     @torch.no_grad()
     def select(self, key, kc: torch.Tensor):
-        """kc [B, H, D] candidate keys -> (rep [H, M] candidate positions, valid [H, M]); one representative per
-        non-empty cluster (nearest member, then lowest index), padded with valid = False (memory.py:58-93)"""
-        x = F.normalize(kc.float().transpose(0, 1), dim=-1)
-        H, B, D = x.shape
+        """kc [B, H, D] candidate keys (bf16 or fp32, on the GPU) -> (rep [H, M] int64 candidate positions,
+        valid [H, M] bool): per head one representative per non-empty cluster, in cluster order, then padding
+        (0, False)"""
+        if kc.dim() != 3:
+            raise L.HipValueError(f'kc must be [B, H, D], got {tuple(kc.shape)}')
+        B, H, D = kc.shape
+        kc = kc if kc.stride(2) == 1 and kc.stride(1) == D else kc.contiguous()
+        return self._select(key, kc, None, B, H, D)
+
+    def _select(self, key, keys: torch.Tensor, rows, B: int, H: int, D: int):
+        """k-means over rows `rows` (int32 device tensor, or None for rows 0..B-1) of keys [rows, H, D]"""
+        if not keys.is_cuda or keys.dtype not in (torch.bfloat16, torch.float32):
+            raise L.HipTypeError(f'keys must be a bf16 or fp32 GPU tensor, got {keys.dtype} on {keys.device}')
+        dev = keys.device
         M = min(self.M, B)
         c = self.centroids.get(key)
-        if c is None or c.shape != (H, M, D):
-            c = x[:, torch.linspace(0, B - 1, M, device=x.device).round().long()].clone()
-            iters = ITERS_INIT
-        else:
-            iters = ITERS_UPDATE
-        xx = (x * x).sum(-1, keepdim=True)
-        for it in range(iters + 1):
-            d = xx - 2 * x @ c.transpose(1, 2) + (c * c).sum(-1)[:, None]
-            z = d.argmin(-1)
-            if it == iters:
-                break
-            oh = F.one_hot(z, M).float()
-            s, n = oh.transpose(1, 2) @ x, oh.sum(1)
-            prev = c
-            c = torch.where((n > 0)[..., None], s / n.clamp_min(1)[..., None], c)
-            # the first clustering stops once the centroids stand still; the warm updates run their few iterations
-            # without that host read (an iteration after convergence changes nothing, so the result is the same)
-            if iters == ITERS_INIT and torch.equal(c, prev):
-                break
+        cold = c is None or tuple(c.shape) != (H, M, D)
+        if cold:
+            c = torch.empty(H, M, D, dtype=torch.float32, device=dev)
+            init = self._start_columns(B, M, dev)
+        iters = ITERS_INIT if cold else ITERS_UPDATE
+        rep = torch.empty(H, M, dtype=torch.long, device=dev)
+        valid = torch.empty(H, M, dtype=torch.bool, device=dev)
+        ws = self._workspace(B, H, D, M, iters, dev)
+        with torch.cuda.device(dev):
+            L.check(L.lib().or_memory_select(keys.data_ptr(), int(keys.dtype == torch.float32), L.ptr(rows),
+                                             keys.stride(0), B, H, D, M, c.data_ptr(),
+                                             init.data_ptr() if cold else None, iters, rep.data_ptr(),
+                                             valid.data_ptr(), ws.data_ptr(), ws.numel(), L.stream_handle(dev)),
+                    'or_memory_select')
         self.centroids[key] = c
-        dist = d.gather(-1, z[..., None])[..., 0]
-        o1 = dist.argsort(dim=-1, stable=True)
-        o2 = z.gather(-1, o1).argsort(dim=-1, stable=True)
-        order = o1.gather(-1, o2)
-        zs = z.gather(-1, order)
-        first = torch.ones_like(zs, dtype=torch.bool)
-        first[:, 1:] = zs[:, 1:] != zs[:, :-1]
-        rank = first.cumsum(-1) - 1
-        # each cluster's first member goes to column rank; the other members to a spare column M, dropped after
-        # (scatters instead of boolean indexing, which would read the selection's size back to the host)
-        col = torch.where(first, rank, M)
-        rep = torch.zeros(H, M + 1, dtype=torch.long, device=x.device).scatter_(1, col, order)[:, :M]
-        valid = torch.zeros(H, M + 1, dtype=torch.bool, device=x.device).scatter_(1, col, first)[:, :M]
         return rep, valid
 
 
 @dataclass
 class Plan:
-    """query pieces of one layer (memory.py:96-106)"""
+    """one layer's query pieces (the fields of memory.py:96-106), plus host copies of the sizes that the varlen call
+    needs (filled by make_plan; a Plan built field by field gets them from one read of lens / qlen)"""
     qrows: torch.Tensor                  # [sum Q] query rows, piece after piece
     qlen: torch.Tensor                   # [n] queries per piece
     pad: torch.Tensor                    # [n, Lmax] local key rows per piece (padded)
@@ -113,43 +130,125 @@ class Plan:
     mem: torch.Tensor                    # [n] the piece reads the memory
     cand: torch.Tensor                   # [B] key-buffer rows of the boundary candidates
     owner: torch.Tensor                  # [B] their scene
-    max_qlen: int = 0                    # host copies: the longest piece's queries, local keys, and all local keys
-    max_len: int = 0
-    sum_len: int = 0
+    host_qlen: list | None = None        # qlen on the host
+    host_lens: list | None = None        # lens on the host
+    q_first: list | None = None          # per piece its first query row when its rows are consecutive, else None
 
 
 def make_plan(pieces, cand, owner, device) -> Plan:
-    """pieces: [(scene, query rows, local key rows, reads memory)]; cand / owner: candidate key rows and their scene
-    (memory.py:109-121)"""
-    t = lambda x: torch.as_tensor(x, dtype=torch.long, device=device)
-    pieces = [(j, t(q), t(k), m) for j, q, k, m in pieces if len(q)]
-    lens = [len(k) for _, _, k, _ in pieces]
-    pad = torch.zeros(len(pieces), max(lens), dtype=torch.long, device=device)
-    pmask = torch.zeros_like(pad, dtype=torch.bool)
-    for i, (_, _, k, _) in enumerate(pieces):
-        pad[i, :len(k)] = k
-        pmask[i, :len(k)] = True
-    return Plan(qrows=torch.cat([q for _, q, _, _ in pieces]), qlen=t([len(q) for _, q, _, _ in pieces]), pad=pad,
-                pmask=pmask, lens=t(lens), scene=t([j for j, _, _, _ in pieces]),
-                mem=torch.tensor([m for *_, m in pieces], dtype=torch.bool, device=device), cand=t(cand),
-                owner=t(owner), max_qlen=max(len(q) for _, q, _, _ in pieces), max_len=max(lens), sum_len=sum(lens))
+    """pieces: [(scene, query rows, local key rows, reads the memory)]; pieces without queries are dropped. cand /
+    owner: the key-buffer rows of the boundary candidates and their scene."""
+    as_long = lambda x: torch.as_tensor(x, dtype=torch.long)
+    kept = [(j, as_long(q), as_long(k), bool(m)) for j, q, k, m in pieces if len(q)]
+    if not kept:
+        raise L.HipValueError('a plan needs at least one piece with queries')
+    n = len(kept)
+    lens = [int(k.numel()) for _, _, k, _ in kept]
+    width = max(lens)
+    pad = torch.zeros(n, width, dtype=torch.long)
+    pmask = torch.zeros(n, width, dtype=torch.bool)
+    for i, (_, _, k, _) in enumerate(kept):
+        pad[i, :lens[i]] = k
+        pmask[i, :lens[i]] = True
+
+    def first_row(q):
+        return int(q[0]) if bool((q == q[0] + torch.arange(q.numel())).all()) else None
+
+    put = lambda x: x.to(device)
+    return Plan(qrows=put(torch.cat([q for _, q, _, _ in kept])), qlen=put(as_long([q.numel() for _, q, _, _ in kept])),
+                pad=put(pad), pmask=put(pmask), lens=put(as_long(lens)), scene=put(as_long([j for j, *_ in kept])),
+                mem=put(torch.tensor([m for *_, m in kept], dtype=torch.bool)), cand=put(as_long(cand)),
+                owner=put(as_long(owner)), host_qlen=[int(q.numel()) for _, q, _, _ in kept], host_lens=lens,
+                q_first=[first_row(q) for _, q, _, _ in kept])
 
 
 def frame_plan(layout: SceneLayout, T: int, token_row, Lv: int, q_pieces, text_ranges=None, text_for=(), Sq: int = 0,
                device='cuda') -> Plan:
-    """frame-major models (memory.py:124-137). Key buffer: Lv video rows (video token t at token_row[t]), then the
-    text tokens; query buffer: Sq video rows, then the text tokens. q_pieces: [(scene, video query row lo, hi)]. Video
-    queries read their scene, their sentence and the memory; sentence queries (scenes in text_for) read their scene
-    and sentence."""
+    """the pieces of a frame-major model (memory.py:124-137). Key buffer: Lv video rows (video token t at row
+    token_row[t]), then the text tokens; query buffer: Sq video rows, then the text tokens. q_pieces: [(scene, first
+    video query row, end)]. Video queries read their scene's frames, their sentence and the memory; the sentence
+    queries of the scenes in text_for read their scene's frames and their sentence."""
     token_row = torch.as_tensor(token_row)
-    ar = lambda a, b: torch.arange(a, b)
-    frows = lambda fs: token_row[torch.cat([ar(f * T, (f + 1) * T) for f in fs])]
-    text = lambda j: Lv + ar(*text_ranges[j]) if text_ranges else ar(0, 0)
-    pieces = [(j, ar(lo, hi), torch.cat([frows(layout.frames[j]), text(j)]), True) for j, lo, hi in q_pieces]
-    pieces += [(j, Sq + ar(*text_ranges[j]), torch.cat([frows(layout.frames[j]), text(j)]), False)
-               for j in sorted(text_for)]
-    cf, owner = candidate_frames(layout)
-    return make_plan(pieces, frows(cf), torch.tensor(owner).repeat_interleave(T), device)
+
+    def video_rows(frames):
+        tok = (torch.as_tensor(frames, dtype=torch.long)[:, None] * T + torch.arange(T)).flatten()
+        return token_row[tok]
+
+    def sentence(j):
+        if not text_ranges:
+            return torch.zeros(0, dtype=torch.long)
+        a, b = text_ranges[j]
+        return Lv + torch.arange(a, b)
+
+    own = {j: torch.cat([video_rows(layout.frames[j]), sentence(j)]) for j in range(layout.n_scenes)}
+    pieces = [(j, torch.arange(lo, hi), own[j], True) for j, lo, hi in q_pieces]
+    for j in sorted(text_for):
+        a, b = text_ranges[j]
+        pieces.append((j, Sq + torch.arange(a, b), own[j], False))
+    frames, owner = candidate_frames(layout)
+    return make_plan(pieces, video_rows(frames), torch.tensor(owner).repeat_interleave(T), device)
+
+
+class _Static:
+    """the per-(plan, H) device tables of the head-major call: segment (head h, piece i) is number h * n + i"""
+
+    def __init__(self, p: Plan, H: int, Sq: int, device):
+        qlen = p.host_qlen if p.host_qlen is not None else [int(x) for x in p.qlen.tolist()]
+        lens = p.host_lens if p.host_lens is not None else [int(x) for x in p.lens.tolist()]
+        n, B = len(qlen), int(p.cand.numel())
+        self.n, self.B, self.H, self.qlen, self.lens = n, B, H, qlen, lens
+        self.max_q = max(qlen)
+        first = p.q_first if p.q_first is not None else [None] * n
+        # queries in place: every piece's rows consecutive, inside [0, Sq), and no two pieces sharing a row
+        spans = sorted((f, f + c) for f, c in zip(first, qlen) if f is not None)
+        self.in_place = (all(f is not None for f in first) and spans[0][0] >= 0 and spans[-1][1] <= Sq and
+                         all(a[1] <= b[0] for a, b in zip(spans, spans[1:])))
+        self.covers_all = self.in_place and sum(qlen) == Sq
+        t32 = lambda x: torch.tensor(x, dtype=torch.int32, device=device)
+        cu = [0]
+        for _ in range(H):
+            for c in qlen:
+                cu.append(cu[-1] + c)
+        self.cu_q, self.sum_q = t32(cu), cu[-1]
+        if self.in_place:
+            self.seg_q_src = t32([first[i] * H + h for h in range(H) for i in range(n)])
+        else:
+            rows = p.qrows.to(device=device, dtype=torch.int64)
+            lo, hi = int(rows.min()), int(rows.max())        # once per plan
+            if lo < 0 or hi >= Sq:
+                raise L.HipValueError(f'plan query rows span [{lo}, {hi}], the query buffer has {Sq} rows')
+            self.qidx = (rows[None] * H + torch.arange(H, device=device)[:, None]).flatten().to(torch.int32)
+        local = p.pad.to(device)[p.pmask.to(device)]           # the local key rows, piece after piece
+        # the largest key-buffer row the plan names (once per plan), checked against each call's buffer
+        self.max_key_row = max(int(local.max()) if local.numel() else -1, int(p.cand.max()))
+        self.local = local.to(torch.int64)
+        self.cand64 = p.cand.to(device=device, dtype=torch.int64).contiguous()
+        self.cand32 = self.cand64.to(torch.int32)
+        self.owner64 = p.owner.to(device=device, dtype=torch.int64).contiguous()
+        self.scene64 = p.scene.to(device=device, dtype=torch.int64).contiguous()
+        self.piece_len = t32(lens)
+        self.piece_mem = p.mem.to(device=device, dtype=torch.uint8).contiguous()
+        self._slots = {}
+        self.device = device
+
+    def slots(self, M: int):
+        """(k_off, kidx) for M representatives: segment (h, i) owns kidx[k_off .. k_off + lens[i] + M), its local
+        rows (row * H + h) first, written once here; the foreign rows after them are rewritten by each call"""
+        if M not in self._slots:
+            H, n = self.H, self.n
+            off, o = [], 0
+            for _ in range(H):
+                for i in range(n):
+                    off.append(o)
+                    o += self.lens[i] + M
+            k_off = torch.tensor(off, dtype=torch.int32, device=self.device)
+            kidx = torch.zeros(o, dtype=torch.int32, device=self.device)
+            pos = torch.cat([torch.arange(c) for c in self.lens]).to(self.device)
+            piece = torch.cat([torch.full((c,), i) for i, c in enumerate(self.lens)]).to(self.device)
+            for h in range(H):
+                kidx[k_off[h * n + piece].long() + pos] = (self.local * H + h).to(torch.int32)
+            self._slots[M] = (k_off, kidx)
+        return self._slots[M]
 
 
 class MemoryAttention:
@@ -158,37 +257,51 @@ class MemoryAttention:
     def __init__(self, memory: BoundaryMemory):
         self.memory = memory
         self.plans = {}
+        self._static = {}
+
+    def _tables(self, p: Plan, H: int, Sq: int, device) -> _Static:
+        key = (id(p), H, Sq, str(device))
+        hit = self._static.get(key)
+        if hit is None or hit[0] is not p:
+            hit = (p, _Static(p, H, Sq, device))
+            self._static[key] = hit
+        return hit[1]
 
     def __call__(self, key, q, k, v, p: Plan) -> torch.Tensor:
-        """q [Sq, H, D], k / v [L, H, D] bf16 buffers -> [Sq, H, D] (rows outside the plan's queries are zero)"""
+        """q [Sq, H, D], k / v [L, H, D] bf16 on the GPU -> [Sq, H, D] (rows outside the plan's queries are zero)"""
         Sq, H, D = q.shape
-        L = k.shape[0]
+        Lk = k.shape[0]
+        if k.shape[1:] != (H, D) or v.shape != k.shape:
+            raise L.HipValueError(f'k / v must be [rows, {H}, {D}] alike')
+        for x in (q, k, v):
+            if x.stride(2) != 1 or x.stride(1) != D or x.stride(0) != H * D:
+                raise L.HipValueError('q, k and v must be contiguous [rows, H, D]')
         dev = q.device
-        rep, valid = self.memory.select(key, k[p.cand])
-        rep_row, rep_scene = p.cand[rep], p.owner[rep]
-        n = len(p.qlen)
-        hh = torch.arange(H, device=dev)[:, None, None]
-        foreign = valid[:, None, :] & (rep_scene[:, None, :] != p.scene[None, :, None]) & p.mem[None, :, None]
-        idx = torch.cat([p.pad[None].expand(H, -1, -1), rep_row[:, None, :].expand(-1, n, -1)], -1) * H + hh
-        keep = torch.cat([p.pmask[None].expand(H, -1, -1), foreign], -1).flatten()
-        # the kept key rows, compacted in (head, piece, position) order without reading their count back: kidx is
-        # sized for every representative kept (host-known bound); rows past the last segment are row 0, packed but
-        # never read (each segment reads its cu_k range)
-        Mr = rep.shape[1]
-        bound = H * (p.sum_len + n * Mr)
-        at = torch.where(keep, keep.cumsum(0) - 1, bound)
-        kidx = torch.zeros(bound + 1, dtype=torch.int32, device=dev).scatter_(0, at, idx.flatten().to(torch.int32))
-        kidx = kidx[:bound]
-        qidx = (p.qrows[None] * H + hh[:, 0]).flatten().to(torch.int32)
-        lq = p.qlen.repeat(H)
-        lk = (p.lens[None] + foreign.sum(-1)).flatten()
-        cu_q = F.pad(lq.cumsum(0), (1, 0)).to(torch.int32)
-        cu_k = F.pad(lk.cumsum(0), (1, 0)).to(torch.int32)
+        st = self._tables(p, H, Sq, dev)
+        if st.n * H > 4096:
+            raise L.HipValueError(f'{st.n} pieces x {H} heads = {st.n * H} single-head segments; the varlen call '
+                                  f'takes at most 4096')
+        if st.max_key_row >= Lk:
+            raise L.HipValueError(f'the plan reads key row {st.max_key_row}, the key buffer has {Lk} rows')
+        rep, valid = self.memory._select(key, k, st.cand32, st.B, H, D)
+        M = rep.shape[1]
+        k_off, kidx = st.slots(M)
+        k_len = torch.empty(st.n * H, dtype=torch.int32, device=dev)
+        L.check(L.lib().or_memory_index(rep.data_ptr(), valid.data_ptr(), st.cand64.data_ptr(), st.owner64.data_ptr(),
+                                        st.scene64.data_ptr(), st.piece_mem.data_ptr(), st.piece_len.data_ptr(),
+                                        k_off.data_ptr(), st.n, H, M, kidx.data_ptr(), k_len.data_ptr(),
+                                        L.stream_handle(dev)), 'or_memory_index')
         # single-head rows: row * H + head of the [rows, H, D] buffers
-        qp = gather_rows(q.reshape(Sq * H, 1, D), qidx)
-        kp, vp = gather_rows(k.reshape(L * H, 1, D), kidx, v.reshape(L * H, 1, D))
-        # max_q / max_k as host bounds (the kernel checks only that a segment's keys span under 2 GiB)
-        o = varlen(qp, kp, vp, cu_q, cu_k, p.max_qlen, p.max_len + Mr)
-        out = q.new_zeros(Sq * H, 1, D)
-        scatter_rows(o, qidx, out)
-        return out.view(Sq, H, D)
+        kp, vp = gather_rows(k.view(Lk * H, 1, D), kidx, v.view(Lk * H, 1, D))
+        max_k = max(st.lens) + M
+        if st.in_place:
+            out = torch.empty_like(q) if st.covers_all else torch.zeros_like(q)
+            qv, ov = q.view(Sq * H, 1, D), out.view(Sq * H, 1, D)
+            varlen(qv, kp, vp, st.cu_q, None, st.max_q, max_k, k_off=k_off, k_len=k_len, out=ov,
+                   seg_q_src=st.seg_q_src, n_q_video=Sq * H, sum_q=st.sum_q, q_row_step=H)
+            return out
+        qp = gather_rows(q.view(Sq * H, 1, D), st.qidx)
+        o = varlen(qp, kp, vp, st.cu_q, None, st.max_q, max_k, k_off=k_off, k_len=k_len)
+        out = torch.zeros_like(q)
+        scatter_rows(o, st.qidx, out.view(Sq * H, 1, D))
+        return out

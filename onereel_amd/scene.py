@@ -211,9 +211,10 @@ def scatter_rows(packed: torch.Tensor, idx: torch.Tensor, out: torch.Tensor):
 
 def varlen(q, k, v, cu_q, cu_k, max_q, max_k, *, k_off=None, k_len=None, out=None, lse=None, seg_q_src=None,
            q_text=None, o_text=None, n_q_video=None, q_rope=None, cos=None, sin=None, sum_q=None, workspace=None,
-           scale=None, noalloc=False):
+           scale=None, noalloc=False, q_row_step=1):
     """or_varlen_fwd on torch tensors. Returns out (allocated [Nq, H, D] when not given). noalloc=True calls
-    or_varlen_fwd_noalloc instead: no workspace, the library's fixed per-GPU array (calls must not overlap on a GPU)."""
+    or_varlen_fwd_noalloc instead: no workspace, the library's fixed per-GPU array (calls must not overlap on a GPU).
+    q_row_step > 1 (with seg_q_src): query i of segment s is row seg_q_src[s] + i * q_row_step of q and of out."""
     H, D = k.shape[1], k.shape[2]
     _check_bf16(q, k, v, q_text, out, o_text)
     _, qs = _rows2d(q, H, D)
@@ -251,6 +252,7 @@ def varlen(q, k, v, cu_q, cu_k, max_q, max_k, *, k_off=None, k_len=None, out=Non
     a.q_row_stride, a.k_row_stride, a.o_row_stride = qs, ks, os_
     a.n_seg, a.sum_q, a.max_q, a.max_k, a.H, a.D = int(n_seg), int(sum_q), int(max_q), int(max_k), H, D
     a.scale = float(D ** -0.5 if scale is None else scale)
+    a.q_row_step = int(q_row_step)
     if noalloc:
         a.workspace, a.workspace_bytes = None, 0
         with torch.cuda.device(q.device):

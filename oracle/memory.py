@@ -4,10 +4,11 @@ TEST INFRASTRUCTURE ONLY (see `oracle/__init__.py`). Restates src/onereel/memory
 
 - `boundary_rows`     candidate_frames / candidates (memory.py:30-45): the first and last frame of every scene (each
                       frame once), all their tokens, with their scene
-- `select`            BoundaryMemory.select (memory.py:58-93), first call: k-means over the L2-normalised candidate
-                      keys of each head from M evenly spaced candidates (round(linspace(0, B-1, M))), squared
-                      Euclidean distance, an empty cluster keeps its centroid, stop when the centroids are unchanged
-                      (at most 50 passes); per non-empty cluster the member nearest its centroid, then the lowest index
+- `select`            BoundaryMemory.select (memory.py:58-93): k-means over the L2-normalised candidate keys of each
+                      head, from M evenly spaced candidates (round(linspace(0, B-1, M)), at most 50 passes) or, for a
+                      warm call, from the stored centroids (at most 2 passes); squared Euclidean distance, an empty
+                      cluster keeps its centroid, stop when the centroids are unchanged; per non-empty cluster the
+                      member nearest its centroid, then the lowest index
 - `masked_reference`  what MemoryAttention (memory.py:140-174) computes, per head and scene: softmax over the scene's
                       own video keys, its sentence and the other scenes' representatives of that head (video queries),
                       or over the scene's video keys and its sentence (sentence queries), in float32 — the per-head
@@ -33,12 +34,14 @@ def boundary_rows(ranges, T):
     return torch.tensor(rows), torch.tensor(scene)
 
 
-def select(kc, M, iters=50, centroids=False):
-    """kc [B, H, D] -> (rep [H, M] candidate positions, valid [H, M]) (and the final centroids [H, M, D])"""
+def select(kc, M, iters=50, centroids=False, start=None):
+    """kc [B, H, D] -> (rep [H, M] candidate positions, valid [H, M]) (and the final centroids [H, M, D]). start:
+    the centroids a warm call begins from (memory.py:67-72, then ITERS_UPDATE passes); None: the cold start from M
+    evenly spaced candidates"""
     x = F.normalize(kc.float().transpose(0, 1), dim=-1)
     H, B, D = x.shape
     M = min(M, B)
-    c = x[:, torch.linspace(0, B - 1, M).round().long()].clone()
+    c = x[:, torch.linspace(0, B - 1, M).round().long()].clone() if start is None else start.float().clone()
     for it in range(iters + 1):
         d = ((x[:, :, None, :] - c[:, None, :, :]) ** 2).sum(-1)          # [H, B, M], explicit differences
         z = d.argmin(-1)

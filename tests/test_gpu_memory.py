@@ -1,49 +1,65 @@
-"""GPU parity of the head-major bounded memory (onereel_amd.memory) with the oracle: packed single-head attention on
-the pack / varlen / scatter kernels against a per-head masked float32 reference, and the per-head representative
-choice (the reference's tests/test_onereel_memory.py)."""
+"""GPU parity of the head-major bounded memory (onereel_amd.memory, csrc/memory.hip) with the oracle:
+
+- the representative choice (or_memory_select) against the oracle's restatement of BoundaryMemory.select on
+  separated groups of keys, cold and warm (a second call from the stored centroids on perturbed keys), at head_dim 64
+  and 128, with more clusters than one LDS chunk, from bf16 and fp32 keys; the reference's own memory tests (every
+  candidate kept when the budget covers them; each representative the nearest member of its cluster);
+- the packed single-head attention (or_memory_index, pack, varlen with in-place queries, or gather / scatter) against
+  fp32 attention over each piece's local keys plus its head's foreign representatives: the reference test's layouts
+  (tests/test_onereel_memory.py) on two calls in a row, a plan with permuted query rows, and the HunyuanVideo-1.5 480p
+  layer's shape on sampled rows."""
+import numpy as np
 import pytest
 import torch
 
+from helpers import assert_close
 from onereel_amd.layout import SceneLayout
-from onereel_amd.memory import BoundaryMemory, MemoryAttention, candidates, frame_plan
+from onereel_amd.memory import BoundaryMemory, MemoryAttention, candidates, frame_plan, make_plan
 from oracle import memory as OM
 
 pytestmark = [pytest.mark.gpu, pytest.mark.skipif(not torch.cuda.is_available(), reason='needs the GPU')]
 DEV = 'cuda'
 
 
-@pytest.mark.parametrize('lengths,M,D', [([3, 5, 2, 4], 8, 64), ([2, 2, 2], 1000, 64), ([6, 1, 3], 5, 128)])
-def test_memory_attention_matches_masked_reference(lengths, M, D):
-    print(f'memory attention lengths={lengths} M={M} D={D}', flush=True)
-    g = torch.Generator().manual_seed(0)
-    T, H = 16, 4
-    lay = SceneLayout(lengths, halo=0)
-    S = lay.n_frames * T
-    counts = [5, 7, 3, 6][:lay.n_scenes]
-    tr, c = [], 0
-    for n in counts:
-        tr.append((c, c + n))
-        c += n
-    q, k, v = (torch.randn(S, H, D, generator=g).to(torch.bfloat16) for _ in range(3))
-    eq, ek, ev = (torch.randn(c, H, D, generator=g).to(torch.bfloat16) for _ in range(3))
-    plan = frame_plan(lay, T, torch.arange(S), S, [(j, lo * T, hi * T) for j, (lo, hi) in enumerate(lay.ranges)], tr,
-                      set(range(lay.n_scenes)), S, DEV)
-    mem = MemoryAttention(BoundaryMemory(M))
-    out = mem(('l0', True), torch.cat([q, eq]).to(DEV), torch.cat([k, ek]).to(DEV), torch.cat([v, ev]).to(DEV), plan)
-    ov, ot = out[:S].cpu(), out[S:].cpu()
-    # the representatives a fresh memory picks (deterministic) feed the reference
-    rows, owner = candidates(lay, T, DEV)
-    rep, valid = BoundaryMemory(M).select(('l0', True), k.to(DEV)[rows])
-    rv, rt = OM.masked_reference(q, k, v, eq, ek, ev, lay.ranges, T, rows[rep].cpu(), owner[rep].cpu(), valid.cpu(),
-                                 tr)
-    rel = lambda a, b: ((a.float() - b).norm() / b.norm()).item()
-    assert rel(ov, rv) < 2e-2 and rel(ot, rt) < 2e-2
-    assert (ov.float() - rv).abs().max() < 2e-2 and (ot.float() - rt).abs().max() < 2e-2
+def _groups(g, k, per, H, D, noise):
+    base = torch.randn(k, H, D, generator=g)
+    return torch.cat([base[i].expand(per, -1, -1) for i in range(k)]) + noise * torch.randn(k * per, H, D, generator=g)
+
+
+def _same_sets(got, gv, ref, rv):
+    for h in range(got.shape[0]):
+        assert sorted(got[h][gv[h]].cpu().tolist()) == sorted(ref[h][rv[h]].tolist()), h
+
+
+@pytest.mark.parametrize('k,per,H,D,M,dtype', [
+    (5, 9, 3, 64, 5, torch.float32),
+    (6, 7, 2, 128, 6, torch.bfloat16),
+    (40, 5, 2, 128, 40, torch.float32),
+    (150, 3, 2, 64, 150, torch.float32),      # M > 128: two centroid chunks of the distance pass
+])
+def test_select_matches_oracle_cold_and_warm(k, per, H, D, M, dtype):
+    """one cluster per group (M = the group count; more clusters than groups split a group by the noise, and a
+    two-member cluster's members are equidistant from its mean: ties that fp32 rounding decides), members spread
+    (noise 0.1) so that the nearest member of each group is not a tie at the fp32 rounding of the |x|^2 - 2 x.c +
+    |c|^2 distances (the oracle takes explicit differences); the warm call on perturbed keys runs two passes from the
+    stored centroids, as the oracle does from its own"""
+    print(f'select k={k} per={per} H={H} D={D} M={M} {dtype}', flush=True)
+    g = torch.Generator().manual_seed(7 + D + M)
+    xs = _groups(g, k, per, H, D, 0.1).to(dtype)
+    mem = BoundaryMemory(M)
+    got, gv = mem.select('a', xs.to(DEV))
+    ref, rv, c_ref = OM.select(xs, M, centroids=True)
+    _same_sets(got, gv, ref, rv)
+    assert mem.centroids['a'].shape == (H, min(M, k * per), D)
+    xs2 = (xs.float() + 0.02 * torch.randn(xs.shape, generator=g)).to(dtype)
+    got2, gv2 = mem.select('a', xs2.to(DEV))
+    ref2, rv2 = OM.select(xs2, M, iters=2, start=c_ref)
+    _same_sets(got2, gv2, ref2, rv2)
 
 
 def test_select_keeps_every_candidate_when_the_budget_covers_them():
     lay = SceneLayout([3, 4, 2], halo=0)
-    T, H, D = 8, 2, 32
+    T, H, D = 8, 2, 64
     rows, _ = candidates(lay, T, DEV)
     k = torch.randn(lay.n_frames * T, H, D, generator=torch.Generator().manual_seed(1)).to(DEV)
     rep, valid = BoundaryMemory(len(rows)).select('x', k[rows])
@@ -51,22 +67,138 @@ def test_select_keeps_every_candidate_when_the_budget_covers_them():
         assert sorted(rep[h][valid[h]].tolist()) == list(range(len(rows)))
 
 
-def test_select_nearest_member_and_oracle_on_separated_groups():
-    g = torch.Generator().manual_seed(2)
-    x = torch.randn(300, 3, 16, generator=g)
-    mem = BoundaryMemory(12)
+@pytest.mark.parametrize('B,H,D,M', [(300, 3, 64, 12), (2000, 2, 128, 128), (777, 1, 128, 200)])
+def test_select_nearest_member_and_layout(B, H, D, M):
+    """each representative is the member of its cluster nearest the returned centroids (clusters and distances
+    recomputed here in float64), the representatives are distinct, valid ones come first, padding is (0, False)"""
+    g = torch.Generator().manual_seed(B)
+    x = torch.randn(B, H, D, generator=g)
+    mem = BoundaryMemory(M)
     rep, valid = mem.select('y', x.to(DEV))
-    c = mem.centroids['y'].cpu()
-    xn = torch.nn.functional.normalize(x.float().transpose(0, 1), dim=-1)
-    for h in range(3):
-        z = torch.cdist(xn[h], c[h]).argmin(-1)
-        for r in rep[h][valid[h]].cpu().tolist():
+    c = mem.centroids['y'].cpu().double()
+    xn = torch.nn.functional.normalize(x.double().transpose(0, 1), dim=-1)
+    for h in range(H):
+        n = int(valid[h].sum())
+        assert n > 0 and bool(valid[h, :n].all()) and not bool(valid[h, n:].any())
+        chosen = rep[h, :n].cpu().tolist()
+        assert len(set(chosen)) == n and int(rep[h, n:].abs().sum()) == 0
+        d = torch.cdist(xn[h], c[h]) ** 2
+        z = d.argmin(-1)
+        for r in chosen:
             members = (z == z[r]).nonzero().flatten()
-            d = (xn[h, members] - c[h, z[r]]).pow(2).sum(-1)
-            assert d.min() >= (xn[h, r] - c[h, z[r]]).pow(2).sum() - 1e-5
-    base = torch.randn(4, 2, 16, generator=g)
-    xs = torch.cat([base[i].expand(10, -1, -1) for i in range(4)]) + 0.01 * torch.randn(40, 2, 16, generator=g)
-    got, gv = BoundaryMemory(4).select('z', xs.to(DEV))
-    ref, rv = OM.select(xs, 4)
-    for h in range(2):
-        assert sorted(got[h][gv[h]].cpu().tolist()) == sorted(ref[h][rv[h]].tolist())
+            assert d[members, z[r]].min() >= d[r, z[r]] - 1e-5
+
+
+def _inputs(lengths, counts, T, H, D, seed):
+    g = torch.Generator().manual_seed(seed)
+    S, Le = sum(lengths) * T, sum(counts)
+    q, k, v = (torch.randn(S + Le, H, D, generator=g).to(torch.bfloat16) for _ in range(3))
+    tr, c = [], 0
+    for n in counts:
+        tr.append((c, c + n))
+        c += n
+    return q, k, v, tr
+
+
+def _piece_reference(q, k, v, pieces, cand, owner, rep, valid, sample=None, seed=0):
+    """fp32 softmax attention per (piece, head) over the piece's local keys plus, when it reads the memory, its head's
+    valid representatives of other scenes: {piece index: (query rows, out [rows, H, D])}"""
+    H, D = q.shape[1], q.shape[2]
+    rng = np.random.default_rng(seed)
+    out = {}
+    for i, (scene, qrows, krows, reads) in enumerate(pieces):
+        qrows = np.asarray(qrows)
+        if sample is not None and len(qrows) > sample:
+            qrows = np.unique(np.concatenate([qrows[[0, -1]], rng.choice(qrows, sample, replace=False)]))
+        o = torch.empty(len(qrows), H, D)
+        for h in range(H):
+            far = [int(cand[r]) for r, ok in zip(rep[h].tolist(), valid[h].tolist())
+                   if ok and reads and int(owner[r]) != scene]
+            keys = torch.as_tensor(list(krows) + far)
+            p = torch.softmax(q[qrows, h].float() @ k[keys, h].float().T * D ** -0.5, -1)
+            o[:, h] = p @ v[keys, h].float()
+        out[i] = (qrows, o)
+    return out
+
+
+def _frame_pieces(lay, T, S, tr):
+    own = {j: [f * T + t for f in lay.frames[j] for t in range(T)] + [S + t for t in range(*tr[j])]
+           for j in range(lay.n_scenes)}
+    return ([(j, list(range(lo * T, hi * T)), own[j], True) for j, (lo, hi) in enumerate(lay.ranges)] +
+            [(j, [S + t for t in range(*tr[j])], own[j], False) for j in range(lay.n_scenes)])
+
+
+@pytest.mark.parametrize('lengths,M,D', [([3, 5, 2, 4], 8, 64), ([2, 2, 2], 1000, 64), ([6, 1, 3], 5, 128)])
+def test_memory_attention_two_calls_match_reference(lengths, M, D):
+    """the reference test's layouts (16 tokens per frame, 4 heads): a cold call, then a warm call on new keys and
+    values (the stored centroids move two passes); each against fp32 attention with the representatives an identical
+    memory picks (the choice is deterministic)"""
+    print(f'memory attention lengths={lengths} M={M} D={D}', flush=True)
+    T, H = 16, 4
+    lay = SceneLayout(lengths, halo=0)
+    S = lay.n_frames * T
+    counts = [5, 7, 3, 6][:lay.n_scenes]
+    plan_q = None
+    mem, twin = MemoryAttention(BoundaryMemory(M)), BoundaryMemory(M)
+    for call in range(2):
+        q, k, v, tr = _inputs(lengths, counts, T, H, D, call)
+        if plan_q is None:
+            plan_q = frame_plan(lay, T, torch.arange(S), S, [(j, lo * T, hi * T) for j, (lo, hi) in
+                                                            enumerate(lay.ranges)], tr, set(range(lay.n_scenes)), S,
+                                DEV)
+        out = mem(('l0', True), q.to(DEV), k.to(DEV), v.to(DEV), plan_q).cpu()
+        rows, owner = candidates(lay, T, 'cpu')
+        rep, valid = twin.select(('l0', True), k.to(DEV)[rows.to(DEV)])
+        ref = _piece_reference(q, k, v, _frame_pieces(lay, T, S, tr), rows, owner, rep.cpu(), valid.cpu())
+        for i, (qr, o) in ref.items():
+            assert_close(out[qr], o, what=f'call {call} piece {i}')
+
+
+def test_memory_attention_permuted_query_rows():
+    """a plan whose pieces list their query rows out of order (the gather / scatter path); rows no piece names stay
+    zero"""
+    T, H, D, M = 8, 2, 128, 6
+    lay = SceneLayout([3, 2], halo=0)
+    S = lay.n_frames * T
+    q, k, v, tr = _inputs([3, 2], [0, 0], T, H, D, 5)
+    rows, owner = candidates(lay, T, 'cpu')
+    g = np.random.default_rng(3)
+    pieces = [(0, g.permutation(24)[:20].tolist(), list(range(24)), True), (1, list(range(39, 23, -1)),
+                                                                           list(range(24, 40)), True)]
+    plan = make_plan(pieces, rows, owner, DEV)
+    out = MemoryAttention(BoundaryMemory(M))('p', q.to(DEV), k.to(DEV), v.to(DEV), plan).cpu()
+    rep, valid = BoundaryMemory(M).select('p', k.to(DEV)[rows.to(DEV)])
+    ref = _piece_reference(q, k, v, pieces, rows, owner, rep.cpu(), valid.cpu())
+    named = set()
+    for i, (qr, o) in ref.items():
+        assert_close(out[qr], o, what=f'permuted piece {i}')
+        named |= set(qr.tolist())
+    rest = [r for r in range(S) if r not in named]
+    assert out[rest].abs().max().item() == 0
+
+
+def test_memory_attention_at_480p_shape():
+    """the HunyuanVideo-1.5 480p layer's shape (4 scenes x 8 frames x 1590 tokens + 128 text each, 16 heads x 128,
+    M = 128): two calls in a row, sampled query rows of every piece against fp32 attention over the same keys"""
+    T, H, D, M = 1590, 16, 128, 128
+    lengths, counts = [8] * 4, [128] * 4
+    lay = SceneLayout(lengths, halo=0)
+    S = lay.n_frames * T
+    dev_gen = torch.Generator(device=DEV)
+    mem, twin = MemoryAttention(BoundaryMemory(M)), BoundaryMemory(M)
+    tr = [(128 * j, 128 * j + 128) for j in range(4)]
+    plan = frame_plan(lay, T, torch.arange(S), S, [(j, lo * T, hi * T) for j, (lo, hi) in enumerate(lay.ranges)], tr,
+                      set(range(4)), S, DEV)
+    rows, owner = candidates(lay, T, 'cpu')
+    pieces = _frame_pieces(lay, T, S, tr)
+    for call in range(2):
+        print(f'memory attention 480p call {call}', flush=True)
+        dev_gen.manual_seed(40 + call)
+        q, k, v = (torch.randn(S + 512, H, D, generator=dev_gen, device=DEV).to(torch.bfloat16) for _ in range(3))
+        out = mem(('layer', True), q, k, v, plan).cpu()
+        rep, valid = twin.select(('layer', True), k[rows.to(DEV)])
+        assert int(valid.sum(1).min()) > 100        # 128 clusters over 12720 keys: almost all non-empty
+        ref = _piece_reference(q.cpu(), k.cpu(), v.cpu(), pieces, rows, owner, rep.cpu(), valid.cpu(), sample=12,
+                               seed=call)
+        for i, (qr, o) in ref.items():
+            assert_close(out[qr], o, what=f'480p call {call} piece {i}')

@@ -1,49 +1,45 @@
-"""CPU checks of the bounded memory's representative choice (onereel_amd.memory.BoundaryMemory.select is torch ops,
-device-agnostic): against the oracle's selection (oracle/memory.py, memory.py:58-93) on separated groups, through the
-warm update path, and the layout of the (rep, valid) result."""
+"""CPU checks of the bounded memory's host side (onereel_amd.memory): the boundary candidates against the oracle, the
+plan a frame-major model builds (pieces, their query rows and local keys), and that the representative choice has no
+CPU path."""
+import pytest
 import torch
 
-from onereel_amd.memory import BoundaryMemory
+from onereel_amd import _lib as L
+from onereel_amd.layout import SceneLayout
+from onereel_amd.memory import BoundaryMemory, candidate_frames, candidates, frame_plan, make_plan
 from oracle import memory as OM
 
 
-def _groups(g, k, per, H, D, noise=0.01):
-    base = torch.randn(k, H, D, generator=g)
-    return torch.cat([base[i].expand(per, -1, -1) for i in range(k)]) + noise * torch.randn(k * per, H, D, generator=g)
+@pytest.mark.parametrize('lengths', [[3, 5, 2, 4], [1, 2, 1], [6]])
+def test_boundary_candidates_match_oracle(lengths):
+    lay = SceneLayout(lengths, halo=0)
+    T = 7
+    rows, scene = candidates(lay, T, 'cpu')
+    ref_rows, ref_scene = OM.boundary_rows(lay.ranges, T)
+    assert torch.equal(rows, ref_rows) and torch.equal(scene, ref_scene)
+    frames, owner = candidate_frames(lay)
+    assert len(frames) == len(set(frames)) and owner == sorted(owner)
 
 
-def test_select_matches_oracle_on_separated_groups():
-    """members spread enough (noise 0.1) that the nearest member of each group is not a tie at the fp32 rounding of
-    the product's |x|^2 - 2 x.c + |c|^2 distances (the oracle takes explicit differences)"""
-    g = torch.Generator().manual_seed(7)
-    xs = _groups(g, 5, 9, 3, 16, noise=0.1)
-    got, gv = BoundaryMemory(5).select('a', xs)
-    ref, rv = OM.select(xs, 5)
-    for h in range(3):
-        assert sorted(got[h][gv[h]].tolist()) == sorted(ref[h][rv[h]].tolist())
+def test_frame_plan_pieces():
+    """video pieces read their scene's frames and sentence and the memory; sentence pieces their scene's frames and
+    sentence; consecutive query rows are recognised (the in-place query path)"""
+    lay = SceneLayout([2, 3], halo=0)
+    T, S = 4, 20
+    tr = [(0, 3), (3, 5)]
+    p = frame_plan(lay, T, torch.arange(S), S, [(j, lo * T, hi * T) for j, (lo, hi) in enumerate(lay.ranges)], tr,
+                   {0, 1}, S, 'cpu')
+    assert p.host_qlen == [8, 12, 3, 2] and p.host_lens == [11, 14, 11, 14]
+    assert p.q_first == [0, 8, 20, 23]
+    assert p.mem.tolist() == [True, True, False, False] and p.scene.tolist() == [0, 1, 0, 1]
+    assert p.pad[1, :14].tolist() == list(range(8, 20)) + [23, 24]
+    assert p.cand.tolist() == [0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 16, 17, 18, 19]
+    assert p.owner.tolist() == [0] * 8 + [1] * 8
+    q = make_plan([(0, [5, 3, 4], [1, 2], True), (1, [], [0], True)], [0], [0], 'cpu')
+    assert q.q_first == [None] and q.host_qlen == [3]          # empty pieces dropped, permuted rows not in place
 
 
-def test_warm_update_keeps_a_converged_choice():
-    """the second call on a key starts from the stored centroids and runs the short update without the convergence
-    read: on the same candidates it returns the same representatives and valid flags"""
-    g = torch.Generator().manual_seed(8)
-    xs = _groups(g, 6, 7, 2, 32)
-    mem = BoundaryMemory(8)
-    r1, v1 = mem.select('k', xs)
-    r2, v2 = mem.select('k', xs)
-    assert torch.equal(r1, r2) and torch.equal(v1, v2)
-
-
-def test_rep_valid_layout():
-    """valid representatives come first, are distinct candidates, one per non-empty cluster; padding is 0 / False"""
-    g = torch.Generator().manual_seed(9)
-    x = torch.randn(200, 4, 16, generator=g)
-    M = 32
-    rep, valid = BoundaryMemory(M).select('l', x)
-    assert rep.shape == (4, M) and valid.shape == (4, M)
-    for h in range(4):
-        n = int(valid[h].sum())
-        assert n > 0 and bool(valid[h, :n].all()) and not bool(valid[h, n:].any())
-        chosen = rep[h, :n].tolist()
-        assert len(set(chosen)) == n and all(0 <= r < 200 for r in chosen)
-        assert int(rep[h, n:].abs().sum()) == 0
+def test_select_has_no_cpu_path():
+    with pytest.raises(TypeError, match='GPU'):
+        BoundaryMemory(4).select('k', torch.randn(10, 2, 64))
+    assert issubclass(L.HipTypeError, RuntimeError)

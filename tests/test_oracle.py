@@ -409,6 +409,24 @@ def test_memory_select_one_representative_per_separated_group():
         assert sorted(r // 10 for r in rep[h][valid[h]].tolist()) == [0, 1, 2, 3]
 
 
+def test_memory_select_warm_start():
+    """a warm call (two passes from stored centroids) that starts from the centroids a converged cold call ended on,
+    over the same keys, is a fixed point: the same centroids and representatives; from the cold start's own
+    centroids it gives what the cold call's first two passes give"""
+    from oracle import memory as OM
+    g = torch.Generator().manual_seed(4)
+    base = torch.randn(5, 2, 16, generator=g)
+    x = torch.cat([base[i].expand(8, -1, -1) for i in range(5)]) + 0.1 * torch.randn(40, 2, 16, generator=g)
+    rep, valid, c = OM.select(x, 5, centroids=True)
+    rep2, valid2, c2 = OM.select(x, 5, iters=2, centroids=True, start=c)
+    assert torch.equal(rep, rep2) and torch.equal(valid, valid2) and torch.equal(c, c2)
+    xn = torch.nn.functional.normalize(x.float().transpose(0, 1), dim=-1)
+    c0 = xn[:, torch.linspace(0, 39, 5).round().long()]
+    a = OM.select(x, 5, iters=2, centroids=True, start=c0)
+    b = OM.select(x, 5, iters=2, centroids=True)
+    assert all(torch.equal(u, w) for u, w in zip(a, b))
+
+
 @pytest.mark.parametrize('mode', ['raw', 'rotated', 'none'])
 @pytest.mark.parametrize('adjacent', [False, True])
 def test_sampled_row_references_match_the_full_pack(mode, adjacent):
