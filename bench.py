@@ -330,6 +330,102 @@ def run_bounded_memory(args):
     print(json.dumps(out), flush=True)
 
 
+def run_power(args):
+    """board power and clocks while the headline layer's attention kernel runs back to back (about 8 s), then while
+    the bf16 GEMM reference does, sampled with amd-smi every ~0.25 s: whether each sits at the board's power limit
+    and at what clock. One JSON line: per phase the median socket power, the mean over samples of the XCDs' mean
+    clock, and the kernel's ms per call and TFLOP/s over the phase."""
+    import statistics
+    import subprocess
+    import threading
+    import torch
+    from onereel_amd import scene
+    from onereel_amd.layout import SceneLayout
+    dev = torch.device('cuda:0')
+    torch.cuda.set_device(dev)
+    W = workload('hunyuan480p')
+    lay = SceneLayout(W['lengths'], halo=0, extra=extra_from_reps(W['lengths'], W['reps']))
+    S, Le = sum(W['lengths']) * W['T'], sum(W['counts'])
+    g = torch.Generator(device=dev).manual_seed(0)
+    q, k, v = (torch.randn(S, H, D, generator=g, device=dev).to(torch.bfloat16) for _ in range(3))
+    eq, ek, ev = (torch.randn(Le, H, D, generator=g, device=dev).to(torch.bfloat16) for _ in range(3))
+    cos, sin = (x.to(dev) for x in rope_table(*W['grid'], D))
+    plan = scene.ScopePlan(lay, W['T'], W['counts'], Le, True, None, True, True, dev)
+    kp, vp = scene.pack_rows(plan, k, ek, 'k', b_video=v, b_text=ev, cos=cos, sin=sin, mode='raw')
+    ov = torch.empty_like(q)
+    ot = torch.empty(Le, H, D, dtype=torch.bfloat16, device=dev)
+    ws = plan.workspace(H, D)
+    lq = [int(x) for x in (plan.cu_q[1:] - plan.cu_q[:-1]).tolist()]
+    lk = [int(x) for x in (plan.cu_k[1:] - plan.cu_k[:-1]).tolist()]
+    flops = float(sum(4.0 * a * b * H * D for a, b in zip(lq, lk)))
+    attn = lambda: scene.varlen(q, kp, vp, plan.cu_q, plan.cu_k, plan.max_q, plan.max_k, out=ov,
+                                seg_q_src=plan.seg_q_src, q_text=eq, o_text=ot, n_q_video=plan.n_video,
+                                q_rope=plan.q_rope, cos=cos, sin=sin, sum_q=plan.sum_q, workspace=ws)
+    n_g = 16384
+    a = torch.randn(n_g, n_g, generator=g, device=dev).to(torch.bfloat16)
+    b = torch.randn(n_g, n_g, generator=g, device=dev).to(torch.bfloat16)
+    c = a @ b
+    gemm = lambda: torch.matmul(a, b, out=c)
+    samples, phase, stop = [], ['idle'], threading.Event()
+
+    def sample():
+        while not stop.is_set():
+            try:
+                r = subprocess.run(['amd-smi', 'metric', '-g', '0', '-p', '-c', '--json'], capture_output=True,
+                                   text=True, timeout=10)
+                d = json.loads(r.stdout)
+                d = d['gpu_data'][0] if isinstance(d, dict) else d[0]
+                clk = [x['clk']['value'] for name, x in d['clock'].items() if name.startswith('gfx_')]
+                samples.append((phase[0], float(d['power']['socket_power']['value']), sum(clk) / len(clk)))
+            except Exception as e:      # no amd-smi, or a format this parser does not know: no samples
+                samples.append((phase[0], None, repr(e)[:200]))
+                return
+            time.sleep(0.25)
+
+    th = threading.Thread(target=sample, daemon=True)
+    th.start()
+    time.sleep(1.5)
+    out = dict(metric='board power (W) and clock (MHz) while the attention kernel and the bf16 GEMM reference run',
+               unit='W', n_gpus=1, data='synthetic',
+               config=dict(workload='hunyuan15-480p-4scene-attention-kernel-vs-gemm16384', sampler='amd-smi metric '
+                           '-p -c, every ~0.25 s'))
+    for name, fn, fl in (('attention', attn, flops), ('gemm_reference', gemm, 2.0 * n_g ** 3)):
+        fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        phase[0] = 'warm'
+        t_end, n = time.perf_counter() + 1.0, 0
+        while time.perf_counter() < t_end:   # one second to reach the limit before sampling
+            fn()
+            torch.cuda.synchronize()
+        phase[0] = name
+        e0.record()
+        t_end = time.perf_counter() + 8.0
+        while time.perf_counter() < t_end:
+            for _ in range(20):
+                fn()
+            n += 20
+            torch.cuda.synchronize()
+        e1.record()
+        phase[0] = 'idle'
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / n
+        got = [(p_, c_) for ph, p_, c_ in samples if ph == name and p_ is not None]
+        out[name] = dict(ms=round(ms, 4), tflops=round(fl / ms / 1e9, 1), calls=n, samples=len(got),
+                         socket_power_w=statistics.median([p_ for p_, _ in got]) if got else None,
+                         mean_gfx_clock_mhz=round(sum(c_ for _, c_ in got) / len(got), 1) if got else None)
+        time.sleep(1.5)
+    stop.set()
+    th.join(timeout=15)
+    idle = [p_ for ph, p_, _ in samples if ph == 'idle' and p_ is not None]
+    out['idle_socket_power_w'] = statistics.median(idle) if idle else None
+    errs = [c_ for _, p_, c_ in samples if p_ is None]
+    if errs:
+        out['sampler_error'] = errs[0]
+    out['value'] = out['attention']['socket_power_w']
+    print(json.dumps(out), flush=True)
+
+
 def run_frame_memory(args):
     """frame memory at the DiT-step shape: pooling of one observed layer (16 scenes x 15 frames x 880 tokens x 3072
     bf16, 1.3 GB) per frame, and the k-means choice of 4 representatives among the 240 frames; each call timed alone
@@ -390,14 +486,15 @@ def main():
     ap.add_argument('--no-gemm-ref', action='store_true', help='skip the bf16 GEMM reference')
     ap.add_argument('--workload', default='hunyuan480p',
                     choices=['hunyuan480p', 'wan704'] + UNEVEN + ['wan-dit-step', 'frame-memory', 'lse-merge',
-                                                                   'bounded-memory'],
+                                                                   'bounded-memory', 'power'],
                     help='hunyuan480p (default, the headline): the HunyuanVideo-1.5 480p 4-scene layer; wan704 and '
                          'unevenK: the same layer at the Wan2.2 704x1280 shape and at the K-scene uneven sweep points '
                          '(K = 2, 4, 8, 12); wan-dit-step: '
                          'one forward of a random-init Wan2.2-TI2V-5B-shaped DiT over 16 scenes x 15 frames x 880 '
                          'tokens with frame memory 4 (end-to-end ms per step); frame-memory: the pooling and '
                          'selection kernels at that shape; lse-merge: the log-sum-exp merge at the 480p layer shape; '
-                         'bounded-memory: the head-major bounded memory layer at that shape')
+                         'bounded-memory: the head-major bounded memory layer at that shape; power: board power and '
+                         'clocks under the attention kernel and under the bf16 GEMM reference (amd-smi)')
     ap.add_argument('--once', action='store_true',
                     help='profiling mode: a 1 GiB device copy (counter calibration), then the layout, pack-gather, '
                          'attention and scatter kernels once each, then one bf16 16384^3 torch.matmul (the GEMM '
@@ -416,6 +513,8 @@ def main():
         return run_lse_merge(args)
     if args.workload == 'bounded-memory':
         return run_bounded_memory(args)
+    if args.workload == 'power':
+        return run_power(args)
     args.steps = 20 if args.steps is None else args.steps
     args.warmup = 3 if args.warmup is None else args.warmup
     W = workload(args.workload)
@@ -459,19 +558,30 @@ def main():
         print('once: copy 1 GiB, layout, pack_gather, plan + attention, scatter, bf16 GEMM reference', flush=True)
         return
 
-    def step():
-        plan.build()
-        return scene.scene_attention(plan, q, k, v, eq, ek, ev, cos, sin, mode='raw', fused=True, kbuf=kbuf,
-                                     vbuf=vbuf)
+    def make_step(p):
+        def step():
+            p.build()
+            return scene.scene_attention(p, q, k, v, eq, ek, ev, cos, sin, mode='raw', fused=True, kbuf=kbuf,
+                                         vbuf=vbuf)
+        return step
 
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        step()
-    torch.cuda.synchronize()
-    ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    def time_steps(step):
+        for _ in range(args.warmup):
+            step()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            step()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) * 1e3 / args.steps
+
+    ms = time_steps(make_step(plan))
+    # the other shared-frame layout of a frame-memory run: before shared_switch the shared keys keep their own
+    # positions ('source'), from it on they sit next to the scene ('adjacent'); same scopes and FLOPs, other rotations
+    other = None
+    if W['reps'] and W['scene_rope']:
+        plan_o = scene.ScopePlan(lay, T_, W['counts'], Le, W['scene_rope'], None, not W['adjacent'], True, dev)
+        ms_o = time_steps(make_step(plan_o))
 
     # per-kernel durations with HIP events on the launch stream
     R = args.kernel_reps
@@ -490,6 +600,25 @@ def main():
     scat()
     torch.cuda.synchronize()
     t_attn = time_events(attn, R, stream)
+    if W['reps'] and W['scene_rope']:
+        pack_o = lambda: scene.pack_rows(plan_o, k, ek, 'k', out=kbuf, b_video=v, b_text=ev, b_out=vbuf, cos=cos,
+                                         sin=sin, mode='raw')
+        attn_o = lambda: scene.varlen(q, kbuf, vbuf, plan_o.cu_q, plan_o.cu_k, plan_o.max_q, plan_o.max_k, out=ov,
+                                      seg_q_src=plan_o.seg_q_src, q_text=eq, o_text=ot, n_q_video=plan_o.n_video,
+                                      q_rope=plan_o.q_rope, cos=cos, sin=sin, sum_q=plan_o.sum_q, workspace=ws)
+        pack_o()
+        attn_o()
+        torch.cuda.synchronize()
+        t_attn_o = time_events(attn_o, R, stream)
+        pack()                                      # the adjacent layout's keys back in the buffers
+        torch.cuda.synchronize()
+        v_o = flops / (ms_o * 1e-3) / 1e12
+        other = dict(shared_pos='source' if W['adjacent'] else 'adjacent',
+                     when='denoising steps before shared_switch (5)' if W['adjacent'] else 'from shared_switch on',
+                     ms_per_step=round(ms_o, 4), tflops_step=round(v_o, 2),
+                     frac_bf16_peak_step=round(v_o / PEAK_BF16_TFLOPS, 4),
+                     attention=dict(ms=round(t_attn_o, 4), tflops=round(flops / t_attn_o / 1e9, 1),
+                                    frac_bf16_peak=round(flops / t_attn_o / 1e9 / PEAK_BF16_TFLOPS, 4)))
     # HBM-bound kernels: each call timed alone after the caches were evicted (cold), and back to back (warm: inputs
     # that fit the 256 MB last-level cache are then partly served from it)
     evict = torch.ones(128 << 20, dtype=torch.int32, device=dev)
@@ -537,6 +666,8 @@ def main():
                              unit='TFLOP/s', frac=round(flops / t_attn / 1e9 / PEAK_BF16_TFLOPS, 4), traffic=traffic,
                              kernel=f'{kname} (+ plan_kernel, one block, ~10 us)'),
                kernels=kernels)
+    if other:
+        out['other_layout'] = other
     if copy_ref:
         out['copy_reference'] = copy_ref
     if headline and not args.no_gemm_ref:
