@@ -4,7 +4,8 @@ Workload (one step = one pass of the hot path over one layer's synthetic inputs,
 4 scenes x 8 latent frames x 1590 tokens (30 x 53 latent grid) + 128 text tokens per scene, frame memory of 4 frames
 (representatives {0, 10, 21, 31}), shared frames at their adjacent positions (step >= shared_switch 5), scene RoPE
 over a 3D table, 16 heads x 128, bf16 q / k / v ~ N(0, 1). A step runs the layout kernel, the K/V pack-gather (RoPE
-on the keys), the varlen attention (RoPE on the Q load, output in place) and the text-padding write-back.
+on the keys), the RoPE of the video queries (once, in token order), the varlen attention (queries and outputs in
+place) and the text-padding write-back.
 
 value = useful attention TFLOP/s of the whole step (sum over scopes of 4 * Lq * Lk * H * D per step time).
 roofline: the attention kernel alone, timed with HIP events on the stream it runs on.
@@ -358,9 +359,10 @@ def run_power(args):
     lq = [int(x) for x in (plan.cu_q[1:] - plan.cu_q[:-1]).tolist()]
     lk = [int(x) for x in (plan.cu_k[1:] - plan.cu_k[:-1]).tolist()]
     flops = float(sum(4.0 * a * b * H * D for a, b in zip(lq, lk)))
-    attn = lambda: scene.varlen(q, kp, vp, plan.cu_q, plan.cu_k, plan.max_q, plan.max_k, out=ov,
+    qr = scene.rotate_queries(plan, q, cos, sin)
+    attn = lambda: scene.varlen(qr, kp, vp, plan.cu_q, plan.cu_k, plan.max_q, plan.max_k, out=ov,
                                 seg_q_src=plan.seg_q_src, q_text=eq, o_text=ot, n_q_video=plan.n_video,
-                                q_rope=plan.q_rope, cos=cos, sin=sin, sum_q=plan.sum_q, workspace=ws)
+                                sum_q=plan.sum_q, workspace=ws)
     n_g = 16384
     a = torch.randn(n_g, n_g, generator=g, device=dev).to(torch.bfloat16)
     b = torch.randn(n_g, n_g, generator=g, device=dev).to(torch.bfloat16)
@@ -542,6 +544,7 @@ def main():
     flops = float(sum(4.0 * a * b * H * D for a, b in zip(lq, lk)))
     kbuf = torch.empty(plan.sum_k, H, D, dtype=torch.bfloat16, device=dev)
     vbuf = torch.empty_like(kbuf)
+    qbuf = torch.empty_like(q)                   # the video queries rotated once per layer
 
     if args.once:
         src = torch.empty(1 << 29, dtype=torch.int16, device=dev)
@@ -550,19 +553,20 @@ def main():
         torch.cuda.synchronize()
         plan.build()
         ov, ot = scene.scene_attention(plan, q, k, v, eq, ek, ev, cos, sin, mode='raw', fused=True, kbuf=kbuf,
-                                       vbuf=vbuf)
+                                       vbuf=vbuf, qbuf=qbuf)
         scene.scatter(plan, torch.zeros(plan.sum_q, H, D, dtype=torch.bfloat16, device=dev), ov, ot)
         torch.cuda.synchronize()
         if headline:
             gemm_reference(reps=1)
-        print('once: copy 1 GiB, layout, pack_gather, plan + attention, scatter, bf16 GEMM reference', flush=True)
+        print('once: copy 1 GiB, layout, pack_gather, rotate_q, plan + attention, scatter, bf16 GEMM reference',
+              flush=True)
         return
 
     def make_step(p):
         def step():
             p.build()
             return scene.scene_attention(p, q, k, v, eq, ek, ev, cos, sin, mode='raw', fused=True, kbuf=kbuf,
-                                         vbuf=vbuf)
+                                         vbuf=vbuf, qbuf=qbuf)
         return step
 
     def time_steps(step):
@@ -588,13 +592,16 @@ def main():
     ov = torch.empty_like(q)
     ot = torch.empty(Le, H, D, dtype=torch.bfloat16, device=dev)
     ws = plan.workspace(H, D)
-    attn = lambda: scene.varlen(q, kbuf, vbuf, plan.cu_q, plan.cu_k, plan.max_q, plan.max_k, out=ov,
+    # the attention kernel as the step runs it: video queries already rotated (qbuf), read in place
+    attn = lambda: scene.varlen(qbuf, kbuf, vbuf, plan.cu_q, plan.cu_k, plan.max_q, plan.max_k, out=ov,
                                 seg_q_src=plan.seg_q_src, q_text=eq, o_text=ot, n_q_video=plan.n_video,
-                                q_rope=plan.q_rope, cos=cos, sin=sin, sum_q=plan.sum_q, workspace=ws)
+                                sum_q=plan.sum_q, workspace=ws)
     pack = lambda: scene.pack_rows(plan, k, ek, 'k', out=kbuf, b_video=v, b_text=ev, b_out=vbuf, cos=cos, sin=sin,
                                    mode='raw')
+    rotq = lambda: scene.rotate_queries(plan, q, cos, sin, out=qbuf)
     qpk = torch.empty(plan.sum_q, H, D, dtype=torch.bfloat16, device=dev)
     scat = lambda: scene.scatter(plan, qpk, ov, ot)
+    rotq()
     attn()
     pack()
     scat()
@@ -603,14 +610,16 @@ def main():
     if W['reps'] and W['scene_rope']:
         pack_o = lambda: scene.pack_rows(plan_o, k, ek, 'k', out=kbuf, b_video=v, b_text=ev, b_out=vbuf, cos=cos,
                                          sin=sin, mode='raw')
-        attn_o = lambda: scene.varlen(q, kbuf, vbuf, plan_o.cu_q, plan_o.cu_k, plan_o.max_q, plan_o.max_k, out=ov,
-                                      seg_q_src=plan_o.seg_q_src, q_text=eq, o_text=ot, n_q_video=plan_o.n_video,
-                                      q_rope=plan_o.q_rope, cos=cos, sin=sin, sum_q=plan_o.sum_q, workspace=ws)
+        attn_o = lambda: scene.varlen(qbuf, kbuf, vbuf, plan_o.cu_q, plan_o.cu_k, plan_o.max_q, plan_o.max_k,
+                                      out=ov, seg_q_src=plan_o.seg_q_src, q_text=eq, o_text=ot,
+                                      n_q_video=plan_o.n_video, sum_q=plan_o.sum_q, workspace=ws)
+        scene.rotate_queries(plan_o, q, cos, sin, out=qbuf)
         pack_o()
         attn_o()
         torch.cuda.synchronize()
         t_attn_o = time_events(attn_o, R, stream)
         pack()                                      # the adjacent layout's keys back in the buffers
+        rotq()
         torch.cuda.synchronize()
         v_o = flops / (ms_o * 1e-3) / 1e12
         other = dict(shared_pos='source' if W['adjacent'] else 'adjacent',
@@ -627,16 +636,21 @@ def main():
     pack_bytes = 2 * 2 * plan.sum_k * row            # K and V rows read + written
     t_pack, t_pack_w = time_cold(pack, R, stream, flush), time_events(pack, R, stream)
     t_layout = time_cold(plan.build, R, stream, flush)
+    t_rot = time_cold(rotq, R, stream, flush)
     t_scat, t_scat_w = time_cold(scat, R, stream, flush), time_events(scat, R, stream)
     copy_ref = copy_reference(pack_bytes // 2, R, stream, flush) if headline else None
     del evict
     scat_bytes = 2 * plan.sum_q * row                # packed rows read + written
+    rot_bytes = 2 * plan.n_video * row + plan.n_video * D * 8   # video query rows read + written, fp32 cos / sin rows
     kernels = {
         'attention': dict(ms=round(t_attn, 4), tflops=round(flops / t_attn / 1e9, 1),
                           frac_bf16_peak=round(flops / t_attn / 1e9 / PEAK_BF16_TFLOPS, 4)),
         'pack_gather_kv': dict(ms=round(t_pack, 4), gbs=round(pack_bytes / t_pack / 1e6, 1),
                                frac_hbm_peak=round(pack_bytes / t_pack / 1e6 / PEAK_HBM_GBS, 4), bytes=pack_bytes,
                                warm_ms=round(t_pack_w, 4), timing='cold caches, single calls'),
+        'rotate_q': dict(ms=round(t_rot, 4), gbs=round(rot_bytes / t_rot / 1e6, 1),
+                         frac_hbm_peak=round(rot_bytes / t_rot / 1e6 / PEAK_HBM_GBS, 4), bytes=rot_bytes,
+                         timing='cold caches, single calls'),
         'layout': dict(us=round(t_layout * 1e3, 2), gbs=round(plan.index_bytes() / t_layout / 1e6, 1),
                        bytes=plan.index_bytes(),
                        bound=f'launch latency ({plan.index_bytes() / 1e6:.1f} MB of int32 indices)'),

@@ -4,6 +4,7 @@
  * One DiT attention layer of OneReel's scene attention on one GPU runs as:
  *   or_layout_build   scope layout on the device: cu_seqlens, per-row gather indices and scene-RoPE rows
  *   or_pack_gather    K/V (or Q) rows of every scope packed densely, RoPE applied on the way
+ *   or_rotate_rows    the video queries rotated once, in token order (RoPE ahead of in-place attention)
  *   or_varlen_fwd     packed varlen attention (bf16 MFMA), optional RoPE on the Q load, optional in-place Q / O
  *   or_scatter        packed output rows written back to token order, text padding rows zeroed
  *   or_lse_merge      log-sum-exp merge of two partial attention results (attention split over key sets)
@@ -106,6 +107,16 @@ int or_pack_gather(const void* a_video, const void* a_text, const void* b_video,
                    const int32_t* src_idx, const int32_t* rope_row, const int32_t* move_from,
                    const float* cos_table, const float* sin_table, int64_t n_rope_rows,
                    int64_t n_rows, int32_t H, int32_t D, void* a_out, void* b_out, void* stream);
+
+/* Replaces the RoPE of the video queries in Processor.__call__ (src/onereel/models/hunyuan15.py:183-191, diffusers
+ * apply_rotary_emb on q): for every r < n_rows with src = src_idx[r] < n_video, row src of out = row src of x
+ * rotated at table row rope_row[r] (not rotated when rope_row[r] < 0 or past the table), with the rounding of
+ * or_pack_gather; rows src >= n_video are skipped. With a layout's q_src / q_rope it rotates every video query once,
+ * in token order, ahead of an attention call that reads the queries in place. x, out: bf16 rows of H * D elements
+ * (row strides in elements); out may not alias x. */
+int or_rotate_rows(const void* x, int64_t x_row_stride, int64_t n_video, const int32_t* src_idx,
+                   const int32_t* rope_row, const float* cos_table, const float* sin_table, int64_t n_rope_rows,
+                   int64_t n_rows, int32_t H, int32_t D, void* out, int64_t out_row_stride, void* stream);
 
 /* Replaces the write-back of Processor.scene (hunyuan15.py:226,231-235) after attention.packed's split
  * (attention.py:71): o_video[dst] / o_text[dst - n_video] = packed[r] for dst = dst_idx[r]; then the text rows

@@ -53,6 +53,7 @@ SIGNATURES = {
     'or_layout_build': (i32, [ctypes.POINTER(LayoutDesc), ctypes.POINTER(LayoutOut), vp]),
     'or_pack_gather': (i32, [vp, vp, vp, vp, i64, i64, i64, vp, vp, vp, vp, vp, i64, i64, i32, i32, vp, vp, vp]),
     'or_scatter': (i32, [vp, vp, i64, i64, vp, vp, i64, i64, i64, i64, i32, i32, vp]),
+    'or_rotate_rows': (i32, [vp, i64, i64, vp, vp, vp, vp, i64, i64, i32, i32, vp, i64, vp]),
     'or_varlen_workspace_size': (i64, [i32, i32, i32, i32]),
     'or_varlen_fwd': (i32, [ctypes.POINTER(VarlenArgs), vp]),
     'or_varlen_fwd_noalloc': (i32, [ctypes.POINTER(VarlenArgs), vp]),

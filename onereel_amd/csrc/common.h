@@ -166,13 +166,21 @@ __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2_t));
 }
 
-// 8 bf16 in `v` rotated with the table entries at element offset `off` of rows `row` (sign +1) or its inverse (-1)
-__device__ __forceinline__ u32x4 rotate8(u32x4 v, const float* __restrict__ cos_t, const float* __restrict__ sin_t,
-                                int64_t off, float sign) {
-  f32x4 c0 = *(const f32x4*)(cos_t + off), c1 = *(const f32x4*)(cos_t + off + 4);
-  f32x4 s0 = *(const f32x4*)(sin_t + off), s1 = *(const f32x4*)(sin_t + off + 4);
-  float c[8] = {c0[0], c0[1], c0[2], c0[3], c1[0], c1[1], c1[2], c1[3]};
-  float s[8] = {s0[0], s0[1], s0[2], s0[3], s1[0], s1[1], s1[2], s1[3]};
+// the table entries of 8 consecutive elements: cos and sin of one table row at one element offset
+struct Tab8 {
+  f32x4 c0, c1, s0, s1;
+};
+
+__device__ __forceinline__ Tab8 load_tab8(const float* __restrict__ cos_t, const float* __restrict__ sin_t,
+                                          int64_t off) {
+  return Tab8{*(const f32x4*)(cos_t + off), *(const f32x4*)(cos_t + off + 4), *(const f32x4*)(sin_t + off),
+              *(const f32x4*)(sin_t + off + 4)};
+}
+
+// 8 bf16 in `v` rotated with the table entries t (sign +1) or its inverse (-1)
+__device__ __forceinline__ u32x4 rotate8(u32x4 v, const Tab8& t, float sign) {
+  float c[8] = {t.c0[0], t.c0[1], t.c0[2], t.c0[3], t.c1[0], t.c1[1], t.c1[2], t.c1[3]};
+  float s[8] = {t.s0[0], t.s0[1], t.s0[2], t.s0[3], t.s1[0], t.s1[1], t.s1[2], t.s1[3]};
   u32x4 r;
 #pragma unroll
   for (int p = 0; p < 4; ++p) {
@@ -182,6 +190,12 @@ __device__ __forceinline__ u32x4 rotate8(u32x4 v, const float* __restrict__ cos_
     r[p] = pack2(y0, y1);
   }
   return r;
+}
+
+// 8 bf16 in `v` rotated with the table entries at element offset `off` of rows `row` (sign +1) or its inverse (-1)
+__device__ __forceinline__ u32x4 rotate8(u32x4 v, const float* __restrict__ cos_t, const float* __restrict__ sin_t,
+                                int64_t off, float sign) {
+  return rotate8(v, load_tab8(cos_t, sin_t, off), sign);
 }
 
 // Sum over the 64 lanes of a wavefront, the same in every lane: DPP adds within rows of 16 lanes (pairs, quads,

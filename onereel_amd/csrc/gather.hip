@@ -40,6 +40,8 @@ struct GatherArgs {
   int H, D;
   uint16_t* a_out;
   uint16_t* b_out;
+  int64_t out_stride;   // IN_PLACE: row stride of a_out (rows are written at their source row)
+  int shared_d0;        // every chunk of a lane has the same offset within its head: (8 * lanes per row) % D == 0
 };
 
 // Rows narrower than 64 chunks (e.g. the single-head rows of the bounded memory, 16 chunks) share a wavefront: lane
@@ -56,7 +58,9 @@ __device__ __forceinline__ RowLanes row_lanes(int chunks, int lane) {
   return RowLanes{cp, 64 / cp, lane / cp, lane % cp};
 }
 
-template <bool NARROW>
+// IN_PLACE (or_rotate_rows): row r is written to the same row src_idx[r] of a_out, not to packed row r, and rows of
+// the second source (src >= n_video) are skipped
+template <bool NARROW, bool IN_PLACE>
 __global__ __launch_bounds__(kThreads) void pack_gather_kernel(GatherArgs g) {
   const int lane = threadIdx.x & 63;
   const int64_t wave = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6);
@@ -69,6 +73,7 @@ __global__ __launch_bounds__(kThreads) void pack_gather_kernel(GatherArgs g) {
     if (r >= g.n_rows) continue;
     const int src = g.src_idx[r];
     const bool text = src >= g.n_video;
+    if (IN_PLACE && text) continue;
     const int64_t off = text ? (int64_t)(src - g.n_video) * g.text_stride : (int64_t)src * g.src_stride;
     const uint16_t* a = (text ? g.a_text : g.a_video) + off;
     const uint16_t* b = g.b_out ? (text ? g.b_text : g.b_video) + off : nullptr;
@@ -85,21 +90,30 @@ __global__ __launch_bounds__(kThreads) void pack_gather_kernel(GatherArgs g) {
         if (b) vb[i] = *(const u32x4*)(b + 8 * c);
       }
     }
-    uint16_t* ao = g.a_out + r * (int64_t)row_elems;
+    // every chunk of a lane sits at the same offset within its head (8 cp a multiple of D): the lane's table entries
+    // are loaded once per row, next to the row's loads, instead of once per chunk
+    const bool rot = g.move_from ? (mfrom >= 0 && rope >= 0) : rope >= 0;
+    Tab8 tr, tm;
+    if (g.shared_d0 && rot) {
+      const int d0 = (8 * rl.cl) % g.D;
+      tr = load_tab8(g.cos_t, g.sin_t, (int64_t)rope * g.D + d0);
+      if (g.move_from) tm = load_tab8(g.cos_t, g.sin_t, (int64_t)mfrom * g.D + d0);
+    }
+    uint16_t* ao = IN_PLACE ? g.a_out + (int64_t)src * g.out_stride : g.a_out + r * (int64_t)row_elems;
     uint16_t* bo = g.b_out ? g.b_out + r * (int64_t)row_elems : nullptr;
 #pragma unroll
     for (int i = 0; i < kMaxChunksPerLane; ++i) {
       const int c = rl.cl + rl.cp * i;
       if (c < chunks) {
         u32x4 x = va[i];
-        const int d0 = (8 * c) % g.D;
-        if (g.move_from) {
-          if (mfrom >= 0 && rope >= 0) {
-            x = rotate8(x, g.cos_t, g.sin_t, (int64_t)mfrom * g.D + d0, -1.0f);
-            x = rotate8(x, g.cos_t, g.sin_t, (int64_t)rope * g.D + d0, 1.0f);
+        if (rot) {
+          if (!g.shared_d0) {
+            const int d0 = (8 * c) % g.D;
+            tr = load_tab8(g.cos_t, g.sin_t, (int64_t)rope * g.D + d0);
+            if (g.move_from) tm = load_tab8(g.cos_t, g.sin_t, (int64_t)mfrom * g.D + d0);
           }
-        } else if (rope >= 0) {
-          x = rotate8(x, g.cos_t, g.sin_t, (int64_t)rope * g.D + d0, 1.0f);
+          if (g.move_from) x = rotate8(x, tm, -1.0f);
+          x = rotate8(x, tr, 1.0f);
         }
         store_nt(ao + 8 * c, x);
         if (bo) store_nt(bo + 8 * c, vb[i]);
@@ -192,6 +206,18 @@ int check_row_shape(int H, int D, const char* who) {
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
+// lanes per row as pack_gather_kernel lays them out (64 for rows of 64 chunks or more), times 8 elements per chunk,
+// a multiple of D: then every chunk a lane moves starts at the same element within its head
+int shared_d0(int H, int D) {
+  const int chunks = H * D / 8;
+  int cp = 64;
+  if (chunks < 64) {
+    cp = 1;
+    while (cp < chunks) cp <<= 1;
+  }
+  return (8 * cp) % D == 0 ? 1 : 0;
+}
+
 }  // namespace
 }  // namespace onereel
 
@@ -216,11 +242,38 @@ extern "C" int or_pack_gather(const void* a_video, const void* a_text, const voi
   GatherArgs g{(const uint16_t*)a_video, (const uint16_t*)(a_text ? a_text : a_video),
                (const uint16_t*)b_video, (const uint16_t*)(b_text ? b_text : b_video),
                src_row_stride, text_row_stride, n_video, src_idx, rope_row, move_from, cos_table, sin_table,
-               n_rope_rows, n_rows, H, D, (uint16_t*)a_out, (uint16_t*)b_out};
+               n_rope_rows, n_rows, H, D, (uint16_t*)a_out, (uint16_t*)b_out, 0, shared_d0(H, D)};
   if ((int64_t)H * D < 64 * 8)   // rows under 64 chunks share a wavefront
-    hipLaunchKernelGGL(pack_gather_kernel<true>, dim3(row_grid(n_rows)), dim3(kThreads), 0, (hipStream_t)stream, g);
+    hipLaunchKernelGGL((pack_gather_kernel<true, false>), dim3(row_grid(n_rows)), dim3(kThreads), 0,
+                       (hipStream_t)stream, g);
   else
-    hipLaunchKernelGGL(pack_gather_kernel<false>, dim3(row_grid(n_rows)), dim3(kThreads), 0, (hipStream_t)stream, g);
+    hipLaunchKernelGGL((pack_gather_kernel<false, false>), dim3(row_grid(n_rows)), dim3(kThreads), 0,
+                       (hipStream_t)stream, g);
+  return check_hip(hipGetLastError(), "pack_gather_kernel launch");
+}
+
+extern "C" int or_rotate_rows(const void* x, int64_t x_row_stride, int64_t n_video, const int32_t* src_idx,
+                              const int32_t* rope_row, const float* cos_table, const float* sin_table,
+                              int64_t n_rope_rows, int64_t n_rows, int32_t H, int32_t D, void* out,
+                              int64_t out_row_stride, void* stream) {
+  if (int rc = check_row_shape(H, D, "or_rotate_rows")) return rc;
+  if (n_rows < 0) return fail_arg("or_rotate_rows: n_rows < 0");
+  if (n_rows == 0) return 0;
+  if (!x || !src_idx || !rope_row || !out || !cos_table || !sin_table || n_rope_rows < 1)
+    return fail_arg("or_rotate_rows: x, src_idx, rope_row, out and the cos / sin tables are required");
+  if (x_row_stride < (int64_t)H * D || out_row_stride < (int64_t)H * D)
+    return fail_arg("or_rotate_rows: row strides must cover H * D elements");
+  if (!aligned16(x) || !aligned16(out) || x_row_stride % 8 || out_row_stride % 8)
+    return fail_arg("or_rotate_rows: pointers must be 16-byte aligned and row strides multiples of 8 elements");
+  GatherArgs g{(const uint16_t*)x, (const uint16_t*)x, nullptr, nullptr, x_row_stride, x_row_stride, n_video, src_idx,
+               rope_row, nullptr, cos_table, sin_table, n_rope_rows, n_rows, H, D, (uint16_t*)out, nullptr,
+               out_row_stride, shared_d0(H, D)};
+  if ((int64_t)H * D < 64 * 8)
+    hipLaunchKernelGGL((pack_gather_kernel<true, true>), dim3(row_grid(n_rows)), dim3(kThreads), 0,
+                       (hipStream_t)stream, g);
+  else
+    hipLaunchKernelGGL((pack_gather_kernel<false, true>), dim3(row_grid(n_rows)), dim3(kThreads), 0,
+                       (hipStream_t)stream, g);
   return check_hip(hipGetLastError(), "pack_gather_kernel launch");
 }
 

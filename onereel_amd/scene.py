@@ -1,11 +1,12 @@
 """The scene-attention layer engine: device layout, K/V pack-gather, varlen attention and write-back.
 
-One layer of `Processor.scene` on one GPU (src/onereel/models/hunyuan15.py:212-251) runs here as at most four
+One layer of `Processor.scene` on one GPU (src/onereel/models/hunyuan15.py:212-251) runs here as at most five
 launches on the caller's current stream, with no host synchronisation:
 
     ScopePlan.build      or_layout_build   cu_seqlens, gather rows, RoPE rows (cached per layout and step mode)
     pack_kv              or_pack_gather    K (rotated on the way) and V rows of every scope, one pass
-    attention            or_varlen_fwd     Q read in place (rotated on the load), output written in place
+    rotate_queries       or_rotate_rows    the video queries rotated once, in token order
+    attention            or_varlen_fwd     Q read in place, output written in place
     zero text padding    or_scatter        ot rows past the valid text (ot = eq.new_zeros in the reference)
 
 `mode` says what q / k hold: 'raw' (before RoPE: the fused path, the table row of every query and key comes from
@@ -289,12 +290,35 @@ def zero_text_padding(plan: ScopePlan, ot: torch.Tensor):
     return ot
 
 
+def rotate_queries(plan: ScopePlan, q, cos, sin, out=None):
+    """every video query row rotated at its scene-RoPE table row, in token order (or_rotate_rows over the plan's
+    packed queries; text rows are not rotated and stay in the text tensor): [F*T, H, D] bf16"""
+    H, D = q.shape[1], q.shape[2]
+    _check_bf16(q, out)
+    _, qs = _rows2d(q, H, D)
+    cos, sin, n_rows = _tables(cos, sin, D)
+    if cos is None:
+        raise L.HipValueError('RoPE needs the (cos, sin) tables')
+    if plan.max_rope_row >= n_rows:
+        raise L.HipValueError(f'layout needs rotary row {plan.max_rope_row} but the table has {n_rows} rows')
+    out = torch.empty(plan.n_video, H, D, dtype=q.dtype, device=q.device) if out is None else out
+    _, os_ = _rows2d(out, H, D)
+    if out.shape[0] < plan.n_video:
+        raise L.HipValueError(f'out holds {out.shape[0]} rows, the layout has {plan.n_video} video rows')
+    L.check(L.lib().or_rotate_rows(q.data_ptr(), qs, plan.n_video, plan.q_src.data_ptr(), plan.q_rope.data_ptr(),
+                                   cos.data_ptr(), sin.data_ptr(), n_rows, plan.sum_q, H, D, out.data_ptr(), os_,
+                                   L.stream_handle(q.device)), 'or_rotate_rows')
+    return out
+
+
 def scene_attention(plan: ScopePlan, q, k, v, eq, ek, ev, cos=None, sin=None, mode='raw', fused=True,
-                    kbuf=None, vbuf=None):
+                    kbuf=None, vbuf=None, qbuf=None, rotate_q='pre'):
     """(ov, ot) of one scene-attention layer. q / k / v [F*T, H, D] and eq / ek / ev [Le, H, D] bf16 on the GPU.
 
     fused=True: K/V packed once, Q read in place, outputs written in place. fused=False: the reference's data flow
-    (Q, K, V packed, one varlen call on packed tensors, write-back by the scatter kernel)."""
+    (Q, K, V packed, one varlen call on packed tensors, write-back by the scatter kernel). With mode 'raw' and
+    fused=True the video queries are rotated once ahead of the attention call (rotate_q='pre', into qbuf when given;
+    the attention kernel then reads no rotary table), or on the attention kernel's Q load (rotate_q='load')."""
     if mode not in MODES:
         raise L.HipValueError(mode)
     H, D = q.shape[1], q.shape[2]
@@ -307,8 +331,13 @@ def scene_attention(plan: ScopePlan, q, k, v, eq, ek, ev, cos=None, sin=None, mo
     ot = torch.empty(eq.shape[0], H, D, dtype=q.dtype, device=q.device) if eq is not None else None
     qmode = 'raw' if mode == 'raw' else 'none'
     if fused:
+        if rotate_q not in ('pre', 'load'):
+            raise L.HipValueError(f"rotate_q must be 'pre' or 'load', got {rotate_q!r}")
+        on_load = qmode == 'raw' and rotate_q == 'load'
+        if qmode == 'raw' and not on_load:
+            q = rotate_queries(plan, q, cos, sin, out=qbuf)
         varlen(q, kp, vp, plan.cu_q, plan.cu_k, plan.max_q, plan.max_k, out=ov, seg_q_src=plan.seg_q_src,
-               q_text=eq, o_text=ot, n_q_video=plan.n_video, q_rope=plan.q_rope if qmode == 'raw' else None,
+               q_text=eq, o_text=ot, n_q_video=plan.n_video, q_rope=plan.q_rope if on_load else None,
                cos=cos, sin=sin, sum_q=plan.sum_q, workspace=plan.workspace(H, D))
         if ot is not None:
             zero_text_padding(plan, ot)

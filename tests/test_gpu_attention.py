@@ -189,20 +189,23 @@ def _layer_inputs(case, seed=0):
     return q, k, v, eq, ek, ev, cos, sin
 
 
-@pytest.mark.parametrize('name,per_seg', [('cpu_plumbing', None), ('hunyuan480p', 48), ('wan704', 48),
-                                          ('uneven_K2', 32), ('uneven_K4', 24), ('uneven_K8', 24), ('uneven_K12', 24)])
+@pytest.mark.parametrize('name,per_seg,rotate_q', [
+    ('cpu_plumbing', None, 'pre'), ('cpu_plumbing', None, 'load'), ('hunyuan480p', 48, 'pre'),
+    ('hunyuan480p', 48, 'load'), ('wan704', 48, 'pre'), ('uneven_K2', 32, 'pre'), ('uneven_K4', 24, 'pre'),
+    ('uneven_K8', 24, 'pre'), ('uneven_K12', 24, 'pre')])
 @pytest.mark.parametrize('adjacent', [False, True])
-def test_scene_layer_matches_oracle(name, per_seg, adjacent):
-    """the fused layer (K/V pack with RoPE, Q RoPE on the load, in-place output) against the oracle's packing plus
-    per-scope fp32 attention; full outputs for the CPU-plumbing layout, sampled query rows (every segment's first / last
-    rows included) at the full-size configs, each segment's reference built from that segment's keys alone"""
+def test_scene_layer_matches_oracle(name, per_seg, rotate_q, adjacent):
+    """the fused layer (K/V pack with RoPE, the video queries rotated once ahead of the attention call or on its Q
+    load, in-place output) against the oracle's packing plus per-scope fp32 attention; full outputs for the
+    CPU-plumbing layout, sampled query rows (every segment's first / last rows included) at the full-size configs, each
+    segment's reference built from that segment's keys alone"""
     case = layout_case(name)
-    print(f'layer {name} adjacent={adjacent}', flush=True)
+    print(f'layer {name} adjacent={adjacent} rotate_q={rotate_q}', flush=True)
     q, k, v, eq, ek, ev, cos, sin = _layer_inputs(case)
     lay = SceneLayout(case['lengths'], halo=case['halo'], sides=case['sides'], extra=case['extra'])
     plan = scene.ScopePlan(lay, case['T'], case['counts'], case['Le'], case['scene_rope'], None, adjacent, True, DEV)
     g = [x.to(DEV) for x in (q, k, v, eq, ek, ev, cos, sin)]
-    ov, ot = scene.scene_attention(plan, *g[:6], g[6], g[7], mode='raw', fused=True)
+    ov, ot = scene.scene_attention(plan, *g[:6], g[6], g[7], mode='raw', fused=True, rotate_q=rotate_q)
     olay = OL.SceneLayout(case['lengths'], case['halo'], case['sides'], case['extra'])
     sc = OL.hunyuan_scopes(olay, case['T'], case['counts'], case['Le'], scene_rope=case['scene_rope'],
                            adjacent=adjacent)

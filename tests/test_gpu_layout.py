@@ -6,7 +6,7 @@ import torch
 
 from helpers import bits, layout_case, packed_rows_reference, rand_bf16, sample_packed
 from onereel_amd.layout import SceneLayout
-from onereel_amd.scene import ScopePlan, pack_rows, scatter
+from onereel_amd.scene import ScopePlan, pack_rows, rotate_queries, scatter
 from oracle import attention as OA
 from oracle import layout as OL
 
@@ -162,6 +162,27 @@ def test_pack_gather_bit_exact_uneven_sweep(name, adjacent):
         assert torch.equal(bits(vp[tk].cpu()), bits(rv)), mode
         assert torch.equal(bits(qp[tq].cpu()), bits(rq)), mode
         del kp, vp, qp
+
+
+@pytest.mark.parametrize('name', ['cpu_plumbing', 'hunyuan480p', 'uneven_K4'])
+@pytest.mark.parametrize('adjacent', [False, True])
+def test_rotate_queries_bit_exact(name, adjacent):
+    """or_rotate_rows through rotate_queries: every video query row, rotated at its scene-RoPE row and written to its
+    own token row, equals the oracle's packed (rotated) query row bit for bit; text rows are not touched"""
+    case = layout_case(name)
+    print(f'rotate queries {name} adjacent={adjacent}', flush=True)
+    H, D, T = case['H'], case['D'], case['T']
+    S = sum(case['lengths']) * T
+    plan, sc = _plans(case, adjacent)
+    cos, sin = _tables(case)
+    q = rand_bf16((S, H, D), 7)
+    eq = rand_bf16((case['Le'], H, D), 8)
+    qr = rotate_queries(plan, q.to(DEV), cos.to(DEV), sin.to(DEV)).cpu()
+    vid = np.nonzero(np.asarray(sc.q_src) < S)[0]
+    assert len(np.unique(np.asarray(sc.q_src)[vid])) == S          # every video row is some segment's query
+    sel = vid if S * H * D <= (1 << 22) else np.unique(np.concatenate([vid[::37], vid[[0, -1]]]))
+    ref = packed_rows_reference(sc, q, eq, q, eq, sel, cos, sin, mode='raw', which='q', q=q, eq=eq)
+    assert torch.equal(bits(qr[torch.as_tensor(np.asarray(sc.q_src)[sel])]), bits(ref))
 
 
 @pytest.mark.parametrize('name', ['cpu_plumbing', 'hunyuan480p'])
