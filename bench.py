@@ -4,8 +4,9 @@ Workload (one step = one pass of the hot path over one layer's synthetic inputs,
 4 scenes x 8 latent frames x 1590 tokens (30 x 53 latent grid) + 128 text tokens per scene, frame memory of 4 frames
 (representatives {0, 10, 21, 31}), shared frames at their adjacent positions (step >= shared_switch 5), scene RoPE
 over a 3D table, 16 heads x 128, bf16 q / k / v ~ N(0, 1). A step runs the layout kernel, the K/V pack-gather (RoPE
-on the keys), the RoPE of the video queries (once, in token order), the varlen attention (queries and outputs in
-place) and the text-padding write-back.
+on the keys; each scene's text segment reads its keys in place from its video segment's packed rows), the RoPE of
+the video queries (once, in token order), the varlen attention (queries and outputs in place) and the text-padding
+write-back.
 
 value = useful attention TFLOP/s of the whole step (sum over scopes of 4 * Lq * Lk * H * D per step time).
 roofline: the attention kernel alone, timed with HIP events on the stream it runs on.
@@ -351,18 +352,18 @@ def run_power(args):
     q, k, v = (torch.randn(S, H, D, generator=g, device=dev).to(torch.bfloat16) for _ in range(3))
     eq, ek, ev = (torch.randn(Le, H, D, generator=g, device=dev).to(torch.bfloat16) for _ in range(3))
     cos, sin = (x.to(dev) for x in rope_table(*W['grid'], D))
-    plan = scene.ScopePlan(lay, W['T'], W['counts'], Le, True, None, True, True, dev)
+    plan = scene.ScopePlan(lay, W['T'], W['counts'], Le, True, None, True, True, dev, text_keys_in_place=True)
     kp, vp = scene.pack_rows(plan, k, ek, 'k', b_video=v, b_text=ev, cos=cos, sin=sin, mode='raw')
     ov = torch.empty_like(q)
     ot = torch.empty(Le, H, D, dtype=torch.bfloat16, device=dev)
     ws = plan.workspace(H, D)
     lq = [int(x) for x in (plan.cu_q[1:] - plan.cu_q[:-1]).tolist()]
-    lk = [int(x) for x in (plan.cu_k[1:] - plan.cu_k[:-1]).tolist()]
+    lk = [int(x) for x in plan.k_len.tolist()]
     flops = float(sum(4.0 * a * b * H * D for a, b in zip(lq, lk)))
     qr = scene.rotate_queries(plan, q, cos, sin)
-    attn = lambda: scene.varlen(qr, kp, vp, plan.cu_q, plan.cu_k, plan.max_q, plan.max_k, out=ov,
-                                seg_q_src=plan.seg_q_src, q_text=eq, o_text=ot, n_q_video=plan.n_video,
-                                sum_q=plan.sum_q, workspace=ws)
+    attn = lambda: scene.varlen(qr, kp, vp, plan.cu_q, plan.cu_k, plan.max_q, plan.max_k, k_off=plan.k_off,
+                                k_len=plan.k_len, out=ov, seg_q_src=plan.seg_q_src, q_text=eq, o_text=ot,
+                                n_q_video=plan.n_video, sum_q=plan.sum_q, workspace=ws)
     n_g = 16384
     a = torch.randn(n_g, n_g, generator=g, device=dev).to(torch.bfloat16)
     b = torch.randn(n_g, n_g, generator=g, device=dev).to(torch.bfloat16)
@@ -537,10 +538,12 @@ def main():
     q, k, v = (torch.randn(S, H_, D_, generator=g, device=dev).to(torch.bfloat16) for _ in range(3))
     eq, ek, ev = (torch.randn(Le, H_, D_, generator=g, device=dev).to(torch.bfloat16) for _ in range(3))
     cos, sin = (x.to(dev) for x in rope_table(*W['grid'], D_))
-    plan = scene.ScopePlan(lay, T_, W['counts'], Le, W['scene_rope'], None, W['adjacent'], True, dev)
+    # text segments read their keys in place from their scene's video segment (no packed copy)
+    plan = scene.ScopePlan(lay, T_, W['counts'], Le, W['scene_rope'], None, W['adjacent'], True, dev,
+                           text_keys_in_place=True)
     H, D = H_, D_
     lq = [int(x) for x in (plan.cu_q[1:] - plan.cu_q[:-1]).tolist()]
-    lk = [int(x) for x in (plan.cu_k[1:] - plan.cu_k[:-1]).tolist()]
+    lk = [int(x) for x in plan.k_len.tolist()]
     flops = float(sum(4.0 * a * b * H * D for a, b in zip(lq, lk)))
     kbuf = torch.empty(plan.sum_k, H, D, dtype=torch.bfloat16, device=dev)
     vbuf = torch.empty_like(kbuf)
@@ -584,7 +587,8 @@ def main():
     # positions ('source'), from it on they sit next to the scene ('adjacent'); same scopes and FLOPs, other rotations
     other = None
     if W['reps'] and W['scene_rope']:
-        plan_o = scene.ScopePlan(lay, T_, W['counts'], Le, W['scene_rope'], None, not W['adjacent'], True, dev)
+        plan_o = scene.ScopePlan(lay, T_, W['counts'], Le, W['scene_rope'], None, not W['adjacent'], True, dev,
+                                 text_keys_in_place=True)
         ms_o = time_steps(make_step(plan_o))
 
     # per-kernel durations with HIP events on the launch stream
@@ -593,9 +597,9 @@ def main():
     ot = torch.empty(Le, H, D, dtype=torch.bfloat16, device=dev)
     ws = plan.workspace(H, D)
     # the attention kernel as the step runs it: video queries already rotated (qbuf), read in place
-    attn = lambda: scene.varlen(qbuf, kbuf, vbuf, plan.cu_q, plan.cu_k, plan.max_q, plan.max_k, out=ov,
-                                seg_q_src=plan.seg_q_src, q_text=eq, o_text=ot, n_q_video=plan.n_video,
-                                sum_q=plan.sum_q, workspace=ws)
+    attn = lambda: scene.varlen(qbuf, kbuf, vbuf, plan.cu_q, plan.cu_k, plan.max_q, plan.max_k, k_off=plan.k_off,
+                                k_len=plan.k_len, out=ov, seg_q_src=plan.seg_q_src, q_text=eq, o_text=ot,
+                                n_q_video=plan.n_video, sum_q=plan.sum_q, workspace=ws)
     pack = lambda: scene.pack_rows(plan, k, ek, 'k', out=kbuf, b_video=v, b_text=ev, b_out=vbuf, cos=cos, sin=sin,
                                    mode='raw')
     rotq = lambda: scene.rotate_queries(plan, q, cos, sin, out=qbuf)
@@ -611,8 +615,9 @@ def main():
         pack_o = lambda: scene.pack_rows(plan_o, k, ek, 'k', out=kbuf, b_video=v, b_text=ev, b_out=vbuf, cos=cos,
                                          sin=sin, mode='raw')
         attn_o = lambda: scene.varlen(qbuf, kbuf, vbuf, plan_o.cu_q, plan_o.cu_k, plan_o.max_q, plan_o.max_k,
-                                      out=ov, seg_q_src=plan_o.seg_q_src, q_text=eq, o_text=ot,
-                                      n_q_video=plan_o.n_video, sum_q=plan_o.sum_q, workspace=ws)
+                                      k_off=plan_o.k_off, k_len=plan_o.k_len, out=ov, seg_q_src=plan_o.seg_q_src,
+                                      q_text=eq, o_text=ot, n_q_video=plan_o.n_video, sum_q=plan_o.sum_q,
+                                      workspace=ws)
         scene.rotate_queries(plan_o, q, cos, sin, out=qbuf)
         pack_o()
         attn_o()

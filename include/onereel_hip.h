@@ -52,6 +52,11 @@ typedef struct or_layout_desc {
   int32_t adjacent;                      /* shared frames' keys at their adjacent positions (_move_shared) */
   int32_t n_rope_lengths;                /* 0: the scene lengths; else the rope_lengths entries */
   int32_t text_rows;                     /* Le: rows of the text q/k/v (valid tokens first, padding after) */
+  int32_t text_keys_in_place;            /* with text: 0 packs every segment's keys in _segments' order (V_j: own
+                                            frames, shared frames, sentence; T_j: own frames, sentence); 1 orders
+                                            V_j's keys as own frames, sentence, shared frames, so that T_j's keys
+                                            (hunyuan15.py:167-168: the same rows) are a prefix of V_j's: T_j packs
+                                            no rows and reads that range in place (k_off / k_len) */
   int32_t lengths[OR_MAX_SCENES];        /* latent frames per scene, each > 0 */
   int32_t rope_lengths[OR_MAX_SCENES];
   int32_t counts[OR_MAX_SCENES];         /* valid text tokens of sentence j */
@@ -65,7 +70,7 @@ typedef struct or_layout_sizes {
   int64_t sum_q;       /* packed query rows */
   int64_t sum_k;       /* packed key / value rows */
   int64_t max_q;
-  int64_t max_k;
+  int64_t max_k;       /* largest key count of a segment (k_len) */
   int64_t n_video;     /* F * T */
   int64_t max_rope_row;/* largest rotary-table row any index array names (-1 if none) */
 } or_layout_sizes;
@@ -82,6 +87,9 @@ typedef struct or_layout_out {
                           at their adjacent position when moved, else their own; -1 for text rows */
   int32_t* k_move_a;   /* [sum_k] already-rotated keys: _move_shared's inverse-rotation row a*T+s, -1 if not moved */
   int32_t* k_move_b;   /* [sum_k] already-rotated keys: _move_shared's rotation row (a+d)*T+s, -1 if not moved */
+  int32_t* k_off;      /* [n_seg] first packed key row of segment s (cu_k[s], or V_j's first row for T_j with
+                          text_keys_in_place) */
+  int32_t* k_len;      /* [n_seg] its key count (the varlen call's k_off / k_len) */
 } or_layout_out;
 
 /* Replaces the host-side layout logic of SceneLayout.shared_frames / key_frames (src/onereel/layout.py:54-78),

@@ -11,6 +11,11 @@
 // The packed rows then split into runs that share every index but the spatial offset: one run per (segment, frame)
 // and one per (segment, sentence). A block takes one run at a time, derives its bases once, and writes its rows as
 // base + offset with coalesced int32 stores, so no per-row search or division is left.
+//
+// T_j's keys (own frames, then the sentence) are the rows of V_j's own frames and sentence. With text_keys_in_place
+// V_j's keys are packed as own frames, sentence, shared frames, so T_j's keys are the first rows of V_j's: T_j packs
+// none and its key range (k_off / k_len) points there. The attention result does not depend on the order of a
+// segment's keys.
 #include <stdarg.h>
 #include <stdio.h>
 #include <string.h>
@@ -38,18 +43,19 @@ struct SegTable {
 __host__ __device__ inline int seg_scene(int with_text, int s) { return with_text ? s >> 1 : s; }
 __host__ __device__ inline bool seg_is_text(int with_text, int s) { return with_text && (s & 1); }
 
-// query / key counts of segment s
+// key count of segment s (the rows its queries attend to)
+__host__ __device__ inline int seg_keys(const LayoutDerived& L, int s) {
+  const int j = seg_scene(L.with_text, s);
+  const int own = (L.hi[j] - L.lo[j]) * L.T, txt = L.t1[j] - L.t0[j];
+  return seg_is_text(L.with_text, s) ? own + txt : own + (L.sh_ptr[j + 1] - L.sh_ptr[j]) * L.T + txt;
+}
+
+// query count and packed key rows of segment s (T_j packs no keys when they are read in place from V_j's)
 __host__ __device__ inline void seg_lengths(const LayoutDerived& L, int s, int* lq, int* lk) {
   const int j = seg_scene(L.with_text, s);
-  const int own = (L.hi[j] - L.lo[j]) * L.T;
-  const int txt = L.t1[j] - L.t0[j];
-  if (seg_is_text(L.with_text, s)) {
-    *lq = txt;
-    *lk = own + txt;
-  } else {
-    *lq = own;
-    *lk = own + (L.sh_ptr[j + 1] - L.sh_ptr[j]) * L.T + txt;
-  }
+  const bool text = seg_is_text(L.with_text, s);
+  *lq = text ? L.t1[j] - L.t0[j] : (L.hi[j] - L.lo[j]) * L.T;
+  *lk = text && L.text_in_place ? 0 : seg_keys(L, s);
 }
 
 // runs of segment s: query side (its own frames, or its sentence) and key side (own frames, shared frames, sentence)
@@ -59,7 +65,7 @@ __host__ __device__ inline void seg_runs(const LayoutDerived& L, int s, int* uq,
   const int txt = L.t1[j] - L.t0[j] > 0 ? 1 : 0;
   if (seg_is_text(L.with_text, s)) {
     *uq = txt;
-    *uk = own + txt;
+    *uk = L.text_in_place ? 0 : own + txt;
   } else {
     *uq = own;
     *uk = own + (L.sh_ptr[j + 1] - L.sh_ptr[j]) + txt;
@@ -74,6 +80,7 @@ int derive_host(const or_layout_desc& d, LayoutDerived& L) {
   L.scene_rope = d.scene_rope;
   L.adjacent = d.adjacent;
   L.text_rows = d.text_rows;
+  L.text_in_place = d.with_text && d.text_keys_in_place;
   int f = 0, t = 0;
   for (int j = 0; j < d.n_scenes; ++j) {
     L.lo[j] = f;
@@ -136,7 +143,7 @@ __device__ inline int upper_bound(const int* a, int n, int x) {  // first i in [
 }
 
 struct RowOut {
-  int32_t *q_src, *q_rope, *k_src, *k_rope, *k_move_a, *k_move_b;
+  int32_t *q_src, *q_rope, *k_src, *k_rope, *k_move_a, *k_move_b, *k_off, *k_len;
 };
 
 __global__ __launch_bounds__(kThreads) void layout_kernel(const or_layout_desc d, RowOut out, int32_t* cu_q_out,
@@ -173,6 +180,7 @@ __global__ __launch_bounds__(kThreads) void layout_kernel(const or_layout_desc d
       L.scene_rope = d.scene_rope;
       L.adjacent = d.adjacent;
       L.text_rows = d.text_rows;
+      L.text_in_place = d.with_text && d.text_keys_in_place;
       L.n_rope = nr;
     }
     if (lane == ns - 1) L.F = lo + len;
@@ -244,9 +252,12 @@ __global__ __launch_bounds__(kThreads) void layout_kernel(const or_layout_desc d
     for (int s = tid; s <= n_seg; s += kThreads) {
       if (cu_q_out) cu_q_out[s] = S.cu_q[s];
       if (cu_k_out) cu_k_out[s] = S.cu_k[s];
-      if (seg_q_src_out && s < n_seg) {
+      if (s < n_seg) {
         const int j = seg_scene(L.with_text, s);
-        seg_q_src_out[s] = seg_is_text(L.with_text, s) ? L.F * L.T + L.t0[j] : L.lo[j] * L.T;
+        const bool text = seg_is_text(L.with_text, s);
+        if (seg_q_src_out) seg_q_src_out[s] = text ? L.F * L.T + L.t0[j] : L.lo[j] * L.T;
+        if (out.k_off) out.k_off[s] = text && L.text_in_place ? S.cu_k[s - 1] : S.cu_k[s];
+        if (out.k_len) out.k_len[s] = seg_keys(L, s);
       }
     }
   }
@@ -264,21 +275,43 @@ __global__ __launch_bounds__(kThreads) void layout_kernel(const or_layout_desc d
     const int s = upper_bound(cu_u, n_seg + 1, uu) - 1;
     const int slot = uu - cu_u[s];
     const int j = seg_scene(L.with_text, s);
+    const bool tseg = seg_is_text(L.with_text, s);
     const int own = L.hi[j] - L.lo[j];
-    const int nsh = seg_is_text(L.with_text, s) ? 0 : L.sh_ptr[j + 1] - L.sh_ptr[j];
-    const int nfr = qside ? (seg_is_text(L.with_text, s) ? 0 : own) : own + nsh;
-    int row0, count, src0, rope0 = -1, ma0 = -1, mb0 = -1;
+    const int nsh = tseg ? 0 : L.sh_ptr[j + 1] - L.sh_ptr[j];
+    const int txt = L.t1[j] - L.t0[j];
+    const int base = qside ? S.cu_q[s] : S.cu_k[s];
+    // the run's place in the segment: queries are V_j's own frames or T_j's sentence; keys are the own frames, then
+    // the shared frames and the sentence (or, with the text keys in place, the sentence and the shared frames)
+    int kind, idx = 0, row0;   // kind 0: own frame idx, 1: shared frame idx, 2: sentence
+    if (qside) {
+      kind = tseg ? 2 : 0;
+      idx = slot;
+      row0 = base + (tseg ? 0 : slot * T);
+    } else if (slot < own) {
+      kind = 0;
+      idx = slot;
+      row0 = base + slot * T;
+    } else if (L.text_in_place && !tseg) {
+      const int has_txt = txt > 0 ? 1 : 0;
+      kind = slot == own && has_txt ? 2 : 1;
+      idx = slot - own - has_txt;
+      row0 = base + own * T + (kind == 2 ? 0 : txt + idx * T);
+    } else {
+      kind = slot < own + nsh ? 1 : 2;
+      idx = slot - own;
+      row0 = base + (kind == 1 ? slot : own + nsh) * T;
+    }
+    int count, src0, rope0 = -1, ma0 = -1, mb0 = -1;
     bool rope = false, move = false;
-    if (slot < nfr) {
-      row0 = (qside ? S.cu_q[s] : S.cu_k[s]) + slot * T;
+    if (kind != 2) {
       count = T;
       rope = true;
       int f;
-      if (slot < own) {
-        f = L.lo[j] + slot;
+      if (kind == 0) {
+        f = L.lo[j] + idx;
         rope0 = L.scene_rope ? frame_position(L, f) * T : f * T;
       } else {
-        const int e = L.sh_ptr[j] + (slot - own);
+        const int e = L.sh_ptr[j] + idx;
         f = L.sh[e];
         if (L.adjacent) {
           const int dst = L.sh_dst[e];
@@ -294,8 +327,7 @@ __global__ __launch_bounds__(kThreads) void layout_kernel(const or_layout_desc d
       }
       src0 = f * T;
     } else {
-      row0 = (qside ? S.cu_q[s] : S.cu_k[s]) + nfr * T;
-      count = L.t1[j] - L.t0[j];
+      count = txt;
       src0 = n_video + L.t0[j];
     }
     if (qside) {
@@ -359,6 +391,9 @@ static int plan_impl(const or_layout_desc* dp, or_layout_sizes* sz, LayoutDerive
   if (d.T < 1) return fail_arg("T must be positive (got %d)", d.T);
   if (d.halo < 0) return fail_arg("halo must be >= 0 (got %d)", d.halo);
   if (d.sides < 0 || d.sides > 2) return fail_arg("sides must be 0 'adj', 1 'prev' or 2 'next' (got %d)", d.sides);
+  if (d.text_keys_in_place != 0 && (d.text_keys_in_place != 1 || !d.with_text))
+    return fail_arg("text_keys_in_place must be 0, or 1 with text scopes (got %d, with_text %d)", d.text_keys_in_place,
+                    d.with_text);
   if (d.n_rope_lengths < 0 || d.n_rope_lengths > OR_MAX_SCENES)
     return fail_arg("n_rope_lengths %d outside [0, %d]", d.n_rope_lengths, OR_MAX_SCENES);
   int64_t F = 0, ctext = 0;
@@ -411,7 +446,7 @@ static int plan_impl(const or_layout_desc* dp, or_layout_sizes* sz, LayoutDerive
     sq += lq;
     sk += lk;
     mq = lq > mq ? lq : mq;
-    mk = lk > mk ? lk : mk;
+    mk = seg_keys(L, s) > mk ? seg_keys(L, s) : mk;
   }
   if (sq >= ((int64_t)1 << 31) || sk >= ((int64_t)1 << 31)) return fail_arg("packed rows exceed int32");
   // rotary rows: own tokens, shared frames at their source or adjacent position, move rows
@@ -453,7 +488,7 @@ extern "C" int or_layout_build(const or_layout_desc* desc, const or_layout_out* 
   int rc = plan_impl(desc, &sz, &L);
   if (rc) return rc;
   if (!out) return fail_arg("or_layout_build: out is NULL");
-  RowOut ro{out->q_src, out->q_rope, out->k_src, out->k_rope, out->k_move_a, out->k_move_b};
+  RowOut ro{out->q_src, out->q_rope, out->k_src, out->k_rope, out->k_move_a, out->k_move_b, out->k_off, out->k_len};
   // one block per run (frame or sentence of a segment), at most 2048
   int64_t runs = 0;
   for (int s = 0; s < sz.n_seg; ++s) {

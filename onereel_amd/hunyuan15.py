@@ -108,7 +108,7 @@ def scope_plan(ctx: Context, Le: int, device, moves: bool = False) -> ScopePlan:
     key = _key(ctx, Le, adjacent, moves, device)
     if key not in ctx._cache:
         ctx._cache[key] = ScopePlan(ctx.layout, ctx.T, ctx.counts[ctx.cond()], Le, ctx.scene_rope, ctx.rope_lengths,
-                                    adjacent, True, device, moves=moves)
+                                    adjacent, True, device, moves=moves, text_keys_in_place=True)
     return ctx._cache[key]
 
 

@@ -26,7 +26,7 @@ MODES = ('raw', 'rotated', 'none')
 
 
 def _desc(lay: SceneLayout, T: int, counts, text_rows: int, scene_rope: bool, rope_lengths, adjacent: bool,
-          with_text: bool) -> L.LayoutDesc:
+          with_text: bool, text_keys_in_place: bool = False) -> L.LayoutDesc:
     d = L.LayoutDesc()
     n = lay.n_scenes
     if n > L.OR_MAX_SCENES:
@@ -35,6 +35,7 @@ def _desc(lay: SceneLayout, T: int, counts, text_rows: int, scene_rope: bool, ro
     d.sides = ('adj', 'prev', 'next').index(lay.sides)
     d.with_text, d.scene_rope, d.adjacent = int(with_text), int(scene_rope), int(adjacent)
     d.text_rows = int(text_rows)
+    d.text_keys_in_place = int(bool(text_keys_in_place) and bool(with_text))
     for j, x in enumerate(lay.lengths):
         d.lengths[j] = int(x)
     counts = list(counts) if with_text else [0] * n
@@ -64,18 +65,25 @@ def _desc(lay: SceneLayout, T: int, counts, text_rows: int, scene_rope: bool, ro
 class ScopePlan:
     """The packed layout of one request's scopes, built on the device by `or_layout_build`.
 
-    Attributes (int32 device tensors): cu_q, cu_k [n_seg+1], seg_q_src [n_seg], q_src / q_rope [sum_q], k_src /
-    k_rope [sum_k], and for mode 'rotated' with moved shared frames k_move_a / k_move_b [sum_k]. Host ints: n_seg,
-    sum_q, sum_k, max_q, max_k, n_video, text_rows, max_rope_row."""
+    Attributes (int32 device tensors): cu_q, cu_k [n_seg+1], seg_q_src, k_off, k_len [n_seg], q_src / q_rope
+    [sum_q], k_src / k_rope [sum_k], and for mode 'rotated' with moved shared frames k_move_a / k_move_b [sum_k].
+    Host ints: n_seg, sum_q, sum_k, max_q, max_k, n_video, text_rows, max_rope_row.
+
+    text_keys_in_place: each scene's video segment packs its keys as own frames, sentence, shared frames, and the
+    text segment (whose keys are the same own-frame and sentence rows) reads the first of them in place (k_off,
+    k_len) instead of packing its own copy; the default packs every segment in the reference's order."""
 
     def __init__(self, lay: SceneLayout, T: int, counts=None, text_rows: int | None = None, scene_rope=False,
-                 rope_lengths=None, adjacent=False, with_text=True, device=None, moves=False):
+                 rope_lengths=None, adjacent=False, with_text=True, device=None, moves=False,
+                 text_keys_in_place=False):
         counts = list(counts) if counts is not None else [0] * lay.n_scenes
         if text_rows is None:
             text_rows = sum(counts) if with_text else 0
         self.layout, self.T, self.counts, self.text_rows = lay, int(T), counts, int(text_rows)
         self.scene_rope, self.adjacent, self.with_text = bool(scene_rope), bool(adjacent), bool(with_text)
-        self.desc = _desc(lay, T, counts, text_rows, scene_rope, rope_lengths, adjacent, with_text)
+        self.text_keys_in_place = bool(text_keys_in_place) and self.with_text
+        self.desc = _desc(lay, T, counts, text_rows, scene_rope, rope_lengths, adjacent, with_text,
+                          self.text_keys_in_place)
         sz = L.LayoutSizes()
         L.check(L.lib().or_layout_plan(ctypes.byref(self.desc), ctypes.byref(sz)), 'or_layout_plan')
         self.n_seg, self.sum_q, self.sum_k = sz.n_seg, sz.sum_q, sz.sum_k
@@ -83,6 +91,7 @@ class ScopePlan:
         dev = torch.device(device) if device is not None else torch.device('cuda', torch.cuda.current_device())
         new = lambda n: torch.empty(int(n), dtype=torch.int32, device=dev)
         self.cu_q, self.cu_k, self.seg_q_src = new(self.n_seg + 1), new(self.n_seg + 1), new(self.n_seg)
+        self.k_off, self.k_len = new(self.n_seg), new(self.n_seg)
         self.q_src, self.q_rope = new(self.sum_q), new(self.sum_q)
         self.k_src, self.k_rope = new(self.sum_k), new(self.sum_k)
         self.k_move_a = new(self.sum_k) if moves and adjacent else None
@@ -94,7 +103,8 @@ class ScopePlan:
     def build(self):
         """(re)run the layout kernel on the current stream"""
         out = L.LayoutOut(*(L.ptr(t) for t in (self.cu_q, self.cu_k, self.seg_q_src, self.q_src, self.q_rope,
-                                                self.k_src, self.k_rope, self.k_move_a, self.k_move_b)))
+                                                self.k_src, self.k_rope, self.k_move_a, self.k_move_b, self.k_off,
+                                                self.k_len)))
         with torch.cuda.device(self.device):
             L.check(L.lib().or_layout_build(ctypes.byref(self.desc), ctypes.byref(out), L.stream_handle()),
                     'or_layout_build')
@@ -110,7 +120,7 @@ class ScopePlan:
 
     def index_bytes(self) -> int:
         """bytes the layout kernel writes"""
-        n = 2 * (self.n_seg + 1) + self.n_seg + 2 * self.sum_q + 2 * self.sum_k
+        n = 2 * (self.n_seg + 1) + 3 * self.n_seg + 2 * self.sum_q + 2 * self.sum_k
         if self.k_move_a is not None:
             n += 2 * self.sum_k
         return 4 * n
@@ -336,13 +346,15 @@ def scene_attention(plan: ScopePlan, q, k, v, eq, ek, ev, cos=None, sin=None, mo
         on_load = qmode == 'raw' and rotate_q == 'load'
         if qmode == 'raw' and not on_load:
             q = rotate_queries(plan, q, cos, sin, out=qbuf)
-        varlen(q, kp, vp, plan.cu_q, plan.cu_k, plan.max_q, plan.max_k, out=ov, seg_q_src=plan.seg_q_src,
-               q_text=eq, o_text=ot, n_q_video=plan.n_video, q_rope=plan.q_rope if on_load else None,
-               cos=cos, sin=sin, sum_q=plan.sum_q, workspace=plan.workspace(H, D))
+        varlen(q, kp, vp, plan.cu_q, plan.cu_k, plan.max_q, plan.max_k, k_off=plan.k_off, k_len=plan.k_len, out=ov,
+               seg_q_src=plan.seg_q_src, q_text=eq, o_text=ot, n_q_video=plan.n_video,
+               q_rope=plan.q_rope if on_load else None, cos=cos, sin=sin, sum_q=plan.sum_q,
+               workspace=plan.workspace(H, D))
         if ot is not None:
             zero_text_padding(plan, ot)
     else:
         qp = pack_rows(plan, q, eq, 'q', cos=cos, sin=sin, mode=qmode)
-        op = varlen(qp, kp, vp, plan.cu_q, plan.cu_k, plan.max_q, plan.max_k, workspace=plan.workspace(H, D))
+        op = varlen(qp, kp, vp, plan.cu_q, plan.cu_k, plan.max_q, plan.max_k, k_off=plan.k_off, k_len=plan.k_len,
+                    workspace=plan.workspace(H, D))
         scatter(plan, op, ov, ot)
     return ov, ot

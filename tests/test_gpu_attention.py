@@ -189,21 +189,27 @@ def _layer_inputs(case, seed=0):
     return q, k, v, eq, ek, ev, cos, sin
 
 
-@pytest.mark.parametrize('name,per_seg,rotate_q', [
-    ('cpu_plumbing', None, 'pre'), ('cpu_plumbing', None, 'load'), ('hunyuan480p', 48, 'pre'),
-    ('hunyuan480p', 48, 'load'), ('wan704', 48, 'pre'), ('uneven_K2', 32, 'pre'), ('uneven_K4', 24, 'pre'),
-    ('uneven_K8', 24, 'pre'), ('uneven_K12', 24, 'pre')])
+@pytest.mark.parametrize('name,per_seg,rotate_q,in_place', [
+    ('cpu_plumbing', None, 'pre', False), ('cpu_plumbing', None, 'load', False), ('cpu_plumbing', None, 'pre', True),
+    ('hunyuan480p', 48, 'pre', False), ('hunyuan480p', 48, 'load', False), ('hunyuan480p', 48, 'pre', True),
+    ('wan704', 48, 'pre', False), ('wan704', 48, 'pre', True), ('uneven_K2', 32, 'pre', False),
+    ('uneven_K4', 24, 'pre', False), ('uneven_K4', 24, 'pre', True), ('uneven_K8', 24, 'pre', False),
+    ('uneven_K12', 24, 'pre', False), ('uneven_K12', 24, 'pre', True)])
 @pytest.mark.parametrize('adjacent', [False, True])
-def test_scene_layer_matches_oracle(name, per_seg, rotate_q, adjacent):
+def test_scene_layer_matches_oracle(name, per_seg, rotate_q, in_place, adjacent):
     """the fused layer (K/V pack with RoPE, the video queries rotated once ahead of the attention call or on its Q
-    load, in-place output) against the oracle's packing plus per-scope fp32 attention; full outputs for the
-    CPU-plumbing layout, sampled query rows (every segment's first / last rows included) at the full-size configs, each
-    segment's reference built from that segment's keys alone"""
+    load, in-place output; with in_place, each text segment's keys read from its video segment's packed rows) against
+    the oracle's packing plus per-scope fp32 attention; full outputs for the CPU-plumbing layout, sampled query rows
+    (every segment's first / last rows included) at the full-size configs, each segment's reference built from that
+    segment's keys alone"""
     case = layout_case(name)
-    print(f'layer {name} adjacent={adjacent} rotate_q={rotate_q}', flush=True)
+    print(f'layer {name} adjacent={adjacent} rotate_q={rotate_q} text keys in place={in_place}', flush=True)
     q, k, v, eq, ek, ev, cos, sin = _layer_inputs(case)
     lay = SceneLayout(case['lengths'], halo=case['halo'], sides=case['sides'], extra=case['extra'])
-    plan = scene.ScopePlan(lay, case['T'], case['counts'], case['Le'], case['scene_rope'], None, adjacent, True, DEV)
+    plan = scene.ScopePlan(lay, case['T'], case['counts'], case['Le'], case['scene_rope'], None, adjacent, True, DEV,
+                           text_keys_in_place=in_place)
+    if in_place:
+        assert plan.sum_k < int(plan.k_len.sum())
     g = [x.to(DEV) for x in (q, k, v, eq, ek, ev, cos, sin)]
     ov, ot = scene.scene_attention(plan, *g[:6], g[6], g[7], mode='raw', fused=True, rotate_q=rotate_q)
     olay = OL.SceneLayout(case['lengths'], case['halo'], case['sides'], case['extra'])
@@ -227,22 +233,24 @@ def test_scene_layer_reference_flow_and_rotated_inputs(adjacent):
     lay = SceneLayout(case['lengths'], halo=0, extra=case['extra'])
     olay = OL.SceneLayout(case['lengths'], 0, 'adj', case['extra'])
     sc = OL.hunyuan_scopes(olay, case['T'], case['counts'], case['Le'], scene_rope=True, adjacent=adjacent)
-    plan = scene.ScopePlan(lay, case['T'], case['counts'], case['Le'], True, None, adjacent, True, DEV, moves=True)
     g = [x.to(DEV) for x in (q, k, v, eq, ek, ev, cos, sin)]
     rv, rt = OA.scene_layer(sc, q, k, v, eq, ek, ev, cos, sin, mode='raw')
-    ov, ot = scene.scene_attention(plan, *g, mode='raw', fused=False)
-    assert_close(ov.cpu(), rv, what='unfused video')
-    assert_close(ot.cpu(), rt, what='unfused text')
-    assert ot[32:].abs().max().item() == 0
     # already-rotated inputs, as the reference's Processor.scene receives them
     rows = torch.as_tensor(OL.scene_rope_rows(olay, case['T']))
     qr = OA.apply_rotary_emb(q, cos[rows], sin[rows])
     kr = OA.apply_rotary_emb(k, cos[rows], sin[rows])
     rv2, rt2 = OA.scene_layer(sc, qr, kr, v, eq, ek, ev, cos, sin, mode='rotated')
-    for fused in (True, False):
-        ov2, ot2 = scene.scene_attention(plan, qr.to(DEV), kr.to(DEV), *g[2:], mode='rotated', fused=fused)
-        assert_close(ov2.cpu(), rv2, what=f'rotated video fused={fused}')
-        assert_close(ot2.cpu(), rt2, what=f'rotated text fused={fused}')
+    for in_place in (False, True):
+        plan = scene.ScopePlan(lay, case['T'], case['counts'], case['Le'], True, None, adjacent, True, DEV,
+                               moves=True, text_keys_in_place=in_place)
+        ov, ot = scene.scene_attention(plan, *g, mode='raw', fused=False)
+        assert_close(ov.cpu(), rv, what=f'unfused video, text keys in place={in_place}')
+        assert_close(ot.cpu(), rt, what=f'unfused text, text keys in place={in_place}')
+        assert ot[32:].abs().max().item() == 0
+        for fused in (True, False):
+            ov2, ot2 = scene.scene_attention(plan, qr.to(DEV), kr.to(DEV), *g[2:], mode='rotated', fused=fused)
+            assert_close(ov2.cpu(), rv2, what=f'rotated video fused={fused} in place={in_place}')
+            assert_close(ot2.cpu(), rt2, what=f'rotated text fused={fused} in place={in_place}')
 
 
 @pytest.mark.parametrize('adjacent', [False, True])

@@ -104,6 +104,58 @@ def test_layout_kernel_more_runs_than_blocks():
         _check_plan(plan, sc, adjacent)
 
 
+def _check_in_place(case, adjacent):
+    """text keys in place: V_j's packed rows are _segments' V_j rows with the sentence moved ahead of the shared frames
+    (own frames, sentence, shared frames), T_j packs none, and T_j's key range (k_off, k_len) covers exactly the rows
+    of _segments' T_j (own frames, then sentence), in order; every per-key array (source row, RoPE row, the two
+    _move_shared rows) follows the same order"""
+    lay = SceneLayout(case['lengths'], halo=case['halo'], sides=case['sides'], extra=case['extra'])
+    plan = ScopePlan(lay, case['T'], case['counts'], case['Le'], case['scene_rope'], case['rope_lengths'], adjacent,
+                     True, DEV, moves=True, text_keys_in_place=True)
+    _, sc = _plans(case, adjacent)
+    torch.cuda.synchronize()
+    n = len(case['lengths'])
+    names = ('k_src', 'k_rope') + (('k_move_a', 'k_move_b') if adjacent else ())
+    got = {a: getattr(plan, a).cpu().numpy() for a in names}
+    ref = {a: np.asarray(getattr(sc, a)) for a in got}
+    cu_q, cu_k, k_off, k_len = (getattr(plan, a).cpu().tolist() for a in ('cu_q', 'cu_k', 'k_off', 'k_len'))
+    assert cu_q == list(sc.cu_q)
+    assert (plan.sum_k, plan.max_k) == (sum(sc.lk[0::2]), max(sc.lk))
+    assert k_len == list(sc.lk)
+    for j in range(n):
+        v, t = 2 * j, 2 * j + 1
+        own, txt, lk = sc.lq[v], sc.lq[t], sc.lk[v]
+        assert cu_k[t + 1] - cu_k[t] == 0 and k_off[v] == cu_k[v] and k_off[t] == cu_k[v]
+        b, rb = cu_k[v], sc.cu_k[v]
+        order = np.r_[rb:rb + own, rb + lk - txt:rb + lk, rb + own:rb + lk - txt]
+        for a in got:
+            assert np.array_equal(got[a][b:b + lk], ref[a][order]), (j, a)
+            tb = sc.cu_k[t]
+            assert np.array_equal(got[a][k_off[t]:k_off[t] + k_len[t]], ref[a][tb:tb + sc.lk[t]]), (j, a)
+
+
+@pytest.mark.parametrize('name', ['cpu_plumbing', 'hunyuan480p', 'uneven_K4', 'uneven_K12'])
+@pytest.mark.parametrize('adjacent', [False, True])
+def test_layout_text_keys_in_place(name, adjacent):
+    print(f'layout text keys in place {name} adjacent={adjacent}', flush=True)
+    _check_in_place(layout_case(name), adjacent)
+
+
+def test_layout_text_keys_in_place_random_layouts():
+    """random layouts with empty sentences, halos and extra frames"""
+    rng = np.random.default_rng(17)
+    for it in range(30):
+        n = int(rng.integers(1, 8))
+        lengths = rng.integers(1, 6, n).tolist()
+        F = sum(lengths)
+        extra = {j: rng.integers(0, F, int(rng.integers(0, 4))).tolist() for j in range(n) if rng.random() < 0.7}
+        case = dict(lengths=lengths, halo=int(rng.integers(0, 3)), sides=['adj', 'prev', 'next'][int(rng.integers(3))],
+                    extra=extra, T=int(rng.integers(1, 10)), counts=rng.integers(0, 5, n).tolist(),
+                    scene_rope=bool(rng.integers(2)), rope_lengths=None)
+        case['Le'] = sum(case['counts']) + int(rng.integers(0, 3))
+        _check_in_place(case, bool(rng.integers(2)))
+
+
 def _tables(case):
     F, Hh, Ww = case['table']
     assert Hh * Ww == case['T']

@@ -124,6 +124,19 @@ def test_host_planner_sizes_match_oracle():
         assert (sz.max_q, sz.max_k) == (max(sc.lq), max(sc.lk))
         rows = np.concatenate([sc.q_rope, sc.k_rope, sc.k_move_a, sc.k_move_b])
         assert sz.max_rope_row >= rows.max()
+        if with_text:   # text keys read in place from the video segments: only V_j's keys are packed
+            d = _desc(lay, T, counts, Le, scene_rope, None, adjacent, with_text, text_keys_in_place=True)
+            s2 = L.LayoutSizes()
+            L.check(L.lib().or_layout_plan(ctypes.byref(d), ctypes.byref(s2)), 'plan')
+            assert (s2.n_seg, s2.sum_q, s2.max_q, s2.max_k) == (sz.n_seg, sz.sum_q, sz.max_q, sz.max_k)
+            assert s2.sum_k == sum(lk for lk, kind in zip(sc.lk, sc.kind) if kind == 'v')
+
+
+def test_text_keys_in_place_needs_text_scopes():
+    d = _desc(SceneLayout([2, 3], halo=0), 4, [1, 1], 2, False, None, False, False)
+    d.text_keys_in_place = 1
+    with pytest.raises(L.HipPathError, match='text_keys_in_place'):
+        L.check(L.lib().or_layout_plan(ctypes.byref(d), ctypes.byref(L.LayoutSizes())), 'or_layout_plan')
 
 
 @pytest.mark.parametrize('bad, msg', [
