@@ -16,6 +16,8 @@ Per call, all on the caller's stream and without host reads:
                        (first row of p + i) * H + head (q_row_step = H), when every piece's query rows are contiguous
 
 A plan's static parts (segment offsets, the local key rows, the query rows) are built once per (plan, H) and kept.
+A piece that does not read the memory and has the local rows of another (a scene's sentence queries beside its
+video queries) reads them in place from that piece's segment, so they are packed once.
 """
 from __future__ import annotations
 
@@ -222,6 +224,24 @@ class _Static:
         # the largest key-buffer row the plan names (once per plan), checked against each call's buffer
         self.max_key_row = max(int(local.max()) if local.numel() else -1, int(p.cand.max()))
         self.local = local.to(torch.int64)
+        # a piece that does not read the memory and has the same local rows as another piece (a scene's sentence
+        # queries beside its video queries) reads that piece's local rows in place: its keys are their slot's first
+        # rows, and it packs none of its own (compared once per plan)
+        mem = [bool(x) for x in p.mem.tolist()]
+        starts = [0]
+        for c in lens:
+            starts.append(starts[-1] + c)
+        part = lambda i: self.local[starts[i]:starts[i + 1]]
+        self.share = [None] * n
+        for i in range(n):
+            if mem[i]:
+                continue
+            for o in sorted(range(n), key=lambda o: (not mem[o], o)):   # pieces reading the memory first
+                if o != i and self.share[o] is None and lens[o] == lens[i] and (mem[o] or o < i) and \
+                        torch.equal(part(o), part(i)):
+                    self.share[i] = o
+                    break
+        self.mem = mem
         self.cand64 = p.cand.to(device=device, dtype=torch.int64).contiguous()
         self.cand32 = self.cand64.to(torch.int32)
         self.owner64 = p.owner.to(device=device, dtype=torch.int64).contiguous()
@@ -232,21 +252,28 @@ class _Static:
         self.device = device
 
     def slots(self, M: int):
-        """(k_off, kidx) for M representatives: segment (h, i) owns kidx[k_off .. k_off + lens[i] + M), its local
-        rows (row * H + h) first, written once here; the foreign rows after them are rewritten by each call"""
+        """(k_off, kidx) for M representatives: segment (h, i) owns kidx[k_off .. k_off + lens[i] + M) (+ 0 when
+        the piece does not read the memory), its local rows (row * H + h) first, written once here; the foreign rows
+        after them are rewritten by each call. A piece that shares another's local rows gets that piece's k_off."""
         if M not in self._slots:
             H, n = self.H, self.n
-            off, o = [], 0
-            for _ in range(H):
+            off, o = [0] * (H * n), 0
+            for h in range(H):
                 for i in range(n):
-                    off.append(o)
-                    o += self.lens[i] + M
+                    if self.share[i] is None:
+                        off[h * n + i] = o
+                        o += self.lens[i] + (M if self.mem[i] else 0)
+                for i in range(n):
+                    if self.share[i] is not None:
+                        off[h * n + i] = off[h * n + self.share[i]]
             k_off = torch.tensor(off, dtype=torch.int32, device=self.device)
             kidx = torch.zeros(o, dtype=torch.int32, device=self.device)
-            pos = torch.cat([torch.arange(c) for c in self.lens]).to(self.device)
-            piece = torch.cat([torch.full((c,), i) for i, c in enumerate(self.lens)]).to(self.device)
+            own = [i for i in range(n) if self.share[i] is None]
+            pos = torch.cat([torch.arange(self.lens[i]) for i in own]).to(self.device)
+            piece = torch.cat([torch.full((self.lens[i],), i) for i in own]).to(self.device)
+            rows = torch.cat([self.local[sum(self.lens[:i]):sum(self.lens[:i + 1])] for i in own])
             for h in range(H):
-                kidx[k_off[h * n + piece].long() + pos] = (self.local * H + h).to(torch.int32)
+                kidx[k_off[h * n + piece].long() + pos] = (rows * H + h).to(torch.int32)
             self._slots[M] = (k_off, kidx)
         return self._slots[M]
 

@@ -6,7 +6,7 @@ import torch
 
 from onereel_amd import _lib as L
 from onereel_amd.layout import SceneLayout
-from onereel_amd.memory import BoundaryMemory, candidate_frames, candidates, frame_plan, make_plan
+from onereel_amd.memory import BoundaryMemory, _Static, candidate_frames, candidates, frame_plan, make_plan
 from oracle import memory as OM
 
 
@@ -43,3 +43,24 @@ def test_select_has_no_cpu_path():
     with pytest.raises(TypeError, match='GPU'):
         BoundaryMemory(4).select('k', torch.randn(10, 2, 64))
     assert issubclass(L.HipTypeError, RuntimeError)
+
+
+def test_sentence_pieces_read_their_video_pieces_local_rows_in_place():
+    """the head-major tables on the host: a sentence piece (no memory) with its scene's local rows takes its video
+    piece's key offset and packs nothing of its own; every segment's local rows (row * H + head) start at its k_off,
+    and a video piece keeps room for M foreign representatives after them"""
+    lay = SceneLayout([2, 3], halo=0)
+    T, S, H, M = 4, 20, 2, 3
+    tr = [(0, 3), (3, 5)]
+    p = frame_plan(lay, T, torch.arange(S), S, [(j, lo * T, hi * T) for j, (lo, hi) in enumerate(lay.ranges)], tr,
+                   {0, 1}, S, 'cpu')
+    st = _Static(p, H, S + 5, 'cpu')
+    assert st.share == [None, None, 0, 1]
+    k_off, kidx = st.slots(M)
+    assert kidx.numel() == H * sum(st.lens[i] + M for i in (0, 1))
+    starts = [sum(st.lens[:i]) for i in range(st.n + 1)]
+    for h in range(H):
+        for i in range(st.n):
+            o = int(k_off[h * st.n + i])
+            assert torch.equal(kidx[o:o + st.lens[i]].long(), st.local[starts[i]:starts[i + 1]] * H + h), (h, i)
+        assert int(k_off[h * st.n + 1]) - int(k_off[h * st.n]) == st.lens[0] + M
