@@ -228,6 +228,7 @@ class _Static:
         # queries beside its video queries) reads that piece's local rows in place: its keys are their slot's first
         # rows, and it packs none of its own (compared once per plan)
         mem = [bool(x) for x in p.mem.tolist()]
+        scene = [int(x) for x in p.scene.tolist()]
         starts = [0]
         for c in lens:
             starts.append(starts[-1] + c)
@@ -236,9 +237,10 @@ class _Static:
         for i in range(n):
             if mem[i]:
                 continue
-            for o in sorted(range(n), key=lambda o: (not mem[o], o)):   # pieces reading the memory first
-                if o != i and self.share[o] is None and lens[o] == lens[i] and (mem[o] or o < i) and \
-                        torch.equal(part(o), part(i)):
+            # candidates: pieces of the same scene with as many local rows, those reading the memory first
+            for o in sorted((o for o in range(n) if scene[o] == scene[i] and lens[o] == lens[i] and o != i),
+                            key=lambda o: (not mem[o], o)):
+                if self.share[o] is None and (mem[o] or o < i) and torch.equal(part(o), part(i)):
                     self.share[i] = o
                     break
         self.mem = mem
