@@ -197,6 +197,41 @@ def test_argument_errors_are_runtime_errors():
 
 
 
+def test_rotate_and_memory_argument_errors_without_gpu():
+    """or_rotate_rows, or_memory_select and or_memory_index refuse bad shapes, missing arrays, short strides and
+    misaligned buffers before they launch anything (device pointers are never dereferenced on the host)"""
+    rot = L.lib().or_rotate_rows
+    x, idx, rope, cos, sin, out = 0x10000, 0x20000, 0x30000, 0x40000, 0x50000, 0x60000
+
+    def rotate(x=x, xs=2048, rope=rope, cos=cos, n_rope=100, H=16, D=128, out=out, os_=2048):
+        return L.check(rot(x, xs, 10, idx, rope, cos, sin, n_rope, 12, H, D, out, os_, None), 'or_rotate_rows')
+    for kw, msg in ((dict(D=12), 'multiple of 8'), (dict(H=64, D=128), 'exceed'), (dict(rope=None), 'required'),
+                    (dict(cos=None), 'required'), (dict(n_rope=0), 'required'), (dict(xs=1024), 'cover H \\* D'),
+                    (dict(os_=2040), 'cover H \\* D'), (dict(x=x + 8), '16-byte aligned'),
+                    (dict(out=out + 2), '16-byte aligned')):
+        with pytest.raises(L.HipPathError, match=msg):
+            rotate(**kw)
+    assert rot(x, 2048, 10, idx, rope, cos, sin, 100, 0, 16, 128, out, 2048, None) == 0   # nothing to do
+    sel = L.lib().or_memory_select
+    keys, rows, cent, rep, valid, ws = 0x10000, 0x20000, 0x30000, 0x40000, 0x50000, 0x100000
+
+    def select(B=100, H=2, D=128, M=8, iters=2, keys=keys, stride=256, ws=ws, wsb=1 << 30):
+        return L.check(sel(keys, 1, rows, stride, B, H, D, M, cent, None, iters, rep, valid, ws, wsb, None),
+                       'or_memory_select')
+    for kw, msg in ((dict(D=96), 'D 64 or 128'), (dict(M=101), 'outside'), (dict(M=0), 'outside'),
+                    (dict(iters=-1), 'iters'), (dict(keys=None), 'required'), (dict(stride=128), 'required'),
+                    (dict(ws=ws + 64), 'aligned workspace'), (dict(wsb=16), 'aligned workspace'),
+                    (dict(keys=keys + 4), '16-byte aligned')):
+        with pytest.raises(L.HipPathError, match=msg):
+            select(**kw)
+    idxf = L.lib().or_memory_index
+    a = 0x10000
+    with pytest.raises(L.HipPathError, match='pieces, heads'):
+        L.check(idxf(a, a, a, a, a, a, a, a, 0, 2, 8, a, a, None), 'or_memory_index')
+    with pytest.raises(L.HipPathError, match='every array'):
+        L.check(idxf(a, a, None, a, a, a, a, a, 3, 2, 8, a, a, None), 'or_memory_index')
+
+
 def test_fused_residual_layernorm_argument_errors_without_gpu():
     """or_residual_layernorm_modulate refuses bad widths, a missing or misaligned addend and an output that is x or
     a before it launches anything (device pointers are never dereferenced on the host)"""
