@@ -2,8 +2,9 @@
  * onereel_hip.h: C ABI of libonereel_hip.so, the MI355X (gfx950) scene-structured attention hot path.
  *
  * One DiT attention layer of OneReel's scene attention on one GPU runs as:
- *   or_layout_build   scope layout on the device: cu_seqlens, per-row gather indices and scene-RoPE rows
- *   or_pack_gather    K/V (or Q) rows of every scope packed densely, RoPE applied on the way
+ *   or_layout_build   scope layout on the device: cu_seqlens, key ranges, per-row gather indices and scene-RoPE rows
+ *   or_pack_gather    K/V (or Q) rows of every scope packed densely, RoPE applied on the way (optionally the text
+ *                     scopes read their keys in place from their video scopes' packed rows)
  *   or_rotate_rows    the video queries rotated once, in token order (RoPE ahead of in-place attention)
  *   or_varlen_fwd     packed varlen attention (bf16 MFMA), optional RoPE on the Q load, optional in-place Q / O
  *   or_scatter        packed output rows written back to token order, text padding rows zeroed
