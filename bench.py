@@ -18,6 +18,9 @@ copy_reference: a device-to-device copy of the pack's size (torch copy_) with co
 practical ceiling of the HBM-bound pack and scatter kernels.
 
     python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--no-cpu] [--no-gemm-ref]
+
+--share R/P runs one rank's share of the layer instead (rank R of P work-balanced video-token ranges): the step a
+rank of a P-GPU run computes once its K/V rows are local, on this one GPU.
 """
 from __future__ import annotations
 
@@ -498,6 +501,10 @@ def main():
                          'selection kernels at that shape; lse-merge: the log-sum-exp merge at the 480p layer shape; '
                          'bounded-memory: the head-major bounded memory layer at that shape; power: board power and '
                          'clocks under the attention kernel and under the bf16 GEMM reference (amd-smi)')
+    ap.add_argument('--share', default=None, metavar='R/P',
+                    help="one rank's share of a layer workload: rank R of P work-balanced video-token ranges "
+                         "(Algorithm 1 over the scenes' modelled query costs), its scenes' clipped queries and their "
+                         "full keys, and the sentences whose scene starts in its range, run on this one GPU")
     ap.add_argument('--once', action='store_true',
                     help='profiling mode: a 1 GiB device copy (counter calibration), then the layout, pack-gather, '
                          'attention and scatter kernels once each, then one bf16 16384^3 torch.matmul (the GEMM '
@@ -521,11 +528,11 @@ def main():
     args.steps = 20 if args.steps is None else args.steps
     args.warmup = 3 if args.warmup is None else args.warmup
     W = workload(args.workload)
-    headline = args.workload == 'hunyuan480p'
+    headline = args.workload == 'hunyuan480p' and args.share is None
     T_, H_, D_ = W['T'], W['H'], W['D']
 
     import torch
-    from onereel_amd import scene
+    from onereel_amd import comm, scene
     from onereel_amd.layout import SceneLayout
 
     dev = torch.device('cuda:0')
@@ -533,6 +540,13 @@ def main():
     stream = torch.cuda.current_stream(dev)
     extra = extra_from_reps(W['lengths'], W['reps']) if W['reps'] else {}
     lay = SceneLayout(W['lengths'], halo=W['halo'], sides=W['sides'], extra=extra)
+    q_range = None
+    if args.share:
+        r, P = (int(x) for x in args.share.split('/'))
+        if not 0 <= r < P:
+            raise SystemExit(f'--share {args.share}: rank R must lie in [0, P)')
+        q_range = comm.partition(lay, P, T_, 'scene', W['counts'])[r]
+        W['workload'] += f'-rank{r}of{P}'
     S, Le = sum(W['lengths']) * T_, sum(W['counts'])
     g = torch.Generator(device=dev).manual_seed(0)
     q, k, v = (torch.randn(S, H_, D_, generator=g, device=dev).to(torch.bfloat16) for _ in range(3))
@@ -540,7 +554,7 @@ def main():
     cos, sin = (x.to(dev) for x in rope_table(*W['grid'], D_))
     # text segments read their keys in place from their scene's video segment (no packed copy)
     plan = scene.ScopePlan(lay, T_, W['counts'], Le, W['scene_rope'], None, W['adjacent'], True, dev,
-                           text_keys_in_place=True)
+                           text_keys_in_place=True, q_range=q_range)
     H, D = H_, D_
     lq = [int(x) for x in (plan.cu_q[1:] - plan.cu_q[:-1]).tolist()]
     lk = [int(x) for x in plan.k_len.tolist()]
@@ -588,7 +602,7 @@ def main():
     other = None
     if W['reps'] and W['scene_rope']:
         plan_o = scene.ScopePlan(lay, T_, W['counts'], Le, W['scene_rope'], None, not W['adjacent'], True, dev,
-                                 text_keys_in_place=True)
+                                 text_keys_in_place=True, q_range=q_range)
         ms_o = time_steps(make_step(plan_o))
 
     # per-kernel durations with HIP events on the launch stream
@@ -646,7 +660,8 @@ def main():
     copy_ref = copy_reference(pack_bytes // 2, R, stream, flush) if headline else None
     del evict
     scat_bytes = 2 * plan.sum_q * row                # packed rows read + written
-    rot_bytes = 2 * plan.n_video * row + plan.n_video * D * 8   # video query rows read + written, fp32 cos / sin rows
+    n_vq = sum(lq[0::2])                             # video query rows (the even segments)
+    rot_bytes = 2 * n_vq * row + n_vq * D * 8        # video query rows read + written, fp32 cos / sin rows
     kernels = {
         'attention': dict(ms=round(t_attn, 4), tflops=round(flops / t_attn / 1e9, 1),
                           frac_bf16_peak=round(flops / t_attn / 1e9 / PEAK_BF16_TFLOPS, 4)),
@@ -680,6 +695,7 @@ def main():
                            tokens_per_frame=T_, text_per_scene=W['counts'], halo=W['halo'], sides=W['sides'],
                            frame_memory=W['reps'], shared_pos='adjacent' if W['adjacent'] else 'source',
                            scene_rope=W['scene_rope'], heads=H, head_dim=D, sum_q=plan.sum_q, sum_k=plan.sum_k,
+                           video_token_range=list(q_range) if q_range else None,
                            useful_flop_per_step=flops, frac_bf16_peak_step=round(value / PEAK_BF16_TFLOPS, 4)),
                roofline=dict(bound='mfma', achieved=round(flops / t_attn / 1e9, 1), peak=PEAK_BF16_TFLOPS,
                              unit='TFLOP/s', frac=round(flops / t_attn / 1e9 / PEAK_BF16_TFLOPS, 4), traffic=traffic,

@@ -58,6 +58,11 @@ typedef struct or_layout_desc {
                                             V_j's keys as own frames, sentence, shared frames, so that T_j's keys
                                             (hunyuan15.py:167-168: the same rows) are a prefix of V_j's: T_j packs
                                             no rows and reads that range in place (k_off / k_len) */
+  int32_t q_lo, q_hi;                    /* q_hi > 0: one rank's share of the layer (Processor.scene with several
+                                            ranks, hunyuan15.py:219-224): only the video queries in tokens
+                                            [q_lo, q_hi) (each scene's clipped to the range, with the scene's full
+                                            keys) and the sentences of the scenes whose first token lies in it; the
+                                            other scenes' segments are empty. q_hi = 0: the whole layer */
   int32_t lengths[OR_MAX_SCENES];        /* latent frames per scene, each > 0 */
   int32_t rope_lengths[OR_MAX_SCENES];
   int32_t counts[OR_MAX_SCENES];         /* valid text tokens of sentence j */

@@ -23,7 +23,7 @@ i32, i64, vp = ctypes.c_int32, ctypes.c_int64, ctypes.c_void_p
 class LayoutDesc(ctypes.Structure):
     _fields_ = [('n_scenes', i32), ('T', i32), ('halo', i32), ('sides', i32), ('with_text', i32),
                 ('scene_rope', i32), ('adjacent', i32), ('n_rope_lengths', i32), ('text_rows', i32),
-                ('text_keys_in_place', i32), ('lengths', i32 * OR_MAX_SCENES), ('rope_lengths', i32 * OR_MAX_SCENES),
+                ('text_keys_in_place', i32), ('q_lo', i32), ('q_hi', i32), ('lengths', i32 * OR_MAX_SCENES), ('rope_lengths', i32 * OR_MAX_SCENES),
                 ('counts', i32 * OR_MAX_SCENES), ('extra_ptr', i32 * (OR_MAX_SCENES + 1)),
                 ('extra', i32 * OR_MAX_EXTRA)]
 

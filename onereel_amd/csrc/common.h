@@ -39,6 +39,7 @@ constexpr int kMaxShared = 1024;  // shared-frame entries over all scenes (halo 
 struct LayoutDerived {
   int n_scenes, T, F, with_text, scene_rope, adjacent, text_rows, n_rope;
   int text_in_place;                               // T_j's keys read in place from V_j's (own frames, sentence first)
+  int qa, qb;                                      // the rank's video query tokens [qa, qb) (all: [0, F T))
   int lo[OR_MAX_SCENES], hi[OR_MAX_SCENES];        // frame range of scene j (layout.py:43-45)
   int t0[OR_MAX_SCENES], t1[OR_MAX_SCENES];        // text range of sentence j (hunyuan15.py:87-89)
   int rope_start[OR_MAX_SCENES + 1];               // frame boundaries of the rope scenes

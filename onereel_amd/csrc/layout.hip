@@ -12,6 +12,9 @@
 // and one per (segment, sentence). A block takes one run at a time, derives its bases once, and writes its rows as
 // base + offset with coalesced int32 stores, so no per-row search or division is left.
 //
+// One rank's share (q_lo, q_hi): V_j's queries are scene j's tokens inside [q_lo, q_hi) with the scene's full keys,
+// T_j runs only when scene j's first token lies in the range, and every other segment is empty.
+//
 // T_j's keys (own frames, then the sentence) are the rows of V_j's own frames and sentence. With text_keys_in_place
 // V_j's keys are packed as own frames, sentence, shared frames, so T_j's keys are the first rows of V_j's: T_j packs
 // none and its key range (k_off / k_len) points there. The attention result does not depend on the order of a
@@ -43,32 +46,56 @@ struct SegTable {
 __host__ __device__ inline int seg_scene(int with_text, int s) { return with_text ? s >> 1 : s; }
 __host__ __device__ inline bool seg_is_text(int with_text, int s) { return with_text && (s & 1); }
 
-// key count of segment s (the rows its queries attend to)
+// the rank's video queries of scene j: tokens [*a, *b), the scene's clipped to [qa, qb) (mine, hunyuan15.py:221);
+// empty when the scene lies outside the range
+__host__ __device__ inline void scene_queries(const LayoutDerived& L, int j, int* a, int* b) {
+  const int lo = L.lo[j] * L.T, hi = L.hi[j] * L.T;
+  *a = lo > L.qa ? lo : L.qa;
+  *b = hi < L.qb ? hi : L.qb;
+  if (*b < *a) *b = *a;
+}
+
+// the rank runs scene j's sentence queries: the scene's first token lies in its range (text_for, hunyuan15.py:223)
+__host__ __device__ inline bool owns_text(const LayoutDerived& L, int j) {
+  const int lo = L.lo[j] * L.T;
+  return L.qa <= lo && lo < L.qb;
+}
+
+// key count of segment s (the rows its queries attend to; none for a segment the rank does not run)
 __host__ __device__ inline int seg_keys(const LayoutDerived& L, int s) {
   const int j = seg_scene(L.with_text, s);
   const int own = (L.hi[j] - L.lo[j]) * L.T, txt = L.t1[j] - L.t0[j];
-  return seg_is_text(L.with_text, s) ? own + txt : own + (L.sh_ptr[j + 1] - L.sh_ptr[j]) * L.T + txt;
+  if (seg_is_text(L.with_text, s)) return owns_text(L, j) ? own + txt : 0;
+  int a, b;
+  scene_queries(L, j, &a, &b);
+  return b > a ? own + (L.sh_ptr[j + 1] - L.sh_ptr[j]) * L.T + txt : 0;
 }
 
 // query count and packed key rows of segment s (T_j packs no keys when they are read in place from V_j's)
 __host__ __device__ inline void seg_lengths(const LayoutDerived& L, int s, int* lq, int* lk) {
   const int j = seg_scene(L.with_text, s);
   const bool text = seg_is_text(L.with_text, s);
-  *lq = text ? L.t1[j] - L.t0[j] : (L.hi[j] - L.lo[j]) * L.T;
+  int a, b;
+  scene_queries(L, j, &a, &b);
+  *lq = text ? (owns_text(L, j) ? L.t1[j] - L.t0[j] : 0) : b - a;
   *lk = text && L.text_in_place ? 0 : seg_keys(L, s);
 }
 
-// runs of segment s: query side (its own frames, or its sentence) and key side (own frames, shared frames, sentence)
+// runs of segment s: query side (the frames its clipped video queries touch, or its sentence) and key side (own
+// frames, shared frames, sentence)
 __host__ __device__ inline void seg_runs(const LayoutDerived& L, int s, int* uq, int* uk) {
   const int j = seg_scene(L.with_text, s);
   const int own = L.hi[j] - L.lo[j];
   const int txt = L.t1[j] - L.t0[j] > 0 ? 1 : 0;
   if (seg_is_text(L.with_text, s)) {
-    *uq = txt;
-    *uk = L.text_in_place ? 0 : own + txt;
+    const bool mine = owns_text(L, j);
+    *uq = mine ? txt : 0;
+    *uk = L.text_in_place || !mine ? 0 : own + txt;
   } else {
-    *uq = own;
-    *uk = own + (L.sh_ptr[j + 1] - L.sh_ptr[j]) + txt;
+    int a, b;
+    scene_queries(L, j, &a, &b);
+    *uq = b > a ? (b - 1) / L.T - a / L.T + 1 : 0;
+    *uk = b > a ? own + (L.sh_ptr[j + 1] - L.sh_ptr[j]) + txt : 0;
   }
 }
 
@@ -91,6 +118,8 @@ int derive_host(const or_layout_desc& d, LayoutDerived& L) {
     L.t1[j] = t;
   }
   L.F = f;
+  L.qa = d.q_hi > 0 ? d.q_lo : 0;
+  L.qb = d.q_hi > 0 ? d.q_hi : f * d.T;
   const int nr = d.n_rope_lengths > 0 ? d.n_rope_lengths : d.n_scenes;
   const int* rl = d.n_rope_lengths > 0 ? d.rope_lengths : d.lengths;
   L.n_rope = nr;
@@ -183,7 +212,11 @@ __global__ __launch_bounds__(kThreads) void layout_kernel(const or_layout_desc d
       L.text_in_place = d.with_text && d.text_keys_in_place;
       L.n_rope = nr;
     }
-    if (lane == ns - 1) L.F = lo + len;
+    if (lane == ns - 1) {
+      L.F = lo + len;
+      L.qa = d.q_hi > 0 ? d.q_lo : 0;
+      L.qb = d.q_hi > 0 ? d.q_hi : (lo + len) * d.T;
+    }
     wave_lds_sync();
 
     // 2. shared frames per scene: upper-bound slots, then compaction (host validation keeps them within kMaxShared)
@@ -255,7 +288,9 @@ __global__ __launch_bounds__(kThreads) void layout_kernel(const or_layout_desc d
       if (s < n_seg) {
         const int j = seg_scene(L.with_text, s);
         const bool text = seg_is_text(L.with_text, s);
-        if (seg_q_src_out) seg_q_src_out[s] = text ? L.F * L.T + L.t0[j] : L.lo[j] * L.T;
+        int qa, qb;
+        scene_queries(L, j, &qa, &qb);
+        if (seg_q_src_out) seg_q_src_out[s] = text ? L.F * L.T + L.t0[j] : qa;
         if (out.k_off) out.k_off[s] = text && L.text_in_place ? S.cu_k[s - 1] : S.cu_k[s];
         if (out.k_len) out.k_len[s] = seg_keys(L, s);
       }
@@ -280,13 +315,16 @@ __global__ __launch_bounds__(kThreads) void layout_kernel(const or_layout_desc d
     const int nsh = tseg ? 0 : L.sh_ptr[j + 1] - L.sh_ptr[j];
     const int txt = L.t1[j] - L.t0[j];
     const int base = qside ? S.cu_q[s] : S.cu_k[s];
-    // the run's place in the segment: queries are V_j's own frames or T_j's sentence; keys are the own frames, then
-    // the shared frames and the sentence (or, with the text keys in place, the sentence and the shared frames)
+    // the run's place in the segment: queries are V_j's own-frame tokens (clipped to the rank's range; a run per frame
+    // they touch) or T_j's sentence; keys are the own frames, then the shared frames and the sentence (or, with the
+    // text keys in place, the sentence and the shared frames)
     int kind, idx = 0, row0;   // kind 0: own frame idx, 1: shared frame idx, 2: sentence
+    int qa = 0, qb = 0;   // video query runs: frame qa / T + slot of the scene's clipped query tokens [qa, qb)
+    scene_queries(L, j, &qa, &qb);
     if (qside) {
       kind = tseg ? 2 : 0;
       idx = slot;
-      row0 = base + (tseg ? 0 : slot * T);
+      row0 = base;
     } else if (slot < own) {
       kind = 0;
       idx = slot;
@@ -303,7 +341,15 @@ __global__ __launch_bounds__(kThreads) void layout_kernel(const or_layout_desc d
     }
     int count, src0, rope0 = -1, ma0 = -1, mb0 = -1;
     bool rope = false, move = false;
-    if (kind != 2) {
+    if (qside && kind == 0) {
+      const int f = qa / T + slot;
+      const int t0 = f * T > qa ? f * T : qa, t1 = (f + 1) * T < qb ? (f + 1) * T : qb;
+      row0 = base + (t0 - qa);
+      count = t1 - t0;
+      rope = true;
+      src0 = t0;
+      rope0 = (L.scene_rope ? frame_position(L, f) * T : f * T) + (t0 - f * T);
+    } else if (kind != 2) {
       count = T;
       rope = true;
       int f;
@@ -391,6 +437,8 @@ static int plan_impl(const or_layout_desc* dp, or_layout_sizes* sz, LayoutDerive
   if (d.T < 1) return fail_arg("T must be positive (got %d)", d.T);
   if (d.halo < 0) return fail_arg("halo must be >= 0 (got %d)", d.halo);
   if (d.sides < 0 || d.sides > 2) return fail_arg("sides must be 0 'adj', 1 'prev' or 2 'next' (got %d)", d.sides);
+  if (d.q_hi < 0 || (d.q_hi == 0 && d.q_lo != 0))
+    return fail_arg("q_lo / q_hi: q_hi = 0 (the whole layer) or 0 <= q_lo < q_hi (got %d, %d)", d.q_lo, d.q_hi);
   if (d.text_keys_in_place != 0 && (d.text_keys_in_place != 1 || !d.with_text))
     return fail_arg("text_keys_in_place must be 0, or 1 with text scopes (got %d, with_text %d)", d.text_keys_in_place,
                     d.with_text);
@@ -434,6 +482,9 @@ static int plan_impl(const or_layout_desc* dp, or_layout_sizes* sz, LayoutDerive
   }
   if (ub > kMaxShared) return fail_arg("%lld shared-frame entries exceed the maximum %d", (long long)ub, kMaxShared);
   if (F * (int64_t)d.T + d.text_rows >= (int64_t)1 << 31) return fail_arg("layout rows exceed int32");
+  if (d.q_hi > 0 && (d.q_lo < 0 || d.q_lo >= d.q_hi || d.q_hi > F * (int64_t)d.T))
+    return fail_arg("query range [%d, %d) outside the layout's %lld video tokens", d.q_lo, d.q_hi,
+                    (long long)(F * (int64_t)d.T));
 
   static thread_local LayoutDerived Lh;
   LayoutDerived& L = Lout ? *Lout : Lh;

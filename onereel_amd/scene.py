@@ -26,7 +26,7 @@ MODES = ('raw', 'rotated', 'none')
 
 
 def _desc(lay: SceneLayout, T: int, counts, text_rows: int, scene_rope: bool, rope_lengths, adjacent: bool,
-          with_text: bool, text_keys_in_place: bool = False) -> L.LayoutDesc:
+          with_text: bool, text_keys_in_place: bool = False, q_range=None) -> L.LayoutDesc:
     d = L.LayoutDesc()
     n = lay.n_scenes
     if n > L.OR_MAX_SCENES:
@@ -36,6 +36,8 @@ def _desc(lay: SceneLayout, T: int, counts, text_rows: int, scene_rope: bool, ro
     d.with_text, d.scene_rope, d.adjacent = int(with_text), int(scene_rope), int(adjacent)
     d.text_rows = int(text_rows)
     d.text_keys_in_place = int(bool(text_keys_in_place) and bool(with_text))
+    if q_range is not None:
+        d.q_lo, d.q_hi = int(q_range[0]), int(q_range[1])
     for j, x in enumerate(lay.lengths):
         d.lengths[j] = int(x)
     counts = list(counts) if with_text else [0] * n
@@ -71,19 +73,25 @@ class ScopePlan:
 
     text_keys_in_place: each scene's video segment packs its keys as own frames, sentence, shared frames, and the
     text segment (whose keys are the same own-frame and sentence rows) reads the first of them in place (k_off,
-    k_len) instead of packing its own copy; the default packs every segment in the reference's order."""
+    k_len) instead of packing its own copy; the default packs every segment in the reference's order.
+
+    q_range=(a, b): one rank's share of the layer when the video tokens are split over several ranks
+    (hunyuan15.py:219-224): the video queries in tokens [a, b) (each scene's clipped to the range, with the scene's
+    full keys) and the sentences of the scenes whose first token lies in the range; the other segments are empty.
+    Query and key rows stay global token rows."""
 
     def __init__(self, lay: SceneLayout, T: int, counts=None, text_rows: int | None = None, scene_rope=False,
                  rope_lengths=None, adjacent=False, with_text=True, device=None, moves=False,
-                 text_keys_in_place=False):
+                 text_keys_in_place=False, q_range=None):
         counts = list(counts) if counts is not None else [0] * lay.n_scenes
         if text_rows is None:
             text_rows = sum(counts) if with_text else 0
         self.layout, self.T, self.counts, self.text_rows = lay, int(T), counts, int(text_rows)
         self.scene_rope, self.adjacent, self.with_text = bool(scene_rope), bool(adjacent), bool(with_text)
         self.text_keys_in_place = bool(text_keys_in_place) and self.with_text
+        self.q_range = None if q_range is None else (int(q_range[0]), int(q_range[1]))
         self.desc = _desc(lay, T, counts, text_rows, scene_rope, rope_lengths, adjacent, with_text,
-                          self.text_keys_in_place)
+                          self.text_keys_in_place, self.q_range)
         sz = L.LayoutSizes()
         L.check(L.lib().or_layout_plan(ctypes.byref(self.desc), ctypes.byref(sz)), 'or_layout_plan')
         self.n_seg, self.sum_q, self.sum_k = sz.n_seg, sz.sum_q, sz.sum_k
@@ -338,7 +346,9 @@ def scene_attention(plan: ScopePlan, q, k, v, eq, ek, ev, cos=None, sin=None, mo
         raise L.HipValueError(f'{eq.shape[0]} text rows, layout has {plan.text_rows}')
     kp, vp = pack_rows(plan, k, ek, 'k', out=kbuf, b_video=v, b_text=ev, b_out=vbuf, cos=cos, sin=sin, mode=mode)
     ov = torch.empty_like(q)
-    ot = torch.empty(eq.shape[0], H, D, dtype=q.dtype, device=q.device) if eq is not None else None
+    # one rank's share writes only its own scenes' sentence rows: the others stay zero (ot = eq.new_zeros)
+    make_ot = torch.zeros if plan.q_range is not None else torch.empty
+    ot = make_ot(eq.shape[0], H, D, dtype=q.dtype, device=q.device) if eq is not None else None
     qmode = 'raw' if mode == 'raw' else 'none'
     if fused:
         if rotate_q not in ('pre', 'load'):

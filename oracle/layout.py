@@ -232,8 +232,14 @@ class Scopes:
 
 
 def hunyuan_scopes(lay, T, counts, text_rows=None, scene_rope=False, rope_lengths=None, adjacent=False,
-                   with_text=True):
+                   with_text=True, token_range=None):
     """Processor.scene on one GPU (hunyuan15.py:212-251) -> the packed layout of its single `A.packed` call.
+
+    token_range=(a, b): one rank's share with several ranks (hunyuan15.py:219-224): the scenes overlapping video
+    tokens [a, b), each with its queries clipped to the range (`mine`) and its full keys, and the sentence segment of
+    the scenes whose first token lies in the range (`text_for`). The reference packs these segments in two calls
+    (scenes whose keys are all local first, then the others, hunyuan15.py:236-246); they are listed here in scene
+    order, each segment's rows as the reference builds them.
 
     Segment order (hunyuan15.py:158-169): V_0, T_0, V_1, T_1, ... V_j: queries = scene j's video rows; keys =
     key_frames(j) rows then sentence j's rows. T_j: queries = sentence j's rows; keys = frames(j) rows then sentence
@@ -244,15 +250,18 @@ def hunyuan_scopes(lay, T, counts, text_rows=None, scene_rope=False, rope_length
     tr = text_ranges(counts) if with_text else [(0, 0)] * lay.n_scenes
     Le = (tr[-1][1] if tr else 0) if text_rows is None else text_rows
     rows = scene_rope_rows(lay, T, rope_lengths) if scene_rope else np.arange(S, dtype=np.int64)
+    ra, rb = token_range if token_range is not None else (0, S)
     kind, scene, lq, lk = [], [], [], []
     qs, ks, qr, kr, ka, kb = [], [], [], [], [], []
     for j, (lo, hi) in enumerate(lay.ranges):
+        if not (lo * T < rb and hi * T > ra):           # not one of this rank's scenes (mine)
+            continue
         t0, t1 = tr[j]
         keys = lay.key_frames(j)
         text = S + np.arange(t0, t1)
         n_own = len(lay.frames[j]) * T
-        # V_j
-        q = np.arange(lo * T, hi * T)
+        # V_j: the scene's video queries inside the range
+        q = np.arange(max(lo * T, ra), min(hi * T, rb))
         kv = _rows(keys, T)
         rope_k = rows[kv].copy()
         move_a = np.full(len(kv), -1, np.int64)
@@ -274,8 +283,8 @@ def hunyuan_scopes(lay, T, counts, text_rows=None, scene_rope=False, rope_length
         kr += [rope_k, np.full(len(text), -1, np.int64)]
         ka += [move_a, np.full(len(text), -1, np.int64)]
         kb += [move_b, np.full(len(text), -1, np.int64)]
-        if with_text:
-            # T_j (text_for = every scene on one GPU, hunyuan15.py:223)
+        if with_text and ra <= lo * T < rb:
+            # T_j (text_for: the scene's first token lies in the range; every scene on one GPU, hunyuan15.py:223)
             kv = _rows(lay.frames[j], T)
             kind.append('t'), scene.append(j), lq.append(t1 - t0), lk.append(len(kv) + len(text))
             qs.append(text), qr.append(np.full(len(text), -1, np.int64))

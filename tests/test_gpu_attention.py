@@ -7,6 +7,7 @@ import torch
 from helpers import assert_close, attn_rows_reference, layout_case, rand_bf16, sample_rows, scope_rows_reference
 from onereel_amd import _lib as L
 from onereel_amd import attention as A
+from onereel_amd import comm
 from onereel_amd import hunyuan15 as HY
 from onereel_amd import scene
 from onereel_amd import wan as W
@@ -222,6 +223,48 @@ def test_scene_layer_matches_oracle(name, per_seg, rotate_q, in_place, adjacent)
     valid = sum(case['counts'])
     if case['Le'] > valid:
         assert ot[valid:].abs().max().item() == 0
+
+
+@pytest.mark.parametrize('name,P,per_seg', [('cpu_plumbing', 3, None), ('hunyuan480p', 3, 32),
+                                            ('uneven_K4', 5, 24)])
+def test_scene_layer_rank_shares(name, P, per_seg):
+    """the layer's video tokens split over P ranks by the work-balanced partition (Algorithm 1; it cuts scenes,
+    mid-frame at the full-size shapes): each rank's share, fused with in-place text keys, on its query rows against
+    the oracle's token_range scopes; the sentence rows of scenes another rank runs stay zero (the reference's
+    ot = eq.new_zeros before its all-reduce), and the ranks' outputs together give the one-GPU layer's"""
+    case = layout_case(name)
+    q, k, v, eq, ek, ev, cos, sin = _layer_inputs(case, 9)
+    g = [x.to(DEV) for x in (q, k, v, eq, ek, ev, cos, sin)]
+    lay = SceneLayout(case['lengths'], halo=case['halo'], sides=case['sides'], extra=case['extra'])
+    olay = OL.SceneLayout(case['lengths'], case['halo'], case['sides'], case['extra'])
+    T = case['T']
+    adjacent = True
+    full = scene.ScopePlan(lay, T, case['counts'], case['Le'], case['scene_rope'], None, adjacent, True, DEV,
+                           text_keys_in_place=True)
+    fv, ft = scene.scene_attention(full, *g, mode='raw', fused=True)
+    text_sum = torch.zeros_like(ft)
+    own = comm.partition(lay, P, T, 'scene', case['counts'])
+    assert any(lo * T < a < hi * T for a, _ in own[1:] for lo, hi in lay.ranges)    # a scene is cut
+    for r, (a, b) in enumerate(own):
+        print(f'layer rank share {name} rank {r}/{P} tokens [{a}, {b})', flush=True)
+        plan = scene.ScopePlan(lay, T, case['counts'], case['Le'], case['scene_rope'], None, adjacent, True, DEV,
+                               text_keys_in_place=True, q_range=(a, b))
+        ov, ot = scene.scene_attention(plan, *g, mode='raw', fused=True)
+        sc = OL.hunyuan_scopes(olay, T, case['counts'], case['Le'], scene_rope=case['scene_rope'],
+                               adjacent=adjacent, token_range=(a, b))
+        rows = np.arange(int(sc.cu_q[-1])) if per_seg is None else sample_rows(sc.cu_q, per_seg)
+        ref = scope_rows_reference(sc, q, k, v, eq, ek, ev, rows, cos, sin, mode='raw')
+        got = torch.cat([ov, ot]).cpu()[torch.as_tensor(sc.q_src[rows])]
+        assert_close(got, ref, what=f'{name} rank {r} of {P}')
+        # the same rows of the one-GPU layer (equal up to the order of a key split's partial sums)
+        assert_close(ov[a:b].cpu(), fv[a:b].cpu(), what=f'rank {r} against the one-GPU layer')
+        tr = OL.text_ranges(case['counts'])
+        for j, (lo, _) in enumerate(lay.ranges):
+            t0, t1 = tr[j]
+            if not a <= lo * T < b and t1 > t0:
+                assert ot[t0:t1].abs().max().item() == 0, (r, j)
+        text_sum += ot                                    # each sentence row is written by one rank alone
+    assert_close(text_sum.cpu(), ft.cpu(), what='sentence rows over the ranks')
 
 
 @pytest.mark.parametrize('adjacent', [False, True])

@@ -156,6 +156,83 @@ def test_layout_text_keys_in_place_random_layouts():
         _check_in_place(case, bool(rng.integers(2)))
 
 
+def _check_rank_share(case, adjacent, q_range, in_place):
+    """one rank's share (q_range): each segment the rank runs holds the oracle's token_range segment (query rows and
+    RoPE rows; key rows, RoPE and _move_shared rows, in the in-place order when the text keys are read in place), and
+    every other segment is empty"""
+    lay = SceneLayout(case['lengths'], halo=case['halo'], sides=case['sides'], extra=case['extra'])
+    plan = ScopePlan(lay, case['T'], case['counts'], case['Le'], case['scene_rope'], case['rope_lengths'], adjacent,
+                     True, DEV, moves=True, text_keys_in_place=in_place, q_range=q_range)
+    olay = OL.SceneLayout(case['lengths'], case['halo'], case['sides'], case['extra'])
+    sc = OL.hunyuan_scopes(olay, case['T'], case['counts'], case['Le'], scene_rope=case['scene_rope'],
+                           rope_lengths=case['rope_lengths'], adjacent=adjacent, token_range=q_range)
+    torch.cuda.synchronize()
+    T, n = case['T'], len(case['lengths'])
+    names = ('q_src', 'q_rope', 'k_src', 'k_rope') + (('k_move_a', 'k_move_b') if adjacent else ())
+    got = {a: getattr(plan, a).cpu().numpy() for a in names}
+    ref = {a: np.asarray(getattr(sc, a)) for a in names}
+    cu_q, cu_k, k_off, k_len, first = (getattr(plan, a).cpu().tolist()
+                                       for a in ('cu_q', 'cu_k', 'k_off', 'k_len', 'seg_q_src'))
+    ran = {(2 * j + (kind == 't')): i for i, (kind, j) in enumerate(zip(sc.kind, sc.scene))}
+    assert plan.n_seg == 2 * n and plan.sum_q == int(sc.cu_q[-1])
+    for s in range(2 * n):
+        lq = cu_q[s + 1] - cu_q[s]
+        if s not in ran:
+            assert lq == 0 and k_len[s] == 0 and cu_k[s + 1] == cu_k[s], s
+            continue
+        i, j = ran[s], s // 2
+        qa, qb, ka, kb = sc.cu_q[i], sc.cu_q[i + 1], sc.cu_k[i], sc.cu_k[i + 1]
+        assert lq == qb - qa and k_len[s] == kb - ka, s
+        assert qb == qa or first[s] == ref['q_src'][qa], s
+        for a in ('q_src', 'q_rope'):
+            assert np.array_equal(got[a][cu_q[s]:cu_q[s + 1]], ref[a][qa:qb]), (s, a)
+        order = np.arange(ka, kb)
+        if in_place and s % 2 == 0:   # own frames, sentence, shared frames
+            own, txt = len(lay.frames[j]) * T, case['counts'][j]
+            order = np.r_[ka:ka + own, kb - txt:kb, ka + own:kb - txt]
+        if in_place and s % 2 == 1:
+            assert cu_k[s + 1] == cu_k[s] and k_off[s] == cu_k[s - 1], s
+        else:
+            assert k_off[s] == cu_k[s] and cu_k[s + 1] - cu_k[s] == kb - ka, s
+        for a in names[2:]:
+            assert np.array_equal(got[a][k_off[s]:k_off[s] + k_len[s]], ref[a][order]), (s, a)
+
+
+def _equal_token_ranges(case, P):
+    S = sum(case['lengths']) * case['T']
+    return [(r * S // P, (r + 1) * S // P) for r in range(P)]
+
+
+@pytest.mark.parametrize('name, P', [('cpu_plumbing', 3), ('hunyuan480p', 3), ('hunyuan480p', 8), ('uneven_K4', 5),
+                                     ('uneven_K12', 8)])
+def test_layout_rank_shares(name, P):
+    """the layer's video tokens split over P ranks by equal token counts (cutting scenes and frames): every rank's
+    share, with and without the text keys in place, in both shared-position modes"""
+    case = layout_case(name)
+    for r, q_range in enumerate(_equal_token_ranges(case, P)):
+        for adjacent in (False, True):
+            for in_place in (False, True):
+                print(f'layout rank share {name} rank {r}/{P} {q_range} adjacent={adjacent} in_place={in_place}',
+                      flush=True)
+                _check_rank_share(case, adjacent, q_range, in_place)
+
+
+def test_layout_rank_shares_random_layouts():
+    rng = np.random.default_rng(23)
+    for it in range(40):
+        n = int(rng.integers(1, 8))
+        lengths = rng.integers(1, 6, n).tolist()
+        F = sum(lengths)
+        extra = {j: rng.integers(0, F, int(rng.integers(0, 4))).tolist() for j in range(n) if rng.random() < 0.7}
+        case = dict(lengths=lengths, halo=int(rng.integers(0, 3)), sides=['adj', 'prev', 'next'][int(rng.integers(3))],
+                    extra=extra, T=int(rng.integers(1, 10)), counts=rng.integers(0, 5, n).tolist(),
+                    scene_rope=bool(rng.integers(2)), rope_lengths=None)
+        case['Le'] = sum(case['counts']) + int(rng.integers(0, 3))
+        S = F * case['T']
+        a = int(rng.integers(0, S))
+        _check_rank_share(case, bool(rng.integers(2)), (a, int(rng.integers(a + 1, S + 1))), bool(rng.integers(2)))
+
+
 def _tables(case):
     F, Hh, Ww = case['table']
     assert Hh * Ww == case['T']

@@ -132,6 +132,40 @@ def test_host_planner_sizes_match_oracle():
             assert s2.sum_k == sum(lk for lk, kind in zip(sc.lk, sc.kind) if kind == 'v')
 
 
+def test_host_planner_sizes_of_rank_shares_match_oracle():
+    """q_lo / q_hi (one rank's share): segment sizes against the oracle's token_range scopes, the segments the rank
+    does not run empty; ranges cut scenes mid-frame"""
+    rng = np.random.default_rng(5)
+    for _ in range(200):
+        lay = _random_layout(rng)
+        T = int(rng.integers(1, 9))
+        counts = rng.integers(0, 5, lay.n_scenes).tolist()
+        S = lay.n_frames * T
+        a = int(rng.integers(0, S))
+        b = int(rng.integers(a + 1, S + 1))
+        scene_rope, adjacent, with_text, in_place = (bool(rng.integers(2)) for _ in range(4))
+        in_place = in_place and with_text
+        d = _desc(lay, T, counts, sum(counts), scene_rope, None, adjacent, with_text, in_place, q_range=(a, b))
+        sz = L.LayoutSizes()
+        L.check(L.lib().or_layout_plan(ctypes.byref(d), ctypes.byref(sz)), 'plan')
+        olay = OL.SceneLayout(lay.lengths, lay.halo, lay.sides, lay.extra)
+        sc = OL.hunyuan_scopes(olay, T, counts if with_text else [0] * lay.n_scenes, sum(counts),
+                               scene_rope=scene_rope, adjacent=adjacent, with_text=with_text, token_range=(a, b))
+        assert sz.n_seg == lay.n_scenes * (2 if with_text else 1)
+        assert (sz.sum_q, sz.max_q, sz.max_k) == (int(sc.cu_q[-1]), max(sc.lq), max(sc.lk))
+        packed = [lk for lk, kind in zip(sc.lk, sc.kind) if kind == 'v' or not in_place]
+        assert sz.sum_k == sum(packed)
+
+
+def test_query_range_errors():
+    lay = SceneLayout([2, 3], halo=0)
+    for q_range, msg in (((3, 3), 'query range'), ((-1, 4), 'query range'), ((0, 21), 'query range'),
+                         ((2, 0), 'q_lo / q_hi'), ((0, -1), 'q_lo / q_hi')):
+        d = _desc(lay, 4, [1, 1], 2, False, None, False, True, q_range=q_range)
+        with pytest.raises(L.HipPathError, match=msg):
+            L.check(L.lib().or_layout_plan(ctypes.byref(d), ctypes.byref(L.LayoutSizes())), 'or_layout_plan')
+
+
 def test_text_keys_in_place_needs_text_scopes():
     d = _desc(SceneLayout([2, 3], halo=0), 4, [1, 1], 2, False, None, False, False)
     d.text_keys_in_place = 1
@@ -321,3 +355,68 @@ def test_host_api_agrees_with_oracle_on_random_layouts():
         for k in range(1, F + 1):
             sc = [f * k // F for f in range(F)]
             assert SceneLayout.even(F, k).lengths == [sc.count(j) for j in range(k)]
+
+
+def test_partition_known_answers():
+    """rank token ranges against the reference's own known answers: equal scenes split at the scene boundary, a
+    boundary that falls inside a frame, Algorithm 1's invariants for 2, 3, 4 and 8 ranks (contiguous ranges, at most
+    n - 1 cut scenes, every rank within one query's cost of the mean work), the clamp that keeps a query per rank,
+    and the equal Ulysses split"""
+    g = RT['partition_equal_scenes']
+    lay = SceneLayout(g['lengths'], halo=g['halo'])
+    assert [list(x) for x in comm.partition(lay, g['n'], g['T'], 'scene')] == g['own']
+    g = RT['partition_mid_frame']
+    lay = SceneLayout(g['lengths'], halo=g['halo'])
+    b = comm.partition(lay, g['n'], g['T'], 'scene')[0][1]
+    assert g['boundary_above'] < b < g['boundary_below'] and b % g['T'] != 0
+    assert [list(x) for x in comm.partition(lay, g['n'], g['T'], 'ulysses')] == g['ulysses']
+    g = RT['partition_invariants']
+    lay, T = SceneLayout(g['lengths'], halo=g['halo']), g['T']
+    cost = comm.query_cost(lay, T)
+    per_token = np.concatenate([[c] * (m * T) for c, m in zip(cost, lay.lengths)])
+    for n in g['ranks']:
+        own = comm.partition(lay, n, T, 'scene')
+        assert own[0][0] == 0 and own[-1][1] == lay.n_frames * T
+        assert all(x[1] == y[0] and x[0] < x[1] for x, y in zip(own, own[1:]))
+        assert sum(any(lo * T < x[0] < hi * T for x in own) for lo, hi in lay.ranges) <= n - 1
+        work = [per_token[a:b].sum() for a, b in own]
+        assert max(abs(w - sum(work) / n) for w in work) <= per_token.max() + 1e-9
+    g = RT['balanced_clamp']
+    assert [list(x) for x in comm.balanced(g['sizes'], g['cost'], g['n'])] == g['own']
+
+
+def test_partition_against_brute_force():
+    """Algorithm 1 on random scene sizes and costs against a direct search over every query: boundary p is the query
+    nearest to where the running work reaches p / n of the total (work measured in whole queries of the scene the
+    goal falls in), clamped to keep a query per rank; the 'scenes' granularity cuts only at scene starts, and 'tokens'
+    splits evenly"""
+    rng = np.random.default_rng(3)
+    for _ in range(300):
+        k = int(rng.integers(1, 7))
+        sizes = rng.integers(1, 30, k).tolist()
+        cost = (rng.random(k) * 3 + 0.1).tolist()
+        n = int(rng.integers(1, min(sum(sizes), 6) + 1))
+        own = comm.balanced(sizes, cost, n)
+        L_ = sum(sizes)
+        per = np.repeat(cost, sizes)
+        cw = np.concatenate([[0.0], np.cumsum(per)])    # work before query t
+        b = [0]
+        for p in range(1, n):
+            goal = p * cw[-1] / n
+            # queries whose start lies in the scene holding the goal, nearest by work
+            j = min(int(np.searchsorted(np.cumsum(np.asarray(sizes) * cost), goal - 1e-9)), k - 1)
+            lo = sum(sizes[:j])
+            cand = np.arange(lo, lo + sizes[j] + 1)
+            at = int(cand[np.argmin(np.abs(cw[cand] - goal))])
+            b.append(min(max(at, b[-1] + 1), L_ - (n - p)))
+        b.append(L_)
+        exp = list(zip(b[:-1], b[1:]))
+        # a goal half-way between two queries may round either way: allow one query of difference there
+        assert all(abs(x[0] - y[0]) <= 1 for x, y in zip(own, exp)), (sizes, cost, n, own, exp)
+        assert own[0][0] == 0 and own[-1][1] == L_ and all(x[0] < x[1] for x in own)
+    lay = SceneLayout([3, 5, 7, 9], halo=1)
+    sc = comm.partition(lay, 3, 10, 'scene', granularity='scenes')
+    assert all(a in (0, 30, 80, 150) for a, _ in sc) and len({a for a, _ in sc}) == 3
+    assert comm.partition(lay, 3, 10, 'scene', granularity='tokens') == [(0, 80), (80, 160), (160, 240)]
+    with pytest.raises(ValueError):
+        comm.partition(lay, 7, 10, 'ulysses')

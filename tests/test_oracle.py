@@ -194,6 +194,47 @@ def test_scopes_brute_force_membership():
         assert keys == exp
 
 
+def test_rank_shares_partition_the_one_gpu_scopes():
+    """token_range: for any split of the video tokens into rank ranges, the ranks' video segments of a scene, in rank
+    order, hold exactly that scene's one-GPU queries and each the scene's one-GPU keys (rows and RoPE / move rows);
+    every sentence segment appears on exactly one rank (the one holding its scene's first token), equal to the
+    one-GPU one; the range covering every token gives the one-GPU scopes"""
+    rng = np.random.default_rng(11)
+    for it in range(40):
+        n = int(rng.integers(1, 6))
+        lengths = rng.integers(1, 5, n).tolist()
+        F = sum(lengths)
+        extra = {j: rng.integers(0, F, int(rng.integers(0, 3))).tolist() for j in range(n) if rng.random() < 0.6}
+        lay = OL.SceneLayout(lengths, int(rng.integers(0, 3)), ['adj', 'prev', 'next'][int(rng.integers(3))], extra)
+        T = int(rng.integers(1, 7))
+        counts = rng.integers(0, 4, n).tolist()
+        kw = dict(scene_rope=bool(rng.integers(2)), adjacent=bool(rng.integers(2)))
+        S = F * T
+        full = OL.hunyuan_scopes(lay, T, counts, **kw)
+        whole = OL.hunyuan_scopes(lay, T, counts, token_range=(0, S), **kw)
+        for a in ('cu_q', 'cu_k', 'q_src', 'k_src', 'q_rope', 'k_rope', 'k_move_a', 'k_move_b'):
+            assert np.array_equal(getattr(full, a), getattr(whole, a)), a
+        P = int(rng.integers(1, min(S, 5) + 1))
+        cuts = sorted(rng.choice(np.arange(1, S), P - 1, replace=False).tolist()) if P > 1 else []
+        bounds = [0] + cuts + [S]
+        seg = lambda sc, i, a, cu: np.asarray(getattr(sc, a))[sc.__dict__[cu][i]:sc.__dict__[cu][i + 1]]
+        ref = {(k, j): i for i, (k, j) in enumerate(zip(full.kind, full.scene))}
+        rope_of = dict(zip(full.q_src.tolist(), full.q_rope.tolist()))     # every query row appears once
+        got_q = {key: [] for key in ref}
+        for r in range(P):
+            sh = OL.hunyuan_scopes(lay, T, counts, token_range=(bounds[r], bounds[r + 1]), **kw)
+            for i, key in enumerate(zip(sh.kind, sh.scene)):
+                rows = seg(sh, i, 'q_src', 'cu_q')
+                got_q[key].append(rows)
+                assert seg(sh, i, 'q_rope', 'cu_q').tolist() == [rope_of[x] for x in rows.tolist()], key
+                for a in ('k_src', 'k_rope', 'k_move_a', 'k_move_b'):
+                    assert np.array_equal(seg(sh, i, a, 'cu_k'), seg(full, ref[key], a, 'cu_k')), (key, a)
+        for key, i in ref.items():
+            parts = got_q[key]
+            assert len(parts) >= 1 and (key[0] == 'v' or len(parts) == 1), key
+            assert np.array_equal(np.concatenate(parts), seg(full, i, 'q_src', 'cu_q')), key
+
+
 # ---------------------------------------------------------------------------------------------- RoPE
 def test_rope_matches_complex_multiplication():
     g = torch.Generator().manual_seed(0)
