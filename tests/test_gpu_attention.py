@@ -258,6 +258,13 @@ def test_scene_layer_rank_shares(name, P, per_seg):
         assert_close(got, ref, what=f'{name} rank {r} of {P}')
         # the same rows of the one-GPU layer (equal up to the order of a key split's partial sums)
         assert_close(ov[a:b].cpu(), fv[a:b].cpu(), what=f'rank {r} against the one-GPU layer')
+        # the reference's data flow (Q, K, V packed, varlen on packed rows, scatter) and the queries rotated on the
+        # attention kernel's load give the same rows
+        for kw in (dict(fused=False), dict(fused=True, rotate_q='load')):
+            ov2, ot2 = scene.scene_attention(plan, *g, mode='raw', **kw)
+            assert_close(ov2[a:b].cpu(), ov[a:b].cpu(), what=f'rank {r} {kw}')
+            assert_close(ot2.cpu(), ot.cpu(), what=f'rank {r} {kw} text')
+            del ov2, ot2
         tr = OL.text_ranges(case['counts'])
         for j, (lo, _) in enumerate(lay.ranges):
             t0, t1 = tr[j]
