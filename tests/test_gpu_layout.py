@@ -156,16 +156,20 @@ def test_layout_text_keys_in_place_random_layouts():
         _check_in_place(case, bool(rng.integers(2)))
 
 
-def _check_rank_share(case, adjacent, q_range, in_place):
+def _check_rank_share(case, adjacent, q_range, in_place, with_text=True):
     """one rank's share (q_range): each segment the rank runs holds the oracle's token_range segment (query rows and
     RoPE rows; key rows, RoPE and _move_shared rows, in the in-place order when the text keys are read in place), and
     every other segment is empty"""
     lay = SceneLayout(case['lengths'], halo=case['halo'], sides=case['sides'], extra=case['extra'])
-    plan = ScopePlan(lay, case['T'], case['counts'], case['Le'], case['scene_rope'], case['rope_lengths'], adjacent,
-                     True, DEV, moves=True, text_keys_in_place=in_place, q_range=q_range)
+    in_place = in_place and with_text
+    counts = case['counts'] if with_text else [0] * len(case['lengths'])
+    Le = case['Le'] if with_text else 0
+    plan = ScopePlan(lay, case['T'], counts if with_text else None, Le, case['scene_rope'], case['rope_lengths'],
+                     adjacent, with_text, DEV, moves=True, text_keys_in_place=in_place, q_range=q_range)
     olay = OL.SceneLayout(case['lengths'], case['halo'], case['sides'], case['extra'])
-    sc = OL.hunyuan_scopes(olay, case['T'], case['counts'], case['Le'], scene_rope=case['scene_rope'],
-                           rope_lengths=case['rope_lengths'], adjacent=adjacent, token_range=q_range)
+    sc = OL.hunyuan_scopes(olay, case['T'], counts, Le, scene_rope=case['scene_rope'],
+                           rope_lengths=case['rope_lengths'], adjacent=adjacent, with_text=with_text,
+                           token_range=q_range)
     torch.cuda.synchronize()
     T, n = case['T'], len(case['lengths'])
     names = ('q_src', 'q_rope', 'k_src', 'k_rope') + (('k_move_a', 'k_move_b') if adjacent else ())
@@ -173,14 +177,15 @@ def _check_rank_share(case, adjacent, q_range, in_place):
     ref = {a: np.asarray(getattr(sc, a)) for a in names}
     cu_q, cu_k, k_off, k_len, first = (getattr(plan, a).cpu().tolist()
                                        for a in ('cu_q', 'cu_k', 'k_off', 'k_len', 'seg_q_src'))
-    ran = {(2 * j + (kind == 't')): i for i, (kind, j) in enumerate(zip(sc.kind, sc.scene))}
-    assert plan.n_seg == 2 * n and plan.sum_q == int(sc.cu_q[-1])
-    for s in range(2 * n):
+    per = 2 if with_text else 1
+    ran = {(per * j + (kind == 't')): i for i, (kind, j) in enumerate(zip(sc.kind, sc.scene))}
+    assert plan.n_seg == per * n and plan.sum_q == int(sc.cu_q[-1])
+    for s in range(per * n):
         lq = cu_q[s + 1] - cu_q[s]
         if s not in ran:
             assert lq == 0 and k_len[s] == 0 and cu_k[s + 1] == cu_k[s], s
             continue
-        i, j = ran[s], s // 2
+        i, j = ran[s], s // per
         qa, qb, ka, kb = sc.cu_q[i], sc.cu_q[i + 1], sc.cu_k[i], sc.cu_k[i + 1]
         assert lq == qb - qa and k_len[s] == kb - ka, s
         assert qb == qa or first[s] == ref['q_src'][qa], s
@@ -188,7 +193,7 @@ def _check_rank_share(case, adjacent, q_range, in_place):
             assert np.array_equal(got[a][cu_q[s]:cu_q[s + 1]], ref[a][qa:qb]), (s, a)
         order = np.arange(ka, kb)
         if in_place and s % 2 == 0:   # own frames, sentence, shared frames
-            own, txt = len(lay.frames[j]) * T, case['counts'][j]
+            own, txt = len(lay.frames[j]) * T, counts[j]
             order = np.r_[ka:ka + own, kb - txt:kb, ka + own:kb - txt]
         if in_place and s % 2 == 1:
             assert cu_k[s + 1] == cu_k[s] and k_off[s] == cu_k[s - 1], s
@@ -230,7 +235,8 @@ def test_layout_rank_shares_random_layouts():
         case['Le'] = sum(case['counts']) + int(rng.integers(0, 3))
         S = F * case['T']
         a = int(rng.integers(0, S))
-        _check_rank_share(case, bool(rng.integers(2)), (a, int(rng.integers(a + 1, S + 1))), bool(rng.integers(2)))
+        _check_rank_share(case, bool(rng.integers(2)), (a, int(rng.integers(a + 1, S + 1))), bool(rng.integers(2)),
+                          with_text=bool(rng.integers(2)))
 
 
 def _tables(case):
