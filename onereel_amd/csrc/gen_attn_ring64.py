@@ -25,8 +25,10 @@ Schedule of iteration j (32 keys; R-slot rings of K and V blocks in LDS, 8 KiB p
     mid      wait until this wavefront's loads of K(j+2), V(j) have landed, barrier; DMA of K(j+R) into slot j % R and
              of V(j+R-2) into slot (j-2) % R (both consumed by iteration j-1) goes out during phase B
     phase B  steps k = 4..7, P(j) of query block 1, and the LDS operands of steps 0..3 of iteration j+1
-    tail     if a row-half sum of P(j) exceeds 2^20 (or is not finite): out-of-line rescale (m moves up by the block
-             max d, O and l scale by 2^(-c d), S(j), S(j+1) and -m shift by -d, P(j) recomputed); then l += row sums
+    tail     if the lane's two row-half sums of P(j) (one per query block) add up to more than 2^20 (or are not
+             finite): out-of-line rescale (per query block, m moves up by d = max(block max, 0), O and l scale by
+             2^(-c d), S(j), S(j+1) and -m shift by -d, P(j) recomputed); then l += row sums. One compare of the sum
+             instead of one per query block leaves the scalar branch a single VALU result to wait for
 Within a phase the eight S MFMAs go before the eight PV MFMAs, and the side work (softmax VALU, LDS reads, DMA) is
 spread between them in proportion to its issue cost (SIDE_COST).
 The running max starts at block 0's own maximum (prologue), so row sums never underflow and m only moves up.
@@ -404,10 +406,10 @@ class Kernel:
         e.raw(f's_waitcnt vmcnt({4 * (R - 3)})')
         e.raw('s_barrier')
         phase([4, 5, 6, 7], self.softmax(par, 1), reads(ks_next, vs_next, range(4)), self.dma_ops(J))
-        # rescale check, row sums
-        e.valu(f'v_cmp_nge_f32_e32 vcc, s{SRR}, v{LS0}', [v(LS0)])
-        e.valu(f'v_cmp_nge_f32_e64 s[{SX}:{SX + 1}], s{SRR}, v{LS0 + 1}', [v(LS0 + 1)])
-        e.raw(f's_or_b64 vcc, vcc, s[{SX}:{SX + 1}]')
+        # rescale check on the sum of the lane's two row-half sums (a sum over 2^20, or not finite, rescales both
+        # query blocks; one with no new maximum keeps its m), then the row sums
+        e.valu(f'v_add_f32_e32 v{TT}, v{LS0}, v{LS0 + 1}', [v(LS0), v(LS0 + 1)], [v(TT)])
+        e.valu(f'v_cmp_nge_f32_e32 vcc, s{SRR}, v{TT}', [v(TT)])
         e.raw(f's_getpc_b64 s[{SRA}:{SRA + 1}]')
         e.raw(f's_cbranch_vccnz .Lrescale{par}_%=')
         e.valu(f'v_add_f32_e32 v{LSUM0}, v{LSUM0}, v{LS0}', [v(LSUM0), v(LS0)], [v(LSUM0)])
