@@ -29,6 +29,9 @@ Schedule of iteration j (32 keys; R-slot rings of K and V blocks in LDS, 8 KiB p
              finite): out-of-line rescale (per query block, m moves up by d = max(block max, 0), O and l scale by
              2^(-c d), S(j), S(j+1) and -m shift by -d, P(j) recomputed); then l += row sums. One compare of the sum
              instead of one per query block leaves the scalar branch a single VALU result to wait for
+    end      one scalar branch, taken at j + 1 >= nb - 1: out of line, either the loop's exit or the mask of the last
+             block's scores (keys past the segment -> -inf) before the last iteration. Each branch of an iteration
+             costs the MFMA pipe: a separate mask check at the iteration's start made the kernel 1.3% slower
 Within a phase the eight S MFMAs go before the eight PV MFMAs, and the side work (softmax VALU, LDS reads, DMA) is
 spread between them in proportion to its issue cost (SIDE_COST).
 The running max starts at block 0's own maximum (prologue), so row sums never underflow and m only moves up.
@@ -340,8 +343,6 @@ class Kernel:
         read half an iteration ahead, so each phase starts with one lgkmcnt(0) and its MFMAs wait for nothing else."""
         R = self.R
         par, npar = J & 1, (J & 1) ^ 1
-        e.raw(f's_cmp_eq_u32 s{SJ}, s{SNB1}')
-        e.raw(f's_cbranch_scc1 .Lmask{J}_%=')
         e.label(f'.Lmaskret{J}_%=')
         ks_now, vs_now = (J + 1) % R, (J - 1) % R          # slots of K(j+1), V(j-1)
         ks_next, vs_next = (J + 2) % R, J % R               # slots of K(j+2), V(j)
@@ -414,9 +415,16 @@ class Kernel:
         e.raw(f's_cbranch_vccnz .Lrescale{par}_%=')
         e.valu(f'v_add_f32_e32 v{LSUM0}, v{LSUM0}, v{LS0}', [v(LSUM0), v(LS0)], [v(LSUM0)])
         e.valu(f'v_add_f32_e32 v{LSUM0 + 1}, v{LSUM0 + 1}, v{LS0 + 1}', [v(LSUM0 + 1), v(LS0 + 1)], [v(LSUM0 + 1)])
+        # one branch per iteration for the loop's end and the last block's mask: at j + 1 >= nb - 1 the out-of-line
+        # code either leaves the loop or masks S(nb - 1) before the last iteration
         e.raw(f's_add_u32 s{SJ}, s{SJ}, 1')
-        e.raw(f's_cmp_ge_u32 s{SJ}, %[nb]')
-        e.raw(f's_cbranch_scc1 .Lexit{J}_%=')
+        e.raw(f's_cmp_ge_u32 s{SJ}, s{SNB1}')
+        e.raw(f's_cbranch_scc1 .Lend{J}_%=')
+
+    def end_block(self, J):
+        """after iteration J with j + 1 >= nb - 1: leave the loop when j + 1 = nb, else mask the last block first"""
+        return [f'.Lend{J}_%=:', f's_cmp_ge_u32 s{SJ}, %[nb]', f's_cbranch_scc1 .Lexit{J}_%=',
+                f's_branch .Lmask{(J + 1) % self.R}_%=']
 
     def mask_block(self, J):
         e = Emitter()
@@ -641,6 +649,8 @@ class Kernel:
         lines = pro_lines + e2.lines
         for J in range(R):
             lines += [f'.Lexit{J}_%=:', f's_mov_b32 s{SVOFF}, {J * SLOT}', f's_branch .Lepi{J & 1}_%=']
+        for J in range(R):
+            lines += self.end_block(J)
         for J in range(R):
             lines += self.mask_block(J)
         for par in range(2):
