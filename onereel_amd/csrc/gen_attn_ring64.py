@@ -27,8 +27,9 @@ Schedule of iteration j (32 keys; R-slot rings of K and V blocks in LDS, 8 KiB p
     phase B  steps k = 4..7, P(j) of query block 1, and the LDS operands of steps 0..3 of iteration j+1
     tail     if the lane's two row-half sums of P(j) (one per query block) add up to more than 2^20 (or are not
              finite): out-of-line rescale (per query block, m moves up by d = max(block max, 0), O and l scale by
-             2^(-c d), S(j), S(j+1) and -m shift by -d, P(j) recomputed); then l += row sums. One compare of the sum
-             instead of one per query block leaves the scalar branch a single VALU result to wait for
+             2^(-c d), S(j), S(j+1) and -m shift by -d, P(j) recomputed). One compare of the sum instead of one
+             per query block leaves the scalar branch a single VALU result to wait for, and the loop's end test
+             fills that wait; then l += row sums
     end      one scalar branch, taken at j + 1 >= nb - 1: out of line, either the loop's exit or the mask of the last
              block's scores (keys past the segment -> -inf) before the last iteration. Each branch of an iteration
              costs the MFMA pipe: a separate mask check at the iteration's start made the kernel 1.3% slower
@@ -411,14 +412,15 @@ class Kernel:
         # query blocks; one with no new maximum keeps its m), then the row sums
         e.valu(f'v_add_f32_e32 v{TT}, v{LS0}, v{LS0 + 1}', [v(LS0), v(LS0 + 1)], [v(TT)])
         e.valu(f'v_cmp_nge_f32_e32 vcc, s{SRR}, v{TT}', [v(TT)])
+        # the loop's end test fills the wait for the compare (the rescale block sets SCC again before it returns)
+        e.raw(f's_add_u32 s{SJ}, s{SJ}, 1')
+        e.raw(f's_cmp_ge_u32 s{SJ}, s{SNB1}')
         e.raw(f's_getpc_b64 s[{SRA}:{SRA + 1}]')
         e.raw(f's_cbranch_vccnz .Lrescale{par}_%=')
         e.valu(f'v_add_f32_e32 v{LSUM0}, v{LSUM0}, v{LS0}', [v(LSUM0), v(LS0)], [v(LSUM0)])
         e.valu(f'v_add_f32_e32 v{LSUM0 + 1}, v{LSUM0 + 1}, v{LS0 + 1}', [v(LSUM0 + 1), v(LS0 + 1)], [v(LSUM0 + 1)])
         # one branch per iteration for the loop's end and the last block's mask: at j + 1 >= nb - 1 the out-of-line
         # code either leaves the loop or masks S(nb - 1) before the last iteration
-        e.raw(f's_add_u32 s{SJ}, s{SJ}, 1')
-        e.raw(f's_cmp_ge_u32 s{SJ}, s{SNB1}')
         e.raw(f's_cbranch_scc1 .Lend{J}_%=')
 
     def end_block(self, J):
@@ -467,6 +469,7 @@ class Kernel:
         e.nop_to(2)
         e.raw(f's_add_u32 s{SRA}, s{SRA}, 4')
         e.raw(f's_addc_u32 s{SRA + 1}, s{SRA + 1}, 0')
+        e.raw(f's_cmp_ge_u32 s{SJ}, s{SNB1}')        # the iteration's end test, for the branch after the return
         e.raw(f's_setpc_b64 s[{SRA}:{SRA + 1}]')
         return e.lines
 
