@@ -252,16 +252,32 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(const int32_t* cu_q,
   }
 }
 
-// next work item of a block (thread 0 calls it): from the queue of the block's XCD (read from HW_REG_XCC_ID), then
-// from the others in turn; -1 when every queue is empty. A queue's counter is read before the atomic so that
-// exhausted queues are not incremented further.
-__device__ inline int next_item(int32_t* ws, int xcc) {
+// Item count and first item of every queue, as the planner wrote them (constant while the kernel runs), copied to
+// LDS once per block so that a claim takes one memory round trip: the atomic on the queue's counter.
+struct QueueInfo {
+  int n[kQueues], first[kQueues];
+};
+
+__device__ inline void load_queues(const int32_t* ws, QueueInfo* qi, int tid) {
+  if (tid < kQueues) {
+    qi->n[tid] = ws[kQueueWords * tid + 1];
+    qi->first[tid] = ws[kQueueWords * tid + 2];
+  }
+}
+
+// next work item of a block (thread 0 calls it): from the queue of the block's XCD (read from HW_REG_XCC_ID) with one
+// atomic, then from the others in turn; -1 when every queue is empty. Another XCD's counter is read before its atomic
+// so that exhausted queues are not incremented further; the block's own queue is taken directly (a counter past the
+// count only reads as empty).
+__device__ inline int next_item(int32_t* ws, int xcc, const QueueInfo* qi) {
   for (int r = 0; r < kQueues; ++r) {
-    int32_t* hq = ws + kQueueWords * ((xcc + r) & (kQueues - 1));
-    const int n = hq[1];
-    if (__hip_atomic_load(hq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= n) continue;
+    const int q = (xcc + r) & (kQueues - 1);
+    const int n = qi->n[q];
+    if (n <= 0) continue;
+    int32_t* hq = ws + kQueueWords * q;
+    if (r > 0 && __hip_atomic_load(hq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= n) continue;
     const int x = atomicAdd(hq, 1);
-    if (x < n) return hq[2] + x;
+    if (x < n) return qi->first[q] + x;
   }
   return -1;
 }
@@ -503,6 +519,7 @@ void attn4_kernel(AttnArgs a, int32_t* ws) {
   __shared__ __attribute__((aligned(16))) uint16_t k0[C::SLOT], k1[C::SLOT], k2[C::SLOT], k3[C::SLOT];
   __shared__ __attribute__((aligned(16))) uint16_t v0[C::SLOT], v1[C::SLOT], v2[C::SLOT], v3[C::SLOT];
   __shared__ int item_sh;
+  __shared__ QueueInfo qinfo;
   const Ring rg = {{k0, k1, k2, k3}, {v0, v1, v2, v3}};
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -533,10 +550,12 @@ void attn4_kernel(AttnArgs a, int32_t* ws) {
   }
 
   const int xcc = xcc_id();
+  load_queues(ws, &qinfo, tid);
+  __syncthreads();
   for (;;) {
-    if (tid == 0) item_sh = next_item(ws, xcc);
+    if (tid == 0) item_sh = next_item(ws, xcc, &qinfo);
     __syncthreads();
-    const int it = item_sh;
+    const int it = __builtin_amdgcn_readfirstlane(item_sh);
     __syncthreads();
     if (it < 0) break;
     const int4 r0 = *(const int4*)(ws + kWsHeader + kItemWords * it);
@@ -659,6 +678,7 @@ void attn8_kernel(AttnArgs a, int32_t* ws) {
   constexpr int D = 128, CH = 16, KS = 8, WQ = 64, BQ = 4 * WQ;
   __shared__ __attribute__((aligned(1024))) uint16_t ring[2 * kRing64 * kSlot64];
   __shared__ int item_sh;
+  __shared__ QueueInfo qinfo;
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31, h = lane >> 5;
@@ -685,10 +705,12 @@ void attn8_kernel(AttnArgs a, int32_t* ws) {
   }
 
   const int xcc = xcc_id();
+  load_queues(ws, &qinfo, tid);
+  __syncthreads();
   for (;;) {
-    if (tid == 0) item_sh = next_item(ws, xcc);
+    if (tid == 0) item_sh = next_item(ws, xcc, &qinfo);
     __syncthreads();
-    const int it = item_sh;
+    const int it = __builtin_amdgcn_readfirstlane(item_sh);
     __syncthreads();
     if (it < 0) break;
     const int4 r0 = *(const int4*)(ws + kWsHeader + kItemWords * it);
