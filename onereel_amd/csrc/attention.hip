@@ -258,6 +258,18 @@ struct QueueInfo {
   int n[kQueues], first[kQueues];
 };
 
+// the record of item `it`, read through the constant address space: the planner writes the records before the
+// attention kernel starts and nothing writes them while it runs, and `it` is wave-uniform, so they load with scalar
+// loads (counted by lgkmcnt: a record does not wait behind earlier O stores in the in-order vmcnt)
+typedef __attribute__((address_space(4))) const int ItemWord;
+struct ItemRec {
+  int4 r0, r1;
+};
+__device__ inline ItemRec item_record(const int32_t* ws, int it) {
+  const ItemWord* x = (const ItemWord*)(ws + kWsHeader + kItemWords * it);
+  return ItemRec{make_int4(x[0], x[1], x[2], x[3]), make_int4(x[4], x[5], x[6], x[7])};
+}
+
 __device__ inline void load_queues(const int32_t* ws, QueueInfo* qi, int tid) {
   if (tid < kQueues) {
     qi->n[tid] = ws[kQueueWords * tid + 1];
@@ -667,8 +679,10 @@ void attn4_kernel(AttnArgs a, int32_t* ws) {
 // live in AGPRs for the whole key loop, which is generated inline asm (gen_attn_ring64.py -> attn_ring64.inc): K and
 // V blocks of 32 keys stream through rings of ONEREEL_RING64 LDS slots each, the barrier sits in the middle of an
 // iteration so that the next iteration's operands are read during this one's MFMAs, and the epilogue normalises O and
-// stores it (rows past the segment masked off). The item queue, the first two K blocks of an item, the Q load
-// (with RoPE) and the lse store are C++.
+// stores it (rows past the segment masked off). Q sits in a128..a191: at its loop's exit, where Q is no longer read,
+// an item loads the next item's queries there ahead of its O stores (the block claims one item ahead), so that the
+// next item does not wait for the stores to drain before its Q lands. The item queue, the first two K blocks of an
+// item, the first item's Q load (and any Q rotated on the load) and the lse store are C++.
 
 constexpr int kRing64 = ONEREEL_RING64;
 constexpr int kSlot64 = kBKB * 128;   // bf16 elements per slot
@@ -704,17 +718,19 @@ void attn8_kernel(AttnArgs a, int32_t* ws) {
     voff[2 + n] = (uint32_t)(row * rs * 2 + (phys ^ swz4_v<CH>(row)) * 16);
   }
 
+  // The block claims its next item before running the current one, so that the current item's key loop can load the
+  // next item's queries at its exit (into a128..a191, ahead of its O stores); have_q says they are there.
   const int xcc = xcc_id();
   load_queues(ws, &qinfo, tid);
   __syncthreads();
-  for (;;) {
-    if (tid == 0) item_sh = next_item(ws, xcc, &qinfo);
-    __syncthreads();
-    const int it = __builtin_amdgcn_readfirstlane(item_sh);
-    __syncthreads();
-    if (it < 0) break;
-    const int4 r0 = *(const int4*)(ws + kWsHeader + kItemWords * it);
-    const int4 r1 = *(const int4*)(ws + kWsHeader + kItemWords * it + 4);
+  if (tid == 0) item_sh = next_item(ws, xcc, &qinfo);
+  __syncthreads();
+  int it = __builtin_amdgcn_readfirstlane(item_sh);
+  __syncthreads();
+  bool have_q = false;
+  while (it >= 0) {
+    const ItemRec rec = item_record(ws, it);
+    const int4 r0 = rec.r0, r1 = rec.r1;
     const int head = r0.x & 255, qt = r0.x >> 8, part = r0.y & 255, ways = r0.y >> 8, sidx = r0.z;
     const int q_beg = r0.w, Lq = r1.x, q_src0 = r1.y;
     int k_beg = r1.z, Lk = r1.w;
@@ -743,10 +759,17 @@ void attn8_kernel(AttnArgs a, int32_t* ws) {
       dma_block<2>(vaddr, 0, voff + 2, vring + (kRing64 - 1) * kSlot64 * 2);
     }
 
-    // Q operands and output rows. Rows past the segment get zero queries: their scores are 0 and their outputs are
-    // not stored, and zero operands cost the MFMA unit less power than real data (the GPU is power-limited here).
-    bf16x8 q[2][KS];
-    uint64_t op[2];
+    // the next item
+    if (tid == 0) item_sh = next_item(ws, xcc, &qinfo);
+    __syncthreads();
+    const int nit = __builtin_amdgcn_readfirstlane(item_sh);
+    __syncthreads();
+    const ItemRec nrec = item_record(ws, max(nit, 0));
+    const int4 n0 = nrec.r0, n1 = nrec.r1;
+
+    // Q operands (unless the previous item's key loop loaded them) and output rows. Rows past the segment take the
+    // queries of the segment's last row (the key loop's loads are unconditional); their outputs are not stored.
+    uint64_t op[2], qa[2], qc[2];
     int ok[2];
 #pragma unroll
     for (int qb = 0; qb < 2; ++qb) {
@@ -755,21 +778,36 @@ void attn8_kernel(AttnArgs a, int32_t* ws) {
       const int i = min(i0, Lq - 1);
       const int64_t row = q_src0 + (int64_t)i * a.qstep;
       const uint16_t* qp = (row < a.n_q_video ? a.q + row * a.qs : a.q_text + (row - a.n_q_video) * a.qs) + head * D;
-      int rr = live && a.q_rope ? a.q_rope[q_beg + i] : -1;
-      if (rr >= a.n_rope_rows) rr = -1;
+      qc[qb] = (uint64_t)(qp + 8 * h);
+      if (!have_q && a.q_rope) {
+        // rotated on the load (rows past the segment get zero queries)
+        int rr = live ? a.q_rope[q_beg + i] : -1;
+        if (rr >= a.n_rope_rows) rr = -1;
 #pragma unroll
-      for (int k = 0; k < KS; ++k) {
-        const int d = 16 * k + 8 * h;
-        u32x4 x = {0u, 0u, 0u, 0u};
-        if (live) x = *(const u32x4*)(qp + d);
-        if (rr >= 0) x = rotate8(x, a.cos_t, a.sin_t, (int64_t)rr * D + d, 1.0f);
-        q[qb][k] = as_bf16x8(x);
+        for (int k = 0; k < KS; ++k) {
+          const int d = 16 * k + 8 * h;
+          u32x4 x = {0u, 0u, 0u, 0u};
+          if (live) x = *(const u32x4*)(qp + d);
+          if (rr >= 0) x = rotate8(x, a.cos_t, a.sin_t, (int64_t)rr * D + d, 1.0f);
+          ONEREEL_RING64_QSET_STEP(qb, k, x);
+        }
+      }
+      // the lane's query row of the next item (its last row past the end), or this one's when there is none
+      qa[qb] = qc[qb];
+      if (nit >= 0) {
+        const int nLq = n1.x;
+        const int ni = min((n0.x >> 8) * BQ + w * WQ + qb * 32 + l32, nLq - 1);
+        const int64_t nrow = n1.y + (int64_t)ni * a.qstep;
+        qa[qb] = (uint64_t)((nrow < a.n_q_video ? a.q + nrow * a.qs : a.q_text + (nrow - a.n_q_video) * a.qs) +
+                            (n0.x & 255) * D + 8 * h);
       }
       uint16_t* o = (row < a.n_q_video ? a.o + row * a.os : a.o_text + (row - a.n_q_video) * a.os) + head * D + 4 * h;
       // a split item's part writes O / l of its keys in fp32 to its partial rows instead
       op[qb] = part_o ? (uint64_t)(part_o + (w * WQ + qb * 32 + l32) * D + 4 * h) : (uint64_t)o;
       ok[qb] = live;
     }
+    if (!have_q && !a.q_rope)
+      asm volatile(ONEREEL_RING64_QLOAD :: [qa0] "v"(qc[0]), [qa1] "v"(qc[1]) : ONEREEL_RING64_QCLOBBERS);
     if (nb == 0) {
       // no keys: O = 0 and lse = -inf, as attn4_kernel
 #pragma unroll
@@ -782,6 +820,8 @@ void attn8_kernel(AttnArgs a, int32_t* ws) {
             for (int gg = 0; gg < 4; ++gg) *(uint2*)(o + db * 32 + 8 * gg) = make_uint2(0u, 0u);
           if (a.lse && h == 0) a.lse[(int64_t)head * a.sum_q + q_beg + q0 + qb * 32 + l32] = -__builtin_inff();
         }
+      have_q = false;
+      it = nit;
       continue;
     }
     const int valid = Lk - (nb - 1) * kBKB - 16 * h;
@@ -789,18 +829,17 @@ void attn8_kernel(AttnArgs a, int32_t* ws) {
     float mo0, mo1, lo0, lo1;   // per query: the running max of q k^T, and the row sum relative to it
     asm volatile(ONEREEL_RING64_ASM
                  : [mo0] "=&v"(mo0), [mo1] "=&v"(mo1), [lo0] "=&v"(lo0), [lo1] "=&v"(lo1)
-                 : [q00] "a"(q[0][0]), [q01] "a"(q[0][1]), [q02] "a"(q[0][2]), [q03] "a"(q[0][3]),
-                   [q04] "a"(q[0][4]), [q05] "a"(q[0][5]), [q06] "a"(q[0][6]), [q07] "a"(q[0][7]),
-                   [q10] "a"(q[1][0]), [q11] "a"(q[1][1]), [q12] "a"(q[1][2]), [q13] "a"(q[1][3]),
-                   [q14] "a"(q[1][4]), [q15] "a"(q[1][5]), [q16] "a"(q[1][6]), [q17] "a"(q[1][7]),
-                   [c] "s"(a.c), [nb] "s"(nb), [valid] "v"(valid), [kb] "v"(kb), [vb] "v"(vb),
-                   [vk0] "v"(voff[0]), [vk1] "v"(voff[1]), [vv0] "v"(voff[2]), [vv1] "v"(voff[3]),
+                 : [qa0] "v"(qa[0]), [qa1] "v"(qa[1]), [c] "s"(a.c), [nb] "s"(nb), [valid] "v"(valid), [kb] "v"(kb),
+                   [vb] "v"(vb), [vk0] "v"(voff[0]), [vk1] "v"(voff[1]), [vv0] "v"(voff[2]), [vv1] "v"(voff[3]),
                    [sbase] "s"(sbase), [bb] "s"(bb), [kb_lo] "s"((uint32_t)kaddr2), [kb_hi] "s"((uint32_t)(kaddr2 >> 32)),
                    [vb_lo] "s"((uint32_t)vaddr), [vb_hi] "s"((uint32_t)(vaddr >> 32)), [rem0] "s"(rem0), [remk] "s"(rem0 - 2 * bb),
                    [op0] "v"(op[0]), [op1] "v"(op[1]), [ok0] "v"(ok[0]), [ok1] "v"(ok[1]),
                    [f32] "s"(__builtin_amdgcn_readfirstlane(ways > 1 ? 1 : 0)),
                    [dead] "s"(__builtin_amdgcn_readfirstlane(q0 >= Lq ? 1 : 0))
                  : ONEREEL_RING64_CLOBBERS);
+    // the next item's queries are in a128..a191 unless they must be rotated on the load
+    have_q = nit >= 0 && !a.q_rope;
+    it = nit;
     if (ways <= 1) {
       if (a.lse && h == 0) {
         if (ok[0]) a.lse[(int64_t)head * a.sum_q + q_beg + q0 + l32] = mo0 * a.scale + logf(lo0);

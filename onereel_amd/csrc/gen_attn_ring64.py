@@ -9,15 +9,20 @@ does not keep such a split from source (it moves accumulators between the regist
 emitted here with fixed registers:
 
     a0..a127    O^T accumulators, acc(qb, db) = a[64 qb + 16 db : +15]
+    a128..a191  Q: k-step k of query block qb at a[128 + 32 qb + 4 k : +3], the MFMAs' B operand
     v36..v99    S, s(par, qb) = v[36 + 32 par + 16 qb : +15] (par = key block parity; S(j+1) fills while S(j) is read)
     v100..v131  P as bf16 pairs, p(par, qb, half) = v[100 + 16 par + 8 qb + 4 half : +3]
     v132..v163  K operands of the 8 k-steps, v164..v195 V^T operands of the 8 (half, db) steps
     v196..v227  -m per query block, broadcast over 16 registers: the first QK^T MFMA of a block accumulates onto it
     v228..v254  softmax temporaries, running max, row sums, LDS read addresses
     s64..s83    K and V buffer descriptors, their remaining byte counts, loop counters, return address
-Q comes in as 16 AGPR operands (the compiler places them above a127). S = q k^T - m comes out of the MFMAs (the
-first of each block accumulates onto -m), so P = 2^(c S), c = scale * log2(e), takes one v_mul_f32 and one v_exp_f32
-per score: the fp32 scores of FlashAttention's exp2(s c - m c), with the subtraction folded into the accumulator.
+The kernel puts Q into a128..a191 before the block (ONEREEL_RING64_QLOAD, or ONEREEL_RING64_QSET_STEP for queries
+rotated on the load), or the previous item's block left it there: at its loop's exit, where Q is no longer read, a
+block loads the queries of the work-group's next item into those registers (%[qa0], %[qa1]: the lane's query rows of
+that item), so that these loads are not queued behind its O stores in the in-order vmcnt.
+S = q k^T - m comes out of the MFMAs (the first of each block accumulates onto -m), so P = 2^(c S), c = scale *
+log2(e), takes one v_mul_f32 and one v_exp_f32 per score: the fp32 scores of FlashAttention's exp2(s c - m c), with
+the subtraction folded into the accumulator.
 
 Schedule of iteration j (32 keys; R-slot rings of K and V blocks in LDS, 8 KiB per slot):
     phase A  MFMA steps k = 0..3: S(j+1) += K(j+1)_k Q_k^T for both query blocks, O += V(j-1)_k P(j-1)_k; the VALU
@@ -85,6 +90,10 @@ def MCV(qb):
 
 T0, A0, TT, LS0, M0, LSUM0, KADDR0, VADDR0 = 228, 232, 236, 237, 239, 241, 243, 251
 FIRST_FIXED = 36
+
+
+def QA(qb, k):
+    return 128 + 32 * qb + 4 * k
 
 
 def ACC(qb, db):
@@ -311,7 +320,8 @@ class Kernel:
         else:
             c = Sx(par_next, qb)
             reads = [vr(KOP(k), 4), vr(S(par_next, qb, 0), 16)]
-        e.mfma(Sx(par_next, qb), f'v[{KOP(k)}:{KOP(k) + 3}]', f'%[q{qb}{k}]', c, [vr(S(par_next, qb, 0), 16)], reads)
+        e.mfma(Sx(par_next, qb), f'v[{KOP(k)}:{KOP(k) + 3}]', f'a[{QA(qb, k)}:{QA(qb, k) + 3}]', c,
+               [vr(S(par_next, qb, 0), 16)], reads)
 
     def mfma_pv(self, e, par_prev, qb, k):
         half, db = divmod(k, 4)
@@ -473,12 +483,21 @@ class Kernel:
         e.raw(f's_setpc_b64 s[{SRA}:{SRA + 1}]')
         return e.lines
 
+    @staticmethod
+    def q_prefetch():
+        """the next item's queries into a128..a191: issued at the loop's exit, where Q is no longer read and before
+        the O stores, which are then the last 16 ... 48 vector memory operations of the block"""
+        return [f'global_load_dwordx4 a[{QA(qb, k)}:{QA(qb, k) + 3}], %[qa{qb}], off offset:{32 * k}'
+                for qb in range(2) for k in range(8)]
+
     def epilogue(self, par):
-        """O += V(nb-1) P(nb-1): steps 0..3 were prefetched by the last iteration, steps 4..7 are read from the slot
-        whose byte offset is in s77"""
+        """the next item's Q loads, then O += V(nb-1) P(nb-1): steps 0..3 were prefetched by the last iteration,
+        steps 4..7 are read from the slot whose byte offset is in s77"""
         e = Emitter()
         e.lds = self._regs_prefetch()
         e.label(f'.Lepi{par}_%=')
+        for line in self.q_prefetch():
+            e.raw(line)
         for db in range(4):
             e.raw(f'v_add_u32_e32 v{T0 + db}, s{SVOFF}, v{VADDR0 + db}')
         for k in range(4, 8):
@@ -499,12 +518,13 @@ class Kernel:
 
     def store_block(self):
         """O / l to the output rows (rows past the segment masked off): bf16, or fp32 when %[f32] is non-zero (the
-        partial results of a work item split by keys); 16 wait states after the last MFMA. Temporaries live in the
-        S registers, which are dead here."""
+        partial results of a work item split by keys); 16 wait states after the last MFMA. The ring's last loads
+        have landed before the stores (the next item's 16 Q loads, issued after them, may still be in flight).
+        Temporaries live in the S registers, which are dead here."""
         e = Emitter()
         e.label('.Lstore_%=')
         e.nop_to(16)
-        e.raw('s_waitcnt vmcnt(0) lgkmcnt(0)')
+        e.raw('s_waitcnt vmcnt(16) lgkmcnt(0)')
         x = [S(0, 0, i) for i in (0, 1, 2, 4, 5, 6, 7)]   # v[40:41] is the even-aligned store pair
         for qb in range(2):
             e.valu(f'v_mov_b32_e32 v{x[0]}, v{LSUM0 + qb}', [v(LSUM0 + qb)], [v(x[0])])
@@ -609,7 +629,8 @@ class Kernel:
     def dead_loop(self):
         """the key loop of a wavefront without live queries: per iteration only the barrier and its share of the
         K/V refill, the same as a body's, so that the block's barriers and LDS DMA stay in step; no MFMA, softmax or
-        LDS read. Exits to the end of the asm block once every DMA has landed (no output is written)."""
+        LDS read. Exits to the end of the asm block once every DMA has landed, with the next item's Q loads issued
+        (no output is written)."""
         R = self.R
         lines = ['.Ldead_%=:']
         for J in range(R):
@@ -620,7 +641,8 @@ class Kernel:
                 if op[0] == 'm0':
                     lines.append('s_nop 0')          # an SALU write of M0 and the LDS DMA reading it
             lines += [f's_add_u32 s{SJ}, s{SJ}, 1', f's_cmp_ge_u32 s{SJ}, %[nb]', 's_cbranch_scc1 .Ldeadexit_%=']
-        lines += ['s_branch .Ldead_%=', '.Ldeadexit_%=:', 's_waitcnt vmcnt(0)', 's_branch .Ldone_%=']
+        lines += ['s_branch .Ldead_%=', '.Ldeadexit_%=:'] + self.q_prefetch()
+        lines += ['s_waitcnt vmcnt(16)', 's_branch .Ldone_%=']
         return lines
 
     def generate(self):
@@ -670,14 +692,37 @@ def render(ring):
     k = Kernel(ring)
     lines = k.generate()
     body = '\n'.join(f'  "{l}\\n\\t"' if not l.endswith(':') else f'  "{l}\\n"' for l in lines)
-    clob = ', '.join(f'"v{i}"' for i in range(FIRST_FIXED, 256)) + ', ' + ', '.join(f'"a{i}"' for i in range(128))
+    clob = ', '.join(f'"v{i}"' for i in range(FIRST_FIXED, 256)) + ', ' + ', '.join(f'"a{i}"' for i in range(192))
     clob += ', ' + ', '.join(f'"s{i}"' for i in range(64, 84)) + ', "vcc", "scc", "memory"'
+    qload = ' \\\n  '.join(f'"{l}\\n\\t"' for l in Kernel.q_prefetch())
+    qclob = ', '.join(f'"a{i}"' for i in range(128, 192))
+    cases = []
+    for qb in range(2):
+        for k in range(8):
+            # the first step waits until earlier loads into these registers (a key loop's exit) have landed
+            w = 's_waitcnt vmcnt(0)\\n\\t' if qb == k == 0 else ''
+            w += ''.join(f'v_accvgpr_write_b32 a{QA(qb, k) + i}, %{i}\\n\\t' for i in range(4))
+            cl = ', '.join(f'"a{QA(qb, k) + i}"' for i in range(4))
+            cases.append(f'case {8 * qb + k}: asm volatile("{w}" :: "v"((x)[0]), "v"((x)[1]), "v"((x)[2]), '
+                         f'"v"((x)[3]) : {cl}); break;')
+    qset = ' \\\n    '.join(cases)
     hdr = f'''// Generated by gen_attn_ring64.py (ring of {ring} K and {ring} V slots): do not edit.
 // The key loop of attn8_kernel; operands and fixed registers are described in the generator.
 #define ONEREEL_RING64 {ring}
 #define ONEREEL_RING64_ASM \\
 {body.replace(chr(10), " " + chr(92) + chr(10))}
 #define ONEREEL_RING64_CLOBBERS {clob}
+// an item's queries into the key loop's registers a128..a191 (query block qb, k-step k at a[128 + 32 qb + 4 k : +3]):
+// loaded from the lane's two rows (%[qa0], %[qa1]), or written from four dwords x[0..3] per (qb, k) (qb and k
+// compile-time constants)
+#define ONEREEL_RING64_QLOAD {qload}
+#define ONEREEL_RING64_QCLOBBERS {qclob}
+#define ONEREEL_RING64_QSET_STEP(qb, k, x) \\
+  do {{ \\
+    switch (8 * (qb) + (k)) {{ \\
+    {qset} \\
+    }} \\
+  }} while (0)
 '''
     return hdr
 
