@@ -749,6 +749,9 @@ void attn8_kernel(AttnArgs a, int32_t* ws) {
     const int32_t rb = (int32_t)rs * 2;
     const int32_t rem0 = Lk * rb - rb + D * 2;
     const int32_t bb = kBKB * rb;
+    // every wavefront is done with the previous item's ring: a wavefront without live queries leaves its key loop
+    // while the others' epilogues still read the last V block, and its refill below would overwrite a slot
+    __syncthreads();
     if (nb > 0) {
       // the head of the ring, ahead of the Q loads so that both latencies overlap: K blocks 0 and 1 into slots 0
       // and 1, and zeros (record count 0) into the last V slot, the V operand of the key loop's first PV step; the

@@ -126,6 +126,37 @@ def test_varlen_random_shapes():
             assert (lse[:, cq[s]:cq[s + 1]].cpu() - lref).abs().max() < 2e-3
 
 
+def test_varlen_many_items_per_block():
+    """several work items per work-group (~2.8 per CU at 256 CUs), so that each item's key loop loads the next
+    item's queries at its exit: segments without keys (items with no key loop) and without queries between them,
+    O and lse against the fp32 oracle over every row"""
+    rng = np.random.default_rng(77)
+    n, H, D = 30, 8, 128
+    lq = rng.integers(1, 1500, n).tolist()
+    lk = rng.integers(1, 700, n).tolist()
+    for s in (3, 4, 11, 20):
+        lk[s] = 0
+    for s in (7, 21):
+        lq[s] = 0
+    print(f'varlen many items: lq={lq} lk={lk} H={H}', flush=True)
+    q, k, v, cq, ck = _segments_case(lq, lk, H, D, 300)
+    args = (q.to(DEV), k.to(DEV), v.to(DEV), torch.tensor(cq, dtype=torch.int32, device=DEV),
+            torch.tensor(ck, dtype=torch.int32, device=DEV), max(lq), max(lk))
+    ref = OA.packed_attention(q, k, v, cq, ck)
+    assert_close(A.varlen(*args).cpu(), ref, what='varlen, many items per block')
+    o, lse = A.varlen_lse(*args)
+    assert_close(o.cpu(), ref, what='varlen_lse, many items per block')
+    for s in range(n):
+        if lq[s] == 0:
+            continue
+        if lk[s] == 0:
+            assert torch.isneginf(lse[:, cq[s]:cq[s + 1]].cpu()).all()
+            continue
+        qs, ks = q[cq[s]:cq[s + 1]].float(), k[ck[s]:ck[s + 1]].float()
+        lref = torch.logsumexp(torch.einsum('qhd,khd->hqk', qs, ks) * D ** -0.5, -1)
+        assert (lse[:, cq[s]:cq[s + 1]].cpu() - lref).abs().max() < 2e-3
+
+
 def test_key_split_of_overlapping_ranges():
     """Wan-style in-place key ranges with few work items (3 scenes x 400 tokens per frame, 2 heads): the split parts
     take their key blocks from inside each scene's range"""
