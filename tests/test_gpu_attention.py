@@ -143,7 +143,12 @@ def test_varlen_many_items_per_block():
     args = (q.to(DEV), k.to(DEV), v.to(DEV), torch.tensor(cq, dtype=torch.int32, device=DEV),
             torch.tensor(ck, dtype=torch.int32, device=DEV), max(lq), max(lk))
     ref = OA.packed_attention(q, k, v, cq, ck)
-    assert_close(A.varlen(*args).cpu(), ref, what='varlen, many items per block')
+    o = A.varlen(*args)
+    assert_close(o.cpu(), ref, what='varlen, many items per block')
+    # each item's result does not depend on which work-group ran it or when: repeated calls are bit-identical (a
+    # race between the wavefronts of a work-group, or between items, would show as a difference)
+    for _ in range(3):
+        assert torch.equal(A.varlen(*args), o)
     o, lse = A.varlen_lse(*args)
     assert_close(o.cpu(), ref, what='varlen_lse, many items per block')
     for s in range(n):
@@ -254,6 +259,24 @@ def test_scene_layer_matches_oracle(name, per_seg, rotate_q, in_place, adjacent)
     valid = sum(case['counts'])
     if case['Le'] > valid:
         assert ot[valid:].abs().max().item() == 0
+
+
+@pytest.mark.parametrize('rotate_q', ['pre', 'load'])
+def test_scene_layer_repeatable_at_480p(rotate_q):
+    """the full 480p layer (3264 work items, ~13 per work-group, partly filled query tiles with idle wavefronts)
+    run four times: every output bit-identical, so no item's result depends on scheduling (a race between the
+    wavefronts of a work-group, or between consecutive items of one, would show as a difference)"""
+    case = layout_case('hunyuan480p')
+    print(f'layer hunyuan480p repeatability rotate_q={rotate_q}', flush=True)
+    g = [x.to(DEV) for x in _layer_inputs(case)]
+    lay = SceneLayout(case['lengths'], halo=case['halo'], sides=case['sides'], extra=case['extra'])
+    plan = scene.ScopePlan(lay, case['T'], case['counts'], case['Le'], case['scene_rope'], None, True, True, DEV,
+                           text_keys_in_place=True)
+    ov, ot = scene.scene_attention(plan, *g[:6], g[6], g[7], mode='raw', fused=True, rotate_q=rotate_q)
+    assert torch.isfinite(ov).all() and torch.isfinite(ot).all()
+    for _ in range(3):
+        ov2, ot2 = scene.scene_attention(plan, *g[:6], g[6], g[7], mode='raw', fused=True, rotate_q=rotate_q)
+        assert torch.equal(ov2, ov) and torch.equal(ot2, ot)
 
 
 @pytest.mark.parametrize('name,P,per_seg', [('cpu_plumbing', 3, None), ('hunyuan480p', 3, 32),
