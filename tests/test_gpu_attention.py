@@ -262,6 +262,57 @@ def test_scene_layer_matches_oracle(name, per_seg, rotate_q, in_place, adjacent)
         assert ot[valid:].abs().max().item() == 0
 
 
+def _random_layer_case(rng):
+    """a random layout: 2-7 scenes of 1-6 frames, 160-1590 tokens per frame (a Hh x Ww grid), 1-200 text tokens
+    per scene, a halo of 0-1 frames or frame memory of up to 4 representatives, 4-12 heads of 128"""
+    K = int(rng.integers(2, 8))
+    lengths = rng.integers(1, 7, K).tolist()
+    F = sum(lengths)
+    Hh, Ww = int(rng.integers(8, 31)), int(rng.integers(20, 54))
+    counts = rng.integers(1, 201, K).tolist()
+    halo = int(rng.integers(0, 2))
+    sides = str(rng.choice(['adj', 'next', 'prev']))
+    extra = {}
+    if halo == 0 and F > 1:
+        lay = OL.SceneLayout(lengths, halo=0)
+        reps = sorted({int(x) for x in rng.choice(F, min(F, int(rng.integers(1, 5))), replace=False)})
+        fm = OL.FrameMemoryExtra(budget=4, fallback=(0, 'adj'))
+        fm.reset(lay)
+        fm.propose(reps)
+        fm.begin_step(1)
+        extra = lay.extra
+    return dict(lengths=lengths, halo=halo, sides=sides, extra=extra, T=Hh * Ww, counts=counts, Le=sum(counts) + 3,
+                H=int(rng.choice([4, 8, 12])), D=128, scene_rope=bool(rng.integers(2)), rope_lengths=None,
+                table=(F + 8, Hh, Ww))
+
+
+@pytest.mark.parametrize('seed', range(6))
+def test_scene_layer_random_layouts(seed):
+    """random layouts through the fused layer (query rotation ahead of the call or on the load, text keys in place
+    or packed, both shared-frame positions), 24 sampled rows per segment against the oracle, and a second call
+    bit-identical to the first"""
+    rng = np.random.default_rng(500 + seed)
+    case = _random_layer_case(rng)
+    adjacent, in_place = bool(rng.integers(2)), bool(rng.integers(2))
+    rotate_q = str(rng.choice(['pre', 'load']))
+    print(f'random layer {seed}: {case} adjacent={adjacent} in_place={in_place} rotate_q={rotate_q}', flush=True)
+    q, k, v, eq, ek, ev, cos, sin = _layer_inputs(case, seed=40 + seed)
+    lay = SceneLayout(case['lengths'], halo=case['halo'], sides=case['sides'], extra=case['extra'])
+    plan = scene.ScopePlan(lay, case['T'], case['counts'], case['Le'], case['scene_rope'], None, adjacent, True, DEV,
+                           text_keys_in_place=in_place)
+    g = [x.to(DEV) for x in (q, k, v, eq, ek, ev, cos, sin)]
+    ov, ot = scene.scene_attention(plan, *g[:6], g[6], g[7], mode='raw', fused=True, rotate_q=rotate_q)
+    ov2, ot2 = scene.scene_attention(plan, *g[:6], g[6], g[7], mode='raw', fused=True, rotate_q=rotate_q)
+    assert torch.equal(ov2, ov) and torch.equal(ot2, ot)
+    olay = OL.SceneLayout(case['lengths'], case['halo'], case['sides'], case['extra'])
+    sc = OL.hunyuan_scopes(olay, case['T'], case['counts'], case['Le'], scene_rope=case['scene_rope'],
+                           adjacent=adjacent)
+    rows = sample_rows(sc.cu_q, 24)
+    ref = scope_rows_reference(sc, q, k, v, eq, ek, ev, rows, cos, sin, mode='raw')
+    got = torch.cat([ov, ot]).cpu()[torch.as_tensor(sc.q_src[rows])]
+    assert_close(got, ref, what=f'random layer {seed}')
+
+
 @pytest.mark.parametrize('rotate_q', ['pre', 'load'])
 def test_scene_layer_repeatable_at_480p(rotate_q):
     """the full 480p layer (3264 work items, ~13 per work-group, partly filled query tiles with idle wavefronts)
