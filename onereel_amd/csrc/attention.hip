@@ -718,15 +718,25 @@ void attn8_kernel(AttnArgs a, int32_t* ws) {
     voff[2 + n] = (uint32_t)(row * rs * 2 + (phys ^ swz4_v<CH>(row)) * 16);
   }
 
-  // The block claims its next item before running the current one, so that the current item's key loop can load the
-  // next item's queries at its exit (into a128..a191, ahead of its O stores); have_q says they are there.
-  const int xcc = xcc_id();
+  // While its XCD's queue holds more than kAheadMin items, the block claims its next item before running the current
+  // one, so that the current item's key loop can load the next item's queries at its exit (into a128..a191, ahead of
+  // its O stores); have_q says they are there. Near the end of the queue it claims after each item, as a block that
+  // holds two items cannot take work that another block left: the last rounds stay balanced.
+  constexpr int kAheadMin = 64, kLater = -2;
+  const int xcc = xcc_id(), own = xcc & (kQueues - 1);
   load_queues(ws, &qinfo, tid);
   __syncthreads();
-  if (tid == 0) item_sh = next_item(ws, xcc, &qinfo);
-  __syncthreads();
-  int it = __builtin_amdgcn_readfirstlane(item_sh);
-  __syncthreads();
+  auto claim = [&](bool ahead) {
+    if (tid == 0) {
+      const int taken = __hip_atomic_load(ws + kQueueWords * own, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      item_sh = !ahead || qinfo.n[own] - taken > kAheadMin ? next_item(ws, xcc, &qinfo) : kLater;
+    }
+    __syncthreads();
+    const int x = __builtin_amdgcn_readfirstlane(item_sh);
+    __syncthreads();
+    return x;
+  };
+  int it = claim(false);
   bool have_q = false;
   while (it >= 0) {
     const ItemRec rec = item_record(ws, it);
@@ -762,11 +772,8 @@ void attn8_kernel(AttnArgs a, int32_t* ws) {
       dma_block<2>(vaddr, 0, voff + 2, vring + (kRing64 - 1) * kSlot64 * 2);
     }
 
-    // the next item
-    if (tid == 0) item_sh = next_item(ws, xcc, &qinfo);
-    __syncthreads();
-    const int nit = __builtin_amdgcn_readfirstlane(item_sh);
-    __syncthreads();
+    // the next item, now or (kLater) after this one
+    const int nit = claim(true);
     const ItemRec nrec = item_record(ws, max(nit, 0));
     const int4 n0 = nrec.r0, n1 = nrec.r1;
 
@@ -795,7 +802,7 @@ void attn8_kernel(AttnArgs a, int32_t* ws) {
           ONEREEL_RING64_QSET_STEP(qb, k, x);
         }
       }
-      // the lane's query row of the next item (its last row past the end), or this one's when there is none
+      // the lane's query row of the next item (its last row past the end), or this one's when it is not claimed yet
       qa[qb] = qc[qb];
       if (nit >= 0) {
         const int nLq = n1.x;
@@ -824,7 +831,7 @@ void attn8_kernel(AttnArgs a, int32_t* ws) {
           if (a.lse && h == 0) a.lse[(int64_t)head * a.sum_q + q_beg + q0 + qb * 32 + l32] = -__builtin_inff();
         }
       have_q = false;
-      it = nit;
+      it = nit == kLater ? claim(false) : nit;
       continue;
     }
     const int valid = Lk - (nb - 1) * kBKB - 16 * h;
@@ -842,7 +849,7 @@ void attn8_kernel(AttnArgs a, int32_t* ws) {
                  : ONEREEL_RING64_CLOBBERS);
     // the next item's queries are in a128..a191 unless they must be rotated on the load
     have_q = nit >= 0 && !a.q_rope;
-    it = nit;
+    it = nit == kLater ? claim(false) : nit;
     if (ways <= 1) {
       if (a.lse && h == 0) {
         if (ok[0]) a.lse[(int64_t)head * a.sum_q + q_beg + q0 + l32] = mo0 * a.scale + logf(lo0);
