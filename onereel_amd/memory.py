@@ -123,15 +123,16 @@ class BoundaryMemory:
 class Plan:
     """one layer's query pieces (the fields of memory.py:96-106), plus host copies of the sizes that the varlen call
     needs (filled by make_plan; a Plan built field by field gets them from one read of lens / qlen)"""
-    qrows: torch.Tensor                  # [sum Q] query rows, piece after piece
-    qlen: torch.Tensor                   # [n] queries per piece
-    pad: torch.Tensor                    # [n, Lmax] local key rows per piece (padded)
-    pmask: torch.Tensor                  # [n, Lmax]
-    lens: torch.Tensor                   # [n] local keys per piece
-    scene: torch.Tensor                  # [n] scene of each piece
-    mem: torch.Tensor                    # [n] the piece reads the memory
-    cand: torch.Tensor                   # [B] key-buffer rows of the boundary candidates
-    owner: torch.Tensor                  # [B] their scene
+    # field names as memory.py:102-111 (make_plan's result); n pieces, B boundary candidates
+    qrows: torch.Tensor                  # [sum of qlen] the pieces' query rows, concatenated in piece order
+    qlen: torch.Tensor                   # [n] how many query rows each piece has
+    pad: torch.Tensor                    # [n, Lmax] each piece's own key rows, right-padded to the longest
+    pmask: torch.Tensor                  # [n, Lmax] True where pad holds a real row
+    lens: torch.Tensor                   # [n] how many own key rows each piece has
+    scene: torch.Tensor                  # [n] the scene a piece belongs to
+    mem: torch.Tensor                    # [n] whether a piece also attends to the other scenes' representatives
+    cand: torch.Tensor                   # [B] key rows that may be chosen as representatives
+    owner: torch.Tensor                  # [B] the scene each candidate row comes from
     host_qlen: list | None = None        # qlen on the host
     host_lens: list | None = None        # lens on the host
     q_first: list | None = None          # per piece its first query row when its rows are consecutive, else None
