@@ -337,8 +337,8 @@ def run_bounded_memory(args):
 
 def run_power(args):
     """board power and clocks while the headline layer's attention kernel runs back to back (about 8 s), then while
-    the bf16 GEMM reference does, sampled with amd-smi every ~0.25 s: whether each sits at the board's power limit
-    and at what clock. One JSON line: per phase the median socket power, the mean over samples of the XCDs' mean
+    the bf16 GEMM reference does, then the attention kernel again on operands with two mantissa bits, sampled with
+    amd-smi every ~0.25 s: whether each sits at the board's power limit and at what clock. One JSON line: per phase the median socket power, the mean over samples of the XCDs' mean
     clock, and the kernel's ms per call and TFLOP/s over the phase."""
     import statistics
     import subprocess
@@ -367,6 +367,13 @@ def run_power(args):
     attn = lambda: scene.varlen(qr, kp, vp, plan.cu_q, plan.cu_k, plan.max_q, plan.max_k, k_off=plan.k_off,
                                 k_len=plan.k_len, out=ov, seg_q_src=plan.seg_q_src, q_text=eq, o_text=ot,
                                 n_q_video=plan.n_video, sum_q=plan.sum_q, workspace=ws)
+    # the same call on operands with two mantissa bits (bf16 bits 4..0 cleared): the same FLOP and schedule, less
+    # MFMA switching power, so the rate it reaches at the board's limit shows how much power bounds the kernel
+    low = lambda x: (x.view(torch.int16) & -32).view(torch.bfloat16)
+    qr2, kp2, vp2, eq2 = low(qr), low(kp), low(vp), low(eq)
+    attn2 = lambda: scene.varlen(qr2, kp2, vp2, plan.cu_q, plan.cu_k, plan.max_q, plan.max_k, k_off=plan.k_off,
+                                 k_len=plan.k_len, out=ov, seg_q_src=plan.seg_q_src, q_text=eq2, o_text=ot,
+                                 n_q_video=plan.n_video, sum_q=plan.sum_q, workspace=ws)
     n_g = 16384
     a = torch.randn(n_g, n_g, generator=g, device=dev).to(torch.bfloat16)
     b = torch.randn(n_g, n_g, generator=g, device=dev).to(torch.bfloat16)
@@ -395,7 +402,8 @@ def run_power(args):
                unit='W', n_gpus=1, data='synthetic',
                config=dict(workload='hunyuan15-480p-4scene-attention-kernel-vs-gemm16384', sampler='amd-smi metric '
                            '-p -c, every ~0.25 s'))
-    for name, fn, fl in (('attention', attn, flops), ('gemm_reference', gemm, 2.0 * n_g ** 3)):
+    for name, fn, fl in (('attention', attn, flops), ('gemm_reference', gemm, 2.0 * n_g ** 3),
+                         ('attention_two_mantissa_bits', attn2, flops)):
         fn()
         torch.cuda.synchronize()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
