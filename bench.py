@@ -28,6 +28,7 @@ import argparse
 import json
 import os
 import platform
+import re
 import sys
 import time
 from pathlib import Path
@@ -522,6 +523,11 @@ def main():
         print('bench.py measures the single-GPU scene-attention path only: run it with --gpus 1 '
               '(the multi-GPU K/V gathering and Ulysses paths are not implemented)', file=sys.stderr)
         sys.exit(2)
+    if args.share:
+        # argument errors before anything touches the GPU
+        m = re.fullmatch(r'(\d+)/(\d+)', args.share)
+        if not m or not 0 <= int(m.group(1)) < int(m.group(2)):
+            raise SystemExit(f'--share {args.share}: give R/P with the rank R in [0, P)')
 
     if args.workload == 'wan-dit-step':
         return run_dit(args)
@@ -551,8 +557,6 @@ def main():
     q_range = None
     if args.share:
         r, P = (int(x) for x in args.share.split('/'))
-        if not 0 <= r < P:
-            raise SystemExit(f'--share {args.share}: rank R must lie in [0, P)')
         q_range = comm.partition(lay, P, T_, 'scene', W['counts'])[r]
         W['workload'] += f'-rank{r}of{P}'
     S, Le = sum(W['lengths']) * T_, sum(W['counts'])

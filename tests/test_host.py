@@ -420,3 +420,17 @@ def test_partition_against_brute_force():
     assert comm.partition(lay, 3, 10, 'scene', granularity='tokens') == [(0, 80), (80, 160), (160, 240)]
     with pytest.raises(ValueError):
         comm.partition(lay, 7, 10, 'ulysses')
+
+
+def test_bench_refuses_several_gpus_and_bad_shares():
+    """bench.py measures one GPU: --gpus above 1 exits with status 2 and says so, before touching a GPU; a rank share
+    outside [0, P) is an argument error"""
+    import subprocess
+    import sys
+    root = Path(__file__).resolve().parents[1]
+    r = subprocess.run([sys.executable, str(root / 'bench.py'), '--gpus', '2'], capture_output=True, text=True,
+                       timeout=300, cwd=root)
+    assert r.returncode == 2 and 'single-GPU' in r.stdout + r.stderr
+    r = subprocess.run([sys.executable, str(root / 'bench.py'), '--share', '3/3', '--no-cpu'], capture_output=True,
+                       text=True, timeout=300, cwd=root)
+    assert r.returncode != 0 and 'rank R in [0, P)' in r.stdout + r.stderr
