@@ -19,7 +19,8 @@ emitted here with fixed registers:
 The kernel puts Q into a128..a191 before the block (ONEREEL_RING64_QLOAD, or ONEREEL_RING64_QSET_STEP for queries
 rotated on the load), or the previous item's block left it there: at its loop's exit, where Q is no longer read, a
 block loads the queries of the work-group's next item into those registers (%[qa0], %[qa1]: the lane's query rows of
-that item), so that these loads are not queued behind its O stores in the in-order vmcnt.
+that item, or of this item when the next one is not claimed yet: the 16 loads are unconditional), so that these loads
+are not queued behind its O stores in the in-order vmcnt.
 S = q k^T - m comes out of the MFMAs (the first of each block accumulates onto -m), so P = 2^(c S), c = scale *
 log2(e), takes one v_mul_f32 and one v_exp_f32 per score: the fp32 scores of FlashAttention's exp2(s c - m c), with
 the subtraction folded into the accumulator.
@@ -41,9 +42,11 @@ Schedule of iteration j (32 keys; R-slot rings of K and V blocks in LDS, 8 KiB p
 Within a phase the eight S MFMAs go before the eight PV MFMAs, and the side work (softmax VALU, LDS reads, DMA) is
 spread between them in proportion to its issue cost (SIDE_COST).
 The running max starts at block 0's own maximum (prologue), so row sums never underflow and m only moves up.
-After the loop: the epilogue (O += V(nb-1) P(nb-1)) and the store of O / l, as bf16 output rows or, for the parts of
-a key-split work item, as fp32 partial rows (%[f32]). A wavefront whose queries all lie past the segment (%[dead])
-runs a loop of only the barriers and its share of the DMA, so that the block stays in step, and writes nothing.
+After the loop: the next item's Q loads, the epilogue (O += V(nb-1) P(nb-1)) and the store of O / l, as bf16 output
+rows or, for the parts of a key-split work item, as fp32 partial rows (%[f32]). A wavefront whose queries all lie
+past the segment (%[dead]) runs a loop of only the barriers and its share of the DMA, so that the block stays in
+step, issues the next item's Q loads at its exit and writes nothing; it leaves the block before the others'
+epilogues, so the kernel waits for a barrier before it refills the ring for the next item.
 The generator inserts the LDS waits (lgkmcnt) from the order of the reads, and s_nop where gfx950 needs wait states
 between dependent instructions (see Emitter).
 """
