@@ -25,6 +25,7 @@ rank of a P-GPU run computes once its K/V rows are local, on this one GPU.
 from __future__ import annotations
 
 import argparse
+import hashlib
 import json
 import os
 import platform
@@ -39,6 +40,16 @@ sys.path.insert(0, str(ROOT))
 METRIC = 'scene-attn TFLOP/s & % bf16 MFMA peak; ms/layer, HunyuanVideo-1.5 480p 4-scene'
 PEAK_BF16_TFLOPS = 2516.6      # MI355X dense bf16 MFMA (256 CU x 2.4 GHz x 4096 FLOP/clk)
 PEAK_HBM_GBS = 8000.0          # MI355X HBM3E
+# the sources of the attention kernel: profiles/attention_traffic.json holds their digest at the measured commit, and
+# its HBM traffic is reported only while they are unchanged
+ATTN_SOURCES = ['onereel_amd/csrc/attention.hip', 'onereel_amd/csrc/gen_attn_ring64.py', 'onereel_amd/csrc/common.h']
+
+
+def attn_sources_digest():
+    h = hashlib.sha256()
+    for f in ATTN_SOURCES:
+        h.update((ROOT / f).read_bytes())
+    return h.hexdigest()[:16]
 
 LENGTHS, T, COUNTS, H, D = [8, 8, 8, 8], 1590, [128] * 4, 16, 128
 REPS = [0, 10, 21, 31]
@@ -587,7 +598,7 @@ def main():
         torch.cuda.synchronize()
         if headline:
             gemm_reference(reps=1)
-        print('once: copy 1 GiB, layout, pack_gather, rotate_q, plan + attention, scatter, bf16 GEMM reference',
+        print('once: copy 1 GiB, layout, pack_layer, plan + attention, scatter, bf16 GEMM reference',
               flush=True)
         return
 
@@ -622,35 +633,29 @@ def main():
     ov = torch.empty_like(q)
     ot = torch.empty(Le, H, D, dtype=torch.bfloat16, device=dev)
     ws = plan.workspace(H, D)
-    # the attention kernel as the step runs it: video queries already rotated (qbuf), read in place
-    attn = lambda: scene.varlen(qbuf, kbuf, vbuf, plan.cu_q, plan.cu_k, plan.max_q, plan.max_k, k_off=plan.k_off,
-                                k_len=plan.k_len, out=ov, seg_q_src=plan.seg_q_src, q_text=eq, o_text=ot,
-                                n_q_video=plan.n_video, sum_q=plan.sum_q, workspace=ws)
-    pack = lambda: scene.pack_rows(plan, k, ek, 'k', out=kbuf, b_video=v, b_text=ev, b_out=vbuf, cos=cos, sin=sin,
-                                   mode='raw')
-    rotq = lambda: scene.rotate_queries(plan, q, cos, sin, out=qbuf)
+    # the attention kernel as the step runs it: video queries already rotated (qbuf), read in place, the own-frame
+    # values read in place from v
+    attn_of = lambda p: (lambda: scene.varlen(qbuf, kbuf, vbuf, p.cu_q, p.cu_k, p.max_q, p.max_k, k_off=p.k_off,
+                                              k_len=p.k_len, out=ov, seg_q_src=p.seg_q_src, q_text=eq, o_text=ot,
+                                              n_q_video=p.n_video, sum_q=p.sum_q, workspace=ws, v_tok=v,
+                                              v_lead=p.v_lead, v_row=p.v_row))
+    # the step's one pack launch: K rows (rotated), the V rows not read in place, the video queries rotated once
+    pack_of = lambda p: (lambda: scene.pack_layer(p, k, ek, v, ev, cos, sin, 'raw', kbuf, vbuf, q=q, qbuf=qbuf))
+    attn, pack = attn_of(plan), pack_of(plan)
     qpk = torch.empty(plan.sum_q, H, D, dtype=torch.bfloat16, device=dev)
     scat = lambda: scene.scatter(plan, qpk, ov, ot)
-    rotq()
-    attn()
     pack()
+    attn()
     scat()
     torch.cuda.synchronize()
     t_attn = time_events(attn, R, stream)
     if W['reps'] and W['scene_rope']:
-        pack_o = lambda: scene.pack_rows(plan_o, k, ek, 'k', out=kbuf, b_video=v, b_text=ev, b_out=vbuf, cos=cos,
-                                         sin=sin, mode='raw')
-        attn_o = lambda: scene.varlen(qbuf, kbuf, vbuf, plan_o.cu_q, plan_o.cu_k, plan_o.max_q, plan_o.max_k,
-                                      k_off=plan_o.k_off, k_len=plan_o.k_len, out=ov, seg_q_src=plan_o.seg_q_src,
-                                      q_text=eq, o_text=ot, n_q_video=plan_o.n_video, sum_q=plan_o.sum_q,
-                                      workspace=ws)
-        scene.rotate_queries(plan_o, q, cos, sin, out=qbuf)
-        pack_o()
+        attn_o = attn_of(plan_o)
+        pack_of(plan_o)()
         attn_o()
         torch.cuda.synchronize()
         t_attn_o = time_events(attn_o, R, stream)
         pack()                                      # the adjacent layout's keys back in the buffers
-        rotq()
         torch.cuda.synchronize()
         v_o = flops / (ms_o * 1e-3) / 1e12
         other = dict(shared_pos='source' if W['adjacent'] else 'adjacent',
@@ -664,25 +669,24 @@ def main():
     evict = torch.ones(128 << 20, dtype=torch.int32, device=dev)
     flush = lambda: evict.sum()   # reads 512 MB: the caches then hold clean lines of it, nothing to write back
     row = H * D * 2
-    pack_bytes = 2 * 2 * plan.sum_k * row            # K and V rows read + written
+    n_vq = sum(lq[0::2])                             # video query rows (the even segments)
+    n_vcopy = int((plan.v_src >= 0).sum())           # value rows packed (the others are read in place)
+    n_krot = int((plan.k_rope >= 0).sum())           # key rows rotated (video keys)
+    # K rows, packed V rows and video Q rows each read + written, and the fp32 cos / sin rows of every rotated row
+    pack_bytes = 2 * (plan.sum_k + n_vcopy + n_vq) * row + (n_krot + n_vq) * D * 8
     t_pack, t_pack_w = time_cold(pack, R, stream, flush), time_events(pack, R, stream)
     t_layout = time_cold(plan.build, R, stream, flush)
-    t_rot = time_cold(rotq, R, stream, flush)
     t_scat, t_scat_w = time_cold(scat, R, stream, flush), time_events(scat, R, stream)
     copy_ref = copy_reference(pack_bytes // 2, R, stream, flush) if headline else None
     del evict
     scat_bytes = 2 * plan.sum_q * row                # packed rows read + written
-    n_vq = sum(lq[0::2])                             # video query rows (the even segments)
-    rot_bytes = 2 * n_vq * row + n_vq * D * 8        # video query rows read + written, fp32 cos / sin rows
     kernels = {
         'attention': dict(ms=round(t_attn, 4), tflops=round(flops / t_attn / 1e9, 1),
                           frac_bf16_peak=round(flops / t_attn / 1e9 / PEAK_BF16_TFLOPS, 4)),
-        'pack_gather_kv': dict(ms=round(t_pack, 4), gbs=round(pack_bytes / t_pack / 1e6, 1),
-                               frac_hbm_peak=round(pack_bytes / t_pack / 1e6 / PEAK_HBM_GBS, 4), bytes=pack_bytes,
-                               warm_ms=round(t_pack_w, 4), timing='cold caches, single calls'),
-        'rotate_q': dict(ms=round(t_rot, 4), gbs=round(rot_bytes / t_rot / 1e6, 1),
-                         frac_hbm_peak=round(rot_bytes / t_rot / 1e6 / PEAK_HBM_GBS, 4), bytes=rot_bytes,
-                         timing='cold caches, single calls'),
+        'pack_layer': dict(ms=round(t_pack, 4), gbs=round(pack_bytes / t_pack / 1e6, 1),
+                           frac_hbm_peak=round(pack_bytes / t_pack / 1e6 / PEAK_HBM_GBS, 4), bytes=pack_bytes,
+                           rows=dict(keys=plan.sum_k, values=n_vcopy, queries=n_vq), warm_ms=round(t_pack_w, 4),
+                           timing='cold caches, single calls'),
         'layout': dict(us=round(t_layout * 1e3, 2), gbs=round(plan.index_bytes() / t_layout / 1e6, 1),
                        bytes=plan.index_bytes(),
                        bound=f'launch latency ({plan.index_bytes() / 1e6:.1f} MB of int32 indices)'),
@@ -692,12 +696,17 @@ def main():
     }
     # the kernel or_varlen_fwd runs for an O-only call: the 64-query ring kernel at head_dim 128
     kname = 'attn8_kernel' if D == 128 else 'attn4_kernel<64>'
-    traffic = None
+    traffic, traffic_src = None, None
     tf = ROOT / 'profiles' / 'attention_traffic.json'
     if headline and tf.exists():    # measured (PMC) on the headline layer only, for the kernel that runs
         rec = json.loads(tf.read_text())
-        if rec.get('kernel') == kname:
+        same = rec.get('sources_sha256') == attn_sources_digest()
+        if rec.get('kernel') == kname and same:
             traffic = rec.get('hbm_bytes_per_launch')
+        traffic_src = dict(commit=rec.get('commit'), sources_sha256=rec.get('sources_sha256'),
+                           current_sources_sha256=attn_sources_digest(),
+                           status='measured on these kernel sources' if same else
+                           'kernel sources changed since the measurement: traffic not reported')
     value = flops / (ms * 1e-3) / 1e12
     metric = METRIC if headline else f'scene-attn TFLOP/s & % bf16 MFMA peak; ms/layer, {W["workload"]}'
     out = dict(metric=metric, value=round(value, 2), unit='TFLOP/s', n_gpus=1, steps=args.steps, warmup=args.warmup,
@@ -711,7 +720,7 @@ def main():
                            useful_flop_per_step=flops, frac_bf16_peak_step=round(value / PEAK_BF16_TFLOPS, 4)),
                roofline=dict(bound='mfma', achieved=round(flops / t_attn / 1e9, 1), peak=PEAK_BF16_TFLOPS,
                              unit='TFLOP/s', frac=round(flops / t_attn / 1e9 / PEAK_BF16_TFLOPS, 4), traffic=traffic,
-                             kernel=f'{kname} (+ plan_kernel, one block, ~10 us)'),
+                             traffic_source=traffic_src, kernel=f'{kname} (+ plan_kernel, one block, ~10 us)'),
                kernels=kernels)
     if other:
         out['other_layout'] = other

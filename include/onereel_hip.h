@@ -6,6 +6,7 @@
  *   or_pack_gather    K/V (or Q) rows of every scope packed densely, RoPE applied on the way (optionally the text
  *                     scopes read their keys in place from their video scopes' packed rows)
  *   or_rotate_rows    the video queries rotated once, in token order (RoPE ahead of in-place attention)
+ *   or_pack_layer     or_pack_gather (K, and the values not read in place) and or_rotate_rows in one launch
  *   or_varlen_fwd     packed varlen attention (bf16 MFMA), optional RoPE on the Q load, optional in-place Q / O
  *   or_scatter        packed output rows written back to token order, text padding rows zeroed
  *   or_lse_merge      log-sum-exp merge of two partial attention results (attention split over key sets)
@@ -96,7 +97,17 @@ typedef struct or_layout_out {
   int32_t* k_off;      /* [n_seg] first packed key row of segment s (cu_k[s], or V_j's first row for T_j with
                           text_keys_in_place) */
   int32_t* k_len;      /* [n_seg] its key count (the varlen call's k_off / k_len) */
+  int32_t* v_lead;     /* [n_seg] keys at the head of segment s whose value rows the attention call can read in place
+                          from the token-order values: the scene's own-frame keys (every segment's keys start with
+                          them), rounded down to a multiple of OR_VARLEN_KEY_BLOCK; 0 for a segment without keys */
+  int32_t* v_row;      /* [n_seg] token row of segment s's first key (the first own-frame token of its scene) */
+  int32_t* v_src;      /* [sum_k] value row to pack for packed key row r: k_src[r], or -1 when r lies in the first
+                          v_lead keys of its segment (read in place, not packed) */
 } or_layout_out;
+
+/* Keys per block of the attention kernels' K/V stream: a segment's in-place value rows (or_varlen_args.v_lead) come
+ * in whole blocks. */
+#define OR_VARLEN_KEY_BLOCK 32
 
 /* Replaces the host-side layout logic of SceneLayout.shared_frames / key_frames (src/onereel/layout.py:54-78),
  * comm.runs / frame_tokens (src/onereel/parallel/comm.py:84-85,115-123) and the sizes of attention.packed's
@@ -131,6 +142,43 @@ int or_pack_gather(const void* a_video, const void* a_text, const void* b_video,
 int or_rotate_rows(const void* x, int64_t x_row_stride, int64_t n_video, const int32_t* src_idx,
                    const int32_t* rope_row, const float* cos_table, const float* sin_table, int64_t n_rope_rows,
                    int64_t n_rows, int32_t H, int32_t D, void* out, int64_t out_row_stride, void* stream);
+
+/* Arguments of or_pack_layer: the K/V pack of or_pack_gather (keys as its a rows, values as its b rows) and the query
+ * rotation of or_rotate_rows, one launch. */
+typedef struct or_pack_args {
+  const void* k_video;        /* bf16 key rows [video ; text], as or_pack_gather's a_video / a_text */
+  const void* k_text;
+  const void* v_video;        /* bf16 value rows, same strides (NULL with v_out NULL: keys only) */
+  const void* v_text;
+  int64_t video_row_stride;   /* elements between video rows (keys and values) */
+  int64_t text_row_stride;
+  int64_t n_video;            /* rows of the video part: source rows >= n_video are text rows */
+  const int32_t* k_src;       /* [n_keys] source row of packed key r */
+  const int32_t* k_rope;      /* optional [n_keys] as or_pack_gather's rope_row */
+  const int32_t* k_move_from; /* optional [n_keys] as or_pack_gather's move_from */
+  const int32_t* v_src;       /* optional [n_keys] source row of packed value r, -1: not packed (its row of v_out is
+                                 not written; the attention call reads it in place); NULL: k_src */
+  int64_t n_keys;
+  void* k_out;                /* bf16 [n_keys, H, D] */
+  void* v_out;                /* bf16 [n_keys, H, D] or NULL */
+  const void* q;              /* video queries rotated in token order, as or_rotate_rows(q, .., q_out) */
+  int64_t q_row_stride;
+  const int32_t* q_src;       /* [n_queries] */
+  const int32_t* q_rope;      /* [n_queries] */
+  int64_t n_queries;          /* 0: no query rotation */
+  void* q_out;
+  int64_t q_out_row_stride;
+  const float* cos_table;     /* fp32 [n_rope_rows, D] */
+  const float* sin_table;
+  int64_t n_rope_rows;
+  int32_t H;
+  int32_t D;
+} or_pack_args;
+
+/* Replaces the same code as or_pack_gather and or_rotate_rows together (hunyuan15.py:164,168,183-191,225;
+ * attention.py:69): one layer's K/V pack and query rotation in one launch, with the results of those two calls, except
+ * that rows whose v_src is -1 are left out of v_out. */
+int or_pack_layer(const or_pack_args* args, void* stream);
 
 /* Replaces the write-back of Processor.scene (hunyuan15.py:226,231-235) after attention.packed's split
  * (attention.py:71): o_video[dst] / o_text[dst - n_video] = packed[r] for dst = dst_idx[r]; then the text rows
@@ -177,6 +225,15 @@ typedef struct or_varlen_args {
   int32_t q_row_step;       /* 0 or 1: a segment's queries are consecutive source rows; s > 1 (with seg_q_src):
                                query i of segment s is source row seg_q_src[s] + i * s, and its output row too
                                (e.g. one head of [tokens, H, D] rows viewed as [tokens * H, 1, D]: s = H) */
+  const void* v_tok;        /* optional token-order value rows, row stride k_row_stride, read in place: the first
+                               v_lead[s] keys of segment s take their values from rows v_row[s] .. v_row[s] +
+                               v_lead[s] - 1 of v_tok, its other keys from v as without v_tok (rows k_start +
+                               v_lead[s] ..). v_lead[s]: a multiple of OR_VARLEN_KEY_BLOCK, at most k_len; blocks past
+                               v_tok_rows are taken from v. NULL: every value from v. (A layout's v_lead / v_row, with
+                               the values packed per its v_src, read the own-frame values in place.) */
+  const int32_t* v_lead;    /* [n_seg], with v_tok */
+  const int32_t* v_row;     /* [n_seg], with v_tok */
+  int64_t v_tok_rows;       /* rows of v_tok */
 } or_varlen_args;
 
 /* Bytes of device workspace or_varlen_fwd needs for this many segments, packed queries and heads: the work-item

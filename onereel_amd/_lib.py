@@ -35,7 +35,10 @@ class LayoutSizes(ctypes.Structure):
 
 class LayoutOut(ctypes.Structure):
     _fields_ = [(n, vp) for n in ('cu_q', 'cu_k', 'seg_q_src', 'q_src', 'q_rope', 'k_src', 'k_rope', 'k_move_a',
-                                  'k_move_b', 'k_off', 'k_len')]
+                                  'k_move_b', 'k_off', 'k_len', 'v_lead', 'v_row', 'v_src')]
+
+# keys per block of the attention kernels' K/V stream (OR_VARLEN_KEY_BLOCK): in-place value rows come in whole blocks
+KEY_BLOCK = 32
 
 
 class VarlenArgs(ctypes.Structure):
@@ -44,7 +47,16 @@ class VarlenArgs(ctypes.Structure):
                 ('cos_table', vp), ('sin_table', vp), ('n_rope_rows', i64), ('n_q_video', i64),
                 ('q_row_stride', i64), ('k_row_stride', i64), ('o_row_stride', i64), ('n_seg', i32), ('sum_q', i32),
                 ('max_q', i32), ('max_k', i32), ('H', i32), ('D', i32), ('scale', ctypes.c_float),
-                ('workspace', vp), ('workspace_bytes', i64), ('q_row_step', i32)]
+                ('workspace', vp), ('workspace_bytes', i64), ('q_row_step', i32), ('v_tok', vp), ('v_lead', vp),
+                ('v_row', vp), ('v_tok_rows', i64)]
+
+
+class PackArgs(ctypes.Structure):
+    _fields_ = [('k_video', vp), ('k_text', vp), ('v_video', vp), ('v_text', vp), ('video_row_stride', i64),
+                ('text_row_stride', i64), ('n_video', i64), ('k_src', vp), ('k_rope', vp), ('k_move_from', vp),
+                ('v_src', vp), ('n_keys', i64), ('k_out', vp), ('v_out', vp), ('q', vp), ('q_row_stride', i64),
+                ('q_src', vp), ('q_rope', vp), ('n_queries', i64), ('q_out', vp), ('q_out_row_stride', i64),
+                ('cos_table', vp), ('sin_table', vp), ('n_rope_rows', i64), ('H', i32), ('D', i32)]
 
 
 # every exported symbol with its ctypes signature: include/onereel_hip.h
@@ -54,6 +66,7 @@ SIGNATURES = {
     'or_pack_gather': (i32, [vp, vp, vp, vp, i64, i64, i64, vp, vp, vp, vp, vp, i64, i64, i32, i32, vp, vp, vp]),
     'or_scatter': (i32, [vp, vp, i64, i64, vp, vp, i64, i64, i64, i64, i32, i32, vp]),
     'or_rotate_rows': (i32, [vp, i64, i64, vp, vp, vp, vp, i64, i64, i32, i32, vp, i64, vp]),
+    'or_pack_layer': (i32, [ctypes.POINTER(PackArgs), vp]),
     'or_varlen_workspace_size': (i64, [i32, i32, i32, i32]),
     'or_varlen_fwd': (i32, [ctypes.POINTER(VarlenArgs), vp]),
     'or_varlen_fwd_noalloc': (i32, [ctypes.POINTER(VarlenArgs), vp]),

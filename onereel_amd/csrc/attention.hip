@@ -18,6 +18,7 @@
 // - Softmax in base 2, p = 2^(c (s - m)) with c = scale * log2(e), and a running max m raised only when needed.
 // - Optional RoPE on the Q load (table row per packed query), with the rounding of diffusers apply_rotary_emb.
 #include <math.h>
+#include <stdlib.h>
 
 #include <mutex>
 
@@ -40,8 +41,9 @@ constexpr int kQueues = 8;      // item queues: one per XCD
 constexpr int kQueueWords = 32; // words per queue header (head counter, item count, first item), one 128-byte line
 constexpr int kWsHeader = kQueues * kQueueWords;   // int32 words before the item list
 // an item record: tile << 8 | head, part | ways << 8 (0: whole item), split index, and the segment's first query,
-// query count, first source row, first key and key count (a kernel reads the record with two 16-byte loads)
-constexpr int kItemWords = 8;
+// query count, first source row, first key and key count, then the token row of its first in-place value and the
+// number of keys whose values are read there (0 without in-place values), two words unused (three 16-byte loads)
+constexpr int kItemWords = 12;
 constexpr int kPlanThreads = 1024;
 constexpr int kMaxPlanSeg = 4096;
 constexpr int kMaxSplitWays = 8;      // key parts of a split work item
@@ -77,6 +79,9 @@ struct AttnArgs {
   int32_t* split_tab;
   float* split_lse;
   float* split_o;
+  // in-place values: token-order value rows (row stride ks) and their row count
+  const uint16_t* v_tok;
+  int64_t n_vtok;
 };
 
 
@@ -106,7 +111,8 @@ __device__ inline int plan_upper_bound(const int* a, int n, int x) {
 
 __global__ __launch_bounds__(kPlanThreads) void plan_kernel(const int32_t* cu_q, const int32_t* cu_k,
                                                             const int32_t* k_off, const int32_t* k_len,
-                                                            const int32_t* seg_q_src, int n_seg, int H, int bq,
+                                                            const int32_t* seg_q_src, const int32_t* v_lead,
+                                                            const int32_t* v_row, int n_seg, int H, int bq,
                                                             int max_items, int slots, int split_keys, int parts_cap,
                                                             int32_t* ws) {
   __shared__ unsigned long long key[kMaxPlanSeg];
@@ -235,10 +241,12 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(const int32_t* cu_q,
     const int k_beg = k_off ? k_off[s] : cu_k[s];
     const int lk = k_len ? k_len[s] : cu_k[s + 1] - cu_k[s];
     const int q_src0 = seg_q_src ? seg_q_src[s] : q_beg;
+    const int vl = v_lead ? v_lead[s] : 0, vr = v_row ? v_row[s] : 0;
     auto put = [&](int64_t entry, int pw, int sidx) {
       int32_t* e = ws + kWsHeader + kItemWords * entry;
       *(int4*)e = make_int4((t << 8) | head, pw, sidx, q_beg);
       *(int4*)(e + 4) = make_int4(lq, q_src0, k_beg, lk < 0 ? 0 : lk);
+      *(int4*)(e + 8) = make_int4(vr, vl, 0, 0);
     };
     if (pos < keep) {
       put(q_first[q] + pos, 0, 0);
@@ -263,12 +271,14 @@ struct QueueInfo {
 // loads (counted by lgkmcnt: a record does not wait behind earlier O stores in the in-order vmcnt)
 typedef __attribute__((address_space(4))) const int ItemWord;
 struct ItemRec {
-  int4 r0, r1;
+  int4 r0, r1, r2;
 };
 __device__ inline ItemRec item_record(const int32_t* ws, int it) {
   const ItemWord* x = (const ItemWord*)(ws + kWsHeader + kItemWords * it);
-  return ItemRec{make_int4(x[0], x[1], x[2], x[3]), make_int4(x[4], x[5], x[6], x[7])};
+  return ItemRec{make_int4(x[0], x[1], x[2], x[3]), make_int4(x[4], x[5], x[6], x[7]),
+                 make_int4(x[8], x[9], x[10], x[11])};
 }
+
 
 __device__ inline void load_queues(const int32_t* ws, QueueInfo* qi, int tid) {
   if (tid < kQueues) {
@@ -397,15 +407,42 @@ __device__ __forceinline__ void wait_loads_barrier() {
   else asm volatile("s_waitcnt vmcnt(12)\n\ts_barrier" ::: "memory");
 }
 
-// Per-item stream of one segment-head's K or V rows: block b starts at base + b * bb bytes and holds rem0 - b * bb
-// valid bytes (clamped at 0).
+// Per-item stream of one segment-head's K or V rows: block b starts at base + b * bb bytes (abase + b * bb for the
+// in-place value blocks b < nba) and holds rem0 - b * bb valid bytes (clamped at 0).
 struct Stream {
   uint64_t base;
   int32_t rem0;
   int32_t bb;
-  __device__ __forceinline__ uint64_t at(int b) const { return base + (uint64_t)(int64_t)b * (uint32_t)bb; }
+  uint64_t abase;
+  int32_t nba;
+  __device__ __forceinline__ uint64_t at(int b) const {
+    return (b < nba ? abase : base) + (uint64_t)(int64_t)b * (uint32_t)bb;
+  }
   __device__ __forceinline__ int32_t nrec(int b) const { return max(rem0 - b * bb, 0); }
 };
+
+// Value stream of a work item (or of one key part of it): key blocks b < nba read the token-order rows from base a,
+// the others the packed rows from base p; either way block b starts b * bb bytes past its base.
+struct VRange {
+  uint64_t a, p;
+  int32_t nba;
+};
+
+// the in-place blocks of key blocks [b0, b0 + nb) of a segment whose first v_lead keys take their values from token
+// rows v_row.. (whole blocks only, none past the token rows or the segment's last whole block); p: packed rows of
+// block b0
+__device__ inline VRange value_range(const AttnArgs& a, int v_row, int v_lead, int lk_seg, int b0, int nb,
+                                     int64_t head_off, uint64_t p) {
+  VRange r{p, p, 0};
+  if (!a.v_tok || v_lead <= 0 || v_row < 0) return r;
+  int64_t nba = min((int64_t)v_lead, (int64_t)lk_seg) / kBKB;
+  const int64_t fit = (a.n_vtok - v_row) / kBKB;   // blocks that lie inside the token rows
+  nba = min(nba, fit) - b0;
+  nba = nba < 0 ? 0 : (nba > nb ? nb : nba);
+  r.nba = (int32_t)nba;
+  if (nba > 0) r.a = (uint64_t)(a.v_tok + ((int64_t)v_row + (int64_t)kBKB * b0) * a.ks + head_off);
+  return r;
+}
 
 template <int D>
 __device__ __forceinline__ bf16x8 ring_vt(const uint16_t* slot, uint32_t vaddr, int half) {
@@ -572,14 +609,16 @@ void attn4_kernel(AttnArgs a, int32_t* ws) {
     if (it < 0) break;
     const int4 r0 = *(const int4*)(ws + kWsHeader + kItemWords * it);
     const int4 r1 = *(const int4*)(ws + kWsHeader + kItemWords * it + 4);
+    const int4 r2 = *(const int4*)(ws + kWsHeader + kItemWords * it + 8);
     const int head = r0.x & 255, qt = r0.x >> 8;
     const int q_beg = r0.w, Lq = r1.x, q_src0 = r1.y, k_beg = r1.z, Lk = r1.w;
     const int q0 = qt * BQ + w * WQ;
     const bool active = q0 < Lq;
     const int nb = (Lk + kBKB - 1) / kBKB;
     const int32_t rb = (int32_t)rs * 2;
-    const Stream ks = {(uint64_t)(a.k + (int64_t)k_beg * rs + head * D), Lk * rb - rb + D * 2, kBKB * rb};
-    const Stream vs = {(uint64_t)(a.v + (int64_t)k_beg * rs + head * D), Lk * rb - rb + D * 2, kBKB * rb};
+    const VRange vr = value_range(a, r2.x, r2.y, Lk, 0, nb, head * D, (uint64_t)(a.v + (int64_t)k_beg * rs + head * D));
+    const Stream ks = {(uint64_t)(a.k + (int64_t)k_beg * rs + head * D), Lk * rb - rb + D * 2, kBKB * rb, 0, 0};
+    const Stream vs = {vr.p, Lk * rb - rb + D * 2, kBKB * rb, vr.a, vr.nba};
 
     // prologue: K(0) and the group {K(1), V(-1)} (V(-1) fills its slot with zeros: iteration 0 multiplies it by
     // P(-1) = 0) are in flight while Q loads; every load so far is waited for (so the compiler's own waits for Q do
@@ -742,14 +781,16 @@ void attn8_kernel(AttnArgs a, int32_t* ws) {
   bool have_q = false;
   while (it >= 0) {
     const ItemRec rec = item_record(ws, it);
-    const int4 r0 = rec.r0, r1 = rec.r1;
+    const int4 r0 = rec.r0, r1 = rec.r1, r2 = rec.r2;
     const int head = r0.x & 255, qt = r0.x >> 8, part = r0.y & 255, ways = r0.y >> 8, sidx = r0.z;
     const int q_beg = r0.w, Lq = r1.x, q_src0 = r1.y;
-    int k_beg = r1.z, Lk = r1.w;
+    const int lk_seg = r1.w;
+    int k_beg = r1.z, Lk = r1.w, b0 = 0;
     if (ways > 1) {
       // part `part` of `ways`: key blocks [nb_all part / ways, nb_all (part + 1) / ways), at least one each
       const int nb_all = (Lk + kBKB - 1) / kBKB;
-      const int b0 = nb_all * part / ways, b1 = nb_all * (part + 1) / ways;
+      const int b1 = nb_all * (part + 1) / ways;
+      b0 = nb_all * part / ways;
       k_beg += kBKB * b0;
       Lk = min(kBKB * b1, Lk) - kBKB * b0;
     }
@@ -757,10 +798,15 @@ void attn8_kernel(AttnArgs a, int32_t* ws) {
     const int nb = (Lk + kBKB - 1) / kBKB;
     float* part_o = ways > 1 ? a.split_o + (int64_t)(sidx * ways + part) * kSplitRows * D : nullptr;
     const uint64_t kaddr = (uint64_t)(a.k + (int64_t)k_beg * rs + head * D);
-    const uint64_t vaddr = (uint64_t)(a.v + (int64_t)k_beg * rs + head * D);
     const int32_t rb = (int32_t)rs * 2;
     const int32_t rem0 = Lk * rb - rb + D * 2;
     const int32_t bb = kBKB * rb;
+    // values: blocks [0, vr.nba) from the token-order rows, the others from the packed rows (the key loop moves its
+    // stream's base once, to vsw: the packed rows of block vr.nba)
+    const VRange vr = value_range(a, r2.x, r2.y, lk_seg, b0, nb, head * D,
+                                  (uint64_t)(a.v + (int64_t)k_beg * rs + head * D));
+    const uint64_t vaddr = vr.nba > 0 ? vr.a : vr.p;
+    const uint64_t vsw = vr.p + (uint64_t)vr.nba * (uint32_t)bb;
     // every wavefront is done with the previous item's ring: a wavefront without live queries leaves its key loop
     // while the others' epilogues still read the last V block, and its refill below would overwrite a slot
     __syncthreads();
@@ -847,7 +893,7 @@ void attn8_kernel(AttnArgs a, int32_t* ws) {
                    [vb_lo] "s"((uint32_t)vaddr), [vb_hi] "s"((uint32_t)(vaddr >> 32)), [rem0] "s"(rem0), [remk] "s"(rem0 - 2 * bb),
                    [op0] "v"(op[0]), [op1] "v"(op[1]), [ok0] "v"(ok[0]), [ok1] "v"(ok[1]),
                    [f32] "s"(__builtin_amdgcn_readfirstlane(ways > 1 ? 1 : 0)),
-                   [dead] "s"(__builtin_amdgcn_readfirstlane(q0 >= Lq ? 1 : 0))
+                   [dead] "s"(__builtin_amdgcn_readfirstlane(q0 >= Lq ? 1 : 0)), [vsw] "s"(vsw), [nbav] "s"(vr.nba)
                  : ONEREEL_RING64_CLOBBERS);
     // the next item's queries are in a128..a191 unless they must be rotated on the load
     have_q = nit >= 0 && !a.q_rope;
@@ -943,11 +989,26 @@ int64_t min_items_of(int32_t sum_q, int32_t H, int32_t D) {
   return (int64_t)H * ((sum_q + item_bq(D) - 1) / item_bq(D));
 }
 
+// persistent blocks of an attention launch on the current device: one per resident slot (CUs x blocks per CU, one
+// block per CU for the 64-query kernel), or fewer when ONEREEL_ATTN_MAX_BLOCKS (a test setting, read at every call)
+// caps the grid so that each block walks many work items
+int64_t grid_slots(const DevInfo& di, int32_t D) {
+  int64_t grid = (int64_t)di.cus * di.occ[D == 128];
+  if (const char* e = getenv("ONEREEL_ATTN_MAX_BLOCKS")) {
+    const long cap = strtol(e, nullptr, 10);
+    if (cap > 0 && cap < grid) grid = cap;
+  }
+  return grid;
+}
+
 // parts of key-split items a call may hold: only the 64-query kernel (head_dim 128) splits items, and only calls that
-// can have fewer than kSplitMaxRounds rounds of items on kSplitSlots blocks get room for them
-constexpr int kSplitSlots = 256;   // persistent blocks of the 64-query kernel on MI355X (256 CUs, one block each)
+// can have fewer than kSplitMaxRounds rounds of items on the device's persistent blocks get room for them. Without a
+// device (a size query on a host with no GPU) the count is that of MI355X, 256 blocks.
 int64_t split_parts_cap(int32_t n_seg, int32_t sum_q, int32_t H, int32_t D) {
-  if (D != 128 || min_items_of(sum_q, H, D) >= (int64_t)kSplitMaxRounds * kSplitSlots) return 0;
+  if (D != 128) return 0;
+  DevInfo di;
+  const int64_t slots = dev_info(di) == 0 ? grid_slots(di, D) : 256;
+  if (min_items_of(sum_q, H, D) >= (int64_t)kSplitMaxRounds * slots) return 0;
   const int64_t mi = max_items_of(n_seg, sum_q, H);
   return mi * kMaxSplitWays < kMaxSplitParts ? mi * kMaxSplitWays : kMaxSplitParts;
 }
@@ -993,6 +1054,8 @@ int check_args(const or_varlen_args& x, const char* fn) {
   if ((int64_t)(x.max_k + 8 * 32) * x.k_row_stride * 2 > 0x7fffffffLL)
     return fail_arg("%s: a segment's keys span more than 2 GiB (max_k %d x row stride %lld)", fn, x.max_k,
                     (long long)x.k_row_stride);
+  if (x.v_tok && (!x.v_lead || !x.v_row || x.v_tok_rows < 0 || !aligned16(x.v_tok)))
+    return fail_arg("%s: v_tok needs v_lead, v_row, v_tok_rows >= 0 and 16-byte alignment", fn);
   return 0;
 }
 
@@ -1006,7 +1069,7 @@ int launch_varlen(const or_varlen_args& x, void* wsp, int64_t cap, hipStream_t s
   const int64_t max_items = max_items_of(x.n_seg, x.sum_q, x.H);
   // persistent blocks: one per resident slot, but no more than the work entries (items, or their key parts when
   // the planner may split items: only when even the fewest items the call can have come in few rounds)
-  int64_t grid = (int64_t)di.cus * occ;
+  int64_t grid = grid_slots(di, x.D);
   const bool may_split = cap > 0 && min_items_of(x.sum_q, x.H, x.D) < kSplitMaxRounds * grid;
   const int64_t entries = max_items * (may_split ? kMaxSplitWays : 1);
   if (grid > entries) grid = entries;
@@ -1038,13 +1101,16 @@ int launch_varlen(const or_varlen_args& x, void* wsp, int64_t cap, hipStream_t s
   a.c = x.scale * 1.4426950408889634f;
   int32_t* ws = (int32_t*)wsp;
   const WsLayout wl = ws_layout(x.n_seg, x.sum_q, x.H, cap);
+  a.v_tok = (const uint16_t*)x.v_tok;
+  a.n_vtok = x.v_tok ? x.v_tok_rows : 0;
   a.split_tab = (int32_t*)((char*)wsp + wl.tab);
   a.split_lse = (float*)((char*)wsp + wl.lse);
   a.split_o = (float*)((char*)wsp + wl.o);
   // the planner needs key counts only: k_len when given, else the cu_k differences. It writes every word of the
   // workspace the other kernels read (queue headers, item list, split table) before they run.
   hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(kPlanThreads), 0, st, x.cu_q, x.cu_k, x.k_len ? x.k_off : nullptr,
-                     x.k_len, x.seg_q_src, x.n_seg, x.H, item_bq(x.D), (int)max_items, (int)grid,
+                     x.k_len, x.seg_q_src, x.v_tok ? x.v_lead : nullptr, x.v_tok ? x.v_row : nullptr, x.n_seg, x.H,
+                     item_bq(x.D), (int)max_items, (int)grid,
                      may_split ? 1 : 0, (int)cap, ws);
   if (int rc = check_hip(hipGetLastError(), "plan_kernel launch")) return rc;
   hipLaunchKernelGGL(attn_fn(x.D), dim3((unsigned)grid), dim3(kThreads), 0, st, a, ws);

@@ -24,23 +24,36 @@ constexpr int kMaxChunksPerLane = 8;  // rows up to 64 lanes * 8 * 8 elements = 
 // 16-byte store that bypasses the caches (global_store_dwordx4 ... nt)
 __device__ __forceinline__ void store_nt(uint16_t* p, u32x4 v) { __builtin_nontemporal_store(v, (u32x4*)p); }
 
-struct GatherArgs {
+// One job of the row kernel: n_rows rows, row r read from src_idx[r] of [video ; text], rotated per rope_row /
+// move_from, written to packed row r of a_out (in_place: to its own source row of a_out, row stride out_stride, and
+// text rows skipped); the second source's row b_idx[r] (src_idx[r] without b_idx; none where b_idx[r] < 0) copied to
+// packed row r of b_out.
+struct RowJob {
   const uint16_t* a_video;
   const uint16_t* a_text;
   const uint16_t* b_video;
   const uint16_t* b_text;
-  int64_t src_stride, text_stride, n_video;
+  int64_t src_stride, text_stride;
   const int32_t* src_idx;
+  const int32_t* b_idx;
   const int32_t* rope_row;
   const int32_t* move_from;
+  uint16_t* a_out;
+  uint16_t* b_out;
+  int64_t out_stride;
+  int64_t n_rows;
+  int in_place;
+};
+
+// rows [0, job[0].n_rows) run job 0, the next job[1].n_rows rows job 1 (one launch for the K/V pack and the query
+// rotation of a layer)
+struct GatherArgs {
+  RowJob job[2];
+  int64_t n_video;
   const float* cos_t;
   const float* sin_t;
   int64_t n_rope_rows;
-  int64_t n_rows;
   int H, D;
-  uint16_t* a_out;
-  uint16_t* b_out;
-  int64_t out_stride;   // IN_PLACE: row stride of a_out (rows are written at their source row)
   int shared_d0;        // every chunk of a lane has the same offset within its head: (8 * lanes per row) % D == 0
 };
 
@@ -58,9 +71,7 @@ __device__ __forceinline__ RowLanes row_lanes(int chunks, int lane) {
   return RowLanes{cp, 64 / cp, lane / cp, lane % cp};
 }
 
-// IN_PLACE (or_rotate_rows): row r is written to the same row src_idx[r] of a_out, not to packed row r, and rows of
-// the second source (src >= n_video) are skipped
-template <bool NARROW, bool IN_PLACE>
+template <bool NARROW>
 __global__ __launch_bounds__(kThreads) void pack_gather_kernel(GatherArgs g) {
   const int lane = threadIdx.x & 63;
   const int64_t wave = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6);
@@ -68,18 +79,29 @@ __global__ __launch_bounds__(kThreads) void pack_gather_kernel(GatherArgs g) {
   const int row_elems = g.H * g.D;
   const int chunks = row_elems >> 3;
   const RowLanes rl = row_lanes<NARROW>(chunks, lane);
-  for (int64_t r0 = wave * rl.per; r0 < g.n_rows; r0 += n_waves * rl.per) {
-    const int64_t r = r0 + rl.sub;
-    if (r >= g.n_rows) continue;
-    const int src = g.src_idx[r];
+  const int64_t n0 = g.job[0].n_rows, total = n0 + g.job[1].n_rows;
+  for (int64_t r0 = wave * rl.per; r0 < total; r0 += n_waves * rl.per) {
+    const int64_t rr = r0 + rl.sub;
+    if (rr >= total) continue;
+    const bool second = rr >= n0;
+    const RowJob& J = second ? g.job[1] : g.job[0];
+    const int64_t r = second ? rr - n0 : rr;
+    const int src = J.src_idx[r];
     const bool text = src >= g.n_video;
-    if (IN_PLACE && text) continue;
-    const int64_t off = text ? (int64_t)(src - g.n_video) * g.text_stride : (int64_t)src * g.src_stride;
-    const uint16_t* a = (text ? g.a_text : g.a_video) + off;
-    const uint16_t* b = g.b_out ? (text ? g.b_text : g.b_video) + off : nullptr;
+    if (J.in_place && text) continue;
+    const int64_t off = text ? (int64_t)(src - g.n_video) * J.text_stride : (int64_t)src * J.src_stride;
+    const uint16_t* a = (text ? J.a_text : J.a_video) + off;
+    const uint16_t* b = nullptr;
+    if (J.b_out) {
+      const int bs = J.b_idx ? J.b_idx[r] : src;
+      if (bs >= 0) {
+        const bool bt = bs >= g.n_video;
+        b = bt ? J.b_text + (int64_t)(bs - g.n_video) * J.text_stride : J.b_video + (int64_t)bs * J.src_stride;
+      }
+    }
     // table rows outside the table leave the row unrotated (the host validates them; this only keeps reads in bounds)
-    int rope = g.rope_row ? g.rope_row[r] : -1;
-    int mfrom = g.move_from ? g.move_from[r] : -1;
+    int rope = J.rope_row ? J.rope_row[r] : -1;
+    int mfrom = J.move_from ? J.move_from[r] : -1;
     if (rope >= g.n_rope_rows || mfrom >= g.n_rope_rows) rope = mfrom = -1;
     u32x4 va[kMaxChunksPerLane], vb[kMaxChunksPerLane];
 #pragma unroll
@@ -92,15 +114,15 @@ __global__ __launch_bounds__(kThreads) void pack_gather_kernel(GatherArgs g) {
     }
     // every chunk of a lane sits at the same offset within its head (8 cp a multiple of D): the lane's table entries
     // are loaded once per row, next to the row's loads, instead of once per chunk
-    const bool rot = g.move_from ? (mfrom >= 0 && rope >= 0) : rope >= 0;
+    const bool rot = J.move_from ? (mfrom >= 0 && rope >= 0) : rope >= 0;
     Tab8 tr, tm;
     if (g.shared_d0 && rot) {
       const int d0 = (8 * rl.cl) % g.D;
       tr = load_tab8(g.cos_t, g.sin_t, (int64_t)rope * g.D + d0);
-      if (g.move_from) tm = load_tab8(g.cos_t, g.sin_t, (int64_t)mfrom * g.D + d0);
+      if (J.move_from) tm = load_tab8(g.cos_t, g.sin_t, (int64_t)mfrom * g.D + d0);
     }
-    uint16_t* ao = IN_PLACE ? g.a_out + (int64_t)src * g.out_stride : g.a_out + r * (int64_t)row_elems;
-    uint16_t* bo = g.b_out ? g.b_out + r * (int64_t)row_elems : nullptr;
+    uint16_t* ao = J.in_place ? J.a_out + (int64_t)src * J.out_stride : J.a_out + r * (int64_t)row_elems;
+    uint16_t* bo = b ? J.b_out + r * (int64_t)row_elems : nullptr;
 #pragma unroll
     for (int i = 0; i < kMaxChunksPerLane; ++i) {
       const int c = rl.cl + rl.cp * i;
@@ -110,9 +132,9 @@ __global__ __launch_bounds__(kThreads) void pack_gather_kernel(GatherArgs g) {
           if (!g.shared_d0) {
             const int d0 = (8 * c) % g.D;
             tr = load_tab8(g.cos_t, g.sin_t, (int64_t)rope * g.D + d0);
-            if (g.move_from) tm = load_tab8(g.cos_t, g.sin_t, (int64_t)mfrom * g.D + d0);
+            if (J.move_from) tm = load_tab8(g.cos_t, g.sin_t, (int64_t)mfrom * g.D + d0);
           }
-          if (g.move_from) x = rotate8(x, tm, -1.0f);
+          if (J.move_from) x = rotate8(x, tm, -1.0f);
           x = rotate8(x, tr, 1.0f);
         }
         store_nt(ao + 8 * c, x);
@@ -223,6 +245,45 @@ int shared_d0(int H, int D) {
 
 using namespace onereel;
 
+namespace onereel {
+namespace {
+
+int launch_rows(const GatherArgs& g, hipStream_t st) {
+  const int64_t rows = g.job[0].n_rows + g.job[1].n_rows;
+  if (rows == 0) return 0;
+  if ((int64_t)g.H * g.D < 64 * 8)   // rows under 64 chunks share a wavefront
+    hipLaunchKernelGGL(pack_gather_kernel<true>, dim3(row_grid(rows)), dim3(kThreads), 0, st, g);
+  else
+    hipLaunchKernelGGL(pack_gather_kernel<false>, dim3(row_grid(rows)), dim3(kThreads), 0, st, g);
+  return check_hip(hipGetLastError(), "pack_gather_kernel launch");
+}
+
+int check_pack_job(const void* a_video, const void* a_text, const void* b_video, const void* b_text,
+                   int64_t src_row_stride, int64_t text_row_stride, const int32_t* src_idx, const int32_t* rope_row,
+                   const int32_t* move_from, const float* cos_table, const float* sin_table, int64_t n_rope_rows,
+                   const void* a_out, const void* b_out, const char* fn) {
+  if (!a_video || !src_idx || !a_out) return fail_arg("%s: the key rows, src_idx and the key output are required", fn);
+  if (b_out && !b_video) return fail_arg("%s: a value output without value rows", fn);
+  if ((rope_row || move_from) && (!cos_table || !sin_table || n_rope_rows < 1))
+    return fail_arg("%s: rotation needs cos / sin tables", fn);
+  if (move_from && !rope_row) return fail_arg("%s: move_from needs rope_row (the second rotation)", fn);
+  if (!aligned16(a_video) || !aligned16(a_out) || (a_text && !aligned16(a_text)) || (b_video && !aligned16(b_video)) ||
+      (b_text && !aligned16(b_text)) || (b_out && !aligned16(b_out)) || src_row_stride % 8 || text_row_stride % 8)
+    return fail_arg("%s: pointers must be 16-byte aligned and row strides multiples of 8 elements", fn);
+  return 0;
+}
+
+RowJob pack_job(const void* a_video, const void* a_text, const void* b_video, const void* b_text,
+                int64_t src_row_stride, int64_t text_row_stride, const int32_t* src_idx, const int32_t* b_idx,
+                const int32_t* rope_row, const int32_t* move_from, int64_t n_rows, void* a_out, void* b_out) {
+  return RowJob{(const uint16_t*)a_video, (const uint16_t*)(a_text ? a_text : a_video), (const uint16_t*)b_video,
+                (const uint16_t*)(b_text ? b_text : b_video), src_row_stride, text_row_stride, src_idx, b_idx,
+                rope_row, move_from, (uint16_t*)a_out, (uint16_t*)b_out, 0, n_rows, 0};
+}
+
+}  // namespace
+}  // namespace onereel
+
 extern "C" int or_pack_gather(const void* a_video, const void* a_text, const void* b_video, const void* b_text,
                               int64_t src_row_stride, int64_t text_row_stride, int64_t n_video,
                               const int32_t* src_idx, const int32_t* rope_row, const int32_t* move_from,
@@ -231,25 +292,20 @@ extern "C" int or_pack_gather(const void* a_video, const void* a_text, const voi
   if (int rc = check_row_shape(H, D, "or_pack_gather")) return rc;
   if (n_rows < 0) return fail_arg("or_pack_gather: n_rows < 0");
   if (n_rows == 0) return 0;
-  if (!a_video || !src_idx || !a_out) return fail_arg("or_pack_gather: a_video, src_idx and a_out are required");
-  if (b_out && !b_video) return fail_arg("or_pack_gather: b_out given without b_video");
-  if ((rope_row || move_from) && (!cos_table || !sin_table || n_rope_rows < 1))
-    return fail_arg("or_pack_gather: rotation needs cos / sin tables");
-  if (move_from && !rope_row) return fail_arg("or_pack_gather: move_from needs rope_row (the second rotation)");
-  if (!aligned16(a_video) || !aligned16(a_out) || (a_text && !aligned16(a_text)) || (b_video && !aligned16(b_video)) ||
-      (b_text && !aligned16(b_text)) || (b_out && !aligned16(b_out)) || src_row_stride % 8 || text_row_stride % 8)
-    return fail_arg("or_pack_gather: pointers must be 16-byte aligned and row strides multiples of 8 elements");
-  GatherArgs g{(const uint16_t*)a_video, (const uint16_t*)(a_text ? a_text : a_video),
-               (const uint16_t*)b_video, (const uint16_t*)(b_text ? b_text : b_video),
-               src_row_stride, text_row_stride, n_video, src_idx, rope_row, move_from, cos_table, sin_table,
-               n_rope_rows, n_rows, H, D, (uint16_t*)a_out, (uint16_t*)b_out, 0, shared_d0(H, D)};
-  if ((int64_t)H * D < 64 * 8)   // rows under 64 chunks share a wavefront
-    hipLaunchKernelGGL((pack_gather_kernel<true, false>), dim3(row_grid(n_rows)), dim3(kThreads), 0,
-                       (hipStream_t)stream, g);
-  else
-    hipLaunchKernelGGL((pack_gather_kernel<false, false>), dim3(row_grid(n_rows)), dim3(kThreads), 0,
-                       (hipStream_t)stream, g);
-  return check_hip(hipGetLastError(), "pack_gather_kernel launch");
+  if (int rc = check_pack_job(a_video, a_text, b_video, b_text, src_row_stride, text_row_stride, src_idx, rope_row,
+                              move_from, cos_table, sin_table, n_rope_rows, a_out, b_out, "or_pack_gather"))
+    return rc;
+  GatherArgs g{};
+  g.job[0] = pack_job(a_video, a_text, b_video, b_text, src_row_stride, text_row_stride, src_idx, nullptr, rope_row,
+                      move_from, n_rows, a_out, b_out);
+  g.n_video = n_video;
+  g.cos_t = cos_table;
+  g.sin_t = sin_table;
+  g.n_rope_rows = n_rope_rows;
+  g.H = H;
+  g.D = D;
+  g.shared_d0 = shared_d0(H, D);
+  return launch_rows(g, (hipStream_t)stream);
 }
 
 extern "C" int or_rotate_rows(const void* x, int64_t x_row_stride, int64_t n_video, const int32_t* src_idx,
@@ -265,16 +321,54 @@ extern "C" int or_rotate_rows(const void* x, int64_t x_row_stride, int64_t n_vid
     return fail_arg("or_rotate_rows: row strides must cover H * D elements");
   if (!aligned16(x) || !aligned16(out) || x_row_stride % 8 || out_row_stride % 8)
     return fail_arg("or_rotate_rows: pointers must be 16-byte aligned and row strides multiples of 8 elements");
-  GatherArgs g{(const uint16_t*)x, (const uint16_t*)x, nullptr, nullptr, x_row_stride, x_row_stride, n_video, src_idx,
-               rope_row, nullptr, cos_table, sin_table, n_rope_rows, n_rows, H, D, (uint16_t*)out, nullptr,
-               out_row_stride, shared_d0(H, D)};
-  if ((int64_t)H * D < 64 * 8)
-    hipLaunchKernelGGL((pack_gather_kernel<true, true>), dim3(row_grid(n_rows)), dim3(kThreads), 0,
-                       (hipStream_t)stream, g);
-  else
-    hipLaunchKernelGGL((pack_gather_kernel<false, true>), dim3(row_grid(n_rows)), dim3(kThreads), 0,
-                       (hipStream_t)stream, g);
-  return check_hip(hipGetLastError(), "pack_gather_kernel launch");
+  GatherArgs g{};
+  g.job[0] = RowJob{(const uint16_t*)x, (const uint16_t*)x, nullptr, nullptr, x_row_stride, x_row_stride, src_idx,
+                    nullptr, rope_row, nullptr, (uint16_t*)out, nullptr, out_row_stride, n_rows, 1};
+  g.n_video = n_video;
+  g.cos_t = cos_table;
+  g.sin_t = sin_table;
+  g.n_rope_rows = n_rope_rows;
+  g.H = H;
+  g.D = D;
+  g.shared_d0 = shared_d0(H, D);
+  return launch_rows(g, (hipStream_t)stream);
+}
+
+extern "C" int or_pack_layer(const or_pack_args* p, void* stream) {
+  if (!p) return fail_arg("or_pack_layer: args is NULL");
+  const or_pack_args& x = *p;
+  if (int rc = check_row_shape(x.H, x.D, "or_pack_layer")) return rc;
+  if (x.n_keys < 0 || x.n_queries < 0) return fail_arg("or_pack_layer: negative row count");
+  if (x.n_keys > 0) {
+    if (int rc = check_pack_job(x.k_video, x.k_text, x.v_video, x.v_text, x.video_row_stride, x.text_row_stride,
+                                x.k_src, x.k_rope, x.k_move_from, x.cos_table, x.sin_table, x.n_rope_rows, x.k_out,
+                                x.v_out, "or_pack_layer"))
+      return rc;
+  }
+  if (x.n_queries > 0) {
+    if (!x.q || !x.q_src || !x.q_rope || !x.q_out || !x.cos_table || !x.sin_table || x.n_rope_rows < 1)
+      return fail_arg("or_pack_layer: the query rotation needs q, q_src, q_rope, q_out and the cos / sin tables");
+    if (x.q_row_stride < (int64_t)x.H * x.D || x.q_out_row_stride < (int64_t)x.H * x.D)
+      return fail_arg("or_pack_layer: query row strides must cover H * D elements");
+    if (!aligned16(x.q) || !aligned16(x.q_out) || x.q_row_stride % 8 || x.q_out_row_stride % 8)
+      return fail_arg("or_pack_layer: pointers must be 16-byte aligned and row strides multiples of 8 elements");
+  }
+  GatherArgs g{};
+  if (x.n_keys > 0)
+    g.job[0] = pack_job(x.k_video, x.k_text, x.v_video, x.v_text, x.video_row_stride, x.text_row_stride, x.k_src,
+                        x.v_src, x.k_rope, x.k_move_from, x.n_keys, x.k_out, x.v_out);
+  if (x.n_queries > 0)
+    g.job[1] = RowJob{(const uint16_t*)x.q, (const uint16_t*)x.q, nullptr, nullptr, x.q_row_stride, x.q_row_stride,
+                      x.q_src, nullptr, x.q_rope, nullptr, (uint16_t*)x.q_out, nullptr, x.q_out_row_stride,
+                      x.n_queries, 1};
+  g.n_video = x.n_video;
+  g.cos_t = x.cos_table;
+  g.sin_t = x.sin_table;
+  g.n_rope_rows = x.n_rope_rows;
+  g.H = x.H;
+  g.D = x.D;
+  g.shared_d0 = shared_d0(x.H, x.D);
+  return launch_rows(g, (hipStream_t)stream);
 }
 
 extern "C" int or_scatter(const void* packed, const int32_t* dst_idx, int64_t n_rows, int64_t n_video,

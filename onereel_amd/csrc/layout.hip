@@ -19,6 +19,10 @@
 // V_j's keys are packed as own frames, sentence, shared frames, so T_j's keys are the first rows of V_j's: T_j packs
 // none and its key range (k_off / k_len) points there. The attention result does not depend on the order of a
 // segment's keys.
+//
+// Every segment's keys start with its scene's own frames, which are consecutive token rows: the attention call can
+// read their values in place from the token-order V (v_lead / v_row, whole key blocks of them), and the pack copies
+// only the other value rows (v_src = -1 for the rows read in place).
 #include <stdarg.h>
 #include <stdio.h>
 #include <string.h>
@@ -69,6 +73,13 @@ __host__ __device__ inline int seg_keys(const LayoutDerived& L, int s) {
   int a, b;
   scene_queries(L, j, &a, &b);
   return b > a ? own + (L.sh_ptr[j + 1] - L.sh_ptr[j]) * L.T + txt : 0;
+}
+
+// keys at the head of segment s whose values the attention call reads in place from the token-order rows: every
+// segment's keys start with its scene's own frames (tokens lo * T ..), whole key blocks of them
+__host__ __device__ inline int seg_v_lead(const LayoutDerived& L, int s) {
+  const int j = seg_scene(L.with_text, s);
+  return seg_keys(L, s) > 0 ? ((L.hi[j] - L.lo[j]) * L.T) / OR_VARLEN_KEY_BLOCK * OR_VARLEN_KEY_BLOCK : 0;
 }
 
 // query count and packed key rows of segment s (T_j packs no keys when they are read in place from V_j's)
@@ -172,7 +183,7 @@ __device__ inline int upper_bound(const int* a, int n, int x) {  // first i in [
 }
 
 struct RowOut {
-  int32_t *q_src, *q_rope, *k_src, *k_rope, *k_move_a, *k_move_b, *k_off, *k_len;
+  int32_t *q_src, *q_rope, *k_src, *k_rope, *k_move_a, *k_move_b, *k_off, *k_len, *v_lead, *v_row, *v_src;
 };
 
 __global__ __launch_bounds__(kThreads) void layout_kernel(const or_layout_desc d, RowOut out, int32_t* cu_q_out,
@@ -293,6 +304,8 @@ __global__ __launch_bounds__(kThreads) void layout_kernel(const or_layout_desc d
         if (seg_q_src_out) seg_q_src_out[s] = text ? L.F * L.T + L.t0[j] : qa;
         if (out.k_off) out.k_off[s] = text && L.text_in_place ? S.cu_k[s - 1] : S.cu_k[s];
         if (out.k_len) out.k_len[s] = seg_keys(L, s);
+        if (out.v_lead) out.v_lead[s] = seg_v_lead(L, s);
+        if (out.v_row) out.v_row[s] = L.lo[j] * L.T;
       }
     }
   }
@@ -339,6 +352,8 @@ __global__ __launch_bounds__(kThreads) void layout_kernel(const or_layout_desc d
       idx = slot - own;
       row0 = base + (kind == 1 ? slot : own + nsh) * T;
     }
+    // values of the run's rows x < lead0 are read in place (own-frame rows inside the segment's v_lead)
+    const int lead0 = !qside && kind == 0 ? seg_v_lead(L, s) - idx * T : 0;
     int count, src0, rope0 = -1, ma0 = -1, mb0 = -1;
     bool rope = false, move = false;
     if (qside && kind == 0) {
@@ -387,6 +402,7 @@ __global__ __launch_bounds__(kThreads) void layout_kernel(const or_layout_desc d
         if (out.k_rope) out.k_rope[row0 + x] = rope ? rope0 + x : -1;
         if (out.k_move_a) out.k_move_a[row0 + x] = move ? ma0 + x : -1;
         if (out.k_move_b) out.k_move_b[row0 + x] = move ? mb0 + x : -1;
+        if (out.v_src) out.v_src[row0 + x] = x < lead0 ? -1 : src0 + x;
       }
     }
   }
@@ -539,7 +555,8 @@ extern "C" int or_layout_build(const or_layout_desc* desc, const or_layout_out* 
   int rc = plan_impl(desc, &sz, &L);
   if (rc) return rc;
   if (!out) return fail_arg("or_layout_build: out is NULL");
-  RowOut ro{out->q_src, out->q_rope, out->k_src, out->k_rope, out->k_move_a, out->k_move_b, out->k_off, out->k_len};
+  RowOut ro{out->q_src, out->q_rope, out->k_src, out->k_rope, out->k_move_a, out->k_move_b, out->k_off, out->k_len,
+            out->v_lead, out->v_row, out->v_src};
   // one block per run (frame or sentence of a segment), at most 2048
   int64_t runs = 0;
   for (int s = 0; s < sz.n_seg; ++s) {

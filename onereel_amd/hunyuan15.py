@@ -3,8 +3,10 @@
 `Processor.__call__` keeps the diffusers processor signature (hunyuan15.py:177-210): the QKV projections and the
 RMSNorms run as the model's own torch modules; the scene-attention layer (RoPE, scope packing, varlen attention,
 write-back) runs as HIP kernels through `onereel_amd.scene`, with the scene RoPE fused into the K pack and the Q
-load. The multi-GPU modes of the reference (K/V gathering, Ulysses, ring) and subject links are not implemented; the
-head-major bounded memory is `onereel_amd.memory`, called directly rather than through this processor.
+load. With `Context.memory` = M > 0 the processor runs the head-major bounded memory instead
+(`Processor.memory`, hunyuan15.py:200-201,305-334): q / k rotated once in token order, then `onereel_amd.memory`'s
+MemoryAttention over every scene's frames, sentence and M representatives per head of the other scenes. The
+multi-GPU modes of the reference (K/V gathering, Ulysses, ring) and subject links are not implemented.
 """
 from __future__ import annotations
 
@@ -14,9 +16,11 @@ from itertools import accumulate
 
 import torch
 
+from . import _lib as L
 from .frame_memory import FrameMemory
 from .layout import SceneLayout
-from .scene import ScopePlan, scene_attention
+from .memory import BoundaryMemory, MemoryAttention, frame_plan
+from .scene import ScopePlan, rotate_queries, scene_attention
 
 
 @dataclass
@@ -29,6 +33,7 @@ class Context:
     shared_switch: int = 10
     scene_rope: bool = False             # temporal RoPE index restarts at every scene (+1 after scene 0)
     rope_lengths: list = None            # scene lengths for scene_rope (default: the attention layout's)
+    memory: int = 0                      # M > 0: bounded cross-scene memory of M representatives per head (halo 0)
     frame_memory: FrameMemory = None
     T: int = 0
     fwd: int = 0
@@ -36,6 +41,7 @@ class Context:
     fused: bool = True                   # Q read and outputs written in place (False: the reference's packed flow)
     _cache: dict = field(default_factory=dict)
     _rot_full: tuple = None
+    _mem: MemoryAttention = None         # the bounded memory's state (centroids per layer and branch, plans)
 
     def step(self) -> int:
         """denoising step of the current forward (forwards count from 1; with CFG a step takes two forwards)"""
@@ -123,6 +129,27 @@ def scene_rope_rows(ctx: Context, device) -> torch.Tensor:
     return ctx._cache[key]
 
 
+def memory_attention(ctx: Context) -> MemoryAttention:
+    """the context's bounded memory of ctx.memory representatives per head, created on first use (the reference's
+    setup creates it, hunyuan15.py:590-592): it replaces the halo frames, so the layout has none"""
+    if ctx._mem is None:
+        if ctx.layout.halo != 0:
+            raise L.HipValueError('the bounded memory replaces the halo frames: use halo = 0')
+        ctx._mem = MemoryAttention(BoundaryMemory(ctx.memory))
+    return ctx._mem
+
+
+def rotate_tokens(ctx: Context, x: torch.Tensor, cos, sin) -> torch.Tensor:
+    """x [F*T, H, D] rotated at every video token's rotary row (its scene row with scene_rope), in token order: the
+    q / k RoPE of Processor.__call__ (hunyuan15.py:183-191) as one or_rotate_rows launch"""
+    lay = ctx.layout
+    key = ('tokens', tuple(lay.lengths), ctx.T, ctx.scene_rope, tuple(ctx.rope_lengths or ()), str(x.device))
+    if key not in ctx._cache:
+        ctx._cache[key] = ScopePlan(SceneLayout(list(lay.lengths), halo=0), ctx.T, None, 0, ctx.scene_rope,
+                                    ctx.rope_lengths, False, False, x.device)
+    return rotate_queries(ctx._cache[key], x, cos, sin)
+
+
 class Processor:
     """the HunyuanVideo-1.5 attention processor with scene attention (hunyuan15.py:173-251), one GPU"""
 
@@ -143,7 +170,11 @@ class Processor:
         if attn.norm_added_k is not None:
             ek = attn.norm_added_k(ek)
         eq, ek, ev = (x[0].to(torch.bfloat16) for x in (eq, ek, ev))
-        hs, ehs = self.scene_raw(q, k, v, eq, ek, ev, cos, sin)
+        if ctx.memory:
+            q, k = rotate_tokens(ctx, q, cos, sin), rotate_tokens(ctx, k, cos, sin)
+            hs, ehs = self.memory(q, k, v, eq, ek, ev)
+        else:
+            hs, ehs = self.scene_raw(q, k, v, eq, ek, ev, cos, sin)
         hs = attn.to_out[1](attn.to_out[0](hs.flatten(1, 2)[None].to(hidden_states.dtype)))
         ehs = attn.to_add_out(ehs.flatten(1, 2)[None].to(hidden_states.dtype))
         return hs, ehs
@@ -163,3 +194,21 @@ class Processor:
         plan = scope_plan(ctx, eq.shape[0], q.device, moves=adjacent)
         cos, sin = ctx._rot_full if adjacent else (None, None)
         return scene_attention(plan, q, k, v, eq, ek, ev, cos, sin, mode='rotated', fused=ctx.fused)
+
+    def memory(self, q, k, v, eq, ek, ev):
+        """the bounded cross-scene memory on one GPU (hunyuan15.py:305-334, world 1): q / k already rotated. Every
+        scene's video queries read its frames, its sentence and M representatives per head of the other scenes'
+        boundary keys; its sentence queries read its frames and its sentence. Returns (video out, text out); text
+        rows past the valid tokens are zero."""
+        ctx, T, lay = self.ctx, self.ctx.T, self.ctx.layout
+        mem = memory_attention(ctx)
+        Sq = q.shape[0]
+        if Sq != lay.n_frames * T:
+            raise L.HipValueError(f'{Sq} video rows, the layout has {lay.n_frames * T}')
+        pk = (ctx.cond(), Sq, k.shape[0])
+        if pk not in mem.plans:
+            pieces = [(j, lo * T, hi * T) for j, (lo, hi) in enumerate(lay.ranges)]
+            mem.plans[pk] = frame_plan(lay, T, torch.arange(Sq), k.shape[0], pieces, ctx.text_ranges(),
+                                       set(range(lay.n_scenes)), Sq, q.device)
+        out = mem((self.layer, ctx.cond()), torch.cat([q, eq]), torch.cat([k, ek]), torch.cat([v, ev]), mem.plans[pk])
+        return out[:Sq], out[Sq:]

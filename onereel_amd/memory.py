@@ -222,7 +222,11 @@ class _Static:
                 raise L.HipValueError(f'plan query rows span [{lo}, {hi}], the query buffer has {Sq} rows')
             self.qidx = (rows[None] * H + torch.arange(H, device=device)[:, None]).flatten().to(torch.int32)
         local = p.pad.to(device)[p.pmask.to(device)]           # the local key rows, piece after piece
-        # the largest key-buffer row the plan names (once per plan), checked against each call's buffer
+        # the key-buffer rows the plan names (once per plan): none negative, the largest checked against each call's
+        # buffer (the kernels dereference them unchecked)
+        lo = min(int(local.min()) if local.numel() else 0, int(p.cand.min()) if p.cand.numel() else 0)
+        if lo < 0:
+            raise L.HipValueError(f'plan key rows include {lo}: rows must be >= 0')
         self.max_key_row = max(int(local.max()) if local.numel() else -1, int(p.cand.max()))
         self.local = local.to(torch.int64)
         # a piece that does not read the memory and has the same local rows as another piece (a scene's sentence
@@ -322,7 +326,7 @@ class MemoryAttention:
                                         k_off.data_ptr(), st.n, H, M, kidx.data_ptr(), k_len.data_ptr(),
                                         L.stream_handle(dev)), 'or_memory_index')
         # single-head rows: row * H + head of the [rows, H, D] buffers
-        kp, vp = gather_rows(k.view(Lk * H, 1, D), kidx, v.view(Lk * H, 1, D))
+        kp, vp = gather_rows(k.view(Lk * H, 1, D), kidx, v.view(Lk * H, 1, D), check=False)  # rows checked per plan
         max_k = max(st.lens) + M
         if st.in_place:
             out = torch.empty_like(q) if st.covers_all else torch.zeros_like(q)
@@ -330,8 +334,8 @@ class MemoryAttention:
             varlen(qv, kp, vp, st.cu_q, None, st.max_q, max_k, k_off=k_off, k_len=k_len, out=ov,
                    seg_q_src=st.seg_q_src, n_q_video=Sq * H, sum_q=st.sum_q, q_row_step=H)
             return out
-        qp = gather_rows(q.view(Sq * H, 1, D), st.qidx)
+        qp = gather_rows(q.view(Sq * H, 1, D), st.qidx, check=False)
         o = varlen(qp, kp, vp, st.cu_q, None, st.max_q, max_k, k_off=k_off, k_len=k_len)
         out = torch.zeros_like(q)
-        scatter_rows(o, st.qidx, out.view(Sq * H, 1, D))
+        scatter_rows(o, st.qidx, out.view(Sq * H, 1, D), check=False)
         return out

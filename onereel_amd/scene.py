@@ -4,9 +4,10 @@ One layer of `Processor.scene` on one GPU (src/onereel/models/hunyuan15.py:212-2
 launches on the caller's current stream, with no host synchronisation:
 
     ScopePlan.build      or_layout_build   cu_seqlens, gather rows, RoPE rows (cached per layout and step mode)
-    pack_kv              or_pack_gather    K (rotated on the way) and V rows of every scope, one pass
-    rotate_queries       or_rotate_rows    the video queries rotated once, in token order
-    attention            or_varlen_fwd     Q read in place, output written in place
+    pack_layer           or_pack_layer     K rows of every scope (rotated on the way), the V rows the attention call
+                                           does not read in place, and the video queries rotated once in token
+                                           order, one pass
+    attention            or_varlen_fwd     Q read in place, the own-frame values read in place, output written in place
     zero text padding    or_scatter        ot rows past the valid text (ot = eq.new_zeros in the reference)
 
 `mode` says what q / k hold: 'raw' (before RoPE: the fused path, the table row of every query and key comes from
@@ -67,8 +68,11 @@ def _desc(lay: SceneLayout, T: int, counts, text_rows: int, scene_rope: bool, ro
 class ScopePlan:
     """The packed layout of one request's scopes, built on the device by `or_layout_build`.
 
-    Attributes (int32 device tensors): cu_q, cu_k [n_seg+1], seg_q_src, k_off, k_len [n_seg], q_src / q_rope
-    [sum_q], k_src / k_rope [sum_k], and for mode 'rotated' with moved shared frames k_move_a / k_move_b [sum_k].
+    Attributes (int32 device tensors): cu_q, cu_k [n_seg+1], seg_q_src, k_off, k_len, v_lead, v_row [n_seg], q_src /
+    q_rope [sum_q], k_src / k_rope / v_src [sum_k], and for mode 'rotated' with moved shared frames k_move_a /
+    k_move_b [sum_k]. v_lead / v_row / v_src: every segment's first keys are its scene's own frames, consecutive token
+    rows; the attention call reads the values of v_lead of them (whole key blocks) in place from token row v_row on,
+    and the pack copies only the values of the other keys (v_src[r] = -1 for the rows read in place).
     Host ints: n_seg, sum_q, sum_k, max_q, max_k, n_video, text_rows, max_rope_row.
 
     text_keys_in_place: each scene's video segment packs its keys as own frames, sentence, shared frames, and the
@@ -100,6 +104,7 @@ class ScopePlan:
         new = lambda n: torch.empty(int(n), dtype=torch.int32, device=dev)
         self.cu_q, self.cu_k, self.seg_q_src = new(self.n_seg + 1), new(self.n_seg + 1), new(self.n_seg)
         self.k_off, self.k_len = new(self.n_seg), new(self.n_seg)
+        self.v_lead, self.v_row, self.v_src = new(self.n_seg), new(self.n_seg), new(self.sum_k)
         self.q_src, self.q_rope = new(self.sum_q), new(self.sum_q)
         self.k_src, self.k_rope = new(self.sum_k), new(self.sum_k)
         self.k_move_a = new(self.sum_k) if moves and adjacent else None
@@ -112,7 +117,7 @@ class ScopePlan:
         """(re)run the layout kernel on the current stream"""
         out = L.LayoutOut(*(L.ptr(t) for t in (self.cu_q, self.cu_k, self.seg_q_src, self.q_src, self.q_rope,
                                                 self.k_src, self.k_rope, self.k_move_a, self.k_move_b, self.k_off,
-                                                self.k_len)))
+                                                self.k_len, self.v_lead, self.v_row, self.v_src)))
         with torch.cuda.device(self.device):
             L.check(L.lib().or_layout_build(ctypes.byref(self.desc), ctypes.byref(out), L.stream_handle()),
                     'or_layout_build')
@@ -128,7 +133,7 @@ class ScopePlan:
 
     def index_bytes(self) -> int:
         """bytes the layout kernel writes"""
-        n = 2 * (self.n_seg + 1) + 3 * self.n_seg + 2 * self.sum_q + 2 * self.sum_k
+        n = 2 * (self.n_seg + 1) + 5 * self.n_seg + 2 * self.sum_q + 3 * self.sum_k
         if self.k_move_a is not None:
             n += 2 * self.sum_k
         return 4 * n
@@ -197,9 +202,20 @@ def pack_rows(plan: ScopePlan, video: torch.Tensor, text: torch.Tensor | None, w
     return (out, b_out) if b_video is not None else out
 
 
-def gather_rows(src: torch.Tensor, idx: torch.Tensor, b_src: torch.Tensor | None = None):
+def _check_row_range(idx: torch.Tensor, n: int, what: str):
+    """every entry of the int32 device tensor idx in [0, n): the kernels dereference them unchecked, so a row out of
+    range is an error here, before any launch (one device reduction and one host read)"""
+    if idx.numel() == 0:
+        return
+    lo, hi = (int(x) for x in torch.aminmax(idx))
+    if lo < 0 or hi >= n:
+        raise L.HipValueError(f'{what}: rows span [{lo}, {hi}], outside [0, {n})')
+
+
+def gather_rows(src: torch.Tensor, idx: torch.Tensor, b_src: torch.Tensor | None = None, check: bool = True):
     """rows idx of src [N, H, D] (and of b_src, same shape and stride) packed into new [len(idx), H, D] tensors in
-    one pass of or_pack_gather; idx: int32 GPU tensor of rows in [0, N)"""
+    one pass of or_pack_gather; idx: int32 GPU tensor of rows in [0, N), checked on the host unless check=False (for
+    callers whose indices are validated once per plan)"""
     N, H, D = src.shape
     _check_bf16(src, b_src)
     _, ss = _rows2d(src, H, D)
@@ -207,6 +223,8 @@ def gather_rows(src: torch.Tensor, idx: torch.Tensor, b_src: torch.Tensor | None
         raise L.HipValueError('b_src must have the shape and row stride of src')
     if idx.dtype != torch.int32 or not idx.is_cuda or not idx.is_contiguous():
         raise L.HipTypeError('idx must be a contiguous int32 GPU tensor')
+    if check:
+        _check_row_range(idx, N, 'gather_rows')
     n = idx.numel()
     out = torch.empty(n, H, D, dtype=src.dtype, device=src.device)
     b_out = torch.empty_like(out) if b_src is not None else None
@@ -216,13 +234,16 @@ def gather_rows(src: torch.Tensor, idx: torch.Tensor, b_src: torch.Tensor | None
     return (out, b_out) if b_src is not None else out
 
 
-def scatter_rows(packed: torch.Tensor, idx: torch.Tensor, out: torch.Tensor):
-    """out[idx[r]] = packed[r] for out [N, H, D] (rows not named keep their contents), one pass of or_scatter"""
+def scatter_rows(packed: torch.Tensor, idx: torch.Tensor, out: torch.Tensor, check: bool = True):
+    """out[idx[r]] = packed[r] for out [N, H, D] (rows not named keep their contents), one pass of or_scatter; idx
+    in [0, N), checked on the host unless check=False"""
     n, H, D = packed.shape
     _check_bf16(packed, out)
     _, os_ = _rows2d(out, H, D)
     if idx.dtype != torch.int32 or not idx.is_cuda or not idx.is_contiguous() or idx.numel() != n:
         raise L.HipTypeError('idx must be a contiguous int32 GPU tensor with one entry per packed row')
+    if check:
+        _check_row_range(idx, out.shape[0], 'scatter_rows')
     L.check(L.lib().or_scatter(packed.data_ptr(), idx.data_ptr(), n, out.shape[0], out.data_ptr(), None, os_, os_, 0,
                                0, H, D, L.stream_handle(out.device)), 'or_scatter')
     return out
@@ -230,10 +251,12 @@ def scatter_rows(packed: torch.Tensor, idx: torch.Tensor, out: torch.Tensor):
 
 def varlen(q, k, v, cu_q, cu_k, max_q, max_k, *, k_off=None, k_len=None, out=None, lse=None, seg_q_src=None,
            q_text=None, o_text=None, n_q_video=None, q_rope=None, cos=None, sin=None, sum_q=None, workspace=None,
-           scale=None, noalloc=False, q_row_step=1):
+           scale=None, noalloc=False, q_row_step=1, v_tok=None, v_lead=None, v_row=None):
     """or_varlen_fwd on torch tensors. Returns out (allocated [Nq, H, D] when not given). noalloc=True calls
     or_varlen_fwd_noalloc instead: no workspace, the library's fixed per-GPU array (calls must not overlap on a GPU).
-    q_row_step > 1 (with seg_q_src): query i of segment s is row seg_q_src[s] + i * q_row_step of q and of out."""
+    q_row_step > 1 (with seg_q_src): query i of segment s is row seg_q_src[s] + i * q_row_step of q and of out.
+    v_tok (with v_lead, v_row): the values of segment s's first v_lead[s] keys are rows v_row[s].. of v_tok (row stride
+    of k), the others rows k_off[s] + v_lead[s].. of v."""
     H, D = k.shape[1], k.shape[2]
     _check_bf16(q, k, v, q_text, out, o_text)
     _, qs = _rows2d(q, H, D)
@@ -243,9 +266,15 @@ def varlen(q, k, v, cu_q, cu_k, max_q, max_k, *, k_off=None, k_len=None, out=Non
     if q_text is not None and q_text.shape[0] and q_text.stride(0) != qs:
         raise L.HipValueError('q and q_text must have the same row stride')
     n_seg = (cu_q.numel() - 1)
-    for t in (cu_q, cu_k, k_off, k_len, seg_q_src, q_rope):
+    for t in (cu_q, cu_k, k_off, k_len, seg_q_src, q_rope, v_lead, v_row):
         if t is not None and (t.dtype != torch.int32 or not t.is_cuda or not t.is_contiguous()):
             raise L.HipTypeError('index arrays must be contiguous int32 GPU tensors')
+    if v_tok is not None:
+        _check_bf16(v_tok)
+        if v_lead is None or v_row is None:
+            raise L.HipValueError('v_tok needs v_lead and v_row')
+        if _rows2d(v_tok, H, D)[1] != ks:
+            raise L.HipValueError('v_tok must have the row stride of k and v')
     if sum_q is None:
         sum_q = q.shape[0] if seg_q_src is None else None
         if sum_q is None:
@@ -272,6 +301,8 @@ def varlen(q, k, v, cu_q, cu_k, max_q, max_k, *, k_off=None, k_len=None, out=Non
     a.n_seg, a.sum_q, a.max_q, a.max_k, a.H, a.D = int(n_seg), int(sum_q), int(max_q), int(max_k), H, D
     a.scale = float(D ** -0.5 if scale is None else scale)
     a.q_row_step = int(q_row_step)
+    if v_tok is not None:
+        a.v_tok, a.v_lead, a.v_row, a.v_tok_rows = v_tok.data_ptr(), v_lead.data_ptr(), v_row.data_ptr(), v_tok.shape[0]
     if noalloc:
         a.workspace, a.workspace_bytes = None, 0
         with torch.cuda.device(q.device):
@@ -329,14 +360,75 @@ def rotate_queries(plan: ScopePlan, q, cos, sin, out=None):
     return out
 
 
+def pack_layer(plan: ScopePlan, k, ek, v, ev, cos=None, sin=None, mode='raw', kbuf=None, vbuf=None, q=None,
+               qbuf=None, values_in_place=True):
+    """One launch of or_pack_layer: the plan's packed keys (rotated per `mode`, as pack_rows) into kbuf, the values
+    into vbuf (only the rows the attention call does not read in place when values_in_place: plan.v_src), and, when q
+    is given, the video queries rotated once in token order into qbuf (as rotate_queries). Returns (kbuf, vbuf,
+    qbuf)."""
+    H, D = k.shape[1], k.shape[2]
+    _check_bf16(k, ek, v, ev, q, kbuf, vbuf, qbuf)
+    _, vs = _rows2d(k, H, D)
+    ts = _rows2d(ek, H, D)[1] if ek is not None and ek.shape[0] else vs
+    if _rows2d(v, H, D)[1] != vs or (ev is not None and ev.shape[0] and ev.stride(0) != ts):
+        raise L.HipValueError('value rows must have the strides of the key rows')
+    if mode not in MODES:
+        raise L.HipValueError(mode)
+    rope = move = None
+    if mode == 'raw':
+        rope = plan.k_rope
+    elif mode == 'rotated' and plan.adjacent:
+        if plan.k_move_a is None:
+            raise L.HipValueError('plan was built without move rows (moves=True)')
+        rope, move = plan.k_move_b, plan.k_move_a
+    need_tab = rope is not None or q is not None
+    cos, sin, n_rows = _tables(cos, sin, D) if need_tab else (None, None, 0)
+    if need_tab and cos is None:
+        raise L.HipValueError('RoPE needs the (cos, sin) tables')
+    if need_tab and plan.max_rope_row >= n_rows:
+        raise L.HipValueError(f'layout needs rotary row {plan.max_rope_row} but the table has {n_rows} rows')
+    new = lambda n: torch.empty(n, H, D, dtype=torch.bfloat16, device=k.device)
+    kbuf = new(plan.sum_k) if kbuf is None else kbuf
+    vbuf = new(plan.sum_k) if vbuf is None else vbuf
+    for t in (kbuf, vbuf):
+        if t.shape[0] < plan.sum_k or not t.is_contiguous():
+            raise L.HipValueError(f'pack buffers must be contiguous with {plan.sum_k} rows')
+    a = L.PackArgs()
+    a.k_video, a.k_text = k.data_ptr(), L.ptr(ek if ek is not None and ek.shape[0] else None)
+    a.v_video, a.v_text = v.data_ptr(), L.ptr(ev if ev is not None and ev.shape[0] else None)
+    a.video_row_stride, a.text_row_stride, a.n_video = vs, ts, plan.n_video
+    a.k_src, a.k_rope, a.k_move_from = plan.k_src.data_ptr(), L.ptr(rope), L.ptr(move)
+    a.v_src = plan.v_src.data_ptr() if values_in_place else None
+    a.n_keys, a.k_out, a.v_out = plan.sum_k, kbuf.data_ptr(), vbuf.data_ptr()
+    if q is not None:
+        _, qs = _rows2d(q, H, D)
+        if q.shape[0] != plan.n_video:
+            raise L.HipValueError(f'{q.shape[0]} video query rows, layout has {plan.n_video}')
+        qbuf = torch.empty_like(q) if qbuf is None else qbuf
+        _, qos = _rows2d(qbuf, H, D)
+        if qbuf.shape[0] < plan.n_video:
+            raise L.HipValueError(f'qbuf holds {qbuf.shape[0]} rows, the layout has {plan.n_video} video rows')
+        a.q, a.q_row_stride, a.q_src, a.q_rope = q.data_ptr(), qs, plan.q_src.data_ptr(), plan.q_rope.data_ptr()
+        a.n_queries, a.q_out, a.q_out_row_stride = plan.sum_q, qbuf.data_ptr(), qos
+    a.cos_table, a.sin_table, a.n_rope_rows = L.ptr(cos), L.ptr(sin), n_rows
+    a.H, a.D = H, D
+    L.check(L.lib().or_pack_layer(ctypes.byref(a), L.stream_handle(k.device)), 'or_pack_layer')
+    return kbuf, vbuf, qbuf
+
+
 def scene_attention(plan: ScopePlan, q, k, v, eq, ek, ev, cos=None, sin=None, mode='raw', fused=True,
-                    kbuf=None, vbuf=None, qbuf=None, rotate_q='pre'):
+                    kbuf=None, vbuf=None, qbuf=None, rotate_q='pre', values_in_place=True):
     """(ov, ot) of one scene-attention layer. q / k / v [F*T, H, D] and eq / ek / ev [Le, H, D] bf16 on the GPU.
 
-    fused=True: K/V packed once, Q read in place, outputs written in place. fused=False: the reference's data flow
-    (Q, K, V packed, one varlen call on packed tensors, write-back by the scatter kernel). With mode 'raw' and
-    fused=True the video queries are rotated once ahead of the attention call (rotate_q='pre', into qbuf when given;
-    the attention kernel then reads no rotary table), or on the attention kernel's Q load (rotate_q='load')."""
+    fused=True: one pack launch (K rows, the V rows not read in place, and the video queries rotated once when
+    mode is 'raw' and rotate_q='pre', into qbuf when given), then the attention call with Q read in place, the own-frame
+    values read in place from v (values_in_place, when v's rows are H * D elements apart, as the packed rows are) and
+    the outputs written in place. rotate_q='load' rotates the queries on the attention kernel's Q load instead.
+    fused=False: the reference's data flow (Q, K, V packed, one varlen call on packed tensors, write-back by the
+    scatter kernel).
+
+    With a plan for one rank's share (q_range), ov rows outside the rank's video tokens are zero, as are ot rows of
+    the sentences the rank does not run (ot = eq.new_zeros in the reference)."""
     if mode not in MODES:
         raise L.HipValueError(mode)
     H, D = q.shape[1], q.shape[2]
@@ -344,25 +436,28 @@ def scene_attention(plan: ScopePlan, q, k, v, eq, ek, ev, cos=None, sin=None, mo
         raise L.HipValueError(f'{q.shape[0]} video rows, layout has {plan.n_video}')
     if plan.with_text and eq.shape[0] != plan.text_rows:
         raise L.HipValueError(f'{eq.shape[0]} text rows, layout has {plan.text_rows}')
-    kp, vp = pack_rows(plan, k, ek, 'k', out=kbuf, b_video=v, b_text=ev, b_out=vbuf, cos=cos, sin=sin, mode=mode)
-    ov = torch.empty_like(q)
-    # one rank's share writes only its own scenes' sentence rows: the others stay zero (ot = eq.new_zeros)
-    make_ot = torch.zeros if plan.q_range is not None else torch.empty
-    ot = make_ot(eq.shape[0], H, D, dtype=q.dtype, device=q.device) if eq is not None else None
+    # one rank's share writes only its own rows: the others stay zero
+    make = torch.zeros if plan.q_range is not None else torch.empty
+    ov = make(q.shape, dtype=q.dtype, device=q.device)
+    ot = make(eq.shape[0], H, D, dtype=q.dtype, device=q.device) if eq is not None else None
     qmode = 'raw' if mode == 'raw' else 'none'
     if fused:
         if rotate_q not in ('pre', 'load'):
             raise L.HipValueError(f"rotate_q must be 'pre' or 'load', got {rotate_q!r}")
         on_load = qmode == 'raw' and rotate_q == 'load'
-        if qmode == 'raw' and not on_load:
-            q = rotate_queries(plan, q, cos, sin, out=qbuf)
-        varlen(q, kp, vp, plan.cu_q, plan.cu_k, plan.max_q, plan.max_k, k_off=plan.k_off, k_len=plan.k_len, out=ov,
-               seg_q_src=plan.seg_q_src, q_text=eq, o_text=ot, n_q_video=plan.n_video,
+        pre = qmode == 'raw' and not on_load
+        in_place = bool(values_in_place) and v.dim() == 3 and v.stride(0) == H * D and v.is_contiguous()
+        kp, vp, qr = pack_layer(plan, k, ek, v, ev, cos, sin, mode, kbuf, vbuf, q=q if pre else None, qbuf=qbuf,
+                                values_in_place=in_place)
+        vi = dict(v_tok=v, v_lead=plan.v_lead, v_row=plan.v_row) if in_place else {}
+        varlen(qr if pre else q, kp, vp, plan.cu_q, plan.cu_k, plan.max_q, plan.max_k, k_off=plan.k_off,
+               k_len=plan.k_len, out=ov, seg_q_src=plan.seg_q_src, q_text=eq, o_text=ot, n_q_video=plan.n_video,
                q_rope=plan.q_rope if on_load else None, cos=cos, sin=sin, sum_q=plan.sum_q,
-               workspace=plan.workspace(H, D))
+               workspace=plan.workspace(H, D), **vi)
         if ot is not None:
             zero_text_padding(plan, ot)
     else:
+        kp, vp = pack_rows(plan, k, ek, 'k', out=kbuf, b_video=v, b_text=ev, b_out=vbuf, cos=cos, sin=sin, mode=mode)
         qp = pack_rows(plan, q, eq, 'q', cos=cos, sin=sin, mode=qmode)
         op = varlen(qp, kp, vp, plan.cu_q, plan.cu_k, plan.max_q, plan.max_k, k_off=plan.k_off, k_len=plan.k_len,
                     workspace=plan.workspace(H, D))

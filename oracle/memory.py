@@ -70,20 +70,26 @@ def select(kc, M, iters=50, centroids=False, start=None):
     return (rep, valid, c) if centroids else (rep, valid)
 
 
-def masked_reference(q, k, v, eq, ek, ev, ranges, T, rep_row, rep_scene, valid, text_ranges):
-    """per head and scene softmax in float32 over the scope's keys -> (video out [S, H, D], text out [Le, H, D])"""
+def masked_reference(q, k, v, eq, ek, ev, ranges, T, rep_row, rep_scene, valid, text_ranges, video_rows=None,
+                     text_rows=None):
+    """per head and scene softmax in float32 over the scope's keys -> (video out [S, H, D], text out [Le, H, D]).
+    video_rows / text_rows (optional): only these query rows (of q / of eq) are computed, the others stay zero."""
     S, H, D = q.shape
     ov, ot = torch.zeros(S, H, D), torch.zeros(ek.shape[0], H, D)
     kk, vv = torch.cat([k, ek]).float(), torch.cat([v, ev]).float()
+    pick = lambda rows, a, b: torch.arange(a, b) if rows is None else torch.as_tensor(
+        [r for r in rows if a <= r < b], dtype=torch.long)
     for h in range(H):
         for j, (lo, hi) in enumerate(ranges):
             t0, t1 = text_ranges[j]
             local = list(range(lo * T, hi * T)) + [S + t for t in range(t0, t1)]
             far = [int(r) for r, s, ok in zip(rep_row[h], rep_scene[h], valid[h]) if ok and int(s) != j]
             keys = torch.tensor(local + far)
-            p = torch.softmax(q[lo * T:hi * T, h].float() @ kk[keys, h].T * D ** -0.5, -1)
-            ov[lo * T:hi * T, h] = p @ vv[keys, h]
+            qr = pick(video_rows, lo * T, hi * T)
+            p = torch.softmax(q[qr, h].float() @ kk[keys, h].T * D ** -0.5, -1)
+            ov[qr, h] = p @ vv[keys, h]
             keys = torch.tensor(local)
-            p = torch.softmax(eq[t0:t1, h].float() @ kk[keys, h].T * D ** -0.5, -1)
-            ot[t0:t1, h] = p @ vv[keys, h]
+            tr = pick(text_rows, t0, t1)
+            p = torch.softmax(eq[tr, h].float() @ kk[keys, h].T * D ** -0.5, -1)
+            ot[tr, h] = p @ vv[keys, h]
     return ov, ot

@@ -157,3 +157,23 @@ def sample_packed(cu, n, seed=0):
     g = np.random.default_rng(seed)
     edges = [x for a, b in zip(cu[:-1], cu[1:]) if b > a for x in (a, b - 1)]
     return np.unique(np.concatenate([g.integers(0, int(cu[-1]), n), np.asarray(edges, dtype=np.int64)]))
+
+
+class Attn(torch.nn.Module):
+    """the attention-module attributes a diffusers HunyuanVideo-1.5 block hands its processor"""
+
+    def __init__(self, C, H, gen):
+        super().__init__()
+        self.heads = H
+        mk = lambda: torch.nn.Linear(C, C, dtype=torch.bfloat16)
+        self.to_q, self.to_k, self.to_v = mk(), mk(), mk()
+        self.add_q_proj, self.add_k_proj, self.add_v_proj = mk(), mk(), mk()
+        self.norm_q = torch.nn.RMSNorm(C // H, eps=1e-6, dtype=torch.bfloat16)
+        self.norm_k = torch.nn.RMSNorm(C // H, eps=1e-6, dtype=torch.bfloat16)
+        self.norm_added_q = torch.nn.RMSNorm(C // H, eps=1e-6, dtype=torch.bfloat16)
+        self.norm_added_k = None
+        self.to_out = torch.nn.ModuleList([mk(), torch.nn.Dropout(0.0)])
+        self.to_add_out = mk()
+        with torch.no_grad():
+            for p in self.parameters():
+                p.copy_(torch.randn(p.shape, generator=gen) * 0.05)

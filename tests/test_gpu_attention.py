@@ -4,6 +4,7 @@ import numpy as np
 import pytest
 import torch
 
+from helpers import Attn as _Attn
 from helpers import assert_close, attn_rows_reference, layout_case, rand_bf16, sample_rows, scope_rows_reference
 from onereel_amd import _lib as L
 from onereel_amd import attention as A
@@ -446,26 +447,6 @@ def test_reference_flow_and_processor_scene_at_480p(adjacent):
         ov, ot = HY.Processor(ctx, 0).scene(gqr, gkr, g[2], g[3], g[4], g[5])
         assert_close(torch.cat([ov, ot]).cpu()[src], ref, what=f'480p Processor.scene fused={fused}')
         del ov, ot
-
-
-class _Attn(torch.nn.Module):
-    """the attention-module attributes a diffusers HunyuanVideo-1.5 block hands its processor"""
-
-    def __init__(self, C, H, gen):
-        super().__init__()
-        self.heads = H
-        mk = lambda: torch.nn.Linear(C, C, dtype=torch.bfloat16)
-        self.to_q, self.to_k, self.to_v = mk(), mk(), mk()
-        self.add_q_proj, self.add_k_proj, self.add_v_proj = mk(), mk(), mk()
-        self.norm_q = torch.nn.RMSNorm(C // H, eps=1e-6, dtype=torch.bfloat16)
-        self.norm_k = torch.nn.RMSNorm(C // H, eps=1e-6, dtype=torch.bfloat16)
-        self.norm_added_q = torch.nn.RMSNorm(C // H, eps=1e-6, dtype=torch.bfloat16)
-        self.norm_added_k = None
-        self.to_out = torch.nn.ModuleList([mk(), torch.nn.Dropout(0.0)])
-        self.to_add_out = mk()
-        with torch.no_grad():
-            for p in self.parameters():
-                p.copy_(torch.randn(p.shape, generator=gen) * 0.05)
 
 
 @torch.no_grad()

@@ -1,0 +1,177 @@
+"""GPU parity of the values read in place: the attention kernels' value stream switching from token-order rows
+(or_varlen_args.v_tok, the first v_lead keys of a segment) to packed rows, the one-launch pack of a layer
+(or_pack_layer: keys, the values not read in place, the rotated queries), and the layer with and without in-place
+values."""
+import numpy as np
+import pytest
+import torch
+
+from helpers import assert_close, layout_case, rand_bf16
+from onereel_amd import scene
+from onereel_amd.layout import SceneLayout
+from oracle import attention as OA
+from oracle import layout as OL
+
+pytestmark = [pytest.mark.gpu, pytest.mark.skipif(not torch.cuda.is_available(), reason='needs the GPU')]
+DEV = 'cuda'
+POISON = 3.0e4   # packed value rows the kernel must not read hold this (a read would move O far out of tolerance)
+
+
+def _lse_ref(q, k, cq, ck, D):
+    out = []
+    for s in range(len(cq) - 1):
+        qs, ks = q[cq[s]:cq[s + 1]].float(), k[ck[s]:ck[s + 1]].float()
+        out.append(torch.logsumexp(torch.einsum('qhd,khd->hqk', qs, ks) * D ** -0.5, -1))
+    return torch.cat(out, 1)
+
+
+def _in_place_case(lq, lk, lead_blocks, H, D, seed):
+    """segments with lq queries and lk keys; segment s takes the values of its first 32 * lead_blocks[s] keys from a
+    token-order tensor (at a random row), the others from the packed values, whose rows under the in-place keys hold
+    POISON. Returns the device arguments and the values as one packed tensor (the reference)."""
+    rng = np.random.default_rng(seed)
+    q = rand_bf16((sum(lq), H, D), seed)
+    k = rand_bf16((sum(lk), H, D), seed + 1)
+    v = rand_bf16((sum(lk), H, D), seed + 2)
+    cq, ck = np.cumsum([0] + lq), np.cumsum([0] + lk)
+    lead = [32 * b for b in lead_blocks]
+    n_tok = sum(lead) + 500
+    vtok = rand_bf16((n_tok, H, D), seed + 3)
+    rows = [int(rng.integers(0, n_tok - x + 1)) for x in lead]
+    vpacked = v.clone()
+    for s in range(len(lk)):
+        assert lead[s] <= lk[s]
+        v[ck[s]:ck[s] + lead[s]] = vtok[rows[s]:rows[s] + lead[s]]      # the values the kernel must use
+        vpacked[ck[s]:ck[s] + lead[s]] = POISON
+    t = lambda x: torch.tensor(x, dtype=torch.int32, device=DEV)
+    dev = dict(q=q.to(DEV), k=k.to(DEV), v=vpacked.to(DEV), cu_q=t(cq), cu_k=t(ck), max_q=max(lq), max_k=max(lk),
+               v_tok=vtok.to(DEV), v_lead=t(lead), v_row=t(rows))
+    return q, k, v, cq, ck, dev
+
+
+def _run(dev, lse=False, vfull=None):
+    a = dict(dev)
+    q, k, v, cu_q, cu_k, mq, mk = (a.pop(x) for x in ('q', 'k', 'v', 'cu_q', 'cu_k', 'max_q', 'max_k'))
+    if vfull is not None:      # every value packed: no in-place rows
+        v, a = vfull, {}
+    if not lse:
+        return scene.varlen(q, k, v, cu_q, cu_k, mq, mk, **a)
+    out = torch.empty_like(q)
+    l = torch.empty(q.shape[1], q.shape[0], dtype=torch.float32, device=DEV)
+    scene.varlen(q, k, v, cu_q, cu_k, mq, mk, out=out, lse=l, **a)
+    return out, l
+
+
+# lead blocks: none, one, the ring fill's range (2..6 for 8 slots), the key loop's (7 on), every whole block
+@pytest.mark.parametrize('D', [128, 64])
+@pytest.mark.parametrize('lq,lk,lead_blocks,H', [
+    ([300, 40, 257, 5], [40, 700, 1000, 300], [0, 1, 6, 9], 3),
+    ([129, 64, 500], [230, 250, 2049], [7, 2, 64], 2),
+    ([33, 1, 700, 90], [64, 32, 257, 5000], [2, 1, 8, 156], 4),
+    ([640, 0, 77], [3000, 100, 32], [93, 3, 1], 8),
+])
+def test_varlen_values_in_place(lq, lk, lead_blocks, H, D):
+    """O and lse against the fp32 oracle on the values the in-place rows name, and bit-identical to the same call
+    with every value packed (the kernels read the same value bits either way)"""
+    print(f'values in place lq={lq} lk={lk} lead blocks={lead_blocks} H={H} D={D}', flush=True)
+    q, k, v, cq, ck, dev = _in_place_case(lq, lk, lead_blocks, H, D, 71)
+    ref = OA.packed_attention(q, k, v, cq, ck)
+    o = _run(dev)
+    assert_close(o.cpu(), ref, what='values in place')
+    assert torch.equal(o, _run(dev, vfull=v.to(DEV)))
+    o2, lse = _run(dev, lse=True)
+    assert_close(o2.cpu(), ref, what='values in place, lse call')
+    assert (lse.cpu() - _lse_ref(q, k, cq, ck, D)).abs().max() < 2e-3
+
+
+@pytest.mark.parametrize('lq,lk,lead_blocks,H', [([1000], [20000], [600], 4), ([300, 7], [5000, 3000], [150, 40], 3),
+                                                 ([256, 256], [4000, 4000], [3, 125], 2)])
+def test_varlen_values_in_place_key_split(lq, lk, lead_blocks, H):
+    """few work items over long key ranges, split into key parts: each part's in-place blocks are those of its key
+    range (none, some, or all of its blocks)"""
+    D = 128
+    print(f'values in place, key split lq={lq} lk={lk} lead blocks={lead_blocks} H={H}', flush=True)
+    q, k, v, cq, ck, dev = _in_place_case(lq, lk, lead_blocks, H, D, 91)
+    ref = OA.packed_attention(q, k, v, cq, ck)
+    ws = torch.zeros(int(scene.L.lib().or_varlen_workspace_size(len(lq), sum(lq), H, D)), dtype=torch.uint8,
+                     device=DEV)
+    a = dict(dev)
+    qq, kk, vv, cu_q, cu_k, mq, mk = (a.pop(x) for x in ('q', 'k', 'v', 'cu_q', 'cu_k', 'max_q', 'max_k'))
+    o = scene.varlen(qq, kk, vv, cu_q, cu_k, mq, mk, workspace=ws, **a)
+    assert int(ws.view(torch.int32)[3]) > 0          # items were split
+    assert_close(o.cpu(), ref, what='values in place, key split')
+    o2, lse = _run(dev, lse=True)
+    assert_close(o2.cpu(), ref, what='values in place, key split, lse call')
+    assert (lse.cpu() - _lse_ref(q, k, cq, ck, D)).abs().max() < 2e-3
+
+
+def test_varlen_values_in_place_rows_past_the_token_rows():
+    """in-place blocks that would reach past the token-order rows are taken from the packed rows instead (here the
+    packed rows hold the right values there), so no read leaves v_tok"""
+    H, D = 2, 128
+    lq, lk = [100], [640]
+    q, k, v = rand_bf16((100, H, D), 5), rand_bf16((640, H, D), 6), rand_bf16((640, H, D), 7)
+    vtok = v[:300].clone()                      # 300 token rows: 9 whole blocks fit from row 0
+    t = lambda x: torch.tensor(x, dtype=torch.int32, device=DEV)
+    o = scene.varlen(q.to(DEV), k.to(DEV), v.to(DEV), t([0, 100]), t([0, 640]), 100, 640, v_tok=vtok.to(DEV),
+                     v_lead=t([640]), v_row=t([0]))
+    assert_close(o.cpu(), OA.packed_attention(q, k, v, [0, 100], [0, 640]), what='in-place blocks cut at v_tok')
+
+
+def _layer(name, adjacent, in_place_text=True, q_range=None):
+    case = layout_case(name)
+    H, D, T = case['H'], case['D'], case['T']
+    S = sum(case['lengths']) * T
+    g = [rand_bf16((S, H, D), i).to(DEV) for i in range(3)] + \
+        [rand_bf16((case['Le'], H, D), 3 + i).to(DEV) for i in range(3)]
+    cos, sin = (x.to(DEV) for x in OA.rope_table_3d(*case['table'], D))
+    lay = SceneLayout(case['lengths'], halo=case['halo'], sides=case['sides'], extra=case['extra'])
+    plan = scene.ScopePlan(lay, T, case['counts'], case['Le'], case['scene_rope'], None, adjacent, True, DEV,
+                           text_keys_in_place=in_place_text, q_range=q_range)
+    return case, plan, g, cos, sin
+
+
+@pytest.mark.parametrize('name', ['cpu_plumbing', 'hunyuan480p', 'uneven_K12', 'wan704'])
+@pytest.mark.parametrize('adjacent', [False, True])
+def test_pack_layer_bit_exact(name, adjacent):
+    """one or_pack_layer launch writes the keys or_pack_gather writes, the value rows whose v_src is not -1 as
+    or_pack_gather writes them (and no other value row), and the queries or_rotate_rows writes, bit for bit"""
+    print(f'pack layer {name} adjacent={adjacent}', flush=True)
+    case, plan, (q, k, v, eq, ek, ev), cos, sin = _layer(name, adjacent)
+    H, D = q.shape[1], q.shape[2]
+    kref, vref = scene.pack_rows(plan, k, ek, 'k', b_video=v, b_text=ev, cos=cos, sin=sin, mode='raw')
+    qref = scene.rotate_queries(plan, q, cos, sin)
+    kbuf = torch.empty(plan.sum_k, H, D, dtype=torch.bfloat16, device=DEV)
+    vbuf = torch.full_like(kbuf, 7.0)
+    qbuf = torch.empty_like(q)
+    scene.pack_layer(plan, k, ek, v, ev, cos, sin, 'raw', kbuf, vbuf, q=q, qbuf=qbuf)
+    bits = lambda x: x.view(torch.int16)
+    assert torch.equal(bits(kbuf), bits(kref))
+    assert torch.equal(bits(qbuf), bits(qref))
+    copied = plan.v_src >= 0
+    assert torch.equal(bits(vbuf[copied]), bits(vref[copied]))
+    assert bool((vbuf[~copied] == 7.0).all())
+    n_in_place = int((~copied).sum())
+    assert n_in_place == sum(int(x) for x in plan.v_lead.tolist()[0::2])   # the video segments own the packed rows
+    # keys only (mode 'rotated' with moves, no query rotation): the same keys as or_pack_gather
+    plan2 = scene.ScopePlan(plan.layout, case['T'], case['counts'], case['Le'], case['scene_rope'], None, adjacent,
+                            True, DEV, moves=True, text_keys_in_place=True)
+    kr2, vr2 = scene.pack_rows(plan2, k, ek, 'k', b_video=v, b_text=ev, cos=cos, sin=sin, mode='rotated')
+    kb2, vb2, _ = scene.pack_layer(plan2, k, ek, v, ev, cos, sin, 'rotated', values_in_place=False)
+    assert torch.equal(bits(kb2), bits(kr2)) and torch.equal(bits(vb2), bits(vr2))
+
+
+@pytest.mark.parametrize('name,q_range', [('hunyuan480p', None), ('uneven_K12', None), ('cpu_plumbing', None),
+                                          ('hunyuan480p', (8000, 30000))])
+@pytest.mark.parametrize('adjacent', [False, True])
+def test_layer_values_in_place_bit_identical(name, q_range, adjacent):
+    """the fused layer with the own-frame values read in place gives the same output bits as with every value
+    packed (text keys in place and packed; one rank's share)"""
+    for in_place_text in (True, False):
+        print(f'layer values in place {name} adjacent={adjacent} text keys in place={in_place_text} '
+              f'q_range={q_range}', flush=True)
+        _, plan, g, cos, sin = _layer(name, adjacent, in_place_text, q_range)
+        ov, ot = scene.scene_attention(plan, *g, cos, sin, mode='raw', fused=True, values_in_place=True)
+        ov2, ot2 = scene.scene_attention(plan, *g, cos, sin, mode='raw', fused=True, values_in_place=False)
+        assert torch.equal(ov, ov2) and torch.equal(ot, ot2)
+        del ov, ot, ov2, ot2

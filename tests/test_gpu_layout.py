@@ -40,6 +40,33 @@ def _check_plan(plan, sc, adjacent):
     if adjacent:
         assert eq(plan.k_move_a, sc.k_move_a) and eq(plan.k_move_b, sc.k_move_b)
     assert (plan.n_seg, plan.sum_q, plan.sum_k) == (len(sc.lq), int(sc.cu_q[-1]), int(sc.cu_k[-1]))
+    _check_values_in_place(plan, sc)
+
+
+def _check_values_in_place(plan, sc):
+    """v_lead / v_row / v_src: the first v_lead keys of every segment (whole 32-key blocks of its scene's own frames)
+    are consecutive token rows from v_row, so their values can be read in place: the oracle's key rows of those keys
+    are exactly v_row, v_row + 1, ...; v_lead is the largest such multiple of 32 within the own frames; the pack's
+    value rows (v_src) are the oracle's key rows except those, which are -1"""
+    k_src = np.asarray(sc.k_src)
+    v_lead, v_row, k_len = (getattr(plan, a).cpu().numpy() for a in ('v_lead', 'v_row', 'k_len'))
+    lay = plan.layout
+    starts = np.cumsum([0] + list(lay.lengths))
+    cu = np.asarray(sc.cu_k)
+    for s in range(plan.n_seg):
+        j = sc.scene[s]
+        own = int(lay.lengths[j]) * plan.T
+        assert v_row[s] == starts[j] * plan.T
+        assert v_lead[s] == (own // 32 * 32 if k_len[s] > 0 else 0), (s, v_lead[s], own)
+        assert v_lead[s] % 32 == 0 and v_lead[s] <= k_len[s]
+        assert np.array_equal(k_src[cu[s]:cu[s] + v_lead[s]], v_row[s] + np.arange(v_lead[s])), s
+    got = plan.v_src.cpu().numpy().astype(np.int64)
+    pcu = plan.cu_k.cpu().numpy()
+    pk = plan.k_src.cpu().numpy().astype(np.int64)
+    want = pk.copy()
+    for s in range(plan.n_seg):   # the segments that own packed rows (T_j owns none with its keys in place)
+        want[pcu[s]:pcu[s] + min(v_lead[s], pcu[s + 1] - pcu[s])] = -1
+    assert np.array_equal(got, want)
 
 
 @pytest.mark.parametrize('name', ['cpu_plumbing', 'hunyuan480p', 'wan704', 'uneven_K2', 'uneven_K4', 'uneven_K8',
@@ -132,6 +159,7 @@ def _check_in_place(case, adjacent):
             assert np.array_equal(got[a][b:b + lk], ref[a][order]), (j, a)
             tb = sc.cu_k[t]
             assert np.array_equal(got[a][k_off[t]:k_off[t] + k_len[t]], ref[a][tb:tb + sc.lk[t]]), (j, a)
+    _check_values_in_place(plan, sc)
 
 
 @pytest.mark.parametrize('name', ['cpu_plumbing', 'hunyuan480p', 'uneven_K4', 'uneven_K12'])

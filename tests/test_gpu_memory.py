@@ -202,3 +202,78 @@ def test_memory_attention_at_480p_shape():
                                seed=call)
         for i, (qr, o) in ref.items():
             assert_close(out[qr], o, what=f'480p call {call} piece {i}')
+
+
+@torch.no_grad()
+def test_processor_call_routes_the_bounded_memory_at_480p():
+    """Processor.__call__ (diffusers signature) with Context.memory = 128 at the HunyuanVideo-1.5 480p shape (4 scenes
+    x 8 frames x 1590 tokens + 128 text tokens each and 6 padding rows, 16 heads x 128, scene RoPE), as the reference
+    routes it (hunyuan15.py:200-201,305-334): the projections, q / k rotated once in token order, the head-major
+    bounded memory, the output projections. Sampled rows of both outputs against oracle.memory.masked_reference over
+    the same module's projections, rotated by the oracle's apply_rotary_emb, with the representatives that an
+    identical memory picks from those keys (the choice is deterministic), then projected by the same output layers"""
+    from helpers import Attn
+    from onereel_amd import hunyuan15 as HY
+    from oracle import attention as OA
+    from oracle import layout as OL
+    gen = torch.Generator().manual_seed(8)
+    T, H, D, M = 1590, 16, 128, 128
+    C = H * D
+    lengths, counts = [8] * 4, [128] * 4
+    lay = SceneLayout(lengths, halo=0)
+    S, Le = lay.n_frames * T, sum(counts) + 6
+    attn = Attn(C, H, gen).to(DEV)
+    hs = (torch.randn(1, S, C, generator=gen) * 0.5).bfloat16().to(DEV)
+    ehs = (torch.randn(1, Le, C, generator=gen) * 0.5).bfloat16().to(DEV)
+    cos, sin = OA.rope_table_3d(lay.n_frames, 30, 53, D)
+    ctx = HY.Context(lay, T=T, scene_rope=True, cfg=False, memory=M)
+    ctx.counts, ctx.fwd = {True: counts}, 1
+    print('processor with bounded memory, 480p', flush=True)
+    out, eout = HY.Processor(ctx, 0)(attn, hs, ehs, None, (cos.to(DEV), sin.to(DEV)))
+    assert ctx._mem is not None and len(ctx._mem.plans) == 1 and (0, True) in ctx._mem.memory.centroids
+    q, k, v = (f(hs).unflatten(2, (H, -1)) for f in (attn.to_q, attn.to_k, attn.to_v))
+    q, k = attn.norm_q(q), attn.norm_k(k)
+    eq, ek, ev = (f(ehs).unflatten(2, (H, -1)) for f in (attn.add_q_proj, attn.add_k_proj, attn.add_v_proj))
+    eq = attn.norm_added_q(eq)
+    rr = torch.as_tensor(OL.scene_rope_rows(OL.SceneLayout(lengths, 0), T))
+    qr, kr = (OA.apply_rotary_emb(x[0].bfloat16().cpu(), cos[rr], sin[rr]) for x in (q, k))
+    cand, owner = candidates(lay, T, 'cpu')
+    rep, valid = BoundaryMemory(M).select((0, True), kr.to(DEV)[cand.to(DEV)])
+    rep, valid = rep.cpu(), valid.cpu()
+    tr = [(128 * j, 128 * j + 128) for j in range(4)]
+    rng = np.random.default_rng(0)
+    vr = sorted({r for lo, hi in lay.ranges for r in [lo * T, hi * T - 1, *rng.integers(lo * T, hi * T, 10).tolist()]})
+    trs = sorted({t for a, b in tr for t in [a, b - 1, *rng.integers(a, b, 4).tolist()]})
+    rv, rt = OM.masked_reference(qr, kr, v[0].cpu(), eq[0].cpu(), ek[0].cpu(), ev[0].cpu(), lay.ranges, T, cand[rep],
+                                 owner[rep], valid, tr, video_rows=vr, text_rows=trs)
+    ref_out = attn.to_out[0](rv[vr].bfloat16().flatten(1).to(DEV)).cpu()
+    ref_eout = attn.to_add_out(rt[trs].bfloat16().flatten(1).to(DEV)).cpu()
+    assert_close(out[0, vr].cpu(), ref_out, max_abs=5e-2, mean_abs=5e-3, what='480p processor hs with memory')
+    assert_close(eout[0, trs].cpu(), ref_eout, max_abs=5e-2, mean_abs=5e-3, what='480p processor ehs with memory')
+    # the padding text rows attend to nothing: their output is the projection of zeros
+    pad = attn.to_add_out(torch.zeros(1, C, dtype=torch.bfloat16, device=DEV)).cpu()
+    assert torch.equal(eout[0, sum(counts):].cpu(), pad.expand(6, -1))
+
+
+@torch.no_grad()
+def test_wan_self_attention_routes_the_bounded_memory():
+    """the Wan processor's self-attention with Context.memory = M (wan.py:100-101,154-173): every scene's queries over
+    its frames plus its head's representatives of the other scenes, against oracle.memory.masked_reference (no
+    text scopes), on two calls in a row (cold, then warm from the stored centroids, as an identical memory picks)"""
+    from onereel_amd import wan as W
+    T, H, D, M = 24, 3, 128, 6
+    lay = SceneLayout([3, 4, 2], halo=0)
+    S = lay.n_frames * T
+    ctx = W.Context(lay, T=T, memory=M)
+    twin = BoundaryMemory(M)
+    cand, owner = candidates(lay, T, 'cpu')
+    empty = torch.zeros(0, H, D, dtype=torch.bfloat16)
+    for call in range(2):
+        q, k, v = (torch.randn(S, H, D, generator=torch.Generator().manual_seed(20 + 3 * call + i)).bfloat16()
+                   for i in range(3))
+        o = W.memory_self(ctx, q.to(DEV), k.to(DEV), v.to(DEV), 4).cpu()
+        rep, valid = twin.select((4, True), k.to(DEV)[cand.to(DEV)])
+        rep, valid = rep.cpu(), valid.cpu()
+        rv, _ = OM.masked_reference(q, k, v, empty, empty, empty, lay.ranges, T, cand[rep], owner[rep], valid,
+                                    [(0, 0)] * 3)
+        assert_close(o, rv, what=f'wan memory call {call}')

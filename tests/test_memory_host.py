@@ -64,3 +64,19 @@ def test_sentence_pieces_read_their_video_pieces_local_rows_in_place():
             o = int(k_off[h * st.n + i])
             assert torch.equal(kidx[o:o + st.lens[i]].long(), st.local[starts[i]:starts[i + 1]] * H + h), (h, i)
         assert int(k_off[h * st.n + 1]) - int(k_off[h * st.n]) == st.lens[0] + M
+
+
+def test_plan_rows_are_checked_before_any_launch():
+    """the kernels dereference key and query rows unchecked: a plan naming a negative key row, or query rows outside
+    the query buffer, is rejected once per plan on the host, and the public row helpers check every call's rows"""
+    from onereel_amd.scene import _check_row_range
+    bad_key = make_plan([(0, [0, 1], [3, -1], True)], [0], [0], 'cpu')
+    with pytest.raises(L.HipValueError, match='>= 0'):
+        _Static(bad_key, 2, 4, 'cpu')
+    bad_query = make_plan([(0, [5, 3, 9], [1, 2], True)], [0], [0], 'cpu')
+    with pytest.raises(L.HipValueError, match='query buffer'):
+        _Static(bad_query, 2, 8, 'cpu')
+    _check_row_range(torch.tensor([0, 7, 3], dtype=torch.int32), 8, 'rows')
+    for rows in ([0, 8], [-1, 2]):
+        with pytest.raises(L.HipValueError, match='outside'):
+            _check_row_range(torch.tensor(rows, dtype=torch.int32), 8, 'rows')

@@ -450,6 +450,51 @@ def test_memory_select_one_representative_per_separated_group():
         assert sorted(r // 10 for r in rep[h][valid[h]].tolist()) == [0, 1, 2, 3]
 
 
+def test_memory_masked_reference_equals_dense_masked_softmax():
+    """MemoryAttention's per-head scopes (memory.py:140-174; the reference test's per-head reference,
+    tests/test_onereel_memory.py:21-37) as one dense float64 softmax over all keys under a boolean mask built from
+    the scope definition: a video query of scene j sees scene j's frames, sentence j and, for its head, the valid
+    representatives of the other scenes; a sentence query of scene j sees scene j's frames and sentence j. The
+    oracle's gathered form agrees; restricted to some rows it gives those rows and zeros elsewhere"""
+    from oracle import memory as OM
+    g = torch.Generator().manual_seed(9)
+    ranges, T, H, D = [(0, 2), (2, 5), (5, 6)], 4, 2, 16
+    tr = [(0, 2), (2, 3), (3, 6)]
+    S, Le = 6 * T, 7                                        # one padding text row
+    q, k, v = (torch.randn(S, H, D, generator=g) for _ in range(3))
+    eq, ek, ev = (torch.randn(Le, H, D, generator=g) for _ in range(3))
+    rows, owner = OM.boundary_rows(ranges, T)
+    M = 5
+    rep = torch.stack([torch.randperm(len(rows), generator=g)[:M] for _ in range(H)])
+    valid = torch.ones(H, M, dtype=torch.bool)
+    valid[1, 3:] = False
+    rv, rt = OM.masked_reference(q, k, v, eq, ek, ev, ranges, T, rows[rep], owner[rep], valid, tr)
+    scene_of = [j for j, (lo, hi) in enumerate(ranges) for _ in range((hi - lo) * T)]
+    kk, vv = torch.cat([k, ek]).double(), torch.cat([v, ev]).double()
+    for h in range(H):
+        mask = torch.zeros(S + Le, S + Le, dtype=torch.bool)   # [query row of q ; eq] x [key row of k ; ek]
+        for j, (lo, hi) in enumerate(ranges):
+            t0, t1 = tr[j]
+            own = list(range(lo * T, hi * T)) + [S + t for t in range(t0, t1)]
+            far = [int(rows[r]) for r, ok in zip(rep[h], valid[h]) if ok and scene_of[int(rows[r])] != j]
+            for qr in range(lo * T, hi * T):
+                mask[qr, own + far] = True
+            for t in range(t0, t1):
+                mask[S + t, own] = True
+        qq = torch.cat([q, eq])[:, h].double()
+        s = (qq @ kk[:, h].T) * D ** -0.5
+        s = s.masked_fill(~mask, float('-inf'))
+        p = torch.softmax(s, -1).nan_to_num(0.0)               # the padding text row sees no key: zero output
+        o = p @ vv[:, h]
+        assert torch.allclose(rv[:, h].double(), o[:S], atol=1e-5)
+        assert torch.allclose(rt[:, h].double(), o[S:], atol=1e-5)
+    vr, trs = [1, 9, 13, 23], [0, 4]
+    sv, st = OM.masked_reference(q, k, v, eq, ek, ev, ranges, T, rows[rep], owner[rep], valid, tr, video_rows=vr,
+                                 text_rows=trs)
+    assert torch.allclose(sv[vr], rv[vr], atol=1e-6) and torch.allclose(st[trs], rt[trs], atol=1e-6)
+    assert sv[[r for r in range(S) if r not in vr]].abs().max() == 0
+
+
 def test_memory_select_warm_start():
     """a warm call (two passes from stored centroids) that starts from the centroids a converged cold call ended on,
     over the same keys, is a fixed point: the same centroids and representatives; from the cold start's own
