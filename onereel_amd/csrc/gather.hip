@@ -71,76 +71,107 @@ __device__ __forceinline__ RowLanes row_lanes(int chunks, int lane) {
   return RowLanes{cp, 64 / cp, lane / cp, lane % cp};
 }
 
-template <bool NARROW>
+// One row of a job in flight: its loads issued by row_load, its rotation and stores done by row_store. CPL: 16-byte
+// chunks per lane (the row's chunks over the lanes of its lane group, rounded up to a power of two).
+template <int CPL>
+struct RowWork {
+  uint16_t* ao;
+  uint16_t* bo;
+  int rope, mfrom;
+  bool live, rot;
+  Tab8 tr, tm;
+  u32x4 va[CPL], vb[CPL];
+};
+
+// MOVE: some job rotates with move_from (a second, inverse rotation first); without it no register holds its table
+template <int CPL, bool MOVE>
+__device__ __forceinline__ void row_load(const GatherArgs& g, int64_t rr, int64_t total, const RowLanes& rl,
+                                         int chunks, RowWork<CPL>& w) {
+  w.live = false;
+  if (rr >= total) return;
+  const bool second = rr >= g.job[0].n_rows;
+  const RowJob& J = second ? g.job[1] : g.job[0];
+  const int64_t r = second ? rr - g.job[0].n_rows : rr;
+  const int src = J.src_idx[r];
+  const bool text = src >= g.n_video;
+  if (J.in_place && text) return;
+  w.live = true;
+  const int64_t off = text ? (int64_t)(src - g.n_video) * J.text_stride : (int64_t)src * J.src_stride;
+  const uint16_t* a = (text ? J.a_text : J.a_video) + off;
+  const uint16_t* b = nullptr;
+  if (J.b_out) {
+    const int bs = J.b_idx ? J.b_idx[r] : src;
+    if (bs >= 0) {
+      const bool bt = bs >= g.n_video;
+      b = bt ? J.b_text + (int64_t)(bs - g.n_video) * J.text_stride : J.b_video + (int64_t)bs * J.src_stride;
+    }
+  }
+  // table rows outside the table leave the row unrotated (the host validates them; this only keeps reads in bounds)
+  int rope = J.rope_row ? J.rope_row[r] : -1;
+  int mfrom = MOVE && J.move_from ? J.move_from[r] : -1;
+  if (rope >= g.n_rope_rows || mfrom >= g.n_rope_rows) rope = mfrom = -1;
+  w.rope = rope;
+  w.mfrom = mfrom;
+  const int row_elems = g.H * g.D;
+#pragma unroll
+  for (int i = 0; i < CPL; ++i) {
+    const int c = rl.cl + rl.cp * i;
+    if (c < chunks) {
+      w.va[i] = *(const u32x4*)(a + 8 * c);
+      if (b) w.vb[i] = *(const u32x4*)(b + 8 * c);
+    }
+  }
+  // every chunk of a lane sits at the same offset within its head (8 cp a multiple of D): the lane's table entries
+  // are loaded once per row, next to the row's loads, instead of once per chunk
+  w.rot = MOVE && J.move_from ? (mfrom >= 0 && rope >= 0) : rope >= 0;
+  if (g.shared_d0 && w.rot) {
+    const int d0 = (8 * rl.cl) % g.D;
+    w.tr = load_tab8(g.cos_t, g.sin_t, (int64_t)rope * g.D + d0);
+    if (MOVE && J.move_from) w.tm = load_tab8(g.cos_t, g.sin_t, (int64_t)mfrom * g.D + d0);
+  }
+  w.ao = J.in_place ? J.a_out + (int64_t)src * J.out_stride : J.a_out + r * (int64_t)row_elems;
+  w.bo = b ? J.b_out + r * (int64_t)row_elems : nullptr;
+}
+
+template <int CPL, bool MOVE>
+__device__ __forceinline__ void row_store(const GatherArgs& g, const RowLanes& rl, int chunks, RowWork<CPL>& w) {
+  if (!w.live) return;
+  const bool move = MOVE && w.mfrom >= 0;
+#pragma unroll
+  for (int i = 0; i < CPL; ++i) {
+    const int c = rl.cl + rl.cp * i;
+    if (c < chunks) {
+      u32x4 x = w.va[i];
+      if (w.rot) {
+        if (!g.shared_d0) {
+          const int d0 = (8 * c) % g.D;
+          w.tr = load_tab8(g.cos_t, g.sin_t, (int64_t)w.rope * g.D + d0);
+          if (move) w.tm = load_tab8(g.cos_t, g.sin_t, (int64_t)w.mfrom * g.D + d0);
+        }
+        if (move) x = rotate8(x, w.tm, -1.0f);
+        x = rotate8(x, w.tr, 1.0f);
+      }
+      store_nt(w.ao + 8 * c, x);
+      if (w.bo) store_nt(w.bo + 8 * c, w.vb[i]);
+    }
+  }
+}
+
+// one row per wavefront (lane group) at a time; the register count per row (CPL chunks, no move table without MOVE)
+// sets how many waves a SIMD holds, and more of them in flight beat more rows per wave (two rows per wave, all loads
+// ahead of the stores, measured 15% slower at the 480p layer: 0.258 against 0.225 ms)
+template <bool NARROW, int CPL, bool MOVE>
 __global__ __launch_bounds__(kThreads) void pack_gather_kernel(GatherArgs g) {
   const int lane = threadIdx.x & 63;
   const int64_t wave = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6);
   const int64_t n_waves = (int64_t)gridDim.x * kWaves;
-  const int row_elems = g.H * g.D;
-  const int chunks = row_elems >> 3;
+  const int chunks = (g.H * g.D) >> 3;
   const RowLanes rl = row_lanes<NARROW>(chunks, lane);
-  const int64_t n0 = g.job[0].n_rows, total = n0 + g.job[1].n_rows;
+  const int64_t total = g.job[0].n_rows + g.job[1].n_rows;
   for (int64_t r0 = wave * rl.per; r0 < total; r0 += n_waves * rl.per) {
-    const int64_t rr = r0 + rl.sub;
-    if (rr >= total) continue;
-    const bool second = rr >= n0;
-    const RowJob& J = second ? g.job[1] : g.job[0];
-    const int64_t r = second ? rr - n0 : rr;
-    const int src = J.src_idx[r];
-    const bool text = src >= g.n_video;
-    if (J.in_place && text) continue;
-    const int64_t off = text ? (int64_t)(src - g.n_video) * J.text_stride : (int64_t)src * J.src_stride;
-    const uint16_t* a = (text ? J.a_text : J.a_video) + off;
-    const uint16_t* b = nullptr;
-    if (J.b_out) {
-      const int bs = J.b_idx ? J.b_idx[r] : src;
-      if (bs >= 0) {
-        const bool bt = bs >= g.n_video;
-        b = bt ? J.b_text + (int64_t)(bs - g.n_video) * J.text_stride : J.b_video + (int64_t)bs * J.src_stride;
-      }
-    }
-    // table rows outside the table leave the row unrotated (the host validates them; this only keeps reads in bounds)
-    int rope = J.rope_row ? J.rope_row[r] : -1;
-    int mfrom = J.move_from ? J.move_from[r] : -1;
-    if (rope >= g.n_rope_rows || mfrom >= g.n_rope_rows) rope = mfrom = -1;
-    u32x4 va[kMaxChunksPerLane], vb[kMaxChunksPerLane];
-#pragma unroll
-    for (int i = 0; i < kMaxChunksPerLane; ++i) {
-      const int c = rl.cl + rl.cp * i;
-      if (c < chunks) {
-        va[i] = *(const u32x4*)(a + 8 * c);
-        if (b) vb[i] = *(const u32x4*)(b + 8 * c);
-      }
-    }
-    // every chunk of a lane sits at the same offset within its head (8 cp a multiple of D): the lane's table entries
-    // are loaded once per row, next to the row's loads, instead of once per chunk
-    const bool rot = J.move_from ? (mfrom >= 0 && rope >= 0) : rope >= 0;
-    Tab8 tr, tm;
-    if (g.shared_d0 && rot) {
-      const int d0 = (8 * rl.cl) % g.D;
-      tr = load_tab8(g.cos_t, g.sin_t, (int64_t)rope * g.D + d0);
-      if (J.move_from) tm = load_tab8(g.cos_t, g.sin_t, (int64_t)mfrom * g.D + d0);
-    }
-    uint16_t* ao = J.in_place ? J.a_out + (int64_t)src * J.out_stride : J.a_out + r * (int64_t)row_elems;
-    uint16_t* bo = b ? J.b_out + r * (int64_t)row_elems : nullptr;
-#pragma unroll
-    for (int i = 0; i < kMaxChunksPerLane; ++i) {
-      const int c = rl.cl + rl.cp * i;
-      if (c < chunks) {
-        u32x4 x = va[i];
-        if (rot) {
-          if (!g.shared_d0) {
-            const int d0 = (8 * c) % g.D;
-            tr = load_tab8(g.cos_t, g.sin_t, (int64_t)rope * g.D + d0);
-            if (J.move_from) tm = load_tab8(g.cos_t, g.sin_t, (int64_t)mfrom * g.D + d0);
-          }
-          if (J.move_from) x = rotate8(x, tm, -1.0f);
-          x = rotate8(x, tr, 1.0f);
-        }
-        store_nt(ao + 8 * c, x);
-        if (bo) store_nt(bo + 8 * c, vb[i]);
-      }
-    }
+    RowWork<CPL> w;
+    row_load<CPL, MOVE>(g, r0 + rl.sub, total, rl, chunks, w);
+    row_store<CPL, MOVE>(g, rl, chunks, w);
   }
 }
 
@@ -248,14 +279,26 @@ using namespace onereel;
 namespace onereel {
 namespace {
 
+template <bool MOVE>
+int launch_rows_t(const GatherArgs& g, int64_t rows, hipStream_t st) {
+  const int chunks = g.H * g.D / 8;
+  const dim3 grid(row_grid(rows)), block(kThreads);
+  // rows under 64 chunks share a wavefront (one chunk per lane); wider rows take 2, 4 or 8 chunks per lane
+  if (chunks <= 64)
+    hipLaunchKernelGGL((pack_gather_kernel<true, 1, MOVE>), grid, block, 0, st, g);
+  else if (chunks <= 128)
+    hipLaunchKernelGGL((pack_gather_kernel<false, 2, MOVE>), grid, block, 0, st, g);
+  else if (chunks <= 256)
+    hipLaunchKernelGGL((pack_gather_kernel<false, 4, MOVE>), grid, block, 0, st, g);
+  else
+    hipLaunchKernelGGL((pack_gather_kernel<false, kMaxChunksPerLane, MOVE>), grid, block, 0, st, g);
+  return check_hip(hipGetLastError(), "pack_gather_kernel launch");
+}
+
 int launch_rows(const GatherArgs& g, hipStream_t st) {
   const int64_t rows = g.job[0].n_rows + g.job[1].n_rows;
   if (rows == 0) return 0;
-  if ((int64_t)g.H * g.D < 64 * 8)   // rows under 64 chunks share a wavefront
-    hipLaunchKernelGGL(pack_gather_kernel<true>, dim3(row_grid(rows)), dim3(kThreads), 0, st, g);
-  else
-    hipLaunchKernelGGL(pack_gather_kernel<false>, dim3(row_grid(rows)), dim3(kThreads), 0, st, g);
-  return check_hip(hipGetLastError(), "pack_gather_kernel launch");
+  return g.job[0].move_from || g.job[1].move_from ? launch_rows_t<true>(g, rows, st) : launch_rows_t<false>(g, rows, st);
 }
 
 int check_pack_job(const void* a_video, const void* a_text, const void* b_video, const void* b_text,

@@ -57,6 +57,44 @@ def test_select_matches_oracle_cold_and_warm(k, per, H, D, M, dtype):
     _same_sets(got2, gv2, ref2, rv2)
 
 
+@pytest.mark.parametrize('k,per,H,D', [(100, 30, 2, 64), (40, 60, 1, 128)])
+def test_select_matches_oracle_beyond_one_sort_chunk(k, per, H, D):
+    """3000 and 2400 candidates, past the 1024 that one pass of the grouping kernel's wavefronts covers (each then
+    sorts several 64-candidate chunks and carries a running per-cluster count between them), in k separated groups
+    with M = k: the oracle's representatives, cold and warm, and every stored centroid the mean of the normalised keys
+    of its cluster (members recomputed here in float64 from the final centroids: a wrong grouping would give wrong
+    means)"""
+    print(f'select beyond one sort chunk k={k} per={per} H={H} D={D}', flush=True)
+    g = torch.Generator().manual_seed(k + per)
+    B = k * per
+    # groups interleaved over the candidates, except that the cold start's evenly spaced candidates are one member
+    # of each group (so that no group starts with two centroids and splits: a split's members sit near two centroids
+    # at once, a tie that the fp32 rounding of the distances decides)
+    init = torch.linspace(0, B - 1, k).round().long()
+    rest = torch.ones(B, dtype=torch.bool)
+    rest[init] = False
+    group = torch.empty(B, dtype=torch.long)
+    group[init] = torch.arange(k)
+    group[rest] = torch.arange(k).repeat_interleave(per - 1)[torch.randperm(B - k, generator=g)]
+    centers = torch.randn(k, H, D, generator=g)
+    xs = centers[group] + 0.1 * torch.randn(B, H, D, generator=g)
+    mem = BoundaryMemory(k)
+    got, gv = mem.select('b', xs.to(DEV))
+    c = mem.centroids['b'].cpu().double()
+    xn = torch.nn.functional.normalize(xs.double().transpose(0, 1), dim=-1)
+    for h in range(H):
+        z = torch.cdist(xn[h], c[h]).argmin(-1)
+        assert torch.equal(torch.unique(z), torch.arange(k))       # one cluster per group, none empty
+        for i in range(k):
+            assert torch.allclose(c[h, i], xn[h, z == i].mean(0), atol=1e-5), (h, i)
+    ref, rv, c_ref = OM.select(xs, k, centroids=True)
+    _same_sets(got, gv, ref, rv)
+    xs2 = xs + 0.02 * torch.randn(xs.shape, generator=g)
+    got2, gv2 = mem.select('b', xs2.to(DEV))
+    ref2, rv2 = OM.select(xs2, k, iters=2, start=c_ref)
+    _same_sets(got2, gv2, ref2, rv2)
+
+
 def test_select_keeps_every_candidate_when_the_budget_covers_them():
     lay = SceneLayout([3, 4, 2], halo=0)
     T, H, D = 8, 2, 64
@@ -277,3 +315,43 @@ def test_wan_self_attention_routes_the_bounded_memory():
         rv, _ = OM.masked_reference(q, k, v, empty, empty, empty, lay.ranges, T, cand[rep], owner[rep], valid,
                                     [(0, 0)] * 3)
         assert_close(o, rv, what=f'wan memory call {call}')
+
+
+def test_select_matches_oracle_at_480p_shape():
+    """the HunyuanVideo-1.5 480p layer's candidate count (12 720 boundary keys per head: 4 scenes x 2 frames x 1590
+    tokens), 16 heads x 128, M = 128: keys in 128 separated groups laid out in candidate order (so that the cold
+    start's evenly spaced candidates seed one centroid per group), cold and then warm on perturbed keys. On heads
+    whose representatives are not decided by rounding (every cluster's nearest member nearer its centroid than the
+    next member by more than 1e-5, float64; checked here, not assumed), the GPU's representatives are the oracle's"""
+    B, H, D, M = 8 * 1590, 16, 128, 128
+    g = torch.Generator().manual_seed(480)
+    group = torch.arange(B) * M // B
+    centers = torch.randn(M, H, D, generator=g)
+    noise = 0.05 * torch.randn(B, H, D, generator=g)
+    noise[torch.unique(group, return_inverse=False, return_counts=True)[1].cumsum(0) - 7] = 0.0
+    xs = centers[group] + noise        # one member of each group at its centre: its medoid by a wide margin
+    xs2 = xs + 0.01 * torch.randn(B, H, D, generator=g)
+    mem = BoundaryMemory(M)
+    print('select at the 480p shape, cold and warm', flush=True)
+    got, gv = mem.select('480p', xs.to(DEV).to(torch.bfloat16))
+    c1 = mem.centroids['480p'].clone()
+    got2, gv2 = mem.select('480p', xs2.to(DEV).to(torch.bfloat16))
+    checked = 0
+    for h in (0, 7, 15):
+        x = xs[:, h:h + 1].to(torch.bfloat16)
+        ref, rv, c_ref = OM.select(x, M, centroids=True)
+        x2 = xs2[:, h:h + 1].to(torch.bfloat16)
+        ref2, rv2 = OM.select(x2, M, iters=2, start=c_ref)
+        # the margin: per cluster, the gap between its nearest and next-nearest member (float64, oracle centroids)
+        xn = torch.nn.functional.normalize(x.double()[:, 0], dim=-1)
+        d = torch.cdist(xn, c_ref[0].double()) ** 2
+        z = d.argmin(-1)
+        gaps = [(lambda s: float(s[1] - s[0]) if len(s) > 1 else 1.0)(d[z == i, i].sort().values)
+                for i in range(M) if bool((z == i).any())]
+        if min(gaps) <= 1e-5:
+            continue
+        checked += 1
+        assert sorted(got[h][gv[h]].tolist()) == sorted(ref[0][rv[0]].tolist()), h
+        assert torch.allclose(c1[h].cpu().double(), c_ref[0].double(), atol=1e-5), h
+        assert sorted(got2[h][gv2[h]].tolist()) == sorted(ref2[0][rv2[0]].tolist()), h
+    assert checked >= 2
