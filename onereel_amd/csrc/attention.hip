@@ -119,7 +119,7 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(const int32_t* cu_q,
   __shared__ int off[kMaxPlanSeg + 1];
   __shared__ int part[kPlanThreads];
   __shared__ int min_nb, split_w;
-  __shared__ int q_n[kQueues], q_s[kQueues], q_first[kQueues], q_sb[kQueues];
+  __shared__ int q_n[kQueues], q_s[kQueues], q_first[kQueues], q_sb[kQueues], q_tot[kQueues];
   const int tid = threadIdx.x;
   if (tid == 0) min_nb = 0x7fffffff;
   int n2 = 1;
@@ -189,6 +189,43 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(const int32_t* cu_q,
   // off[i] / H: query tiles of the sorted segments before i, each counted once
   const int all_tiles = total / H;
   auto heads_of = [&](int q) { return (H - q + kQueues - 1) / kQueues; };   // heads h < H with h % 8 == q
+  // With H not a multiple of 8 (single-head views of the bounded memory: H = 1) dealing by head would leave queues
+  // empty or uneven: there the unit u = i H + h (sorted segment i, head h) goes to queue u mod 8, so that every
+  // queue holds whole segment-heads in LPT order. Its place in the queue is the sum of the tiles of the units before
+  // it there: rows of 8 consecutive units, per-queue exclusive scans over the rows.
+  const bool by_unit = H % kQueues != 0;
+  const int n_units = by_unit && fits ? n_seg * H : 0;
+  const int n_rows8 = (n_units + kQueues - 1) / kQueues;
+  const int rpt = (n_rows8 + kPlanThreads - 1) / kPlanThreads;   // rows of units per thread
+  const int r_lo = min(tid * rpt, n_rows8), r_hi = min(r_lo + rpt, n_rows8);
+  auto unit_tiles = [&](int u) {
+    const int i = u / H;
+    return (off[i + 1] - off[i]) / H;
+  };
+  int uexcl[kQueues];
+  if (by_unit) {
+    int loc[kQueues];
+#pragma unroll
+    for (int q = 0; q < kQueues; ++q) loc[q] = 0;
+    for (int r = r_lo; r < r_hi; ++r)
+#pragma unroll
+      for (int q = 0; q < kQueues; ++q)
+        if (r * kQueues + q < n_units) loc[q] += unit_tiles(r * kQueues + q);
+#pragma unroll
+    for (int q = 0; q < kQueues; ++q) {
+      part[tid] = loc[q];
+      __syncthreads();
+      for (int o = 1; o < kPlanThreads; o <<= 1) {
+        const int x = tid >= o ? part[tid - o] : 0;
+        __syncthreads();
+        part[tid] += x;
+        __syncthreads();
+      }
+      uexcl[q] = part[tid] - loc[q];
+      if (tid == kPlanThreads - 1) q_tot[q] = part[tid];
+      __syncthreads();
+    }
+  }
   if (tid == 0) {
     int W = 1;
     const int rem = slots > 0 ? total % slots : 0;
@@ -207,7 +244,7 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(const int32_t* cu_q,
     }
     int first = 0, sb = 0;
     for (int q = 0; q < kQueues; ++q) {
-      const int n = all_tiles * heads_of(q);
+      const int n = by_unit ? (fits ? q_tot[q] : 0) : all_tiles * heads_of(q);
       const int sq = W > 1 ? min(n, (int)(((int64_t)rem * n + total - 1) / total)) : 0;
       q_n[q] = n;
       q_s[q] = sq;
@@ -227,15 +264,11 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(const int32_t* cu_q,
   }
   int32_t* tab = ws + kWsHeader + (int64_t)kItemWords * (max_items + parts_cap);
   if (tid == 0) ws[3] = W > 1 ? q_sb[kQueues - 1] + q_s[kQueues - 1] : 0;
-  for (int it = tid; it < total; it += kPlanThreads) {
-    int i = plan_upper_bound(off, n_seg + 1, it) - 1;
-    int s = (int)(key[i] & 0xffffffffu);
-    int lq = cu_q[s + 1] - cu_q[s];
-    int tiles = (lq + bq - 1) / bq;
-    int local_it = it - off[i];
-    int head = local_it / tiles, t = local_it - head * tiles;
-    const int q = head % kQueues;
-    const int pos = (off[i] / H) * heads_of(q) + (head / kQueues) * tiles + t;   // position within queue q
+  // the record(s) of tile t of head `head` of sorted segment i, at position pos of queue q (the last q_s[q] positions
+  // of a queue are items split into W key parts)
+  auto emit = [&](int i, int head, int t, int q, int pos) {
+    const int s = (int)(key[i] & 0xffffffffu);
+    const int lq = cu_q[s + 1] - cu_q[s];
     const int keep = q_n[q] - q_s[q];
     const int q_beg = cu_q[s];
     const int k_beg = k_off ? k_off[s] : cu_k[s];
@@ -257,6 +290,26 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(const int32_t* cu_q,
       tab[3 * sidx + 1] = (t << 8) | head;
       tab[3 * sidx + 2] = W;
     }
+  };
+  if (by_unit) {
+    for (int r = r_lo; r < r_hi; ++r)
+#pragma unroll
+      for (int q = 0; q < kQueues; ++q) {
+        const int u = r * kQueues + q;
+        if (u >= n_units) break;
+        const int tiles = unit_tiles(u);
+        for (int t = 0; t < tiles; ++t) emit(u / H, u % H, t, q, uexcl[q] + t);
+        uexcl[q] += tiles;
+      }
+    return;
+  }
+  for (int it = tid; it < total; it += kPlanThreads) {
+    const int i = plan_upper_bound(off, n_seg + 1, it) - 1;
+    const int tiles = (off[i + 1] - off[i]) / H;
+    const int local_it = it - off[i];
+    const int head = local_it / tiles, t = local_it - head * tiles;
+    const int q = head % kQueues;
+    emit(i, head, t, q, (off[i] / H) * heads_of(q) + (head / kQueues) * tiles + t);   // position within queue q
   }
 }
 
