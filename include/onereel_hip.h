@@ -153,14 +153,16 @@ typedef struct or_pack_args {
   int64_t video_row_stride;   /* elements between video rows (keys and values) */
   int64_t text_row_stride;
   int64_t n_video;            /* rows of the video part: source rows >= n_video are text rows */
-  const int32_t* k_src;       /* [n_keys] source row of packed key r */
+  const int32_t* k_src;       /* [n_keys] source row of packed key r (-1: nothing written for r) */
   const int32_t* k_rope;      /* optional [n_keys] as or_pack_gather's rope_row */
   const int32_t* k_move_from; /* optional [n_keys] as or_pack_gather's move_from */
   const int32_t* v_src;       /* optional [n_keys] source row of packed value r, -1: not packed (its row of v_out is
                                  not written; the attention call reads it in place); NULL: k_src */
   int64_t n_keys;
-  void* k_out;                /* bf16 [n_keys, H, D] */
-  void* v_out;                /* bf16 [n_keys, H, D] or NULL */
+  const int32_t* k_dst;       /* optional [n_keys]: the row of k_out / v_out that packed key r is written to (r when
+                                 NULL) */
+  void* k_out;                /* bf16 [rows, H, D]: n_keys rows, or the rows k_dst names */
+  void* v_out;                /* bf16, as k_out, or NULL */
   const void* q;              /* video queries rotated in token order, as or_rotate_rows(q, .., q_out) */
   int64_t q_row_stride;
   const int32_t* q_src;       /* [n_queries] */
@@ -234,6 +236,9 @@ typedef struct or_varlen_args {
   const int32_t* v_lead;    /* [n_seg], with v_tok */
   const int32_t* v_row;     /* [n_seg], with v_tok */
   int64_t v_tok_rows;       /* rows of v_tok */
+  const int32_t* k_len_head;/* optional [n_seg * H] (with k_len): head h of segment s attends to the first
+                               min(k_len_head[s * H + h], k_len[s]) keys of the segment's range, e.g. a shared prefix
+                               followed by rows that differ per head (the bounded memory's representatives) */
 } or_varlen_args;
 
 /* Bytes of device workspace or_varlen_fwd needs for this many segments, packed queries and heads: the work-item
@@ -343,6 +348,18 @@ int or_memory_index(const int64_t* rep, const uint8_t* valid, const int64_t* can
                     const int64_t* piece_scene, const uint8_t* piece_mem, const int32_t* piece_len,
                     const int32_t* k_off, int32_t n_pieces, int32_t H, int32_t M, int32_t* kidx, int32_t* k_len,
                     void* stream);
+
+/* Replaces the same key-list building (memory.py:152-168) for the multi-head form of the bounded memory's attention,
+ * where the packed K / V rows hold every head and each head's foreign representatives sit in its own head slot after
+ * the piece's piece_len[i] local keys (packed rows k_off[i] ..): for piece i, head h and slot r < M, fsrc / fdst
+ * [n_pieces * H * M] (index (i * H + h) * M + r) get the source row cand_row[rep[h, x]] * H + h of head h's x-th
+ * valid representative whose scene differs from piece_scene[i] (in order; -1 past the last, and for pieces with
+ * piece_mem[i] = 0) and the packed row (k_off[i] + piece_len[i] + r) * H + h, both rows of [rows * H, 1, D] views
+ * (an or_pack_layer job with H = 1 moves them); k_len_head[i * H + h] = piece_len[i] + their count. One launch. */
+int or_memory_foreign(const int64_t* rep, const uint8_t* valid, const int64_t* cand_row, const int64_t* cand_scene,
+                      const int64_t* piece_scene, const uint8_t* piece_mem, const int32_t* piece_len,
+                      const int32_t* k_off, int32_t n_pieces, int32_t H, int32_t M, int32_t* fsrc, int32_t* fdst,
+                      int32_t* k_len_head, void* stream);
 
 /* Message of the calling thread's last failed call ("" if none). */
 const char* or_last_error(void);

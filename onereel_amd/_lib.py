@@ -48,13 +48,14 @@ class VarlenArgs(ctypes.Structure):
                 ('q_row_stride', i64), ('k_row_stride', i64), ('o_row_stride', i64), ('n_seg', i32), ('sum_q', i32),
                 ('max_q', i32), ('max_k', i32), ('H', i32), ('D', i32), ('scale', ctypes.c_float),
                 ('workspace', vp), ('workspace_bytes', i64), ('q_row_step', i32), ('v_tok', vp), ('v_lead', vp),
-                ('v_row', vp), ('v_tok_rows', i64)]
+                ('v_row', vp), ('v_tok_rows', i64), ('k_len_head', vp)]
 
 
 class PackArgs(ctypes.Structure):
     _fields_ = [('k_video', vp), ('k_text', vp), ('v_video', vp), ('v_text', vp), ('video_row_stride', i64),
                 ('text_row_stride', i64), ('n_video', i64), ('k_src', vp), ('k_rope', vp), ('k_move_from', vp),
-                ('v_src', vp), ('n_keys', i64), ('k_out', vp), ('v_out', vp), ('q', vp), ('q_row_stride', i64),
+                ('v_src', vp), ('n_keys', i64), ('k_dst', vp), ('k_out', vp), ('v_out', vp), ('q', vp),
+                ('q_row_stride', i64),
                 ('q_src', vp), ('q_rope', vp), ('n_queries', i64), ('q_out', vp), ('q_out_row_stride', i64),
                 ('cos_table', vp), ('sin_table', vp), ('n_rope_rows', i64), ('H', i32), ('D', i32)]
 
@@ -78,6 +79,7 @@ SIGNATURES = {
     'or_memory_select_workspace_size': (i64, [i32, i32, i32, i32, i32]),
     'or_memory_select': (i32, [vp, i32, vp, i64, i32, i32, i32, i32, vp, vp, i32, vp, vp, vp, i64, vp]),
     'or_memory_index': (i32, [vp, vp, vp, vp, vp, vp, vp, vp, i32, i32, i32, vp, vp, vp]),
+    'or_memory_foreign': (i32, [vp, vp, vp, vp, vp, vp, vp, vp, i32, i32, i32, vp, vp, vp, vp]),
     'or_layernorm_modulate': (i32, [vp, vp, i64, i32, i64, i64, ctypes.c_float, vp, vp, vp, vp, vp]),
     'or_gated_residual': (i32, [vp, vp, vp, i64, i32, i64, i64, vp]),
     'or_residual_layernorm_modulate': (i32, [vp, vp, vp, vp, i64, i32, i64, i64, i64, ctypes.c_float, vp, vp, vp, vp,

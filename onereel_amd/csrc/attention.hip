@@ -112,7 +112,8 @@ __device__ inline int plan_upper_bound(const int* a, int n, int x) {
 __global__ __launch_bounds__(kPlanThreads) void plan_kernel(const int32_t* cu_q, const int32_t* cu_k,
                                                             const int32_t* k_off, const int32_t* k_len,
                                                             const int32_t* seg_q_src, const int32_t* v_lead,
-                                                            const int32_t* v_row, int n_seg, int H, int bq,
+                                                            const int32_t* v_row, const int32_t* k_len_head,
+                                                            int n_seg, int H, int bq,
                                                             int max_items, int slots, int split_keys, int parts_cap,
                                                             int32_t* ws) {
   __shared__ unsigned long long key[kMaxPlanSeg];
@@ -161,7 +162,13 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(const int32_t* cu_q,
       int tiles = lq > 0 ? (lq + bq - 1) / bq : 0;
       off[i] = tiles * H;
       local += tiles * H;
-      if (tiles > 0) atomicMin(&min_nb, (int)((0x7fffffffu - (unsigned)(key[i] >> 32) + 31) / 32));
+      if (tiles > 0) {
+        // the fewest key blocks of any item (a key-split item keeps at least one block per part)
+        int lk_min = (int)(0x7fffffffu - (unsigned)(key[i] >> 32));
+        if (k_len_head)
+          for (int h = 0; h < H; ++h) lk_min = min(lk_min, max(k_len_head[(int64_t)s * H + h], 0));
+        atomicMin(&min_nb, (lk_min + 31) / 32);
+      }
     }
   }
   part[tid] = local;
@@ -272,7 +279,8 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(const int32_t* cu_q,
     const int keep = q_n[q] - q_s[q];
     const int q_beg = cu_q[s];
     const int k_beg = k_off ? k_off[s] : cu_k[s];
-    const int lk = k_len ? k_len[s] : cu_k[s + 1] - cu_k[s];
+    const int lk_seg = k_len ? k_len[s] : cu_k[s + 1] - cu_k[s];
+    const int lk = k_len_head ? min(k_len_head[(int64_t)s * H + head], lk_seg) : lk_seg;   // this head's keys
     const int q_src0 = seg_q_src ? seg_q_src[s] : q_beg;
     const int vl = v_lead ? v_lead[s] : 0, vr = v_row ? v_row[s] : 0;
     auto put = [&](int64_t entry, int pw, int sidx) {
@@ -1107,6 +1115,7 @@ int check_args(const or_varlen_args& x, const char* fn) {
   if ((int64_t)(x.max_k + 8 * 32) * x.k_row_stride * 2 > 0x7fffffffLL)
     return fail_arg("%s: a segment's keys span more than 2 GiB (max_k %d x row stride %lld)", fn, x.max_k,
                     (long long)x.k_row_stride);
+  if (x.k_len_head && !x.k_len) return fail_arg("%s: k_len_head needs k_len (each segment's largest key count)", fn);
   if (x.v_tok && (!x.v_lead || !x.v_row || x.v_tok_rows < 0 || !aligned16(x.v_tok)))
     return fail_arg("%s: v_tok needs v_lead, v_row, v_tok_rows >= 0 and 16-byte alignment", fn);
   return 0;
@@ -1162,7 +1171,8 @@ int launch_varlen(const or_varlen_args& x, void* wsp, int64_t cap, hipStream_t s
   // the planner needs key counts only: k_len when given, else the cu_k differences. It writes every word of the
   // workspace the other kernels read (queue headers, item list, split table) before they run.
   hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(kPlanThreads), 0, st, x.cu_q, x.cu_k, x.k_len ? x.k_off : nullptr,
-                     x.k_len, x.seg_q_src, x.v_tok ? x.v_lead : nullptr, x.v_tok ? x.v_row : nullptr, x.n_seg, x.H,
+                     x.k_len, x.seg_q_src, x.v_tok ? x.v_lead : nullptr, x.v_tok ? x.v_row : nullptr, x.k_len_head,
+                     x.n_seg, x.H,
                      item_bq(x.D), (int)max_items, (int)grid,
                      may_split ? 1 : 0, (int)cap, ws);
   if (int rc = check_hip(hipGetLastError(), "plan_kernel launch")) return rc;

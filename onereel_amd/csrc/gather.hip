@@ -24,10 +24,10 @@ constexpr int kMaxChunksPerLane = 8;  // rows up to 64 lanes * 8 * 8 elements = 
 // 16-byte store that bypasses the caches (global_store_dwordx4 ... nt)
 __device__ __forceinline__ void store_nt(uint16_t* p, u32x4 v) { __builtin_nontemporal_store(v, (u32x4*)p); }
 
-// One job of the row kernel: n_rows rows, row r read from src_idx[r] of [video ; text], rotated per rope_row /
-// move_from, written to packed row r of a_out (in_place: to its own source row of a_out, row stride out_stride, and
-// text rows skipped); the second source's row b_idx[r] (src_idx[r] without b_idx; none where b_idx[r] < 0) copied to
-// packed row r of b_out.
+// One job of the row kernel: n_rows rows, row r read from src_idx[r] of [video ; text] (none where src_idx[r] < 0),
+// rotated per rope_row / move_from, written to packed row dst_idx[r] (r without dst_idx) of a_out (in_place: to its
+// own source row of a_out, row stride out_stride, and text rows skipped); the second source's row b_idx[r] (src_idx[r]
+// without b_idx; none where b_idx[r] < 0) copied to the same packed row of b_out.
 struct RowJob {
   const uint16_t* a_video;
   const uint16_t* a_text;
@@ -36,6 +36,7 @@ struct RowJob {
   int64_t src_stride, text_stride;
   const int32_t* src_idx;
   const int32_t* b_idx;
+  const int32_t* dst_idx;
   const int32_t* rope_row;
   const int32_t* move_from;
   uint16_t* a_out;
@@ -94,7 +95,7 @@ __device__ __forceinline__ void row_load(const GatherArgs& g, int64_t rr, int64_
   const int64_t r = second ? rr - g.job[0].n_rows : rr;
   const int src = J.src_idx[r];
   const bool text = src >= g.n_video;
-  if (J.in_place && text) return;
+  if (src < 0 || (J.in_place && text)) return;
   w.live = true;
   const int64_t off = text ? (int64_t)(src - g.n_video) * J.text_stride : (int64_t)src * J.src_stride;
   const uint16_t* a = (text ? J.a_text : J.a_video) + off;
@@ -129,8 +130,9 @@ __device__ __forceinline__ void row_load(const GatherArgs& g, int64_t rr, int64_
     w.tr = load_tab8(g.cos_t, g.sin_t, (int64_t)rope * g.D + d0);
     if (MOVE && J.move_from) w.tm = load_tab8(g.cos_t, g.sin_t, (int64_t)mfrom * g.D + d0);
   }
-  w.ao = J.in_place ? J.a_out + (int64_t)src * J.out_stride : J.a_out + r * (int64_t)row_elems;
-  w.bo = b ? J.b_out + r * (int64_t)row_elems : nullptr;
+  const int64_t dst = J.dst_idx ? J.dst_idx[r] : r;
+  w.ao = J.in_place ? J.a_out + (int64_t)src * J.out_stride : J.a_out + dst * row_elems;
+  w.bo = b ? J.b_out + dst * row_elems : nullptr;
 }
 
 template <int CPL, bool MOVE>
@@ -318,9 +320,10 @@ int check_pack_job(const void* a_video, const void* a_text, const void* b_video,
 
 RowJob pack_job(const void* a_video, const void* a_text, const void* b_video, const void* b_text,
                 int64_t src_row_stride, int64_t text_row_stride, const int32_t* src_idx, const int32_t* b_idx,
-                const int32_t* rope_row, const int32_t* move_from, int64_t n_rows, void* a_out, void* b_out) {
+                const int32_t* dst_idx, const int32_t* rope_row, const int32_t* move_from, int64_t n_rows, void* a_out,
+                void* b_out) {
   return RowJob{(const uint16_t*)a_video, (const uint16_t*)(a_text ? a_text : a_video), (const uint16_t*)b_video,
-                (const uint16_t*)(b_text ? b_text : b_video), src_row_stride, text_row_stride, src_idx, b_idx,
+                (const uint16_t*)(b_text ? b_text : b_video), src_row_stride, text_row_stride, src_idx, b_idx, dst_idx,
                 rope_row, move_from, (uint16_t*)a_out, (uint16_t*)b_out, 0, n_rows, 0};
 }
 
@@ -339,8 +342,8 @@ extern "C" int or_pack_gather(const void* a_video, const void* a_text, const voi
                               move_from, cos_table, sin_table, n_rope_rows, a_out, b_out, "or_pack_gather"))
     return rc;
   GatherArgs g{};
-  g.job[0] = pack_job(a_video, a_text, b_video, b_text, src_row_stride, text_row_stride, src_idx, nullptr, rope_row,
-                      move_from, n_rows, a_out, b_out);
+  g.job[0] = pack_job(a_video, a_text, b_video, b_text, src_row_stride, text_row_stride, src_idx, nullptr, nullptr,
+                      rope_row, move_from, n_rows, a_out, b_out);
   g.n_video = n_video;
   g.cos_t = cos_table;
   g.sin_t = sin_table;
@@ -366,7 +369,7 @@ extern "C" int or_rotate_rows(const void* x, int64_t x_row_stride, int64_t n_vid
     return fail_arg("or_rotate_rows: pointers must be 16-byte aligned and row strides multiples of 8 elements");
   GatherArgs g{};
   g.job[0] = RowJob{(const uint16_t*)x, (const uint16_t*)x, nullptr, nullptr, x_row_stride, x_row_stride, src_idx,
-                    nullptr, rope_row, nullptr, (uint16_t*)out, nullptr, out_row_stride, n_rows, 1};
+                    nullptr, nullptr, rope_row, nullptr, (uint16_t*)out, nullptr, out_row_stride, n_rows, 1};
   g.n_video = n_video;
   g.cos_t = cos_table;
   g.sin_t = sin_table;
@@ -399,10 +402,10 @@ extern "C" int or_pack_layer(const or_pack_args* p, void* stream) {
   GatherArgs g{};
   if (x.n_keys > 0)
     g.job[0] = pack_job(x.k_video, x.k_text, x.v_video, x.v_text, x.video_row_stride, x.text_row_stride, x.k_src,
-                        x.v_src, x.k_rope, x.k_move_from, x.n_keys, x.k_out, x.v_out);
+                        x.v_src, x.k_dst, x.k_rope, x.k_move_from, x.n_keys, x.k_out, x.v_out);
   if (x.n_queries > 0)
     g.job[1] = RowJob{(const uint16_t*)x.q, (const uint16_t*)x.q, nullptr, nullptr, x.q_row_stride, x.q_row_stride,
-                      x.q_src, nullptr, x.q_rope, nullptr, (uint16_t*)x.q_out, nullptr, x.q_out_row_stride,
+                      x.q_src, nullptr, nullptr, x.q_rope, nullptr, (uint16_t*)x.q_out, nullptr, x.q_out_row_stride,
                       x.n_queries, 1};
   g.n_video = x.n_video;
   g.cos_t = x.cos_table;

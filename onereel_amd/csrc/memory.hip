@@ -475,6 +475,52 @@ __global__ __launch_bounds__(256) void mem_index_kernel(const int64_t* rep, cons
   if (tid == 0) k_len[seg] = piece_len[i] + total;
 }
 
+// The multi-head form of the per-call key lists (the packed K / V hold every head of a row, and each head's
+// representatives sit in its own head slot after the piece's local keys): block (i, h) writes, for slot r < M of piece
+// i and head h, src = cand_row[c] * H + h (the representative's row in the [rows * H, 1, D] view of the key buffer, or
+// -1 for an unused slot) and dst = (k_off[i] + piece_len[i] + r) * H + h (its row in that view of the packed buffer),
+// in the representatives' order, and k_len_head[i * H + h] = piece_len[i] + the count. Pieces that do not read the
+// memory get no representatives.
+__global__ __launch_bounds__(256) void mem_foreign_kernel(const int64_t* rep, const uint8_t* valid,
+                                                          const int64_t* cand_row, const int64_t* cand_scene,
+                                                          const int64_t* piece_scene, const uint8_t* piece_mem,
+                                                          const int32_t* piece_len, const int32_t* k_off,
+                                                          int32_t* fsrc, int32_t* fdst, int32_t* k_len_head, int n,
+                                                          int H, int M) {
+  __shared__ int wave_cnt[4];
+  const int i = blockIdx.x, h = blockIdx.y, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int64_t slot0 = ((int64_t)i * H + h) * M;
+  const int64_t dst0 = (int64_t)k_off[i] + piece_len[i];
+  const int64_t scene = piece_scene[i];
+  const bool reads = piece_mem[i] != 0;
+  for (int r = tid; r < M; r += 256) {
+    fsrc[slot0 + r] = -1;
+    fdst[slot0 + r] = (int32_t)((dst0 + r) * H + h);
+  }
+  __syncthreads();
+  int total = 0;
+  for (int r0 = 0; r0 < M; r0 += 256) {
+    const int r = r0 + tid;
+    bool f = false;
+    int64_t row = 0;
+    if (reads && r < M && valid[(int64_t)h * M + r]) {
+      const int64_t c = rep[(int64_t)h * M + r];
+      f = cand_scene[c] != scene;
+      row = cand_row[c];
+    }
+    const uint64_t bal = __ballot(f);
+    if (lane == 0) wave_cnt[w] = __popcll(bal);
+    __syncthreads();
+    int before = total;
+    for (int x = 0; x < w; ++x) before += wave_cnt[x];
+    const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+    if (f) fsrc[slot0 + before + __popcll(bal & below)] = (int32_t)(row * H + h);
+    total += wave_cnt[0] + wave_cnt[1] + wave_cnt[2] + wave_cnt[3];
+    __syncthreads();
+  }
+  if (tid == 0) k_len_head[(int64_t)i * H + h] = piece_len[i] + total;
+}
+
 struct WsParts {
   int64_t X, xx, cc, z, dist, order, start, moved, total;
 };
@@ -579,4 +625,18 @@ extern "C" int or_memory_index(const int64_t* rep, const uint8_t* valid, const i
   hipLaunchKernelGGL(mem_index_kernel, dim3(n_pieces, H), dim3(256), 0, (hipStream_t)stream, rep, valid, cand_row,
                      cand_scene, piece_scene, piece_mem, piece_len, k_off, kidx, k_len, n_pieces, H, M);
   return check_hip(hipGetLastError(), "mem_index_kernel launch");
+}
+
+extern "C" int or_memory_foreign(const int64_t* rep, const uint8_t* valid, const int64_t* cand_row,
+                                 const int64_t* cand_scene, const int64_t* piece_scene, const uint8_t* piece_mem,
+                                 const int32_t* piece_len, const int32_t* k_off, int32_t n_pieces, int32_t H,
+                                 int32_t M, int32_t* fsrc, int32_t* fdst, int32_t* k_len_head, void* stream) {
+  if (n_pieces < 1 || H < 1 || M < 1 || n_pieces > 65535 || H > 65535)
+    return fail_arg("or_memory_foreign: need 1 <= pieces, heads <= 65535 and M >= 1 (n=%d H=%d M=%d)", n_pieces, H, M);
+  if (!rep || !valid || !cand_row || !cand_scene || !piece_scene || !piece_mem || !piece_len || !k_off || !fsrc ||
+      !fdst || !k_len_head)
+    return fail_arg("or_memory_foreign: every array is required");
+  hipLaunchKernelGGL(mem_foreign_kernel, dim3(n_pieces, H), dim3(256), 0, (hipStream_t)stream, rep, valid, cand_row,
+                     cand_scene, piece_scene, piece_mem, piece_len, k_off, fsrc, fdst, k_len_head, n_pieces, H, M);
+  return check_hip(hipGetLastError(), "mem_foreign_kernel launch");
 }

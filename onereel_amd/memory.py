@@ -7,17 +7,23 @@ L2-normalised keys: 50 passes the first time a (layer, branch) key is seen, 2 wa
 after that, one medoid per non-empty cluster. Representatives differ per head, so the attention runs head-major: each
 (head, query piece) pair is one single-head segment over rows of D elements, row = token * H + head.
 
-Per call, all on the caller's stream and without host reads:
+Per call, all on the caller's stream and without host reads, when every piece's query rows are consecutive (the
+frame plans of the models):
 
     or_memory_select   k-means + medoids for every head (fp32 MFMA distances, fixed-order sums, device-side stop)
-    or_memory_index    each (head, piece)'s foreign representatives appended after its local keys
-    or_pack_gather     the K / V rows of every segment (local rows from a per-plan table, then the foreign ones)
-    or_varlen_fwd      single-head attention; queries read and outputs written in place, query i of piece p at row
-                       (first row of p + i) * H + head (q_row_step = H), when every piece's query rows are contiguous
+    or_memory_foreign  each (piece, head)'s foreign representatives: source and packed rows, per-head key counts
+    or_pack_layer      the local K rows of every piece (whole rows, all heads) and the local V rows not read in place
+    or_pack_layer      the foreign K / V rows, one head each, into their head slots after the local rows
+    or_varlen_fwd      multi-head attention over the pieces: queries read and outputs written in place, the leading
+                       run of each piece's local values (its scene's frames) read in place, head h of piece i over
+                       its first k_len_head[i, h] keys (local, then its own representatives)
+
+Otherwise (query rows in any order) the single-head form runs: segment (head, piece) over rows of D elements, row =
+token * H + head, with or_memory_index, or_pack_gather of single-head rows, gathered queries and a scatter.
 
 A plan's static parts (segment offsets, the local key rows, the query rows) are built once per (plan, H) and kept.
 A piece that does not read the memory and has the local rows of another (a scene's sentence queries beside its
-video queries) reads them in place from that piece's segment, so they are packed once.
+video queries) reads them in place from that piece's rows, so they are packed once.
 """
 from __future__ import annotations
 
@@ -27,7 +33,7 @@ import torch
 
 from . import _lib as L
 from .layout import SceneLayout
-from .scene import gather_rows, scatter_rows, varlen
+from .scene import gather_rows, pack_job, scatter_rows, varlen
 
 ITERS_INIT, ITERS_UPDATE = 50, 2
 
@@ -215,6 +221,8 @@ class _Static:
         self.cu_q, self.sum_q = t32(cu), cu[-1]
         if self.in_place:
             self.seg_q_src = t32([first[i] * H + h for h in range(H) for i in range(n)])
+            self.first_q = t32(first)
+            self.cu_piece = t32([0] + [sum(qlen[:i + 1]) for i in range(n)])
         else:
             rows = p.qrows.to(device=device, dtype=torch.int64)
             lo, hi = int(rows.min()), int(rows.max())        # once per plan
@@ -258,6 +266,46 @@ class _Static:
         self._slots = {}
         self.device = device
 
+    def multi_head(self, M: int):
+        """the multi-head form's per-M tables: per piece its packed row offset (k_off), largest key count (k_len),
+        in-place value run (v_lead whole 32-key blocks from token row v_row); the local rows' pack job (src, dst and
+        value rows, -1 where the value is read in place), and the packed row count. A piece that shares another's
+        local rows gets that piece's offset and run."""
+        key = ('mh', M)
+        if key not in self._slots:
+            n, lens = self.n, self.lens
+            starts = [0]
+            for c in lens:
+                starts.append(starts[-1] + c)
+            local = self.local.cpu()
+            off, o = [0] * n, 0
+            for i in range(n):
+                if self.share[i] is None:
+                    off[i] = o
+                    o += lens[i] + (M if self.mem[i] else 0)
+            for i in range(n):
+                if self.share[i] is not None:
+                    off[i] = off[self.share[i]]
+            v_row, v_lead = [0] * n, [0] * n
+            src, dst, vsrc = [], [], []
+            for i in range(n):
+                rows = local[starts[i]:starts[i + 1]]
+                run = 0
+                if len(rows):
+                    step = (rows - rows[0]) == torch.arange(len(rows))
+                    run = len(rows) if bool(step.all()) else int((~step).nonzero()[0])
+                    v_row[i] = int(rows[0])
+                v_lead[i] = run // L.KEY_BLOCK * L.KEY_BLOCK
+                if self.share[i] is None:
+                    src += rows.tolist()
+                    dst += range(off[i], off[i] + lens[i])
+                    vsrc += [-1] * v_lead[i] + rows[v_lead[i]:].tolist()
+            t32 = lambda x: torch.tensor(x, dtype=torch.int32, device=self.device)
+            k_len = [lens[i] + (M if self.mem[i] else 0) for i in range(n)]
+            self._slots[key] = dict(k_off=t32(off), k_len=t32(k_len), max_k=max(k_len), v_row=t32(v_row),
+                                    v_lead=t32(v_lead), src=t32(src), dst=t32(dst), vsrc=t32(vsrc), rows=o)
+        return self._slots[key]
+
     def slots(self, M: int):
         """(k_off, kidx) for M representatives: segment (h, i) owns kidx[k_off .. k_off + lens[i] + M) (+ 0 when
         the piece does not read the memory), its local rows (row * H + h) first, written once here; the foreign rows
@@ -288,10 +336,11 @@ class _Static:
 class MemoryAttention:
     """packed head-major attention with the bounded memory (memory.py:140-174); plans are cached by the caller"""
 
-    def __init__(self, memory: BoundaryMemory):
+    def __init__(self, memory: BoundaryMemory, head_major: bool = False):
         self.memory = memory
         self.plans = {}
         self._static = {}
+        self.head_major = head_major   # True: the single-head form even when the queries can be read in place
 
     def _tables(self, p: Plan, H: int, Sq: int, device) -> _Static:
         key = (id(p), H, Sq, str(device))
@@ -319,6 +368,8 @@ class MemoryAttention:
             raise L.HipValueError(f'the plan reads key row {st.max_key_row}, the key buffer has {Lk} rows')
         rep, valid = self.memory._select(key, k, st.cand32, st.B, H, D)
         M = rep.shape[1]
+        if st.in_place and not self.head_major:
+            return self._multi_head(st, q, k, v, rep, valid, M)
         k_off, kidx = st.slots(M)
         k_len = torch.empty(st.n * H, dtype=torch.int32, device=dev)
         L.check(L.lib().or_memory_index(rep.data_ptr(), valid.data_ptr(), st.cand64.data_ptr(), st.owner64.data_ptr(),
@@ -338,4 +389,31 @@ class MemoryAttention:
         o = varlen(qp, kp, vp, st.cu_q, None, st.max_q, max_k, k_off=k_off, k_len=k_len)
         out = torch.zeros_like(q)
         scatter_rows(o, st.qidx, out.view(Sq * H, 1, D), check=False)
+        return out
+
+    def _multi_head(self, st: _Static, q, k, v, rep, valid, M: int) -> torch.Tensor:
+        """every piece one multi-head segment: its local keys (packed whole rows, the values of their leading run of
+        token rows read in place) then, per head, that head's representatives of the other scenes"""
+        Sq, H, D = q.shape
+        Lk = k.shape[0]
+        dev = q.device
+        n, mh = st.n, st.multi_head(M)
+        fsrc = torch.empty(n * H * M, dtype=torch.int32, device=dev)
+        fdst = torch.empty_like(fsrc)
+        k_len_head = torch.empty(n * H, dtype=torch.int32, device=dev)
+        L.check(L.lib().or_memory_foreign(rep.data_ptr(), valid.data_ptr(), st.cand64.data_ptr(),
+                                          st.owner64.data_ptr(), st.scene64.data_ptr(), st.piece_mem.data_ptr(),
+                                          st.piece_len.data_ptr(), mh['k_off'].data_ptr(), n, H, M, fsrc.data_ptr(),
+                                          fdst.data_ptr(), k_len_head.data_ptr(), L.stream_handle(dev)),
+                'or_memory_foreign')
+        R = mh['rows']
+        kp = torch.empty(R, H, D, dtype=k.dtype, device=dev)
+        vp = torch.empty_like(kp)
+        # local rows (checked once per plan), then the representatives (rows of the checked candidates), one head each
+        pack_job(k, v, mh['src'], mh['dst'], kp, vp, v_src=mh['vsrc'])
+        pack_job(k.view(Lk * H, 1, D), v.view(Lk * H, 1, D), fsrc, fdst, kp.view(R * H, 1, D), vp.view(R * H, 1, D))
+        out = torch.empty_like(q) if st.covers_all else torch.zeros_like(q)
+        varlen(q, kp, vp, st.cu_piece, None, st.max_q, mh['max_k'], k_off=mh['k_off'], k_len=mh['k_len'], out=out,
+               seg_q_src=st.first_q, n_q_video=Sq, sum_q=sum(st.qlen), v_tok=v, v_lead=mh['v_lead'],
+               v_row=mh['v_row'], k_len_head=k_len_head)
         return out

@@ -202,6 +202,31 @@ def pack_rows(plan: ScopePlan, video: torch.Tensor, text: torch.Tensor | None, w
     return (out, b_out) if b_video is not None else out
 
 
+def n_seg_of(cu_q: torch.Tensor) -> int:
+    return cu_q.numel() - 1
+
+
+def pack_job(k, v, src, dst, k_out, v_out, v_src=None):
+    """one or_pack_layer launch without RoPE: packed row dst[r] of k_out / v_out = row src[r] of k / v (nothing for
+    src[r] < 0; values from row v_src[r] when given, none where it is < 0). k, v, k_out, v_out: [rows, H, D] bf16 with
+    contiguous rows; the index arrays are int32 GPU tensors whose rows the caller has checked."""
+    H, D = k.shape[1], k.shape[2]
+    _check_bf16(k, v, k_out, v_out)
+    for t in (k, v, k_out, v_out):
+        if not t.is_contiguous():
+            raise L.HipValueError('pack_job takes contiguous [rows, H, D] tensors')
+    for t in (src, dst, v_src):
+        if t is not None and (t.dtype != torch.int32 or not t.is_cuda or not t.is_contiguous() or
+                              t.numel() != src.numel()):
+            raise L.HipTypeError('src / dst / v_src must be contiguous int32 GPU tensors of one length')
+    a = L.PackArgs()
+    a.k_video, a.v_video, a.video_row_stride, a.text_row_stride, a.n_video = k.data_ptr(), v.data_ptr(), H * D, \
+        H * D, k.shape[0]
+    a.k_src, a.v_src, a.k_dst, a.n_keys = src.data_ptr(), L.ptr(v_src), dst.data_ptr(), src.numel()
+    a.k_out, a.v_out, a.H, a.D = k_out.data_ptr(), v_out.data_ptr(), H, D
+    L.check(L.lib().or_pack_layer(ctypes.byref(a), L.stream_handle(k.device)), 'or_pack_layer')
+
+
 def _check_row_range(idx: torch.Tensor, n: int, what: str):
     """every entry of the int32 device tensor idx in [0, n): the kernels dereference them unchecked, so a row out of
     range is an error here, before any launch (one device reduction and one host read)"""
@@ -251,12 +276,13 @@ def scatter_rows(packed: torch.Tensor, idx: torch.Tensor, out: torch.Tensor, che
 
 def varlen(q, k, v, cu_q, cu_k, max_q, max_k, *, k_off=None, k_len=None, out=None, lse=None, seg_q_src=None,
            q_text=None, o_text=None, n_q_video=None, q_rope=None, cos=None, sin=None, sum_q=None, workspace=None,
-           scale=None, noalloc=False, q_row_step=1, v_tok=None, v_lead=None, v_row=None):
+           scale=None, noalloc=False, q_row_step=1, v_tok=None, v_lead=None, v_row=None, k_len_head=None):
     """or_varlen_fwd on torch tensors. Returns out (allocated [Nq, H, D] when not given). noalloc=True calls
     or_varlen_fwd_noalloc instead: no workspace, the library's fixed per-GPU array (calls must not overlap on a GPU).
     q_row_step > 1 (with seg_q_src): query i of segment s is row seg_q_src[s] + i * q_row_step of q and of out.
     v_tok (with v_lead, v_row): the values of segment s's first v_lead[s] keys are rows v_row[s].. of v_tok (row stride
-    of k), the others rows k_off[s] + v_lead[s].. of v."""
+    of k), the others rows k_off[s] + v_lead[s].. of v. k_len_head [n_seg * H] (with k_len): head h of segment s
+    attends to its first k_len_head[s * H + h] keys."""
     H, D = k.shape[1], k.shape[2]
     _check_bf16(q, k, v, q_text, out, o_text)
     _, qs = _rows2d(q, H, D)
@@ -266,7 +292,9 @@ def varlen(q, k, v, cu_q, cu_k, max_q, max_k, *, k_off=None, k_len=None, out=Non
     if q_text is not None and q_text.shape[0] and q_text.stride(0) != qs:
         raise L.HipValueError('q and q_text must have the same row stride')
     n_seg = (cu_q.numel() - 1)
-    for t in (cu_q, cu_k, k_off, k_len, seg_q_src, q_rope, v_lead, v_row):
+    if k_len_head is not None and (k_len is None or k_len_head.numel() != n_seg_of(cu_q) * H):
+        raise L.HipValueError('k_len_head needs k_len and one entry per segment and head')
+    for t in (cu_q, cu_k, k_off, k_len, seg_q_src, q_rope, v_lead, v_row, k_len_head):
         if t is not None and (t.dtype != torch.int32 or not t.is_cuda or not t.is_contiguous()):
             raise L.HipTypeError('index arrays must be contiguous int32 GPU tensors')
     if v_tok is not None:
@@ -303,6 +331,7 @@ def varlen(q, k, v, cu_q, cu_k, max_q, max_k, *, k_off=None, k_len=None, out=Non
     a.q_row_step = int(q_row_step)
     if v_tok is not None:
         a.v_tok, a.v_lead, a.v_row, a.v_tok_rows = v_tok.data_ptr(), v_lead.data_ptr(), v_row.data_ptr(), v_tok.shape[0]
+    a.k_len_head = L.ptr(k_len_head)
     if noalloc:
         a.workspace, a.workspace_bytes = None, 0
         with torch.cuda.device(q.device):

@@ -355,3 +355,30 @@ def test_select_matches_oracle_at_480p_shape():
         assert torch.allclose(c1[h].cpu().double(), c_ref[0].double(), atol=1e-5), h
         assert sorted(got2[h][gv2[h]].tolist()) == sorted(ref2[0][rv2[0]].tolist()), h
     assert checked >= 2
+
+
+@pytest.mark.parametrize('lengths,T,H,D,M', [([3, 5, 2, 4], 16, 4, 64, 8), ([6, 1, 3], 16, 4, 128, 5),
+                                             ([8] * 4, 1590, 16, 128, 128)])
+def test_multi_head_and_single_head_forms_agree(lengths, T, H, D, M):
+    """the multi-head form (local keys packed as whole rows, their leading token run's values read in place, each
+    head's representatives in its own head slot, per-head key counts) and the single-head form (segment per head and
+    piece over rows of D elements) give the same output bits: the same keys in the same order for every (piece, head),
+    read from other addresses; two calls in a row (cold, then warm)"""
+    print(f'memory forms agree lengths={lengths} T={T} H={H} D={D} M={M}', flush=True)
+    lay = SceneLayout(lengths, halo=0)
+    S = lay.n_frames * T
+    counts = [128] * len(lengths) if T > 100 else [5, 7, 3, 6][:len(lengths)]
+    tr, c = [], 0
+    for x in counts:
+        tr.append((c, c + x))
+        c += x
+    plan = frame_plan(lay, T, torch.arange(S), S, [(j, lo * T, hi * T) for j, (lo, hi) in enumerate(lay.ranges)], tr,
+                      set(range(lay.n_scenes)), S, DEV)
+    mh, sh = MemoryAttention(BoundaryMemory(M)), MemoryAttention(BoundaryMemory(M), head_major=True)
+    g = torch.Generator(device=DEV)
+    for call in range(2):
+        g.manual_seed(70 + call)
+        q, k, v = (torch.randn(S + c, H, D, generator=g, device=DEV).to(torch.bfloat16) for _ in range(3))
+        a = mh(('l', True), q, k, v, plan)
+        b = sh(('l', True), q, k, v, plan)
+        assert torch.equal(a, b), (call, (a.float() - b.float()).abs().max().item())
