@@ -239,6 +239,11 @@ typedef struct or_varlen_args {
   const int32_t* k_len_head;/* optional [n_seg * H] (with k_len): head h of segment s attends to the first
                                min(k_len_head[s * H + h], k_len[s]) keys of the segment's range, e.g. a shared prefix
                                followed by rows that differ per head (the bounded memory's representatives) */
+  const void* k_tok;        /* optional token-order key rows, row stride k_row_stride, read in place as v_tok is: the
+                               first k_lead[s] keys of segment s are rows v_row[s] .. of k_tok, its other keys from k
+                               (rows k_start + k_lead[s] ..); k_lead[s] a multiple of OR_VARLEN_KEY_BLOCK */
+  const int32_t* k_lead;    /* [n_seg], with k_tok (and v_row) */
+  int64_t k_tok_rows;       /* rows of k_tok */
 } or_varlen_args;
 
 /* Bytes of device workspace or_varlen_fwd needs for this many segments, packed queries and heads: the work-item

@@ -48,7 +48,8 @@ class VarlenArgs(ctypes.Structure):
                 ('q_row_stride', i64), ('k_row_stride', i64), ('o_row_stride', i64), ('n_seg', i32), ('sum_q', i32),
                 ('max_q', i32), ('max_k', i32), ('H', i32), ('D', i32), ('scale', ctypes.c_float),
                 ('workspace', vp), ('workspace_bytes', i64), ('q_row_step', i32), ('v_tok', vp), ('v_lead', vp),
-                ('v_row', vp), ('v_tok_rows', i64), ('k_len_head', vp)]
+                ('v_row', vp), ('v_tok_rows', i64), ('k_len_head', vp), ('k_tok', vp), ('k_lead', vp),
+                ('k_tok_rows', i64)]
 
 
 class PackArgs(ctypes.Structure):

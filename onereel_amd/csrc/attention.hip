@@ -41,8 +41,8 @@ constexpr int kQueues = 8;      // item queues: one per XCD
 constexpr int kQueueWords = 32; // words per queue header (head counter, item count, first item), one 128-byte line
 constexpr int kWsHeader = kQueues * kQueueWords;   // int32 words before the item list
 // an item record: tile << 8 | head, part | ways << 8 (0: whole item), split index, and the segment's first query,
-// query count, first source row, first key and key count, then the token row of its first in-place value and the
-// number of keys whose values are read there (0 without in-place values), two words unused (three 16-byte loads)
+// query count, first source row, first key and key count, then the token row of its first in-place key / value, the
+// number of keys whose values and whose keys are read there (0 without them), one word unused (three 16-byte loads)
 constexpr int kItemWords = 12;
 constexpr int kPlanThreads = 1024;
 constexpr int kMaxPlanSeg = 4096;
@@ -79,9 +79,11 @@ struct AttnArgs {
   int32_t* split_tab;
   float* split_lse;
   float* split_o;
-  // in-place values: token-order value rows (row stride ks) and their row count
+  // in-place values and keys: token-order rows (row stride ks) and their row counts
   const uint16_t* v_tok;
   int64_t n_vtok;
+  const uint16_t* k_tok;
+  int64_t n_ktok;
 };
 
 
@@ -112,7 +114,8 @@ __device__ inline int plan_upper_bound(const int* a, int n, int x) {
 __global__ __launch_bounds__(kPlanThreads) void plan_kernel(const int32_t* cu_q, const int32_t* cu_k,
                                                             const int32_t* k_off, const int32_t* k_len,
                                                             const int32_t* seg_q_src, const int32_t* v_lead,
-                                                            const int32_t* v_row, const int32_t* k_len_head,
+                                                            const int32_t* v_row, const int32_t* k_lead,
+                                                            const int32_t* k_len_head,
                                                             int n_seg, int H, int bq,
                                                             int max_items, int slots, int split_keys, int parts_cap,
                                                             int32_t* ws) {
@@ -282,12 +285,12 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(const int32_t* cu_q,
     const int lk_seg = k_len ? k_len[s] : cu_k[s + 1] - cu_k[s];
     const int lk = k_len_head ? min(k_len_head[(int64_t)s * H + head], lk_seg) : lk_seg;   // this head's keys
     const int q_src0 = seg_q_src ? seg_q_src[s] : q_beg;
-    const int vl = v_lead ? v_lead[s] : 0, vr = v_row ? v_row[s] : 0;
+    const int vl = v_lead ? v_lead[s] : 0, vr = v_row ? v_row[s] : 0, kl = k_lead ? k_lead[s] : 0;
     auto put = [&](int64_t entry, int pw, int sidx) {
       int32_t* e = ws + kWsHeader + kItemWords * entry;
       *(int4*)e = make_int4((t << 8) | head, pw, sidx, q_beg);
       *(int4*)(e + 4) = make_int4(lq, q_src0, k_beg, lk < 0 ? 0 : lk);
-      *(int4*)(e + 8) = make_int4(vr, vl, 0, 0);
+      *(int4*)(e + 8) = make_int4(vr, vl, kl, 0);
     };
     if (pos < keep) {
       put(q_first[q] + pos, 0, 0);
@@ -482,26 +485,25 @@ struct Stream {
   __device__ __forceinline__ int32_t nrec(int b) const { return max(rem0 - b * bb, 0); }
 };
 
-// Value stream of a work item (or of one key part of it): key blocks b < nba read the token-order rows from base a,
+// K or V stream of a work item (or of one key part of it): key blocks b < nba read the token-order rows from base a,
 // the others the packed rows from base p; either way block b starts b * bb bytes past its base.
 struct VRange {
   uint64_t a, p;
   int32_t nba;
 };
 
-// the in-place blocks of key blocks [b0, b0 + nb) of a segment whose first v_lead keys take their values from token
-// rows v_row.. (whole blocks only, none past the token rows or the segment's last whole block); p: packed rows of
-// block b0
-__device__ inline VRange value_range(const AttnArgs& a, int v_row, int v_lead, int lk_seg, int b0, int nb,
-                                     int64_t head_off, uint64_t p) {
+// the in-place blocks of key blocks [b0, b0 + nb) of a segment whose first `lead` keys are token rows row.. of tok
+// (whole blocks only, none past the n_tok token rows or the item's last whole block); p: packed rows of block b0
+__device__ inline VRange tok_range(const uint16_t* tok, int64_t n_tok, int64_t rs, int row, int lead, int lk_seg,
+                                   int b0, int nb, int64_t head_off, uint64_t p) {
   VRange r{p, p, 0};
-  if (!a.v_tok || v_lead <= 0 || v_row < 0) return r;
-  int64_t nba = min((int64_t)v_lead, (int64_t)lk_seg) / kBKB;
-  const int64_t fit = (a.n_vtok - v_row) / kBKB;   // blocks that lie inside the token rows
+  if (!tok || lead <= 0 || row < 0) return r;
+  int64_t nba = min((int64_t)lead, (int64_t)lk_seg) / kBKB;
+  const int64_t fit = (n_tok - row) / kBKB;   // blocks that lie inside the token rows
   nba = min(nba, fit) - b0;
   nba = nba < 0 ? 0 : (nba > nb ? nb : nba);
   r.nba = (int32_t)nba;
-  if (nba > 0) r.a = (uint64_t)(a.v_tok + ((int64_t)v_row + (int64_t)kBKB * b0) * a.ks + head_off);
+  if (nba > 0) r.a = (uint64_t)(tok + ((int64_t)row + (int64_t)kBKB * b0) * rs + head_off);
   return r;
 }
 
@@ -677,8 +679,11 @@ void attn4_kernel(AttnArgs a, int32_t* ws) {
     const bool active = q0 < Lq;
     const int nb = (Lk + kBKB - 1) / kBKB;
     const int32_t rb = (int32_t)rs * 2;
-    const VRange vr = value_range(a, r2.x, r2.y, Lk, 0, nb, head * D, (uint64_t)(a.v + (int64_t)k_beg * rs + head * D));
-    const Stream ks = {(uint64_t)(a.k + (int64_t)k_beg * rs + head * D), Lk * rb - rb + D * 2, kBKB * rb, 0, 0};
+    const VRange vr = tok_range(a.v_tok, a.n_vtok, rs, r2.x, r2.y, Lk, 0, nb, head * D,
+                                (uint64_t)(a.v + (int64_t)k_beg * rs + head * D));
+    const VRange kr = tok_range(a.k_tok, a.n_ktok, rs, r2.x, r2.z, Lk, 0, nb, head * D,
+                                (uint64_t)(a.k + (int64_t)k_beg * rs + head * D));
+    const Stream ks = {kr.p, Lk * rb - rb + D * 2, kBKB * rb, kr.a, kr.nba};
     const Stream vs = {vr.p, Lk * rb - rb + D * 2, kBKB * rb, vr.a, vr.nba};
 
     // prologue: K(0) and the group {K(1), V(-1)} (V(-1) fills its slot with zeros: iteration 0 multiplies it by
@@ -858,16 +863,21 @@ void attn8_kernel(AttnArgs a, int32_t* ws) {
     const int q0 = qt * BQ + w * WQ;
     const int nb = (Lk + kBKB - 1) / kBKB;
     float* part_o = ways > 1 ? a.split_o + (int64_t)(sidx * ways + part) * kSplitRows * D : nullptr;
-    const uint64_t kaddr = (uint64_t)(a.k + (int64_t)k_beg * rs + head * D);
     const int32_t rb = (int32_t)rs * 2;
     const int32_t rem0 = Lk * rb - rb + D * 2;
     const int32_t bb = kBKB * rb;
-    // values: blocks [0, vr.nba) from the token-order rows, the others from the packed rows (the key loop moves its
-    // stream's base once, to vsw: the packed rows of block vr.nba)
-    const VRange vr = value_range(a, r2.x, r2.y, lk_seg, b0, nb, head * D,
-                                  (uint64_t)(a.v + (int64_t)k_beg * rs + head * D));
+    // keys and values: blocks [0, nba) from the token-order rows, the others from the packed rows (the key loop moves
+    // each stream's base once, to ksw / vsw: the packed rows of block nba)
+    const VRange vr = tok_range(a.v_tok, a.n_vtok, rs, r2.x, r2.y, lk_seg, b0, nb, head * D,
+                                (uint64_t)(a.v + (int64_t)k_beg * rs + head * D));
+    const VRange kr = tok_range(a.k_tok, a.n_ktok, rs, r2.x, r2.z, lk_seg, b0, nb, head * D,
+                                (uint64_t)(a.k + (int64_t)k_beg * rs + head * D));
     const uint64_t vaddr = vr.nba > 0 ? vr.a : vr.p;
     const uint64_t vsw = vr.p + (uint64_t)vr.nba * (uint32_t)bb;
+    const uint64_t ksw = kr.p + (uint64_t)kr.nba * (uint32_t)bb;
+    // K block b of the ring head (b = 0, 1) and the block the key loop's descriptor starts at (2)
+    auto kblock = [&](int b) { return (b < kr.nba ? kr.a : kr.p) + (uint64_t)b * (uint32_t)bb; };
+    const uint64_t kaddr = kblock(0);
     // every wavefront is done with the previous item's ring: a wavefront without live queries leaves its key loop
     // while the others' epilogues still read the last V block, and its refill below would overwrite a slot
     __syncthreads();
@@ -877,7 +887,7 @@ void attn8_kernel(AttnArgs a, int32_t* ws) {
       // generated prologue fetches the rest of the ring
       const uint32_t vring = sbase + (uint32_t)(kRing64 * kSlot64 * 2);
       dma_block<2>(kaddr, max(rem0, 0), voff, sbase);
-      dma_block<2>(kaddr + bb, max(rem0 - bb, 0), voff, sbase + kSlot64 * 2);
+      dma_block<2>(kblock(1), max(rem0 - bb, 0), voff, sbase + kSlot64 * 2);
       dma_block<2>(vaddr, 0, voff + 2, vring + (kRing64 - 1) * kSlot64 * 2);
     }
 
@@ -944,7 +954,7 @@ void attn8_kernel(AttnArgs a, int32_t* ws) {
       continue;
     }
     const int valid = Lk - (nb - 1) * kBKB - 16 * h;
-    const uint64_t kaddr2 = kaddr + 2 * (uint64_t)bb;   // K block 2, where the prologue's ring fill starts
+    const uint64_t kaddr2 = kblock(2);   // K block 2, where the prologue's ring fill starts
     float mo0, mo1, lo0, lo1;   // per query: the running max of q k^T, and the row sum relative to it
     asm volatile(ONEREEL_RING64_ASM
                  : [mo0] "=&v"(mo0), [mo1] "=&v"(mo1), [lo0] "=&v"(lo0), [lo1] "=&v"(lo1)
@@ -954,7 +964,8 @@ void attn8_kernel(AttnArgs a, int32_t* ws) {
                    [vb_lo] "s"((uint32_t)vaddr), [vb_hi] "s"((uint32_t)(vaddr >> 32)), [rem0] "s"(rem0), [remk] "s"(rem0 - 2 * bb),
                    [op0] "v"(op[0]), [op1] "v"(op[1]), [ok0] "v"(ok[0]), [ok1] "v"(ok[1]),
                    [f32] "s"(__builtin_amdgcn_readfirstlane(ways > 1 ? 1 : 0)),
-                   [dead] "s"(__builtin_amdgcn_readfirstlane(q0 >= Lq ? 1 : 0)), [vsw] "s"(vsw), [nbav] "s"(vr.nba)
+                   [dead] "s"(__builtin_amdgcn_readfirstlane(q0 >= Lq ? 1 : 0)), [vsw] "s"(vsw), [nbav] "s"(vr.nba),
+                   [ksw] "s"(ksw), [nbak] "s"(kr.nba)
                  : ONEREEL_RING64_CLOBBERS);
     // the next item's queries are in a128..a191 unless they must be rotated on the load
     have_q = nit >= 0 && !a.q_rope;
@@ -1118,6 +1129,8 @@ int check_args(const or_varlen_args& x, const char* fn) {
   if (x.k_len_head && !x.k_len) return fail_arg("%s: k_len_head needs k_len (each segment's largest key count)", fn);
   if (x.v_tok && (!x.v_lead || !x.v_row || x.v_tok_rows < 0 || !aligned16(x.v_tok)))
     return fail_arg("%s: v_tok needs v_lead, v_row, v_tok_rows >= 0 and 16-byte alignment", fn);
+  if (x.k_tok && (!x.k_lead || !x.v_row || x.k_tok_rows < 0 || !aligned16(x.k_tok)))
+    return fail_arg("%s: k_tok needs k_lead, v_row, k_tok_rows >= 0 and 16-byte alignment", fn);
   return 0;
 }
 
@@ -1165,13 +1178,16 @@ int launch_varlen(const or_varlen_args& x, void* wsp, int64_t cap, hipStream_t s
   const WsLayout wl = ws_layout(x.n_seg, x.sum_q, x.H, cap);
   a.v_tok = (const uint16_t*)x.v_tok;
   a.n_vtok = x.v_tok ? x.v_tok_rows : 0;
+  a.k_tok = (const uint16_t*)x.k_tok;
+  a.n_ktok = x.k_tok ? x.k_tok_rows : 0;
   a.split_tab = (int32_t*)((char*)wsp + wl.tab);
   a.split_lse = (float*)((char*)wsp + wl.lse);
   a.split_o = (float*)((char*)wsp + wl.o);
   // the planner needs key counts only: k_len when given, else the cu_k differences. It writes every word of the
   // workspace the other kernels read (queue headers, item list, split table) before they run.
   hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(kPlanThreads), 0, st, x.cu_q, x.cu_k, x.k_len ? x.k_off : nullptr,
-                     x.k_len, x.seg_q_src, x.v_tok ? x.v_lead : nullptr, x.v_tok ? x.v_row : nullptr, x.k_len_head,
+                     x.k_len, x.seg_q_src, x.v_tok ? x.v_lead : nullptr, x.v_tok || x.k_tok ? x.v_row : nullptr,
+                     x.k_tok ? x.k_lead : nullptr, x.k_len_head,
                      x.n_seg, x.H,
                      item_bq(x.D), (int)max_items, (int)grid,
                      may_split ? 1 : 0, (int)cap, ws);

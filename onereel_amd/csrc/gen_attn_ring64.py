@@ -15,8 +15,8 @@ emitted here with fixed registers:
     v132..v163  K operands of the 8 k-steps, v164..v195 V^T operands of the 8 (half, db) steps
     v196..v227  -m per query block, broadcast over 16 registers: the first QK^T MFMA of a block accumulates onto it
     v228..v254  softmax temporaries, running max, row sums, LDS read addresses
-    s64..s87    K and V buffer descriptors, their remaining byte counts, loop counters, return address, the V
-                stream's switch point and base
+    s64..s90    K and V buffer descriptors, their remaining byte counts, loop counters, return address, the K and
+                V streams' switch points and bases
 The kernel puts Q into a128..a191 before the block (ONEREEL_RING64_QLOAD, or ONEREEL_RING64_QSET_STEP for queries
 rotated on the load), or the previous item's block left it there: at its loop's exit, where Q is no longer read, a
 block loads the queries of the work-group's next item into those registers (%[qa0], %[qa1]: the lane's query rows of
@@ -48,11 +48,12 @@ rows or, for the parts of a key-split work item, as fp32 partial rows (%[f32]). 
 past the segment (%[dead]) runs a loop of only the barriers and its share of the DMA, so that the block stays in
 step, issues the next item's Q loads at its exit and writes nothing; it leaves the block before the others'
 epilogues, so the kernel waits for a barrier before it refills the ring for the next item.
-In-place values: V blocks 0 .. nbav-1 (%[nbav]) are read from the token-order value rows (the descriptor's first
+In-place keys and values: V blocks 0 .. nbav-1 (%[nbav]) are read from token-order value rows (the descriptor's first
 base, %[vb_lo] / %[vb_hi]), the others from the packed rows (%[vsw]: the base of block nbav there; both advance by
-%[bb] per block). The base is replaced once per work item, with no cost in the steady-state loop: in the ring fill
-when nbav <= R - 2, else at the end of the iteration whose refill fetched block nbav - 1, which the loop's end test
-already stops at (its bound is min(nb - 1, that iteration)).
+%[bb] per block), and K blocks 0 .. nbak-1 likewise (%[ksw]). Each base is replaced once per work item, with no cost
+in the steady-state loop: in the ring fill (V: nbav <= R - 2; K: nbak <= R, the kernel's ring head covering nbak <=
+2), else at the end of the iteration whose refill fetched the stream's last in-place block, which the loop's end test
+already stops at (its bound is the least of nb - 1 and those iterations).
 The generator inserts the LDS waits (lgkmcnt) from the order of the reads, and s_nop where gfx950 needs wait states
 between dependent instructions (see Emitter).
 """
@@ -114,7 +115,8 @@ KRES, VRES = 64, 68             # s[64:67], s[68:71]
 KREM, VREM, SJ, SNB1, SRR, SVOFF = 72, 73, 74, 75, 76, 77
 SRA, SX, SEX = 78, 80, 82       # s[78:79], s[80:81], s[82:83]
 SVTHR, SVSW = 84, 86            # s84: loop count at which the V stream leaves the in-place rows; s[86:87]: its new base
-LAST_SGPR = 87
+SKTHR, SKSW, STMP = 85, 88, 90  # s85, s[88:89]: the same for the K stream; s90: a temporary of the end test
+LAST_SGPR = 90
 NEG_INF = '0xff800000'
 
 
@@ -445,16 +447,24 @@ class Kernel:
         e.raw(f's_cbranch_scc1 .Lend{J}_%=')
 
     def end_block(self, J):
-        """after iteration J with j + 1 >= s75 = min(nb - 1, s84): at j + 1 = s84 the V stream's base moves to the
-        packed rows (%[vsw], the next refill fetches block nbav) and s75 becomes nb - 1; then, at j + 1 >= nb - 1,
-        leave the loop when j + 1 = nb, else mask the last block first, or go on with the next iteration"""
+        """after iteration J with j + 1 >= s75 = min(nb - 1, s84, s85): at j + 1 = s84 the V stream's base moves to
+        the packed rows (%[vsw]: the next refill fetches block nbav), at j + 1 = s85 the K stream's (%[ksw], block
+        nbak); s75 becomes the least of nb - 1 and the switch points still ahead. Then, below nb - 1, go on with the
+        next iteration; at j + 1 >= nb - 1 leave the loop when j + 1 = nb, else mask the last block first"""
         R = self.R
-        return [f'.Lend{J}_%=:', f's_cmp_eq_u32 s{SJ}, s{SVTHR}', f's_cbranch_scc1 .Lvsw{J}_%=',
-                f'.Lendb{J}_%=:', f's_cmp_ge_u32 s{SJ}, %[nb]', f's_cbranch_scc1 .Lexit{J}_%=',
-                f's_branch .Lmask{(J + 1) % R}_%=',
-                f'.Lvsw{J}_%=:', f's_mov_b64 s[{VRES}:{VRES + 1}], s[{SVSW}:{SVSW + 1}]',
-                f's_sub_u32 s{SNB1}, %[nb], 1', f's_cmp_ge_u32 s{SJ}, s{SNB1}', f's_cbranch_scc1 .Lendb{J}_%=',
-                f's_branch .Lmaskret{(J + 1) % R}_%=']
+        return [f'.Lend{J}_%=:',
+                f's_cmp_eq_u32 s{SJ}, s{SVTHR}',
+                f's_cselect_b64 s[{VRES}:{VRES + 1}], s[{SVSW}:{SVSW + 1}], s[{VRES}:{VRES + 1}]',
+                f's_cmp_eq_u32 s{SJ}, s{SKTHR}',
+                f's_cselect_b64 s[{KRES}:{KRES + 1}], s[{SKSW}:{SKSW + 1}], s[{KRES}:{KRES + 1}]',
+                f's_sub_u32 s{SNB1}, %[nb], 1',
+                f's_cmp_gt_u32 s{SVTHR}, s{SJ}', f's_cselect_b32 s{STMP}, s{SVTHR}, s{SNB1}',
+                f's_min_u32 s{SNB1}, s{SNB1}, s{STMP}',
+                f's_cmp_gt_u32 s{SKTHR}, s{SJ}', f's_cselect_b32 s{STMP}, s{SKTHR}, s{SNB1}',
+                f's_min_u32 s{SNB1}, s{SNB1}, s{STMP}',
+                f's_cmp_lt_u32 s{SJ}, s{SNB1}', f's_cbranch_scc1 .Lmaskret{(J + 1) % R}_%=',
+                f's_cmp_ge_u32 s{SJ}, %[nb]', f's_cbranch_scc1 .Lexit{J}_%=',
+                f's_branch .Lmask{(J + 1) % R}_%=']
 
     def mask_block(self, J):
         e = Emitter()
@@ -595,8 +605,15 @@ class Kernel:
         e.raw(f's_add_u32 s{SVTHR}, %[nbav], {2 - R}')
         e.raw(f's_cmp_lt_u32 %[nbav], {R - 1}')
         e.raw(f's_cselect_b32 s{SVTHR}, 0x7fffffff, s{SVTHR}')
+        # K blocks 0 .. nbak-1 likewise (%[ksw]: the packed rows of block nbak): the kernel's ring head covers
+        # nbak <= 2, the ring fill nbak <= R, the loop's end test the rest (j + 1 = nbak - R, in s85)
+        e.raw(f's_mov_b64 s[{SKSW}:{SKSW + 1}], %[ksw]')
+        e.raw(f's_add_u32 s{SKTHR}, %[nbak], {-R}')
+        e.raw(f's_cmp_lt_u32 %[nbak], {R + 1}')
+        e.raw(f's_cselect_b32 s{SKTHR}, 0x7fffffff, s{SKTHR}')
         e.raw(f's_sub_u32 s{SNB1}, %[nb], 1')
         e.raw(f's_min_u32 s{SNB1}, s{SNB1}, s{SVTHR}')
+        e.raw(f's_min_u32 s{SNB1}, s{SNB1}, s{SKTHR}')
         # the K descriptor starts at block 2 (%[kb_lo], %[kb_hi], %[remk]): the kernel fetched the ring's head
         for res, rem, lo, hi, r0 in ((KRES, KREM, 'kb_lo', 'kb_hi', 'remk'), (VRES, VREM, 'vb_lo', 'vb_hi', 'rem0')):
             e.raw(f's_mov_b32 s{res}, %[{lo}]')
@@ -622,6 +639,8 @@ class Kernel:
         # (vmcnt(0) above); the barrier makes every wavefront's part visible.
         for b in range(R - 2):
             self.dma_k(e, b + 2)
+            e.raw(f's_cmp_eq_u32 %[nbak], {b + 3}')
+            e.raw(f's_cselect_b64 s[{KRES}:{KRES + 1}], s[{SKSW}:{SKSW + 1}], s[{KRES}:{KRES + 1}]')
             self.dma_v(e, b)
             e.raw(f's_cmp_eq_u32 %[nbav], {b + 1}')
             e.raw(f's_cselect_b64 s[{VRES}:{VRES + 1}], s[{SVSW}:{SVSW + 1}], s[{VRES}:{VRES + 1}]')
@@ -670,6 +689,8 @@ class Kernel:
                     lines.append('s_nop 0')          # an SALU write of M0 and the LDS DMA reading it
             lines += [f's_add_u32 s{SJ}, s{SJ}, 1', f's_cmp_eq_u32 s{SJ}, s{SVTHR}',
                       f's_cselect_b64 s[{VRES}:{VRES + 1}], s[{SVSW}:{SVSW + 1}], s[{VRES}:{VRES + 1}]',
+                      f's_cmp_eq_u32 s{SJ}, s{SKTHR}',
+                      f's_cselect_b64 s[{KRES}:{KRES + 1}], s[{SKSW}:{SKSW + 1}], s[{KRES}:{KRES + 1}]',
                       f's_cmp_ge_u32 s{SJ}, %[nb]', 's_cbranch_scc1 .Ldeadexit_%=']
         lines += ['s_branch .Ldead_%=', '.Ldeadexit_%=:'] + self.q_prefetch()
         lines += ['s_waitcnt vmcnt(16)', 's_branch .Ldone_%=']

@@ -268,9 +268,9 @@ class _Static:
 
     def multi_head(self, M: int):
         """the multi-head form's per-M tables: per piece its packed row offset (k_off), largest key count (k_len),
-        in-place value run (v_lead whole 32-key blocks from token row v_row); the local rows' pack job (src, dst and
-        value rows, -1 where the value is read in place), and the packed row count. A piece that shares another's
-        local rows gets that piece's offset and run."""
+        in-place run (lead: whole 32-key blocks of keys and values from token row v_row); the pack job of the local
+        rows past the run (src, dst), and the packed row count. A piece that shares another's local rows gets that
+        piece's offset and run."""
         key = ('mh', M)
         if key not in self._slots:
             n, lens = self.n, self.lens
@@ -287,7 +287,7 @@ class _Static:
                 if self.share[i] is not None:
                     off[i] = off[self.share[i]]
             v_row, v_lead = [0] * n, [0] * n
-            src, dst, vsrc = [], [], []
+            src, dst = [], []
             for i in range(n):
                 rows = local[starts[i]:starts[i + 1]]
                 run = 0
@@ -297,13 +297,12 @@ class _Static:
                     v_row[i] = int(rows[0])
                 v_lead[i] = run // L.KEY_BLOCK * L.KEY_BLOCK
                 if self.share[i] is None:
-                    src += rows.tolist()
-                    dst += range(off[i], off[i] + lens[i])
-                    vsrc += [-1] * v_lead[i] + rows[v_lead[i]:].tolist()
+                    src += rows[v_lead[i]:].tolist()
+                    dst += range(off[i] + v_lead[i], off[i] + lens[i])
             t32 = lambda x: torch.tensor(x, dtype=torch.int32, device=self.device)
             k_len = [lens[i] + (M if self.mem[i] else 0) for i in range(n)]
             self._slots[key] = dict(k_off=t32(off), k_len=t32(k_len), max_k=max(k_len), v_row=t32(v_row),
-                                    v_lead=t32(v_lead), src=t32(src), dst=t32(dst), vsrc=t32(vsrc), rows=o)
+                                    lead=t32(v_lead), src=t32(src), dst=t32(dst), rows=o)
         return self._slots[key]
 
     def slots(self, M: int):
@@ -392,8 +391,9 @@ class MemoryAttention:
         return out
 
     def _multi_head(self, st: _Static, q, k, v, rep, valid, M: int) -> torch.Tensor:
-        """every piece one multi-head segment: its local keys (packed whole rows, the values of their leading run of
-        token rows read in place) then, per head, that head's representatives of the other scenes"""
+        """every piece one multi-head segment: its local keys (the leading run of token rows, whole key blocks of it,
+        read in place from k / v, the rest packed as whole rows) then, per head, that head's representatives of the
+        other scenes in its own head slot"""
         Sq, H, D = q.shape
         Lk = k.shape[0]
         dev = q.device
@@ -409,11 +409,13 @@ class MemoryAttention:
         R = mh['rows']
         kp = torch.empty(R, H, D, dtype=k.dtype, device=dev)
         vp = torch.empty_like(kp)
-        # local rows (checked once per plan), then the representatives (rows of the checked candidates), one head each
-        pack_job(k, v, mh['src'], mh['dst'], kp, vp, v_src=mh['vsrc'])
+        # local rows past the in-place run (checked once per plan), then the representatives (rows of the checked
+        # candidates), one head each
+        if mh['src'].numel():
+            pack_job(k, v, mh['src'], mh['dst'], kp, vp)
         pack_job(k.view(Lk * H, 1, D), v.view(Lk * H, 1, D), fsrc, fdst, kp.view(R * H, 1, D), vp.view(R * H, 1, D))
         out = torch.empty_like(q) if st.covers_all else torch.zeros_like(q)
         varlen(q, kp, vp, st.cu_piece, None, st.max_q, mh['max_k'], k_off=mh['k_off'], k_len=mh['k_len'], out=out,
-               seg_q_src=st.first_q, n_q_video=Sq, sum_q=sum(st.qlen), v_tok=v, v_lead=mh['v_lead'],
-               v_row=mh['v_row'], k_len_head=k_len_head)
+               seg_q_src=st.first_q, n_q_video=Sq, sum_q=sum(st.qlen), v_tok=v, v_lead=mh['lead'],
+               v_row=mh['v_row'], k_tok=k, k_lead=mh['lead'], k_len_head=k_len_head)
         return out

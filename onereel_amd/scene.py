@@ -276,13 +276,14 @@ def scatter_rows(packed: torch.Tensor, idx: torch.Tensor, out: torch.Tensor, che
 
 def varlen(q, k, v, cu_q, cu_k, max_q, max_k, *, k_off=None, k_len=None, out=None, lse=None, seg_q_src=None,
            q_text=None, o_text=None, n_q_video=None, q_rope=None, cos=None, sin=None, sum_q=None, workspace=None,
-           scale=None, noalloc=False, q_row_step=1, v_tok=None, v_lead=None, v_row=None, k_len_head=None):
+           scale=None, noalloc=False, q_row_step=1, v_tok=None, v_lead=None, v_row=None, k_len_head=None,
+           k_tok=None, k_lead=None):
     """or_varlen_fwd on torch tensors. Returns out (allocated [Nq, H, D] when not given). noalloc=True calls
     or_varlen_fwd_noalloc instead: no workspace, the library's fixed per-GPU array (calls must not overlap on a GPU).
     q_row_step > 1 (with seg_q_src): query i of segment s is row seg_q_src[s] + i * q_row_step of q and of out.
     v_tok (with v_lead, v_row): the values of segment s's first v_lead[s] keys are rows v_row[s].. of v_tok (row stride
-    of k), the others rows k_off[s] + v_lead[s].. of v. k_len_head [n_seg * H] (with k_len): head h of segment s
-    attends to its first k_len_head[s * H + h] keys."""
+    of k), the others rows k_off[s] + v_lead[s].. of v; k_tok with k_lead (and v_row) likewise for the keys.
+    k_len_head [n_seg * H] (with k_len): head h of segment s attends to its first k_len_head[s * H + h] keys."""
     H, D = k.shape[1], k.shape[2]
     _check_bf16(q, k, v, q_text, out, o_text)
     _, qs = _rows2d(q, H, D)
@@ -294,7 +295,7 @@ def varlen(q, k, v, cu_q, cu_k, max_q, max_k, *, k_off=None, k_len=None, out=Non
     n_seg = (cu_q.numel() - 1)
     if k_len_head is not None and (k_len is None or k_len_head.numel() != n_seg_of(cu_q) * H):
         raise L.HipValueError('k_len_head needs k_len and one entry per segment and head')
-    for t in (cu_q, cu_k, k_off, k_len, seg_q_src, q_rope, v_lead, v_row, k_len_head):
+    for t in (cu_q, cu_k, k_off, k_len, seg_q_src, q_rope, v_lead, v_row, k_len_head, k_lead):
         if t is not None and (t.dtype != torch.int32 or not t.is_cuda or not t.is_contiguous()):
             raise L.HipTypeError('index arrays must be contiguous int32 GPU tensors')
     if v_tok is not None:
@@ -303,6 +304,12 @@ def varlen(q, k, v, cu_q, cu_k, max_q, max_k, *, k_off=None, k_len=None, out=Non
             raise L.HipValueError('v_tok needs v_lead and v_row')
         if _rows2d(v_tok, H, D)[1] != ks:
             raise L.HipValueError('v_tok must have the row stride of k and v')
+    if k_tok is not None:
+        _check_bf16(k_tok)
+        if k_lead is None or v_row is None:
+            raise L.HipValueError('k_tok needs k_lead and v_row')
+        if _rows2d(k_tok, H, D)[1] != ks:
+            raise L.HipValueError('k_tok must have the row stride of k and v')
     if sum_q is None:
         sum_q = q.shape[0] if seg_q_src is None else None
         if sum_q is None:
@@ -332,6 +339,8 @@ def varlen(q, k, v, cu_q, cu_k, max_q, max_k, *, k_off=None, k_len=None, out=Non
     if v_tok is not None:
         a.v_tok, a.v_lead, a.v_row, a.v_tok_rows = v_tok.data_ptr(), v_lead.data_ptr(), v_row.data_ptr(), v_tok.shape[0]
     a.k_len_head = L.ptr(k_len_head)
+    if k_tok is not None:
+        a.k_tok, a.k_lead, a.v_row, a.k_tok_rows = k_tok.data_ptr(), k_lead.data_ptr(), v_row.data_ptr(), k_tok.shape[0]
     if noalloc:
         a.workspace, a.workspace_bytes = None, 0
         with torch.cuda.device(q.device):

@@ -1,7 +1,7 @@
-"""GPU parity of the values read in place: the attention kernels' value stream switching from token-order rows
-(or_varlen_args.v_tok, the first v_lead keys of a segment) to packed rows, the one-launch pack of a layer
-(or_pack_layer: keys, the values not read in place, the rotated queries), and the layer with and without in-place
-values."""
+"""GPU parity of the keys and values read in place: the attention kernels' value stream switching from token-order
+rows (or_varlen_args.v_tok, the first v_lead keys of a segment) to packed rows, the key stream likewise (k_tok,
+k_lead), the one-launch pack of a layer (or_pack_layer: keys, the values not read in place, the rotated queries), and
+the layer with and without in-place values."""
 import numpy as np
 import pytest
 import torch
@@ -175,3 +175,74 @@ def test_layer_values_in_place_bit_identical(name, q_range, adjacent):
         ov2, ot2 = scene.scene_attention(plan, *g, cos, sin, mode='raw', fused=True, values_in_place=False)
         assert torch.equal(ov, ov2) and torch.equal(ot, ot2)
         del ov, ot, ov2, ot2
+
+
+def _kv_in_place_case(lq, lk, v_blocks, k_blocks, H, D, seed):
+    """as _in_place_case, with the keys too: segment s reads the K rows of its first 32 * k_blocks[s] keys and the V
+    rows of its first 32 * v_blocks[s] from token-order tensors that hold them at one common row (the packed rows
+    under them hold POISON)"""
+    rng = np.random.default_rng(seed)
+    q = rand_bf16((sum(lq), H, D), seed)
+    k = rand_bf16((sum(lk), H, D), seed + 1)
+    v = rand_bf16((sum(lk), H, D), seed + 2)
+    cq, ck = np.cumsum([0] + lq), np.cumsum([0] + lk)
+    lead = [32 * max(a, b) for a, b in zip(v_blocks, k_blocks)]
+    n_tok = sum(lead) + 300
+    ktok, vtok = rand_bf16((n_tok, H, D), seed + 3), rand_bf16((n_tok, H, D), seed + 4)
+    rows = [int(rng.integers(0, n_tok - x + 1)) for x in lead]
+    kp, vp = k.clone(), v.clone()
+    for s in range(len(lk)):
+        kl, vl = 32 * k_blocks[s], 32 * v_blocks[s]
+        assert max(kl, vl) <= lk[s]
+        k[ck[s]:ck[s] + kl] = ktok[rows[s]:rows[s] + kl]
+        v[ck[s]:ck[s] + vl] = vtok[rows[s]:rows[s] + vl]
+        kp[ck[s]:ck[s] + kl] = POISON
+        vp[ck[s]:ck[s] + vl] = POISON
+    t = lambda x: torch.tensor(x, dtype=torch.int32, device=DEV)
+    dev = dict(q=q.to(DEV), k=kp.to(DEV), v=vp.to(DEV), cu_q=t(cq), cu_k=t(ck), max_q=max(lq), max_k=max(lk),
+               v_tok=vtok.to(DEV), v_lead=t([32 * b for b in v_blocks]), v_row=t(rows), k_tok=ktok.to(DEV),
+               k_lead=t([32 * b for b in k_blocks]))
+    return q, k, v, cq, ck, dev
+
+
+# K lead blocks: none, the ring head (1, 2), the ring fill (3 .. 8), the key loop (9 on), every whole block; the V
+# lead blocks independent of them
+@pytest.mark.parametrize('D', [128, 64])
+@pytest.mark.parametrize('lq,lk,v_blocks,k_blocks,H', [
+    ([300, 40, 257, 5], [40, 700, 1000, 300], [0, 1, 6, 9], [1, 2, 3, 9], 8),
+    ([129, 64, 500], [230, 250, 2049], [7, 0, 64], [7, 5, 8], 3),
+    ([33, 1, 700, 90], [64, 32, 257, 5000], [2, 1, 0, 156], [0, 1, 8, 100], 2),
+    ([640, 0, 77], [3000, 100, 32], [93, 3, 1], [93, 2, 0], 5),
+])
+def test_varlen_keys_and_values_in_place(lq, lk, v_blocks, k_blocks, H, D):
+    """keys and values read in place with separate leads (each stream's base switching at its own block, in the ring
+    head, the ring fill or the loop): O and lse against the fp32 oracle, and O bit-identical to the call with every
+    key and value packed"""
+    print(f'keys and values in place lq={lq} lk={lk} v blocks={v_blocks} k blocks={k_blocks} H={H} D={D}', flush=True)
+    q, k, v, cq, ck, dev = _kv_in_place_case(lq, lk, v_blocks, k_blocks, H, D, 171)
+    ref = OA.packed_attention(q, k, v, cq, ck)
+    o = _run(dev)
+    assert_close(o.cpu(), ref, what='keys and values in place')
+    full = dict(q=dev['q'], k=k.to(DEV), v=v.to(DEV), cu_q=dev['cu_q'], cu_k=dev['cu_k'], max_q=dev['max_q'],
+                max_k=dev['max_k'])
+    assert torch.equal(o, _run(full))
+    o2, lse = _run(dev, lse=True)
+    assert_close(o2.cpu(), ref, what='keys and values in place, lse call')
+    assert (lse.cpu() - _lse_ref(q, k, cq, ck, D)).abs().max() < 2e-3
+
+
+@pytest.mark.parametrize('lq,lk,v_blocks,k_blocks,H', [([1000], [20000], [600], [602], 4),
+                                                       ([300, 7], [5000, 3000], [150, 0], [140, 40], 3)])
+def test_varlen_keys_in_place_key_split(lq, lk, v_blocks, k_blocks, H):
+    """key parts of split items with keys and values in place: each part's in-place blocks of each stream"""
+    D = 128
+    print(f'keys in place, key split lq={lq} lk={lk} v={v_blocks} k={k_blocks} H={H}', flush=True)
+    q, k, v, cq, ck, dev = _kv_in_place_case(lq, lk, v_blocks, k_blocks, H, D, 191)
+    ref = OA.packed_attention(q, k, v, cq, ck)
+    ws = torch.zeros(int(scene.L.lib().or_varlen_workspace_size(len(lq), sum(lq), H, D)), dtype=torch.uint8,
+                     device=DEV)
+    a = dict(dev)
+    qq, kk, vv, cu_q, cu_k, mq, mk = (a.pop(x) for x in ('q', 'k', 'v', 'cu_q', 'cu_k', 'max_q', 'max_k'))
+    o = scene.varlen(qq, kk, vv, cu_q, cu_k, mq, mk, workspace=ws, **a)
+    assert int(ws.view(torch.int32)[3]) > 0
+    assert_close(o.cpu(), ref, what='keys in place, key split')

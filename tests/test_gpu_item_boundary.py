@@ -38,9 +38,10 @@ def _lse_ref(q, k, cq, ck, D):
     return out
 
 
-def _check(lq, lk, H, D, seed, lead_blocks=None, expect_split=False):
+def _check(lq, lk, H, D, seed, lead_blocks=None, expect_split=False, keys_too=False):
     """one O + lse call against the oracle over every row; with lead_blocks, the first 32 * lead_blocks[s] values of
-    segment s are read from a token-order tensor (the packed rows there hold a poison value)"""
+    segment s (and with keys_too its keys) are read from token-order tensors (the packed rows there hold a poison
+    value)"""
     q = rand_bf16((sum(lq), H, D), seed)
     k = rand_bf16((sum(lk), H, D), seed + 1)
     v = rand_bf16((sum(lk), H, D), seed + 2)
@@ -57,11 +58,18 @@ def _check(lq, lk, H, D, seed, lead_blocks=None, expect_split=False):
             vp[ck[s]:ck[s] + lead[s]] = 3.0e4
         vdev = vp.to(DEV)
         extra = dict(v_tok=vtok.to(DEV), v_lead=t(lead), v_row=t(rows))
+        if keys_too:
+            ktok = torch.cat([k[ck[s]:ck[s] + lead[s]] for s in range(len(lk))] + [rand_bf16((64, H, D), seed + 4)])
+            kpk = k.clone()
+            for s in range(len(lk)):
+                kpk[ck[s]:ck[s] + lead[s]] = 3.0e4
+            extra.update(k_tok=ktok.to(DEV), k_lead=t(lead))
+    kdev = kpk.to(DEV) if lead_blocks is not None and keys_too else k.to(DEV)
     ws = torch.zeros(int(L.lib().or_varlen_workspace_size(len(lq), sum(lq), H, D)), dtype=torch.uint8, device=DEV)
     o = torch.empty(sum(lq), H, D, dtype=torch.bfloat16, device=DEV)
     lse = torch.empty(H, sum(lq), dtype=torch.float32, device=DEV)
-    scene.varlen(q.to(DEV), k.to(DEV), vdev, t(cq), t(ck), max(lq), max(lk), out=o, lse=lse, workspace=ws, **extra)
-    o2 = scene.varlen(q.to(DEV), k.to(DEV), vdev, t(cq), t(ck), max(lq), max(lk), **extra)   # O-only kernel path
+    scene.varlen(q.to(DEV), kdev, vdev, t(cq), t(ck), max(lq), max(lk), out=o, lse=lse, workspace=ws, **extra)
+    o2 = scene.varlen(q.to(DEV), kdev, vdev, t(cq), t(ck), max(lq), max(lk), **extra)   # O-only kernel path
     split = int(ws.view(torch.int32)[3])
     assert (split > 0) == expect_split, split
     ref = OA.packed_attention(q, k, v, cq, ck)
@@ -96,16 +104,18 @@ def test_many_items_per_work_group(monkeypatch, blocks, D):
     _check(lq, lk, 8, D, 200 + blocks, expect_split=False)
 
 
+@pytest.mark.parametrize('keys_too', [False, True])
 @pytest.mark.parametrize('D', [128, 64])
-def test_many_items_with_values_in_place(monkeypatch, D):
-    """the same walk with every segment's first whole key blocks read in place (0 to all of them), so that items whose
-    value stream switches in the ring fill, in the loop, or not at all follow each other on one work-group"""
+def test_many_items_with_values_in_place(monkeypatch, D, keys_too):
+    """the same walk with every segment's first whole key blocks' values (and keys) read in place (0 to all of them),
+    so that items whose streams switch in the ring head, the ring fill, the loop, or not at all follow each other on
+    one work-group"""
     monkeypatch.setenv('ONEREEL_ATTN_MAX_BLOCKS', '4')
     lq, lk = _many_items(21)
     rng = np.random.default_rng(5)
     lead = [int(rng.integers(0, x // 32 + 1)) for x in lk]
-    print(f'item boundaries, values in place: D={D}, lq={lq}, lk={lk}, lead blocks={lead}', flush=True)
-    _check(lq, lk, 8, D, 300, lead_blocks=lead)
+    print(f'item boundaries, in place (keys too: {keys_too}): D={D}, lq={lq}, lk={lk}, lead blocks={lead}', flush=True)
+    _check(lq, lk, 8, D, 300, lead_blocks=lead, keys_too=keys_too)
 
 
 @pytest.mark.parametrize('lq,lk,H,lead', [([300, 40], [5000, 3000], 2, None), ([700], [9000], 3, None),
