@@ -84,32 +84,51 @@ struct RowWork {
   u32x4 va[CPL], vb[CPL];
 };
 
+// The index words of row rr of the launch (source, second source, table rows, destination), loaded one row ahead of
+// the row's data so that their latency overlaps the previous row's loads and stores
+struct RowIdx {
+  int src, bsrc, rope, mfrom;
+  int64_t dst;
+};
+
 // MOVE: some job rotates with move_from (a second, inverse rotation first); without it no register holds its table
+template <bool MOVE>
+__device__ __forceinline__ RowIdx row_index(const GatherArgs& g, int64_t rr, int64_t total) {
+  RowIdx x{-1, -1, -1, -1, 0};
+  if (rr >= total) return x;
+  const bool second = rr >= g.job[0].n_rows;
+  const RowJob& J = second ? g.job[1] : g.job[0];
+  const int64_t r = second ? rr - g.job[0].n_rows : rr;
+  x.src = J.src_idx[r];
+  x.bsrc = J.b_out ? (J.b_idx ? J.b_idx[r] : x.src) : -1;
+  x.rope = J.rope_row ? J.rope_row[r] : -1;
+  x.mfrom = MOVE && J.move_from ? J.move_from[r] : -1;
+  x.dst = J.dst_idx ? J.dst_idx[r] : r;
+  return x;
+}
+
 template <int CPL, bool MOVE>
 __device__ __forceinline__ void row_load(const GatherArgs& g, int64_t rr, int64_t total, const RowLanes& rl,
-                                         int chunks, RowWork<CPL>& w) {
+                                         int chunks, const RowIdx& x, RowWork<CPL>& w) {
   w.live = false;
   if (rr >= total) return;
   const bool second = rr >= g.job[0].n_rows;
   const RowJob& J = second ? g.job[1] : g.job[0];
-  const int64_t r = second ? rr - g.job[0].n_rows : rr;
-  const int src = J.src_idx[r];
+  const int src = x.src;
   const bool text = src >= g.n_video;
   if (src < 0 || (J.in_place && text)) return;
   w.live = true;
   const int64_t off = text ? (int64_t)(src - g.n_video) * J.text_stride : (int64_t)src * J.src_stride;
   const uint16_t* a = (text ? J.a_text : J.a_video) + off;
   const uint16_t* b = nullptr;
-  if (J.b_out) {
-    const int bs = J.b_idx ? J.b_idx[r] : src;
-    if (bs >= 0) {
-      const bool bt = bs >= g.n_video;
-      b = bt ? J.b_text + (int64_t)(bs - g.n_video) * J.text_stride : J.b_video + (int64_t)bs * J.src_stride;
-    }
+  if (J.b_out && x.bsrc >= 0) {
+    const int bs = x.bsrc;
+    const bool bt = bs >= g.n_video;
+    b = bt ? J.b_text + (int64_t)(bs - g.n_video) * J.text_stride : J.b_video + (int64_t)bs * J.src_stride;
   }
   // table rows outside the table leave the row unrotated (the host validates them; this only keeps reads in bounds)
-  int rope = J.rope_row ? J.rope_row[r] : -1;
-  int mfrom = MOVE && J.move_from ? J.move_from[r] : -1;
+  int rope = x.rope;
+  int mfrom = x.mfrom;
   if (rope >= g.n_rope_rows || mfrom >= g.n_rope_rows) rope = mfrom = -1;
   w.rope = rope;
   w.mfrom = mfrom;
@@ -130,7 +149,7 @@ __device__ __forceinline__ void row_load(const GatherArgs& g, int64_t rr, int64_
     w.tr = load_tab8(g.cos_t, g.sin_t, (int64_t)rope * g.D + d0);
     if (MOVE && J.move_from) w.tm = load_tab8(g.cos_t, g.sin_t, (int64_t)mfrom * g.D + d0);
   }
-  const int64_t dst = J.dst_idx ? J.dst_idx[r] : r;
+  const int64_t dst = x.dst;
   w.ao = J.in_place ? J.a_out + (int64_t)src * J.out_stride : J.a_out + dst * row_elems;
   w.bo = b ? J.b_out + dst * row_elems : nullptr;
 }
@@ -161,18 +180,25 @@ __device__ __forceinline__ void row_store(const GatherArgs& g, const RowLanes& r
 
 // one row per wavefront (lane group) at a time; the register count per row (CPL chunks, no move table without MOVE)
 // sets how many waves a SIMD holds, and more of them in flight beat more rows per wave (two rows per wave, all loads
-// ahead of the stores, measured 15% slower at the 480p layer: 0.258 against 0.225 ms)
+// ahead of the stores, measured 15% slower at the 480p layer: 0.258 against 0.225 ms). The wavefront index is made
+// uniform (readfirstlane), so that a wide row's index words are scalar loads into SGPRs: 70 instead of 98 VGPRs, 7
+// waves per SIMD, and with the indices loaded one row ahead the layer's pack took 0.204 ms instead of 0.234 (index
+// words loaded with the row: 0.224 ms; two or three rows ahead, or grids of 1792 or 3584 blocks: within 1%)
 template <bool NARROW, int CPL, bool MOVE>
 __global__ __launch_bounds__(kThreads) void pack_gather_kernel(GatherArgs g) {
   const int lane = threadIdx.x & 63;
-  const int64_t wave = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6);
+  const int64_t wave = (int64_t)__builtin_amdgcn_readfirstlane((int)(blockIdx.x * kWaves + (threadIdx.x >> 6)));
   const int64_t n_waves = (int64_t)gridDim.x * kWaves;
   const int chunks = (g.H * g.D) >> 3;
   const RowLanes rl = row_lanes<NARROW>(chunks, lane);
   const int64_t total = g.job[0].n_rows + g.job[1].n_rows;
-  for (int64_t r0 = wave * rl.per; r0 < total; r0 += n_waves * rl.per) {
+  const int64_t step = n_waves * rl.per;
+  RowIdx next = row_index<MOVE>(g, wave * rl.per + rl.sub, total);
+  for (int64_t r0 = wave * rl.per; r0 < total; r0 += step) {
+    const RowIdx cur = next;
     RowWork<CPL> w;
-    row_load<CPL, MOVE>(g, r0 + rl.sub, total, rl, chunks, w);
+    row_load<CPL, MOVE>(g, r0 + rl.sub, total, rl, chunks, cur, w);
+    next = row_index<MOVE>(g, r0 + step + rl.sub, total);
     row_store<CPL, MOVE>(g, rl, chunks, w);
   }
 }
