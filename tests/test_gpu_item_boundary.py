@@ -11,8 +11,8 @@ The transitions between two items of one work-group that these calls drive:
 - items without keys (nb == 0: O = 0, lse = -inf), which run no key loop, so the next item loads its own queries;
 - query tiles whose last wavefronts lie past the segment (dead wavefronts: a key loop of barriers and DMA only),
   followed by an item whose wavefronts are all live;
-- items whose values are partly read in place (the value stream's base switching in the ring fill or in the loop),
-  next to items whose values are all packed;
+- items whose values (and keys) are partly read in place (each stream's base switching in the ring head, the ring
+  fill or the loop), next to items whose values and keys are all packed;
 - key-split parts of the last items (capped grid, few items), several parts per work-group, merged afterwards.
 """
 import numpy as np
