@@ -7,13 +7,16 @@
  *                     scopes read their keys in place from their video scopes' packed rows)
  *   or_rotate_rows    the video queries rotated once, in token order (RoPE ahead of in-place attention)
  *   or_pack_layer     or_pack_gather (K, and the values not read in place) and or_rotate_rows in one launch
- *   or_varlen_fwd     packed varlen attention (bf16 MFMA), optional RoPE on the Q load, optional in-place Q / O
+ *   or_varlen_fwd     packed varlen attention (bf16 MFMA), optional RoPE on the Q load, optional in-place Q / O,
+ *                     each segment's leading keys and values optionally read in place from token-order rows
  *   or_scatter        packed output rows written back to token order, text padding rows zeroed
  *   or_lse_merge      log-sum-exp merge of two partial attention results (attention split over key sets)
  *   or_rmsnorm_rope   fused RMSNorm + interleaved RoPE of the Wan self-attention's queries and keys
  *   or_frame_pool     frame memory: per-frame sums of hidden states (deterministic)
  *   or_frame_select   frame memory: k-means (cosine) representatives and their medoids, one workgroup
- *   or_memory_select, or_memory_index         bounded memory: per-head k-means representatives, per-piece key lists
+ *   or_memory_select, or_memory_foreign,
+ *   or_memory_index                            bounded memory: per-head k-means representatives, each piece's foreign
+ *                                              representatives (multi-head form) or key lists (single-head form)
  *   or_layernorm_modulate, or_gated_residual,
  *   or_residual_layernorm_modulate             the fused elementwise work of the Wan-shaped DiT block harness
  *

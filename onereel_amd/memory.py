@@ -12,11 +12,12 @@ frame plans of the models):
 
     or_memory_select   k-means + medoids for every head (fp32 MFMA distances, fixed-order sums, device-side stop)
     or_memory_foreign  each (piece, head)'s foreign representatives: source and packed rows, per-head key counts
-    or_pack_layer      the local K rows of every piece (whole rows, all heads) and the local V rows not read in place
+    or_pack_layer      the local K / V rows of every piece past its in-place run (whole rows, all heads)
     or_pack_layer      the foreign K / V rows, one head each, into their head slots after the local rows
     or_varlen_fwd      multi-head attention over the pieces: queries read and outputs written in place, the leading
-                       run of each piece's local values (its scene's frames) read in place, head h of piece i over
-                       its first k_len_head[i, h] keys (local, then its own representatives)
+                       run of each piece's local keys and values (its scene's frames, whole 32-key blocks) read in
+                       place from k and v, head h of piece i over its first k_len_head[i, h] keys (local, then its
+                       own representatives)
 
 Otherwise (query rows in any order) the single-head form runs: segment (head, piece) over rows of D elements, row =
 token * H + head, with or_memory_index, or_pack_gather of single-head rows, gathered queries and a scatter.
