@@ -17,8 +17,9 @@
  *   or_memory_select, or_memory_foreign,
  *   or_memory_index                            bounded memory: per-head k-means representatives, each piece's foreign
  *                                              representatives (multi-head form) or key lists (single-head form)
- *   or_layernorm_modulate, or_gated_residual,
- *   or_residual_layernorm_modulate             the fused elementwise work of the Wan-shaped DiT block harness
+ *
+ * The fused elementwise kernels of the Wan-shaped DiT block harness (a measurement harness around the scene path,
+ * not part of it) are a separate library, libonereel_dit.so (include/onereel_dit.h).
  *
  * Conventions: every tensor is caller-owned device memory passed as a raw pointer; rows are [row][head][dim] with a
  * row stride in elements; bf16 is IEEE bfloat16 stored as uint16_t; index arrays are int32. Every launch goes on the
@@ -308,27 +309,6 @@ int or_frame_pool(const void* hs, int64_t n_rows, int32_t C, int64_t row_stride,
  * frames ascending, -1 after them. work: fp32 [8, C] device scratch. One workgroup; k * C <= 32768. */
 int or_frame_select(const float* feats, int32_t n_frames, int32_t C, const int32_t* cand, int32_t n_cand, int32_t k,
                     int32_t iters, int32_t* reps, float* work, void* stream);
-
-/* Replaces the LayerNorm + modulation chains of the Wan transformer block the reference's processors run in
- * (diffusers' WanTransformerBlock, third-party; installed at src/onereel/models/wan.py:77-108): per bf16 row of C
- * elements, y = (x - mean) * rstd, then * weight, + bias, * (1 + scale), + shift for each of those fp32 [C] vectors
- * that is not NULL, in that order and in fp32; out = bf16(y). */
-int or_layernorm_modulate(const void* x, void* out, int64_t n_rows, int32_t C, int64_t x_row_stride,
-                          int64_t out_row_stride, float eps, const float* weight, const float* bias, const float* scale,
-                          const float* shift, void* stream);
-
-/* Replaces the block's residual adds (same block): x = bf16(float(x) + float(a) * gate), gate fp32 [C], or
- * x = bf16(float(x) + float(a)) when gate is NULL; in place on x. */
-int or_gated_residual(void* x, const void* a, const float* gate, int64_t n_rows, int32_t C, int64_t x_row_stride,
-                      int64_t a_row_stride, void* stream);
-
-/* Replaces a residual add of the block followed by the next LayerNorm + modulation (the same block, or the next
- * block's first norm): or_gated_residual on x, then or_layernorm_modulate of the updated x into out, with the same
- * results bit for bit, in one pass over the rows when C <= 4096 (two passes above). out must be neither x nor a. */
-int or_residual_layernorm_modulate(void* x, const void* a, const float* gate, void* out, int64_t n_rows, int32_t C,
-                                   int64_t x_row_stride, int64_t a_row_stride, int64_t out_row_stride, float eps,
-                                   const float* weight, const float* bias, const float* scale, const float* shift,
-                                   void* stream);
 
 /* Bytes of device workspace or_memory_select needs: the normalised keys [H, B, D] fp32 and per-candidate arrays. */
 int64_t or_memory_select_workspace_size(int32_t B, int32_t H, int32_t D, int32_t M, int32_t iters);

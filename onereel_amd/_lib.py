@@ -13,6 +13,8 @@ from pathlib import Path
 import torch  # noqa: F401  (loads the HIP runtime the library binds to)
 
 LIB_PATH = Path(os.environ.get('ONEREEL_HIP_LIB', Path(__file__).resolve().parent / 'libonereel_hip.so'))
+# the DiT harness's elementwise kernels (include/onereel_dit.h), not on the scene-attention path
+DIT_LIB_PATH = Path(__file__).resolve().parent / 'libonereel_dit.so'
 
 OR_MAX_SCENES = 64
 OR_MAX_EXTRA = 512
@@ -81,15 +83,20 @@ SIGNATURES = {
     'or_memory_select': (i32, [vp, i32, vp, i64, i32, i32, i32, i32, vp, vp, i32, vp, vp, vp, i64, vp]),
     'or_memory_index': (i32, [vp, vp, vp, vp, vp, vp, vp, vp, i32, i32, i32, vp, vp, vp]),
     'or_memory_foreign': (i32, [vp, vp, vp, vp, vp, vp, vp, vp, i32, i32, i32, vp, vp, vp, vp]),
-    'or_layernorm_modulate': (i32, [vp, vp, i64, i32, i64, i64, ctypes.c_float, vp, vp, vp, vp, vp]),
-    'or_gated_residual': (i32, [vp, vp, vp, i64, i32, i64, i64, vp]),
-    'or_residual_layernorm_modulate': (i32, [vp, vp, vp, vp, i64, i32, i64, i64, i64, ctypes.c_float, vp, vp, vp, vp,
-                                             vp]),
     'or_last_error': (ctypes.c_char_p, []),
     'or_version': (ctypes.c_char_p, []),
 }
 
+# libonereel_dit.so: include/onereel_dit.h
+DIT_SIGNATURES = {
+    'or_layernorm_modulate': (i32, [vp, vp, i64, i32, i64, i64, ctypes.c_float, vp, vp, vp, vp, vp]),
+    'or_gated_residual': (i32, [vp, vp, vp, i64, i32, i64, i64, vp]),
+    'or_residual_layernorm_modulate': (i32, [vp, vp, vp, vp, i64, i32, i64, i64, i64, ctypes.c_float, vp, vp, vp, vp,
+                                             vp]),
+}
+
 _lib = None
+_dit_lib = None
 
 
 class HipPathError(RuntimeError):
@@ -120,9 +127,32 @@ def lib():
     return _lib
 
 
+def dit_lib():
+    """the DiT harness's library (it loads libonereel_hip.so beside it and reports errors through its or_last_error,
+    which dit_check reads through this handle)"""
+    global _dit_lib
+    if _dit_lib is None:
+        lib()
+        if not DIT_LIB_PATH.exists():
+            raise RuntimeError(f'{DIT_LIB_PATH} is not built: run python -m onereel_amd.build')
+        h = ctypes.CDLL(str(DIT_LIB_PATH))
+        for name, (res, args) in DIT_SIGNATURES.items():
+            f = getattr(h, name)
+            f.restype, f.argtypes = res, args
+        h.or_last_error.restype, h.or_last_error.argtypes = ctypes.c_char_p, []
+        _dit_lib = h
+    return _dit_lib
+
+
 def check(rc: int, what: str):
     if rc != 0:
         msg = lib().or_last_error().decode()
+        raise HipPathError(f'{what} failed ({rc}): {msg}')
+
+
+def dit_check(rc: int, what: str):
+    if rc != 0:
+        msg = dit_lib().or_last_error().decode()
         raise HipPathError(f'{what} failed ({rc}): {msg}')
 
 

@@ -1,4 +1,5 @@
-// Fused elementwise work of a Wan transformer block: LayerNorm with modulation, and gated residual adds.
+// Fused elementwise work of a Wan transformer block: LayerNorm with modulation, and gated residual adds. Built as
+// libonereel_dit.so (include/onereel_dit.h) for the DiT harness; it uses libonereel_hip.so's error reporting.
 //
 // The reference runs diffusers' WanTransformerBlock (third-party, not vendored; OneReel installs its attention
 // processors into it, src/onereel/models/wan.py:77-108, and xDiT's Wan example applies the same shift / scale
@@ -20,6 +21,7 @@
 
 #include <vector>
 
+#include "../../include/onereel_dit.h"
 #include "common.h"
 
 namespace onereel {

@@ -71,9 +71,10 @@ def layernorm_modulate(x, eps, weight=None, bias=None, scale=None, shift=None):
     x2, C = _rows(x)
     out = torch.empty(x2.shape, dtype=torch.bfloat16, device=x.device)
     w, b, sc, sh = (_vec(t, C) for t in (weight, bias, scale, shift))
-    L.check(L.lib().or_layernorm_modulate(x2.data_ptr(), out.data_ptr(), x2.shape[0], C, x2.stride(0), C, float(eps),
-                                          L.ptr(w), L.ptr(b), L.ptr(sc), L.ptr(sh), L.stream_handle(x.device)),
-            'or_layernorm_modulate')
+    d = L.dit_lib()
+    L.dit_check(d.or_layernorm_modulate(x2.data_ptr(), out.data_ptr(), x2.shape[0], C, x2.stride(0), C, float(eps),
+                                        L.ptr(w), L.ptr(b), L.ptr(sc), L.ptr(sh), L.stream_handle(x.device)),
+                'or_layernorm_modulate')
     return out.view(x.shape)
 
 
@@ -84,8 +85,9 @@ def gated_residual_(x, a, gate=None):
     if Ca != C or a2.shape[0] != x2.shape[0]:
         raise L.HipValueError('x and a must have the same rows')
     g = _vec(gate, C)
-    L.check(L.lib().or_gated_residual(x2.data_ptr(), a2.data_ptr(), L.ptr(g), x2.shape[0], C, x2.stride(0),
-                                      a2.stride(0), L.stream_handle(x.device)), 'or_gated_residual')
+    d = L.dit_lib()
+    L.dit_check(d.or_gated_residual(x2.data_ptr(), a2.data_ptr(), L.ptr(g), x2.shape[0], C, x2.stride(0),
+                                    a2.stride(0), L.stream_handle(x.device)), 'or_gated_residual')
     return x
 
 
@@ -98,10 +100,11 @@ def residual_layernorm_modulate_(x, a, eps, gate=None, weight=None, bias=None, s
         raise L.HipValueError('x and a must have the same rows')
     out = torch.empty(x2.shape, dtype=torch.bfloat16, device=x.device)
     g, w, b, sc, sh = (_vec(t, C) for t in (gate, weight, bias, scale, shift))
-    L.check(L.lib().or_residual_layernorm_modulate(x2.data_ptr(), a2.data_ptr(), L.ptr(g), out.data_ptr(), x2.shape[0],
-                                                   C, x2.stride(0), a2.stride(0), C, float(eps), L.ptr(w), L.ptr(b),
-                                                   L.ptr(sc), L.ptr(sh), L.stream_handle(x.device)),
-            'or_residual_layernorm_modulate')
+    d = L.dit_lib()
+    L.dit_check(d.or_residual_layernorm_modulate(x2.data_ptr(), a2.data_ptr(), L.ptr(g), out.data_ptr(), x2.shape[0],
+                                                 C, x2.stride(0), a2.stride(0), C, float(eps), L.ptr(w), L.ptr(b),
+                                                 L.ptr(sc), L.ptr(sh), L.stream_handle(x.device)),
+                'or_residual_layernorm_modulate')
     return out.view(x.shape)
 
 

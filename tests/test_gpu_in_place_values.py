@@ -231,6 +231,24 @@ def test_varlen_keys_and_values_in_place(lq, lk, v_blocks, k_blocks, H, D):
     assert (lse.cpu() - _lse_ref(q, k, cq, ck, D)).abs().max() < 2e-3
 
 
+@pytest.mark.parametrize('D', [128, 64])
+def test_varlen_keys_in_place_without_values(D):
+    """k_tok without v_tok: every value packed, the keys' base switching at each segment's own point (ring head, ring
+    fill, loop, every whole block)"""
+    lq, lk, k_blocks = [300, 64, 257, 33, 500], [40, 700, 1000, 300, 96], [1, 2, 8, 9, 3]
+    print(f'keys in place only lq={lq} lk={lk} k blocks={k_blocks} D={D}', flush=True)
+    q, k, v, cq, ck, dev = _kv_in_place_case(lq, lk, [0] * len(lk), k_blocks, 4, D, 181)
+    for x in ('v_tok', 'v_lead'):
+        dev.pop(x)
+    dev['v'] = v.to(DEV)
+    ref = OA.packed_attention(q, k, v, cq, ck)
+    o = _run(dev)
+    assert_close(o.cpu(), ref, what='keys in place, values packed')
+    full = dict(q=dev['q'], k=k.to(DEV), v=dev['v'], cu_q=dev['cu_q'], cu_k=dev['cu_k'], max_q=dev['max_q'],
+                max_k=dev['max_k'])
+    assert torch.equal(o, _run(full))
+
+
 @pytest.mark.parametrize('lq,lk,v_blocks,k_blocks,H', [([1000], [20000], [600], [602], 4),
                                                        ([300, 7], [5000, 3000], [150, 0], [140, 40], 3)])
 def test_varlen_keys_in_place_key_split(lq, lk, v_blocks, k_blocks, H):

@@ -83,8 +83,8 @@ def test_position_helpers_known_answers():
     assert ctx.step() == 5 and ctx.adjacent() and ctx.cond()
 
 
-def _header_symbols():
-    text = (ROOT / 'include' / 'onereel_hip.h').read_text()
+def _header_symbols(name='onereel_hip.h'):
+    text = (ROOT / 'include' / name).read_text()
     return sorted(set(re.findall(r'^\s*(?:int|int64_t|const char\*)\s+(or_\w+)\s*\(', text, re.M)))
 
 
@@ -95,6 +95,12 @@ def test_library_exports_every_declared_symbol():
         assert hasattr(h, s), s
     assert set(syms) == set(L.SIGNATURES)
     assert L.lib().or_version().startswith(b'onereel_hip')
+    # the DiT harness's kernels live in their own library, which finds the path's library beside it
+    dit = _header_symbols('onereel_dit.h')
+    assert dit and set(dit) == set(L.DIT_SIGNATURES) and not set(dit) & set(syms)
+    for s in dit:
+        assert not hasattr(h, s), s
+        assert hasattr(L.dit_lib(), s), s
 
 
 def _random_layout(rng):
@@ -267,13 +273,14 @@ def test_rotate_and_memory_argument_errors_without_gpu():
 
 
 def test_fused_residual_layernorm_argument_errors_without_gpu():
-    """or_residual_layernorm_modulate refuses bad widths, a missing or misaligned addend and an output that is x or
-    a before it launches anything (device pointers are never dereferenced on the host)"""
-    f = L.lib().or_residual_layernorm_modulate
+    """or_residual_layernorm_modulate (libonereel_dit.so) refuses bad widths, a missing or misaligned addend and an
+    output that is x or a before it launches anything (device pointers are never dereferenced on the host); its
+    messages come through the path library's or_last_error"""
+    f = L.dit_lib().or_residual_layernorm_modulate
     x, a, out = 0x10000, 0x20000, 0x30000
 
     def call(x=x, a=a, out=out, C=512, a_stride=512):
-        return L.check(f(x, a, None, out, 4, C, C, a_stride, C, 1e-6, None, None, None, None, None),
+        return L.dit_check(f(x, a, None, out, 4, C, C, a_stride, C, 1e-6, None, None, None, None, None),
                        'or_residual_layernorm_modulate')
     for kw, msg in ((dict(C=100), 'multiple of 8'), (dict(C=9000), 'multiple of 8'), (dict(a=None), 'a must be'),
                     (dict(a=a + 8), 'a must be'), (dict(a_stride=256), 'a must be'), (dict(out=x), 'must not be'),
