@@ -739,7 +739,7 @@ def main():
                            useful_flop_per_step=flops, frac_bf16_peak_step=round(value / PEAK_BF16_TFLOPS, 4)),
                roofline=dict(bound='mfma', achieved=round(flops / t_attn / 1e9, 1), peak=PEAK_BF16_TFLOPS,
                              unit='TFLOP/s', frac=round(flops / t_attn / 1e9 / PEAK_BF16_TFLOPS, 4), traffic=traffic,
-                             traffic_source=traffic_src, kernel=f'{kname} (+ plan_kernel, one block, ~10 us)'),
+                             traffic_source=traffic_src, kernel=f'{kname} (+ plan_kernel, up to 8 blocks, ~11 us)'),
                kernels=kernels)
     if other:
         out['other_layout'] = other
