@@ -3,10 +3,10 @@
 Workload (one step = one pass of the hot path over one layer's synthetic inputs, already resident in HBM):
 4 scenes x 8 latent frames x 1590 tokens (30 x 53 latent grid) + 128 text tokens per scene, frame memory of 4 frames
 (representatives {0, 10, 21, 31}), shared frames at their adjacent positions (step >= shared_switch 5), scene RoPE
-over a 3D table, 16 heads x 128, bf16 q / k / v ~ N(0, 1). A step runs the layout kernel, the K/V pack-gather (RoPE
-on the keys; each scene's text segment reads its keys in place from its video segment's packed rows), the RoPE of
-the video queries (once, in token order), the varlen attention (queries and outputs in place) and the text-padding
-write-back.
+over a 3D table, 16 heads x 128, bf16 q / k / v ~ N(0, 1). A step runs the layout kernel, one pack launch (the keys
+with RoPE, each scene's text segment reading its keys in place from its video segment's packed rows; the values the
+attention does not read in place; the RoPE of the video queries, once, in token order), the varlen attention
+(queries, each scope's own-frame values and the outputs in place) and the text-padding write-back (none here).
 
 value = useful attention TFLOP/s of the whole step (sum over scopes of 4 * Lq * Lk * H * D per step time), timed
 over `steps` steps after `warmup` untimed ones; before those, once per process, 0.3 s of untimed steps bring the GPU
