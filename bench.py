@@ -657,7 +657,7 @@ def main():
     attn_of = lambda p: (lambda: scene.varlen(qbuf, kbuf, vbuf, p.cu_q, p.cu_k, p.max_q, p.max_k, k_off=p.k_off,
                                               k_len=p.k_len, out=ov, seg_q_src=p.seg_q_src, q_text=eq, o_text=ot,
                                               n_q_video=p.n_video, sum_q=p.sum_q, workspace=ws, v_tok=v,
-                                              v_lead=p.v_lead, v_row=p.v_row))
+                                              v_lead=p.v_lead, v_row=p.v_row, v_runs=p.v_runs))
     # the step's one pack launch: K rows (rotated), the V rows not read in place, the video queries rotated once
     pack_of = lambda p: (lambda: scene.pack_layer(p, k, ek, v, ev, cos, sin, 'raw', kbuf, vbuf, q=q, qbuf=qbuf))
     attn, pack = attn_of(plan), pack_of(plan)

@@ -106,12 +106,20 @@ typedef struct or_layout_out {
                           them), rounded down to a multiple of OR_VARLEN_KEY_BLOCK; 0 for a segment without keys */
   int32_t* v_row;      /* [n_seg] token row of segment s's first key (the first own-frame token of its scene) */
   int32_t* v_src;      /* [sum_k] value row to pack for packed key row r: k_src[r], or -1 when r lies in the first
-                          v_lead keys of its segment (read in place, not packed) */
+                          v_lead keys of its segment, or (with v_runs) in a whole key block of one of its value runs
+                          (read in place, not packed) */
+  int32_t* v_runs;     /* optional [n_seg * OR_VALUE_RUNS * 3]: the value runs of segment s after its leading run, up
+                          to OR_VALUE_RUNS of them: entry r = (key offset in the segment, key count, first token row)
+                          of its r-th shared frame (T consecutive token rows), (0, 0, 0) past the last; the attention
+                          call reads their whole key blocks in place (or_varlen_args.v_runs). NULL: none, and v_src
+                          packs every value past v_lead */
 } or_layout_out;
 
 /* Keys per block of the attention kernels' K/V stream: a segment's in-place value rows (or_varlen_args.v_lead) come
  * in whole blocks. */
 #define OR_VARLEN_KEY_BLOCK 32
+/* Value runs per segment past its leading one (or_layout_out.v_runs, or_varlen_args.v_runs). */
+#define OR_VALUE_RUNS 4
 
 /* Replaces the host-side layout logic of SceneLayout.shared_frames / key_frames (src/onereel/layout.py:54-78),
  * comm.runs / frame_tokens (src/onereel/parallel/comm.py:84-85,115-123) and the sizes of attention.packed's
@@ -248,6 +256,13 @@ typedef struct or_varlen_args {
                                (rows k_start + k_lead[s] ..); k_lead[s] a multiple of OR_VARLEN_KEY_BLOCK */
   const int32_t* k_lead;    /* [n_seg], with k_tok (and v_row) */
   int64_t k_tok_rows;       /* rows of k_tok */
+  const int32_t* v_runs;    /* optional, with v_tok, head_dim 128 only: [n_seg * OR_VALUE_RUNS * 3] further runs of
+                               segment s's values in v_tok: entry r = (key offset x0, key count n, token row t), keys
+                               x0 .. x0 + n - 1 of the segment taking their values from rows t .. t + n - 1 of v_tok;
+                               runs past the leading v_lead keys, in increasing x0, not overlapping it or each other
+                               (n = 0: unused). Only their whole key blocks (inside the segment, its key count and
+                               v_tok_rows) are read in place, the other keys' values from v (a layout's v_runs, with
+                               the values packed per its v_src) */
 } or_varlen_args;
 
 /* Bytes of device workspace or_varlen_fwd needs for this many segments, packed queries and heads: the work-item

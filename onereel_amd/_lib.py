@@ -37,10 +37,12 @@ class LayoutSizes(ctypes.Structure):
 
 class LayoutOut(ctypes.Structure):
     _fields_ = [(n, vp) for n in ('cu_q', 'cu_k', 'seg_q_src', 'q_src', 'q_rope', 'k_src', 'k_rope', 'k_move_a',
-                                  'k_move_b', 'k_off', 'k_len', 'v_lead', 'v_row', 'v_src')]
+                                  'k_move_b', 'k_off', 'k_len', 'v_lead', 'v_row', 'v_src', 'v_runs')]
 
 # keys per block of the attention kernels' K/V stream (OR_VARLEN_KEY_BLOCK): in-place value rows come in whole blocks
 KEY_BLOCK = 32
+# value runs per segment past its leading one (OR_VALUE_RUNS)
+VALUE_RUNS = 4
 
 
 class VarlenArgs(ctypes.Structure):
@@ -51,7 +53,7 @@ class VarlenArgs(ctypes.Structure):
                 ('max_q', i32), ('max_k', i32), ('H', i32), ('D', i32), ('scale', ctypes.c_float),
                 ('workspace', vp), ('workspace_bytes', i64), ('q_row_step', i32), ('v_tok', vp), ('v_lead', vp),
                 ('v_row', vp), ('v_tok_rows', i64), ('k_len_head', vp), ('k_tok', vp), ('k_lead', vp),
-                ('k_tok_rows', i64)]
+                ('k_tok_rows', i64), ('v_runs', vp)]
 
 
 class PackArgs(ctypes.Structure):

@@ -43,8 +43,15 @@ constexpr int kQueueWords = 32; // words per queue header (head counter, item co
 constexpr int kWsHeader = kQueues * kQueueWords;   // int32 words before the item list
 // an item record: tile << 8 | head, part | ways << 8 (0: whole item), split index, and the segment's first query,
 // query count, first source row, first key and key count, then the token row of its first in-place key / value, the
-// number of keys whose values and whose keys are read there (0 without them), one word unused (three 16-byte loads)
+// number of keys whose values and whose keys are read there (0 without them) and the first value event of its
+// segment (an index in units of 16 bytes into the event table, -1 without value runs) (three 16-byte loads)
 constexpr int kItemWords = 12;
+// value events of a segment with value runs (or_varlen_args.v_runs): the key blocks at which its value stream moves
+// to another base, (block, base lo, base hi, 0) for head 0 in increasing block order, then sentinels (block
+// 0x7fffffff): at most 1 + 2 * OR_VALUE_RUNS events and at least two sentinels, which the key loop's prefetch of the
+// event after the next may read
+constexpr int kVEvents = 2 * OR_VALUE_RUNS + 3;
+constexpr int kNoEvent = 0x7fffffff;
 constexpr int kPlanThreads = 1024;
 constexpr int kMaxPlanSeg = 4096;
 constexpr int kMaxSplitWays = 8;      // key parts of a split work item
@@ -85,6 +92,22 @@ struct AttnArgs {
   int64_t n_vtok;
   const uint16_t* k_tok;
   int64_t n_ktok;
+  // value events of the segments with value runs (kVEvents int4 per segment, written by the planner)
+  const int4* v_events;
+};
+
+// the list a work item without further value events points its key loop at: sentinels only
+__device__ const int4 kNoEvents[4] = {{kNoEvent, 0, 0, 0}, {kNoEvent, 0, 0, 0}, {kNoEvent, 0, 0, 0},
+                                      {kNoEvent, 0, 0, 0}};
+
+// the value runs past the leading one, for the planner: per segment OR_VALUE_RUNS (key offset, count, token row)
+// entries, and the addresses the events point at
+struct VRunArgs {
+  const int32_t* runs;
+  uint64_t v_tok, v;       // token-order values and packed values, head 0
+  int64_t rsb;             // row stride in bytes
+  int64_t n_vtok;
+  int4* events;            // [n_seg * kVEvents]
 };
 
 
@@ -121,7 +144,7 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(const int32_t* cu_q,
                                                             const int32_t* k_len_head,
                                                             int n_seg, int H, int bq,
                                                             int max_items, int slots, int split_keys, int parts_cap,
-                                                            int32_t* ws) {
+                                                            VRunArgs vra, int32_t* ws) {
   __shared__ unsigned long long key[kMaxPlanSeg];
   __shared__ int off[kMaxPlanSeg + 1];
   __shared__ int part[kPlanThreads];
@@ -278,6 +301,43 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(const int32_t* cu_q,
   }
   int32_t* tab = ws + kWsHeader + (int64_t)kItemWords * (max_items + parts_cap);
   if (blockIdx.x == 0 && tid == 0) ws[3] = W > 1 ? q_sb[kQueues - 1] + q_s[kQueues - 1] : 0;
+  // value events of every segment (block 0): the leading run's end, then each further run's whole key blocks (its
+  // start and its end), clipped as the key loop's in-place blocks are (inside the segment's whole blocks and the
+  // token rows, past the leading run and the run before); a run starting where the stream would return to the
+  // packed rows replaces that event
+  if (blockIdx.x == 0 && vra.runs) {
+    for (int s = tid; s < n_seg; s += kPlanThreads) {
+      int4* L = vra.events + (int64_t)s * kVEvents;
+      const int lk_seg = max(k_len ? k_len[s] : cu_k[s + 1] - cu_k[s], 0);
+      const int64_t k_beg = k_off ? k_off[s] : cu_k[s];
+      const int bmax = lk_seg / 32;
+      const int row = v_row ? v_row[s] : -1, lead = v_lead ? v_lead[s] : 0;
+      int64_t la = row >= 0 && lead > 0 ? min((int64_t)lead, (int64_t)lk_seg) / 32 : 0;
+      if (row >= 0) la = min(la, (vra.n_vtok - row) / 32);
+      la = la < 0 ? 0 : la;
+      int n = 0;
+      auto add = [&](int blk, uint64_t at) {
+        if (n > 0 && L[n - 1].x == blk) --n;   // superseded at the same block
+        L[n++] = make_int4(blk, (int)(uint32_t)at, (int)(uint32_t)(at >> 32), 0);
+      };
+      auto packed_at = [&](int blk) { return vra.v + (uint64_t)((k_beg + 32 * (int64_t)blk) * vra.rsb); };
+      if (la > 0) add((int)la, packed_at((int)la));
+      int prev = (int)la;
+      for (int r = 0; r < OR_VALUE_RUNS; ++r) {
+        const int32_t* e = vra.runs + ((int64_t)s * OR_VALUE_RUNS + r) * 3;
+        const int x0 = e[0], cnt = e[1], t = e[2];
+        if (cnt <= 0 || x0 < 0 || t < 0) continue;
+        int bs = (x0 + 31) / 32, be = (int)min((int64_t)(x0 + (int64_t)cnt) / 32, (int64_t)bmax);
+        be = (int)min((int64_t)be, (vra.n_vtok - t + x0) / 32);   // token rows t + 32 B - x0 + i < n_vtok
+        bs = max(bs, prev);
+        if (be <= bs) continue;
+        add(bs, vra.v_tok + (uint64_t)(((int64_t)t + 32 * (int64_t)bs - x0) * vra.rsb));
+        add(be, packed_at(be));
+        prev = be;
+      }
+      for (; n < kVEvents; ++n) L[n] = make_int4(kNoEvent, 0, 0, 0);
+    }
+  }
   // the record(s) of tile t of head `head` of sorted segment i, at position pos of queue q (the last q_s[q] positions
   // of a queue are items split into W key parts)
   auto emit = [&](int i, int head, int t, int q, int pos) {
@@ -294,7 +354,7 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(const int32_t* cu_q,
       int32_t* e = ws + kWsHeader + kItemWords * entry;
       *(int4*)e = make_int4((t << 8) | head, pw, sidx, q_beg);
       *(int4*)(e + 4) = make_int4(lq, q_src0, k_beg, lk < 0 ? 0 : lk);
-      *(int4*)(e + 8) = make_int4(vr, vl, kl, 0);
+      *(int4*)(e + 8) = make_int4(vr, vl, kl, vra.runs ? s * kVEvents : -1);
     };
     if (pos < keep) {
       put(q_first[q] + pos, 0, 0);
@@ -877,8 +937,35 @@ void attn8_kernel(AttnArgs a, int32_t* ws) {
                                 (uint64_t)(a.v + (int64_t)k_beg * rs + head * D));
     const VRange kr = tok_range(a.k_tok, a.n_ktok, rs, r2.x, r2.z, lk_seg, b0, nb, head * D,
                                 (uint64_t)(a.k + (int64_t)k_beg * rs + head * D));
-    const uint64_t vaddr = vr.nba > 0 ? vr.a : vr.p;
-    const uint64_t vsw = vr.p + (uint64_t)vr.nba * (uint32_t)bb;
+    uint64_t vaddr = vr.nba > 0 ? vr.a : vr.p;
+    uint64_t vsw = vr.p + (uint64_t)vr.nba * (uint32_t)bb;
+    int vnext = vr.nba;   // the block (from b0) at which the value stream moves to vsw, 0: never
+    // with value runs the stream moves at every event of the segment's list (the leading run's end among them,
+    // merged with a run that starts on that block): the item walks the list to its first block (the events up to b0
+    // give that block's base), and the key loop takes the events after the first one from vlist
+    const int4* vlist = kNoEvents;
+    const uint32_t hoff = (uint32_t)(head * D * 2);
+    if (r2.w >= 0) {
+      const int4* L = a.v_events + r2.w;
+      int i = 0;
+      int4 e = L[0];
+      while (e.x <= b0) {   // the sentinels end the walk
+        vaddr = (((uint64_t)(uint32_t)e.z << 32) | (uint32_t)e.y) + hoff + (uint64_t)(b0 - e.x) * (uint32_t)bb;
+        e = L[++i];
+      }
+      vnext = e.x - b0 < nb ? e.x - b0 : 0;
+      vsw = (((uint64_t)(uint32_t)e.z << 32) | (uint32_t)e.y) + hoff;
+      vlist = L + i + 1;
+    }
+    // wave-uniform (scalar operands of the key loop)
+    auto uni64 = [](uint64_t x) {
+      return ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(x >> 32)) << 32) |
+             (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)x);
+    };
+    vaddr = uni64(vaddr);
+    vsw = uni64(vsw);
+    vnext = __builtin_amdgcn_readfirstlane(vnext);
+    const uint64_t vlist_u = uni64((uint64_t)vlist);
     const uint64_t ksw = kr.p + (uint64_t)kr.nba * (uint32_t)bb;
     // K block b of the ring head (b = 0, 1) and the block the key loop's descriptor starts at (2)
     auto kblock = [&](int b) { return (b < kr.nba ? kr.a : kr.p) + (uint64_t)b * (uint32_t)bb; };
@@ -969,8 +1056,8 @@ void attn8_kernel(AttnArgs a, int32_t* ws) {
                    [vb_lo] "s"((uint32_t)vaddr), [vb_hi] "s"((uint32_t)(vaddr >> 32)), [rem0] "s"(rem0), [remk] "s"(rem0 - 2 * bb),
                    [op0] "v"(op[0]), [op1] "v"(op[1]), [ok0] "v"(ok[0]), [ok1] "v"(ok[1]),
                    [f32] "s"(__builtin_amdgcn_readfirstlane(ways > 1 ? 1 : 0)),
-                   [dead] "s"(__builtin_amdgcn_readfirstlane(q0 >= Lq ? 1 : 0)), [vsw] "s"(vsw), [nbav] "s"(vr.nba),
-                   [ksw] "s"(ksw), [nbak] "s"(kr.nba)
+                   [dead] "s"(__builtin_amdgcn_readfirstlane(q0 >= Lq ? 1 : 0)), [vsw] "s"(vsw), [nbav] "s"(vnext),
+                   [ksw] "s"(ksw), [nbak] "s"(kr.nba), [vlist] "s"(vlist_u), [hoff] "s"(hoff), [b0] "s"(b0)
                  : ONEREEL_RING64_CLOBBERS);
     // the next item's queries are in a128..a191 unless they must be rotated on the load
     have_q = nit >= 0 && !a.q_rope;
@@ -1093,7 +1180,7 @@ int64_t split_parts_cap(int32_t n_seg, int32_t sum_q, int32_t H, int32_t D) {
 // workspace layout (bytes): queue headers and the item list, the split table (3 words per split item, at most cap / 2
 // of them), then (16-byte aligned) the parts' lse and O / l, for at most `cap` key-split parts
 struct WsLayout {
-  int64_t tab, lse, o, total;
+  int64_t tab, lse, o, ev, total;
 };
 
 WsLayout ws_layout(int32_t n_seg, int32_t sum_q, int32_t H, int64_t cap) {
@@ -1102,7 +1189,8 @@ WsLayout ws_layout(int32_t n_seg, int32_t sum_q, int32_t H, int64_t cap) {
   l.tab = (kWsHeader + kItemWords * (mi + cap)) * 4;
   l.lse = (l.tab + (cap / 2) * 3 * 4 + 15) / 16 * 16;
   l.o = l.lse + cap * kSplitRows * 4;
-  l.total = l.o + cap * kSplitRows * 128 * 4;
+  l.ev = l.o + cap * kSplitRows * 128 * 4;
+  l.total = l.ev + (int64_t)n_seg * kVEvents * 16;
   return l;
 }
 
@@ -1136,6 +1224,8 @@ int check_args(const or_varlen_args& x, const char* fn) {
     return fail_arg("%s: v_tok needs v_lead, v_row, v_tok_rows >= 0 and 16-byte alignment", fn);
   if (x.k_tok && (!x.k_lead || !x.v_row || x.k_tok_rows < 0 || !aligned16(x.k_tok)))
     return fail_arg("%s: k_tok needs k_lead, v_row, k_tok_rows >= 0 and 16-byte alignment", fn);
+  if (x.v_runs && (!x.v_tok || x.D != 128 || x.k_len_head))
+    return fail_arg("%s: v_runs needs v_tok and head_dim 128 (and no k_len_head)", fn);
   return 0;
 }
 
@@ -1188,6 +1278,14 @@ int launch_varlen(const or_varlen_args& x, void* wsp, int64_t cap, hipStream_t s
   a.split_tab = (int32_t*)((char*)wsp + wl.tab);
   a.split_lse = (float*)((char*)wsp + wl.lse);
   a.split_o = (float*)((char*)wsp + wl.o);
+  a.v_events = (const int4*)((char*)wsp + wl.ev);
+  VRunArgs vra;
+  vra.runs = x.v_tok ? x.v_runs : nullptr;
+  vra.v_tok = (uint64_t)x.v_tok;
+  vra.v = (uint64_t)x.v;
+  vra.rsb = x.k_row_stride * 2;
+  vra.n_vtok = x.v_tok ? x.v_tok_rows : 0;
+  vra.events = (int4*)((char*)wsp + wl.ev);
   // the planner needs key counts only: k_len when given, else the cu_k differences. It writes every word of the
   // workspace the other kernels read (queue headers, item list, split table) before they run.
   // the item records are written by up to 8 blocks (each derives the same queues), about 1024 items per block
@@ -1198,7 +1296,7 @@ int launch_varlen(const or_varlen_args& x, void* wsp, int64_t cap, hipStream_t s
                      x.k_tok ? x.k_lead : nullptr, x.k_len_head,
                      x.n_seg, x.H,
                      item_bq(x.D), (int)max_items, (int)grid,
-                     may_split ? 1 : 0, (int)cap, ws);
+                     may_split ? 1 : 0, (int)cap, vra, ws);
   if (int rc = check_hip(hipGetLastError(), "plan_kernel launch")) return rc;
   hipLaunchKernelGGL(attn_fn(x.D), dim3((unsigned)grid), dim3(kThreads), 0, st, a, ws);
   if (int rc = check_hip(hipGetLastError(), "attn_kernel launch")) return rc;

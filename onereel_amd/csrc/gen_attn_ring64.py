@@ -15,8 +15,8 @@ emitted here with fixed registers:
     v132..v163  K operands of the 8 k-steps, v164..v195 V^T operands of the 8 (half, db) steps
     v196..v227  -m per query block, broadcast over 16 registers: the first QK^T MFMA of a block accumulates onto it
     v228..v254  softmax temporaries, running max, row sums, LDS read addresses
-    s64..s90    K and V buffer descriptors, their remaining byte counts, loop counters, return address, the K and
-                V streams' switch points and bases
+    s64..s97    K and V buffer descriptors, their remaining byte counts, loop counters, return address, the K and
+                V streams' switch points and bases, the prefetched value event and the value event list
 The kernel puts Q into a128..a191 before the block (ONEREEL_RING64_QLOAD, or ONEREEL_RING64_QSET_STEP for queries
 rotated on the load), or the previous item's block left it there: at its loop's exit, where Q is no longer read, a
 block loads the queries of the work-group's next item into those registers (%[qa0], %[qa1]: the lane's query rows of
@@ -50,10 +50,13 @@ step, issues the next item's Q loads at its exit and writes nothing; it leaves t
 epilogues, so the kernel waits for a barrier before it refills the ring for the next item.
 In-place keys and values: V blocks 0 .. nbav-1 (%[nbav]) are read from token-order value rows (the descriptor's first
 base, %[vb_lo] / %[vb_hi]), the others from the packed rows (%[vsw]: the base of block nbav there; both advance by
-%[bb] per block), and K blocks 0 .. nbak-1 likewise (%[ksw]). Each base is replaced once per work item, with no cost
-in the steady-state loop: in the ring fill (V: nbav <= R - 2; K: nbak <= R, the kernel's ring head covering nbak <=
-2), else at the end of the iteration whose refill fetched the stream's last in-place block, which the loop's end test
-already stops at (its bound is the least of nb - 1 and those iterations).
+%[bb] per block), and K blocks 0 .. nbak-1 likewise (%[ksw]). Each base is replaced with no cost in the steady-state
+loop: in the ring fill (V: nbav <= R - 2; K: nbak <= R, the kernel's ring head covering nbak <= 2), else at the end of
+the iteration whose refill fetched the block before the switch, which the loop's end test already stops at (its
+bound is the least of nb - 1 and those iterations). The value stream may move more than once (value runs: shared
+frames read in place between packed rows): each move takes the next event from the item's event list (%[vlist]:
+16-byte entries of block, base lo, base hi, for head 0; %[hoff] adds the head's offset, %[b0] makes the block
+relative to the item's first), whose entry after the next is prefetched with a scalar load one event ahead.
 The generator inserts the LDS waits (lgkmcnt) from the order of the reads, and s_nop where gfx950 needs wait states
 between dependent instructions (see Emitter).
 """
@@ -116,7 +119,8 @@ KREM, VREM, SJ, SNB1, SRR, SVOFF = 72, 73, 74, 75, 76, 77
 SRA, SX, SEX = 78, 80, 82       # s[78:79], s[80:81], s[82:83]
 SVTHR, SVSW = 84, 86            # s84: loop count at which the V stream leaves the in-place rows; s[86:87]: its new base
 SKTHR, SKSW, STMP = 85, 88, 90  # s85, s[88:89]: the same for the K stream; s90: a temporary of the end test
-LAST_SGPR = 90
+SLD, SVL = 92, 96               # s[92:95]: the value event after the next one (prefetched); s[96:97]: the list's next entry
+LAST_SGPR = 97
 NEG_INF = '0xff800000'
 
 
@@ -234,6 +238,26 @@ def side_cost(op):
     if op[0] == 'valu':
         return SIDE_COST['trans' if op[4] else 'valu']
     return SIDE_COST[op[0]]
+
+
+def v_advance(R):
+    """the value stream moves to the next event's base (s[86:87]); the prefetched event (s[92:95]: block, base lo,
+    base hi) becomes the next one (its loop count in s84: block - b0 - (R - 2), or never past the item), and the
+    event after it is prefetched. The prefetch was issued an event earlier (or in the prologue), so the wait finds it
+    landed; a wait for all LDS reads too costs little at an iteration's end."""
+    return [f's_mov_b64 s[{VRES}:{VRES + 1}], s[{SVSW}:{SVSW + 1}]',
+            's_waitcnt lgkmcnt(0)',
+            f's_add_u32 s{SVSW}, s{SLD + 1}, %[hoff]',
+            f's_addc_u32 s{SVSW + 1}, s{SLD + 2}, 0',
+            f's_sub_u32 s{STMP}, s{SLD}, %[b0]',
+            f's_cmp_lt_u32 s{STMP}, %[nb]',
+            f's_cselect_b32 s{STMP}, s{STMP}, 0x7fffffff',
+            f's_sub_u32 s{SVTHR}, s{STMP}, {R - 2}',
+            f's_cmp_eq_u32 s{STMP}, 0x7fffffff',
+            f's_cselect_b32 s{SVTHR}, 0x7fffffff, s{SVTHR}',
+            f's_load_dwordx4 s[{SLD}:{SLD + 3}], s[{SVL}:{SVL + 1}], 0x0',
+            f's_add_u32 s{SVL}, s{SVL}, 16',
+            f's_addc_u32 s{SVL + 1}, s{SVL + 1}, 0']
 
 
 class Kernel:
@@ -454,7 +478,8 @@ class Kernel:
         R = self.R
         return [f'.Lend{J}_%=:',
                 f's_cmp_eq_u32 s{SJ}, s{SVTHR}',
-                f's_cselect_b64 s[{VRES}:{VRES + 1}], s[{SVSW}:{SVSW + 1}], s[{VRES}:{VRES + 1}]',
+                f's_cbranch_scc0 .Lvn{J}_%='] + v_advance(R) + [
+                f'.Lvn{J}_%=:',
                 f's_cmp_eq_u32 s{SJ}, s{SKTHR}',
                 f's_cselect_b64 s[{KRES}:{KRES + 1}], s[{SKSW}:{SKSW + 1}], s[{KRES}:{KRES + 1}]',
                 f's_sub_u32 s{SNB1}, %[nb], 1',
@@ -598,22 +623,24 @@ class Kernel:
         e.raw('s_waitcnt vmcnt(0) lgkmcnt(0)')
         e.raw(f's_mov_b32 s{SRR}, 0x49800000')      # 2^20
         e.raw(f's_mov_b32 s{SJ}, 0')
-        # V blocks 0 .. nbav-1 come from the in-place rows, the rest from %[vsw] on (the packed rows of block nbav).
-        # The ring fill below switches when nbav <= R-2; else the loop's end test also stops at the end of the
-        # iteration whose V refill fetched block nbav-1 (j + 1 = nbav - R + 2, in s84), where the base is replaced
+        # the value stream moves to %[vsw] at block nbav (0: never) and then at each event of %[vlist]. s84 holds
+        # nbav - (R - 2): the ring fill below moves it after its fetch of block nbav - 1 when nbav <= R - 2, else the
+        # loop's end test stops at the end of the iteration whose V refill fetched block nbav - 1 (j + 1 = s84);
+        # each move takes the next event (v_advance). The event after the next one is prefetched here.
         e.raw(f's_mov_b64 s[{SVSW}:{SVSW + 1}], %[vsw]')
-        e.raw(f's_add_u32 s{SVTHR}, %[nbav], {2 - R}')
-        e.raw(f's_cmp_lt_u32 %[nbav], {R - 1}')
+        e.raw(f's_sub_u32 s{SVTHR}, %[nbav], {R - 2}')
+        e.raw('s_cmp_eq_u32 %[nbav], 0')
         e.raw(f's_cselect_b32 s{SVTHR}, 0x7fffffff, s{SVTHR}')
+        e.raw(f's_mov_b64 s[{SVL}:{SVL + 1}], %[vlist]')
+        e.raw(f's_load_dwordx4 s[{SLD}:{SLD + 3}], s[{SVL}:{SVL + 1}], 0x0')
+        e.raw(f's_add_u32 s{SVL}, s{SVL}, 16')
+        e.raw(f's_addc_u32 s{SVL + 1}, s{SVL + 1}, 0')
         # K blocks 0 .. nbak-1 likewise (%[ksw]: the packed rows of block nbak): the kernel's ring head covers
         # nbak <= 2, the ring fill nbak <= R, the loop's end test the rest (j + 1 = nbak - R, in s85)
         e.raw(f's_mov_b64 s[{SKSW}:{SKSW + 1}], %[ksw]')
         e.raw(f's_add_u32 s{SKTHR}, %[nbak], {-R}')
         e.raw(f's_cmp_lt_u32 %[nbak], {R + 1}')
         e.raw(f's_cselect_b32 s{SKTHR}, 0x7fffffff, s{SKTHR}')
-        e.raw(f's_sub_u32 s{SNB1}, %[nb], 1')
-        e.raw(f's_min_u32 s{SNB1}, s{SNB1}, s{SVTHR}')
-        e.raw(f's_min_u32 s{SNB1}, s{SNB1}, s{SKTHR}')
         # the K descriptor starts at block 2 (%[kb_lo], %[kb_hi], %[remk]): the kernel fetched the ring's head
         for res, rem, lo, hi, r0 in ((KRES, KREM, 'kb_lo', 'kb_hi', 'remk'), (VRES, VREM, 'vb_lo', 'vb_hi', 'rem0')):
             e.raw(f's_mov_b32 s{res}, %[{lo}]')
@@ -642,8 +669,15 @@ class Kernel:
             e.raw(f's_cmp_eq_u32 %[nbak], {b + 3}')
             e.raw(f's_cselect_b64 s[{KRES}:{KRES + 1}], s[{SKSW}:{SKSW + 1}], s[{KRES}:{KRES + 1}]')
             self.dma_v(e, b)
-            e.raw(f's_cmp_eq_u32 %[nbav], {b + 1}')
-            e.raw(f's_cselect_b64 s[{VRES}:{VRES + 1}], s[{SVSW}:{SVSW + 1}], s[{VRES}:{VRES + 1}]')
+            e.raw(f's_cmp_eq_u32 s{SVTHR}, {(b + 1 - (R - 2)) & 0xffffffff}')
+            e.raw(f's_cbranch_scc0 .Lvf{b}_%=')
+            for line in v_advance(R):
+                e.raw(line)
+            e.label(f'.Lvf{b}_%=')
+        # the value events up to block R - 2 are taken: s84 is now at least 1 (or never)
+        e.raw(f's_sub_u32 s{SNB1}, %[nb], 1')
+        e.raw(f's_min_u32 s{SNB1}, s{SNB1}, s{SVTHR}')
+        e.raw(f's_min_u32 s{SNB1}, s{SNB1}, s{SKTHR}')
         e.raw('s_barrier')
         # a wavefront whose 64 queries all lie past the segment only keeps up the block's K/V stream
         e.raw('s_cmp_eq_u32 %[dead], 0')
@@ -688,7 +722,7 @@ class Kernel:
                 if op[0] == 'm0':
                     lines.append('s_nop 0')          # an SALU write of M0 and the LDS DMA reading it
             lines += [f's_add_u32 s{SJ}, s{SJ}, 1', f's_cmp_eq_u32 s{SJ}, s{SVTHR}',
-                      f's_cselect_b64 s[{VRES}:{VRES + 1}], s[{SVSW}:{SVSW + 1}], s[{VRES}:{VRES + 1}]',
+                      f's_cbranch_scc0 .Ldvn{J}_%='] + v_advance(R) + [f'.Ldvn{J}_%=:',
                       f's_cmp_eq_u32 s{SJ}, s{SKTHR}',
                       f's_cselect_b64 s[{KRES}:{KRES + 1}], s[{SKSW}:{SKSW + 1}], s[{KRES}:{KRES + 1}]',
                       f's_cmp_ge_u32 s{SJ}, %[nb]', 's_cbranch_scc1 .Ldeadexit_%=']
@@ -735,7 +769,8 @@ class Kernel:
             lines += self.epilogue(par)
         lines += self.dead_loop()
         lines += self.store_block()
-        lines.append('.Ldone_%=:')
+        # no scalar load of the value events may land after the block: its registers are the compiler's again
+        lines += ['.Ldone_%=:', 's_waitcnt lgkmcnt(0)']
         return lines
 
 

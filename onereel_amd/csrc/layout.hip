@@ -22,7 +22,9 @@
 //
 // Every segment's keys start with its scene's own frames, which are consecutive token rows: the attention call can
 // read their values in place from the token-order V (v_lead / v_row, whole key blocks of them), and the pack copies
-// only the other value rows (v_src = -1 for the rows read in place).
+// only the other value rows (v_src = -1 for the rows read in place). A video segment's shared frames are T consecutive
+// token rows each: with v_runs, up to OR_VALUE_RUNS of them per segment are listed as further runs, whose whole key
+// blocks are read in place too.
 #include <stdarg.h>
 #include <stdio.h>
 #include <string.h>
@@ -80,6 +82,14 @@ __host__ __device__ inline int seg_keys(const LayoutDerived& L, int s) {
 __host__ __device__ inline int seg_v_lead(const LayoutDerived& L, int s) {
   const int j = seg_scene(L.with_text, s);
   return seg_keys(L, s) > 0 ? ((L.hi[j] - L.lo[j]) * L.T) / OR_VARLEN_KEY_BLOCK * OR_VARLEN_KEY_BLOCK : 0;
+}
+
+// key offset in segment s (a video segment with keys) of its i-th shared frame: after the own frames, and after the
+// sentence when the text keys are read in place (the order the run loop below writes)
+__host__ __device__ inline int seg_shared_key0(const LayoutDerived& L, int s, int i) {
+  const int j = seg_scene(L.with_text, s);
+  const int own = (L.hi[j] - L.lo[j]) * L.T, txt = L.t1[j] - L.t0[j];
+  return own + (L.text_in_place ? txt : 0) + i * L.T;
 }
 
 // query count and packed key rows of segment s (T_j packs no keys when they are read in place from V_j's)
@@ -183,7 +193,7 @@ __device__ inline int upper_bound(const int* a, int n, int x) {  // first i in [
 }
 
 struct RowOut {
-  int32_t *q_src, *q_rope, *k_src, *k_rope, *k_move_a, *k_move_b, *k_off, *k_len, *v_lead, *v_row, *v_src;
+  int32_t *q_src, *q_rope, *k_src, *k_rope, *k_move_a, *k_move_b, *k_off, *k_len, *v_lead, *v_row, *v_src, *v_runs;
 };
 
 __global__ __launch_bounds__(kThreads) void layout_kernel(const or_layout_desc d, RowOut out, int32_t* cu_q_out,
@@ -306,6 +316,17 @@ __global__ __launch_bounds__(kThreads) void layout_kernel(const or_layout_desc d
         if (out.k_len) out.k_len[s] = seg_keys(L, s);
         if (out.v_lead) out.v_lead[s] = seg_v_lead(L, s);
         if (out.v_row) out.v_row[s] = L.lo[j] * L.T;
+        if (out.v_runs) {
+          // the segment's first OR_VALUE_RUNS shared frames (a video segment with keys)
+          const int nsh = !text && seg_keys(L, s) > 0 ? L.sh_ptr[j + 1] - L.sh_ptr[j] : 0;
+          for (int r = 0; r < OR_VALUE_RUNS; ++r) {
+            int32_t* e = out.v_runs + ((int64_t)s * OR_VALUE_RUNS + r) * 3;
+            const bool on = r < nsh;
+            e[0] = on ? seg_shared_key0(L, s, r) : 0;
+            e[1] = on ? L.T : 0;
+            e[2] = on ? L.sh[L.sh_ptr[j] + r] * L.T : 0;
+          }
+        }
       }
     }
   }
@@ -352,8 +373,15 @@ __global__ __launch_bounds__(kThreads) void layout_kernel(const or_layout_desc d
       idx = slot - own;
       row0 = base + (kind == 1 ? slot : own + nsh) * T;
     }
-    // values of the run's rows x < lead0 are read in place (own-frame rows inside the segment's v_lead)
+    // values of the run's rows x < lead0 are read in place (own-frame rows inside the segment's v_lead), and with
+    // v_runs those of rows [in0, in1) (the whole key blocks of one of the segment's first OR_VALUE_RUNS shared frames)
     const int lead0 = !qside && kind == 0 ? seg_v_lead(L, s) - idx * T : 0;
+    int in0 = 0, in1 = 0;
+    if (!qside && kind == 1 && out.v_runs && idx < OR_VALUE_RUNS) {
+      const int x0 = row0 - base;   // the frame's key offset in the segment (= seg_shared_key0(L, s, idx))
+      in0 = (x0 + OR_VARLEN_KEY_BLOCK - 1) / OR_VARLEN_KEY_BLOCK * OR_VARLEN_KEY_BLOCK - x0;
+      in1 = (x0 + T) / OR_VARLEN_KEY_BLOCK * OR_VARLEN_KEY_BLOCK - x0;
+    }
     int count, src0, rope0 = -1, ma0 = -1, mb0 = -1;
     bool rope = false, move = false;
     if (qside && kind == 0) {
@@ -402,7 +430,7 @@ __global__ __launch_bounds__(kThreads) void layout_kernel(const or_layout_desc d
         if (out.k_rope) out.k_rope[row0 + x] = rope ? rope0 + x : -1;
         if (out.k_move_a) out.k_move_a[row0 + x] = move ? ma0 + x : -1;
         if (out.k_move_b) out.k_move_b[row0 + x] = move ? mb0 + x : -1;
-        if (out.v_src) out.v_src[row0 + x] = x < lead0 ? -1 : src0 + x;
+        if (out.v_src) out.v_src[row0 + x] = x < lead0 || (x >= in0 && x < in1) ? -1 : src0 + x;
       }
     }
   }
@@ -556,7 +584,7 @@ extern "C" int or_layout_build(const or_layout_desc* desc, const or_layout_out* 
   if (rc) return rc;
   if (!out) return fail_arg("or_layout_build: out is NULL");
   RowOut ro{out->q_src, out->q_rope, out->k_src, out->k_rope, out->k_move_a, out->k_move_b, out->k_off, out->k_len,
-            out->v_lead, out->v_row, out->v_src};
+            out->v_lead, out->v_row, out->v_src, out->v_runs};
   // one block per run (frame or sentence of a segment), at most 2048
   int64_t runs = 0;
   for (int s = 0; s < sz.n_seg; ++s) {

@@ -72,7 +72,9 @@ class ScopePlan:
     q_rope [sum_q], k_src / k_rope / v_src [sum_k], and for mode 'rotated' with moved shared frames k_move_a /
     k_move_b [sum_k]. v_lead / v_row / v_src: every segment's first keys are its scene's own frames, consecutive token
     rows; the attention call reads the values of v_lead of them (whole key blocks) in place from token row v_row on,
-    and the pack copies only the values of the other keys (v_src[r] = -1 for the rows read in place).
+    and the pack copies only the values of the other keys (v_src[r] = -1 for the rows read in place). With
+    value_runs, v_runs [n_seg * VALUE_RUNS * 3] lists each video segment's first shared frames (key offset, count,
+    token row), whose whole key blocks are read in place too (head_dim 128), and v_src is -1 for them as well.
     Host ints: n_seg, sum_q, sum_k, max_q, max_k, n_video, text_rows, max_rope_row.
 
     text_keys_in_place: each scene's video segment packs its keys as own frames, sentence, shared frames, and the
@@ -86,7 +88,7 @@ class ScopePlan:
 
     def __init__(self, lay: SceneLayout, T: int, counts=None, text_rows: int | None = None, scene_rope=False,
                  rope_lengths=None, adjacent=False, with_text=True, device=None, moves=False,
-                 text_keys_in_place=False, q_range=None):
+                 text_keys_in_place=False, q_range=None, value_runs=True):
         counts = list(counts) if counts is not None else [0] * lay.n_scenes
         if text_rows is None:
             text_rows = sum(counts) if with_text else 0
@@ -105,6 +107,7 @@ class ScopePlan:
         self.cu_q, self.cu_k, self.seg_q_src = new(self.n_seg + 1), new(self.n_seg + 1), new(self.n_seg)
         self.k_off, self.k_len = new(self.n_seg), new(self.n_seg)
         self.v_lead, self.v_row, self.v_src = new(self.n_seg), new(self.n_seg), new(self.sum_k)
+        self.v_runs = new(self.n_seg * L.VALUE_RUNS * 3) if value_runs else None
         self.q_src, self.q_rope = new(self.sum_q), new(self.sum_q)
         self.k_src, self.k_rope = new(self.sum_k), new(self.sum_k)
         self.k_move_a = new(self.sum_k) if moves and adjacent else None
@@ -117,7 +120,7 @@ class ScopePlan:
         """(re)run the layout kernel on the current stream"""
         out = L.LayoutOut(*(L.ptr(t) for t in (self.cu_q, self.cu_k, self.seg_q_src, self.q_src, self.q_rope,
                                                 self.k_src, self.k_rope, self.k_move_a, self.k_move_b, self.k_off,
-                                                self.k_len, self.v_lead, self.v_row, self.v_src)))
+                                                self.k_len, self.v_lead, self.v_row, self.v_src, self.v_runs)))
         with torch.cuda.device(self.device):
             L.check(L.lib().or_layout_build(ctypes.byref(self.desc), ctypes.byref(out), L.stream_handle()),
                     'or_layout_build')
@@ -134,6 +137,8 @@ class ScopePlan:
     def index_bytes(self) -> int:
         """bytes the layout kernel writes"""
         n = 2 * (self.n_seg + 1) + 5 * self.n_seg + 2 * self.sum_q + 3 * self.sum_k
+        if self.v_runs is not None:
+            n += self.v_runs.numel()
         if self.k_move_a is not None:
             n += 2 * self.sum_k
         return 4 * n
@@ -277,12 +282,14 @@ def scatter_rows(packed: torch.Tensor, idx: torch.Tensor, out: torch.Tensor, che
 def varlen(q, k, v, cu_q, cu_k, max_q, max_k, *, k_off=None, k_len=None, out=None, lse=None, seg_q_src=None,
            q_text=None, o_text=None, n_q_video=None, q_rope=None, cos=None, sin=None, sum_q=None, workspace=None,
            scale=None, noalloc=False, q_row_step=1, v_tok=None, v_lead=None, v_row=None, k_len_head=None,
-           k_tok=None, k_lead=None):
+           k_tok=None, k_lead=None, v_runs=None):
     """or_varlen_fwd on torch tensors. Returns out (allocated [Nq, H, D] when not given). noalloc=True calls
     or_varlen_fwd_noalloc instead: no workspace, the library's fixed per-GPU array (calls must not overlap on a GPU).
     q_row_step > 1 (with seg_q_src): query i of segment s is row seg_q_src[s] + i * q_row_step of q and of out.
     v_tok (with v_lead, v_row): the values of segment s's first v_lead[s] keys are rows v_row[s].. of v_tok (row stride
     of k), the others rows k_off[s] + v_lead[s].. of v; k_tok with k_lead (and v_row) likewise for the keys.
+    v_runs [n_seg * VALUE_RUNS * 3] (with v_tok, head_dim 128): further runs of each segment's values in v_tok, entry
+    (key offset, key count, token row), whose whole key blocks are read in place.
     k_len_head [n_seg * H] (with k_len): head h of segment s attends to its first k_len_head[s * H + h] keys."""
     H, D = k.shape[1], k.shape[2]
     _check_bf16(q, k, v, q_text, out, o_text)
@@ -295,7 +302,7 @@ def varlen(q, k, v, cu_q, cu_k, max_q, max_k, *, k_off=None, k_len=None, out=Non
     n_seg = (cu_q.numel() - 1)
     if k_len_head is not None and (k_len is None or k_len_head.numel() != n_seg_of(cu_q) * H):
         raise L.HipValueError('k_len_head needs k_len and one entry per segment and head')
-    for t in (cu_q, cu_k, k_off, k_len, seg_q_src, q_rope, v_lead, v_row, k_len_head, k_lead):
+    for t in (cu_q, cu_k, k_off, k_len, seg_q_src, q_rope, v_lead, v_row, k_len_head, k_lead, v_runs):
         if t is not None and (t.dtype != torch.int32 or not t.is_cuda or not t.is_contiguous()):
             raise L.HipTypeError('index arrays must be contiguous int32 GPU tensors')
     if v_tok is not None:
@@ -304,6 +311,11 @@ def varlen(q, k, v, cu_q, cu_k, max_q, max_k, *, k_off=None, k_len=None, out=Non
             raise L.HipValueError('v_tok needs v_lead and v_row')
         if _rows2d(v_tok, H, D)[1] != ks:
             raise L.HipValueError('v_tok must have the row stride of k and v')
+    if v_runs is not None:
+        if v_tok is None or D != 128 or k_len_head is not None:
+            raise L.HipValueError('v_runs needs v_tok and head_dim 128 (and no k_len_head)')
+        if v_runs.numel() != n_seg_of(cu_q) * L.VALUE_RUNS * 3:
+            raise L.HipValueError(f'v_runs needs {L.VALUE_RUNS} (offset, count, row) entries per segment')
     if k_tok is not None:
         _check_bf16(k_tok)
         if k_lead is None or v_row is None:
@@ -338,6 +350,7 @@ def varlen(q, k, v, cu_q, cu_k, max_q, max_k, *, k_off=None, k_len=None, out=Non
     a.q_row_step = int(q_row_step)
     if v_tok is not None:
         a.v_tok, a.v_lead, a.v_row, a.v_tok_rows = v_tok.data_ptr(), v_lead.data_ptr(), v_row.data_ptr(), v_tok.shape[0]
+    a.v_runs = L.ptr(v_runs)
     a.k_len_head = L.ptr(k_len_head)
     if k_tok is not None:
         a.k_tok, a.k_lead, a.v_row, a.k_tok_rows = k_tok.data_ptr(), k_lead.data_ptr(), v_row.data_ptr(), k_tok.shape[0]
@@ -484,10 +497,13 @@ def scene_attention(plan: ScopePlan, q, k, v, eq, ek, ev, cos=None, sin=None, mo
             raise L.HipValueError(f"rotate_q must be 'pre' or 'load', got {rotate_q!r}")
         on_load = qmode == 'raw' and rotate_q == 'load'
         pre = qmode == 'raw' and not on_load
-        in_place = bool(values_in_place) and v.dim() == 3 and v.stride(0) == H * D and v.is_contiguous()
+        # the value runs past the leading one are read in place by the head_dim 128 kernel only: with another
+        # head_dim such a plan packs every value
+        in_place = (bool(values_in_place) and v.dim() == 3 and v.stride(0) == H * D and v.is_contiguous()
+                    and (plan.v_runs is None or D == 128))
         kp, vp, qr = pack_layer(plan, k, ek, v, ev, cos, sin, mode, kbuf, vbuf, q=q if pre else None, qbuf=qbuf,
                                 values_in_place=in_place)
-        vi = dict(v_tok=v, v_lead=plan.v_lead, v_row=plan.v_row) if in_place else {}
+        vi = dict(v_tok=v, v_lead=plan.v_lead, v_row=plan.v_row, v_runs=plan.v_runs) if in_place else {}
         varlen(qr if pre else q, kp, vp, plan.cu_q, plan.cu_k, plan.max_q, plan.max_k, k_off=plan.k_off,
                k_len=plan.k_len, out=ov, seg_q_src=plan.seg_q_src, q_text=eq, o_text=ot, n_q_video=plan.n_video,
                q_rope=plan.q_rope if on_load else None, cos=cos, sin=sin, sum_q=plan.sum_q,

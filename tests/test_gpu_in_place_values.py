@@ -152,7 +152,10 @@ def test_pack_layer_bit_exact(name, adjacent):
     assert torch.equal(bits(vbuf[copied]), bits(vref[copied]))
     assert bool((vbuf[~copied] == 7.0).all())
     n_in_place = int((~copied).sum())
-    assert n_in_place == sum(int(x) for x in plan.v_lead.tolist()[0::2])   # the video segments own the packed rows
+    # the video segments own the packed rows: their leading runs and their value runs' whole key blocks
+    runs = plan.v_runs.view(plan.n_seg, scene.L.VALUE_RUNS, 3).tolist()
+    whole = sum(max((x0 + n) // 32 - -(-x0 // 32), 0) * 32 for seg in runs for x0, n, _ in seg if n > 0)
+    assert whole > 0 and n_in_place == sum(int(x) for x in plan.v_lead.tolist()[0::2]) + whole
     # keys only (mode 'rotated' with moves, no query rotation): the same keys as or_pack_gather
     plan2 = scene.ScopePlan(plan.layout, case['T'], case['counts'], case['Le'], case['scene_rope'], None, adjacent,
                             True, DEV, moves=True, text_keys_in_place=True)
@@ -165,8 +168,8 @@ def test_pack_layer_bit_exact(name, adjacent):
                                           ('hunyuan480p', (8000, 30000))])
 @pytest.mark.parametrize('adjacent', [False, True])
 def test_layer_values_in_place_bit_identical(name, q_range, adjacent):
-    """the fused layer with the own-frame values read in place gives the same output bits as with every value
-    packed (text keys in place and packed; one rank's share)"""
+    """the fused layer with the own-frame values and the shared frames' values (value runs) read in place gives the
+    same output bits as with every value packed (text keys in place and packed; one rank's share)"""
     for in_place_text in (True, False):
         print(f'layer values in place {name} adjacent={adjacent} text keys in place={in_place_text} '
               f'q_range={q_range}', flush=True)
@@ -264,3 +267,107 @@ def test_varlen_keys_in_place_key_split(lq, lk, v_blocks, k_blocks, H):
     o = scene.varlen(qq, kk, vv, cu_q, cu_k, mq, mk, workspace=ws, **a)
     assert int(ws.view(torch.int32)[3]) > 0
     assert_close(o.cpu(), ref, what='keys in place, key split')
+
+
+def _blocks_in_place(x0, n, t, n_tok, lk, prev):
+    """the whole key blocks [bs, be) of a value run (keys x0 .. x0 + n - 1 from token rows t ..) that the attention
+    kernel reads in place: inside the segment's whole blocks and the token rows, past `prev` (the leading run's or
+    the previous run's end), as or_varlen_args.v_runs states"""
+    bs = max(-(-x0 // 32), prev)
+    be = min((x0 + n) // 32, lk // 32, (n_tok - t + x0) // 32)
+    return (bs, be) if be > bs else (prev, prev)
+
+
+def _runs_case(lq, lk, lead_blocks, runs, H, seed, n_tok=None):
+    """segments with lq queries and lk keys, of which the first 32 * lead_blocks[s] take their values from token rows
+    v_row[s].. and the keys of each run (x0, n) of runs[s] from token rows t.. (t random, the run possibly reaching
+    past the token rows); the packed rows under every block read in place hold POISON. Returns the oracle inputs
+    (the values each key really has) and the device arguments."""
+    D = 128
+    rng = np.random.default_rng(seed)
+    q = rand_bf16((sum(lq), H, D), seed)
+    k = rand_bf16((sum(lk), H, D), seed + 1)
+    v = rand_bf16((sum(lk), H, D), seed + 2)
+    cq, ck = np.cumsum([0] + lq), np.cumsum([0] + lk)
+    need = sum(32 * b for b in lead_blocks) + sum(n for rs in runs for _, n in rs)
+    n_tok = n_tok or need + 200
+    vtok = rand_bf16((n_tok, H, D), seed + 3)
+    vp = v.clone()
+    rows = []
+    tab = np.zeros((len(lk), scene.L.VALUE_RUNS, 3), dtype=np.int32)
+    for s in range(len(lk)):
+        lead = 32 * lead_blocks[s]
+        row = int(rng.integers(0, n_tok - lead + 1))
+        rows.append(row)
+        la = min(min(lead, lk[s]) // 32, (n_tok - row) // 32)
+        v[ck[s]:ck[s] + 32 * la] = vtok[row:row + 32 * la]
+        vp[ck[s]:ck[s] + 32 * la] = POISON
+        prev = la
+        for r, (x0, n) in enumerate(runs[s]):
+            t = int(rng.integers(0, n_tok - n + 1)) if rng.random() < 0.8 else n_tok - n // 2   # some reach past
+            tab[s, r] = (x0, n, t)
+            bs, be = _blocks_in_place(x0, n, t, n_tok, lk[s], prev)
+            if be > bs:
+                a, b = 32 * bs, 32 * be
+                v[ck[s] + a:ck[s] + b] = vtok[t + a - x0:t + b - x0]
+                vp[ck[s] + a:ck[s] + b] = POISON
+                prev = be
+    t32 = lambda x: torch.tensor(np.asarray(x), dtype=torch.int32, device=DEV)
+    dev = dict(q=q.to(DEV), k=k.to(DEV), v=vp.to(DEV), cu_q=t32(cq), cu_k=t32(ck), max_q=max(lq), max_k=max(lk),
+               v_tok=vtok.to(DEV), v_lead=t32([32 * b for b in lead_blocks]), v_row=t32(rows),
+               v_runs=t32(tab.reshape(-1)))
+    return q, k, v, cq, ck, dev
+
+
+# value runs past the leading one: runs whose first whole block falls in the ring fill or the loop, a run starting
+# on the block where the previous one (or the lead) ends, runs with no whole block, runs reaching past the token
+# rows or the segment, segments without a lead (their first event is a run's start), up to four runs per segment
+RUN_CASES = [
+    ([300, 40, 257], [3000, 1500, 700],
+     [10, 2, 0], [[(330, 1590), (1920, 600)], [(64, 100), (170, 900), (1070, 33), (1110, 380)], [(5, 400)]]),
+    ([129, 640], [5000, 4000], [20, 0], [[(700, 1590), (2290, 1590), (3880, 1000)], [(0, 1000), (1000, 1600)]]),
+    ([77, 5, 300, 1], [200, 96, 4096, 64], [1, 0, 3, 0],
+     [[(40, 150)], [(1, 31)], [(96, 992), (1088, 992), (2080, 992), (3072, 992)], [(0, 64)]]),
+]
+
+
+@pytest.mark.parametrize('lq,lk,lead_blocks,runs', RUN_CASES)
+def test_varlen_value_runs(lq, lk, lead_blocks, runs):
+    """values read in place from several runs per segment (the value stream moving at every run's start and end):
+    O and lse against the fp32 oracle, O bit-identical to the call with every value packed"""
+    H = 4
+    print(f'value runs lq={lq} lk={lk} lead={lead_blocks} runs={runs}', flush=True)
+    q, k, v, cq, ck, dev = _runs_case(lq, lk, lead_blocks, runs, H, 211)
+    ref = OA.packed_attention(q, k, v, cq, ck)
+    o = _run(dev)
+    assert_close(o.cpu(), ref, what='value runs')
+    assert torch.equal(o, _run(dev, vfull=v.to(DEV)))
+    o2, lse = _run(dev, lse=True)
+    assert_close(o2.cpu(), ref, what='value runs, lse call')
+    assert (lse.cpu() - _lse_ref(q, k, cq, ck, 128)).abs().max() < 2e-3
+
+
+@pytest.mark.parametrize('lq,lk,lead_blocks,runs,H', [
+    ([1000], [20000], [100], [[(3300, 1590), (4890, 1590), (8000, 5000), (15000, 4999)]], 4),
+    ([300, 7], [5000, 3000], [0, 20], [[(100, 2000), (2200, 2800)], [(700, 1590), (2290, 700)]], 3)])
+def test_varlen_value_runs_key_split(lq, lk, lead_blocks, runs, H):
+    """key parts of split items over value runs: parts that start inside a run, between runs and in the lead walk
+    the segment's event list to their first block"""
+    print(f'value runs, key split lq={lq} lk={lk} lead={lead_blocks} runs={runs} H={H}', flush=True)
+    q, k, v, cq, ck, dev = _runs_case(lq, lk, lead_blocks, runs, H, 223)
+    ref = OA.packed_attention(q, k, v, cq, ck)
+    ws = torch.zeros(int(scene.L.lib().or_varlen_workspace_size(len(lq), sum(lq), H, 128)), dtype=torch.uint8,
+                     device=DEV)
+    a = dict(dev)
+    qq, kk, vv, cu_q, cu_k, mq, mk = (a.pop(x) for x in ('q', 'k', 'v', 'cu_q', 'cu_k', 'max_q', 'max_k'))
+    o = scene.varlen(qq, kk, vv, cu_q, cu_k, mq, mk, workspace=ws, **a)
+    assert int(ws.view(torch.int32)[3]) > 0
+    assert_close(o.cpu(), ref, what='value runs, key split')
+
+
+def test_varlen_value_runs_need_head_dim_128():
+    q = torch.zeros(64, 2, 64, dtype=torch.bfloat16, device=DEV)
+    t32 = lambda x: torch.tensor(x, dtype=torch.int32, device=DEV)
+    with pytest.raises(scene.L.HipPathError, match='head_dim 128'):
+        scene.varlen(q, q, q, t32([0, 64]), t32([0, 64]), 64, 64, v_tok=q, v_lead=t32([0]), v_row=t32([0]),
+                     v_runs=t32([0] * (3 * scene.L.VALUE_RUNS)))

@@ -12,7 +12,8 @@ The transitions between two items of one work-group that these calls drive:
 - query tiles whose last wavefronts lie past the segment (dead wavefronts: a key loop of barriers and DMA only),
   followed by an item whose wavefronts are all live;
 - items whose values (and keys) are partly read in place (each stream's base switching in the ring head, the ring
-  fill or the loop), next to items whose values and keys are all packed;
+  fill or the loop), and items whose value streams move several times (value runs), next to items whose values and
+  keys are all packed;
 - key-split parts of the last items (capped grid, few items), several parts per work-group, merged afterwards.
 """
 import numpy as np
@@ -126,3 +127,46 @@ def test_key_split_parts_on_few_work_groups(monkeypatch, lq, lk, H, lead):
     monkeypatch.setenv('ONEREEL_ATTN_MAX_BLOCKS', '4')
     print(f'item boundaries, key split on 4 work-groups: lq={lq} lk={lk} H={H} lead={lead}', flush=True)
     _check(lq, lk, H, 128, 400, lead_blocks=lead, expect_split=True)
+
+
+def test_many_items_with_value_runs(monkeypatch):
+    """the walk of test_many_items_per_work_group with every segment's values read in place from a leading run and
+    up to two further runs (value events in the ring fill, in the loop, at a key-split part's start), on 4
+    work-groups: items whose value streams move several times follow items whose streams do not move"""
+    monkeypatch.setenv('ONEREEL_ATTN_MAX_BLOCKS', '4')
+    lq, lk = _many_items(31)
+    rng = np.random.default_rng(9)
+    H, D = 8, 128
+    q = rand_bf16((sum(lq), H, D), 500)
+    k = rand_bf16((sum(lk), H, D), 501)
+    v = rand_bf16((sum(lk), H, D), 502)
+    cq, ck = np.cumsum([0] + lq), np.cumsum([0] + lk)
+    n_tok = 4 * sum(lk) + 64
+    vtok = rand_bf16((n_tok, H, D), 503)
+    vp = v.clone()
+    lead, rows, tab = [], [], np.zeros((len(lk), L.VALUE_RUNS, 3), dtype=np.int32)
+    for s, n in enumerate(lk):
+        la = int(rng.integers(0, n // 32 + 1))
+        row = int(rng.integers(0, n_tok - 32 * la + 1))
+        lead.append(32 * la)
+        rows.append(row)
+        v[ck[s]:ck[s] + 32 * la] = vtok[row:row + 32 * la]
+        vp[ck[s]:ck[s] + 32 * la] = 3.0e4
+        x, prev = 32 * la + int(rng.integers(0, 40)), la
+        for r in range(int(rng.integers(0, 3))):
+            cnt = int(rng.integers(1, 200))
+            if x >= n:
+                break
+            t = int(rng.integers(0, n_tok - cnt + 1))
+            tab[s, r] = (x, cnt, t)
+            bs, be = max(-(-x // 32), prev), min((x + cnt) // 32, n // 32)
+            if be > bs:
+                v[ck[s] + 32 * bs:ck[s] + 32 * be] = vtok[t + 32 * bs - x:t + 32 * be - x]
+                vp[ck[s] + 32 * bs:ck[s] + 32 * be] = 3.0e4
+                prev = be
+            x += cnt + int(rng.integers(0, 40))
+    print(f'item boundaries, value runs: lq={lq}, lk={lk}, lead={lead}, runs={tab.tolist()}', flush=True)
+    t32 = lambda x: torch.tensor(np.asarray(x), dtype=torch.int32, device=DEV)
+    o = scene.varlen(q.to(DEV), k.to(DEV), vp.to(DEV), t32(cq), t32(ck), max(lq), max(lk), v_tok=vtok.to(DEV),
+                     v_lead=t32(lead), v_row=t32(rows), v_runs=t32(tab.reshape(-1)))
+    assert_close(o.cpu(), OA.packed_attention(q, k, v, cq, ck), what='O, value runs')

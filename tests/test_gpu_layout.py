@@ -5,6 +5,7 @@ import pytest
 import torch
 
 from helpers import bits, layout_case, packed_rows_reference, rand_bf16, sample_packed
+from onereel_amd import scene
 from onereel_amd.layout import SceneLayout
 from onereel_amd.scene import ScopePlan, pack_rows, rotate_queries, scatter
 from oracle import attention as OA
@@ -46,8 +47,10 @@ def _check_plan(plan, sc, adjacent):
 def _check_values_in_place(plan, sc):
     """v_lead / v_row / v_src: the first v_lead keys of every segment (whole 32-key blocks of its scene's own frames)
     are consecutive token rows from v_row, so their values can be read in place: the oracle's key rows of those keys
-    are exactly v_row, v_row + 1, ...; v_lead is the largest such multiple of 32 within the own frames; the pack's
-    value rows (v_src) are the oracle's key rows except those, which are -1"""
+    are exactly v_row, v_row + 1, ...; v_lead is the largest such multiple of 32 within the own frames. v_runs: each
+    video segment's first shared frames (the oracle's frames, in its order), each T consecutive token rows of the
+    plan's (oracle-checked) key rows. The pack's value rows (v_src) are the key rows except those in the leading
+    run's and the runs' whole key blocks, which are -1"""
     k_src = np.asarray(sc.k_src)
     v_lead, v_row, k_len = (getattr(plan, a).cpu().numpy() for a in ('v_lead', 'v_row', 'k_len'))
     lay = plan.layout
@@ -66,6 +69,24 @@ def _check_values_in_place(plan, sc):
     want = pk.copy()
     for s in range(plan.n_seg):   # the segments that own packed rows (T_j owns none with its keys in place)
         want[pcu[s]:pcu[s] + min(v_lead[s], pcu[s + 1] - pcu[s])] = -1
+    if plan.v_runs is not None:
+        runs = plan.v_runs.cpu().numpy().reshape(plan.n_seg, scene.L.VALUE_RUNS, 3)
+        T = plan.T
+        for s in range(plan.n_seg):
+            j = sc.scene[s]
+            video = not plan.with_text or s % 2 == 0
+            own, txt = int(lay.lengths[j]) * T, (plan.counts[j] if plan.with_text else 0)
+            nsh = (int(k_len[s]) - own - txt) // T if video and k_len[s] > 0 else 0
+            n = min(nsh, scene.L.VALUE_RUNS)
+            assert (runs[s, n:] == 0).all(), s
+            for r in range(n):
+                x0, cnt, t = (int(x) for x in runs[s, r])
+                assert cnt == T and t % T == 0, (s, r, runs[s, r])
+                # the run's keys are the token rows t.. in the plan's key rows (checked against the oracle's)
+                assert np.array_equal(pk[pcu[s] + x0:pcu[s] + x0 + T], t + np.arange(T)), (s, r)
+                a, b = -(-x0 // 32) * 32, (x0 + T) // 32 * 32
+                if b > a:
+                    want[pcu[s] + a:pcu[s] + b] = -1
     assert np.array_equal(got, want)
 
 
