@@ -371,3 +371,37 @@ def test_varlen_value_runs_need_head_dim_128():
     with pytest.raises(scene.L.HipPathError, match='head_dim 128'):
         scene.varlen(q, q, q, t32([0, 64]), t32([0, 64]), 64, 64, v_tok=q, v_lead=t32([0]), v_row=t32([0]),
                      v_runs=t32([0] * (3 * scene.L.VALUE_RUNS)))
+
+
+def test_layer_value_runs_random_layouts():
+    """random layouts (halo frames, extra frames, frames of T tokens not a multiple of 32, empty sentences, both
+    shared-frame layouts, text keys in place or packed): the fused layer with its values read in place (each scope's
+    leading run and its shared frames' value runs) gives the bits of the layer with every value packed"""
+    rng = np.random.default_rng(29)
+    H, D = 2, 128
+    n_runs = 0
+    for it in range(16):
+        n = int(rng.integers(1, 6))
+        lengths = rng.integers(1, 5, n).tolist()
+        F = sum(lengths)
+        extra = {j: sorted({int(x) for x in rng.integers(0, F, int(rng.integers(0, 6)))}) for j in range(n)
+                 if rng.random() < 0.8}
+        T = int(rng.integers(20, 140))
+        counts = rng.integers(0, 40, n).tolist()
+        Le = sum(counts) + int(rng.integers(0, 3))
+        lay = SceneLayout(lengths, halo=int(rng.integers(0, 3)), sides=['adj', 'prev', 'next'][int(rng.integers(3))],
+                          extra=extra)
+        adjacent, tkip = bool(rng.integers(2)), bool(rng.integers(2))
+        print(f'random layer {it}: lengths={lengths} T={T} halo={lay.halo} sides={lay.sides} extra={extra} '
+              f'counts={counts} adjacent={adjacent} text keys in place={tkip}', flush=True)
+        plan = scene.ScopePlan(lay, T, counts, Le, True, None, adjacent, True, DEV, text_keys_in_place=tkip)
+        runs = plan.v_runs.view(plan.n_seg, scene.L.VALUE_RUNS, 3)
+        n_runs += int((runs[:, :, 1] > 0).sum())
+        g = [rand_bf16((F * T, H, D), 40 + 6 * it + i).to(DEV) for i in range(3)] + \
+            [rand_bf16((Le, H, D), 43 + 6 * it + i).to(DEV) for i in range(3)]
+        ang = torch.rand(plan.max_rope_row + 1, D // 2, generator=torch.Generator().manual_seed(it)) * 6.2832
+        cos, sin = (f(ang).repeat_interleave(2, 1).contiguous().to(DEV) for f in (torch.cos, torch.sin))
+        ov, ot = scene.scene_attention(plan, *g, cos, sin, mode='raw', fused=True, values_in_place=True)
+        ov2, ot2 = scene.scene_attention(plan, *g, cos, sin, mode='raw', fused=True, values_in_place=False)
+        assert torch.equal(ov, ov2) and torch.equal(ot, ot2), it
+    assert n_runs > 20
