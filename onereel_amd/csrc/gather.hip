@@ -5,10 +5,10 @@
 // the write-back ov[lo:hi] = o / ot[t0:t1] = o after o.split (hunyuan15.py:226,231-235; attention.py:71).
 //
 // Both kernels are HBM-bound row copies: one wavefront moves one row of H*D bf16 (4 KiB at 16 x 128) per step in
-// 16-byte lanes (the scatter two rows per step), all loads issued before the stores; rows under 1 KiB share a
-// wavefront. Stores are non-temporal: the
-// packed rows and the token-order outputs are written once and read by the next kernel from HBM, so they bypass
-// the caches (about 10% and 25% faster than cached stores for the pack and the scatter). The rotation is done in
+// 16-byte lanes, all loads of a row issued before its stores (the pack loads the next row's index words ahead);
+// rows under 1 KiB share a wavefront. Stores are non-temporal: the packed rows and the token-order outputs are
+// written once and read by the next kernel from HBM, so they bypass the caches (about 10% and 25% faster than
+// cached stores for the pack and the scatter). The rotation is done in
 // fp32 as two rounded products and a rounded sum per element (no fused multiply-add), then rounded to bf16 to
 // nearest even: the same bits as torch's x.float() * cos + rot(x).float() * sin followed by .to(bfloat16).
 #include "common.h"

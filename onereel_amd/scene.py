@@ -472,9 +472,9 @@ def scene_attention(plan: ScopePlan, q, k, v, eq, ek, ev, cos=None, sin=None, mo
     """(ov, ot) of one scene-attention layer. q / k / v [F*T, H, D] and eq / ek / ev [Le, H, D] bf16 on the GPU.
 
     fused=True: one pack launch (K rows, the V rows not read in place, and the video queries rotated once when
-    mode is 'raw' and rotate_q='pre', into qbuf when given), then the attention call with Q read in place, the own-frame
-    values read in place from v (values_in_place, when v's rows are H * D elements apart, as the packed rows are) and
-    the outputs written in place. rotate_q='load' rotates the queries on the attention kernel's Q load instead.
+    mode is 'raw' and rotate_q='pre', into qbuf when given), then the attention call with Q read in place, the
+    own-frame values and the shared frames' values (value runs, head_dim 128) read in place from v (values_in_place,
+    when v's rows are H * D elements apart, as the packed rows are) and the outputs written in place. rotate_q='load' rotates the queries on the attention kernel's Q load instead.
     fused=False: the reference's data flow (Q, K, V packed, one varlen call on packed tensors, write-back by the
     scatter kernel).
 
