@@ -179,11 +179,12 @@ __device__ __forceinline__ void row_store(const GatherArgs& g, const RowLanes& r
 }
 
 // one row per wavefront (lane group) at a time; the register count per row (CPL chunks, no move table without MOVE)
-// sets how many waves a SIMD holds, and more of them in flight beat more rows per wave (two rows per wave, all loads
-// ahead of the stores, measured 15% slower at the 480p layer: 0.258 against 0.225 ms). The wavefront index is made
-// uniform (readfirstlane), so that a wide row's index words are scalar loads into SGPRs: 70 instead of 98 VGPRs, 7
-// waves per SIMD, and with the indices loaded one row ahead the layer's pack took 0.204 ms instead of 0.234 (index
-// words loaded with the row: 0.224 ms; two or three rows ahead, or grids of 1792 or 3584 blocks: within 1%)
+// sets how many waves a SIMD holds. The wavefront index is made uniform (readfirstlane), so that a wide row's index
+// words are scalar loads into SGPRs: 70 instead of 98 VGPRs, 7 waves per SIMD, and with the indices loaded one row
+// ahead the layer's pack took 0.204 ms instead of 0.234 (index words loaded with the row: 0.224 ms; two or three rows
+// ahead, or grids of 1792 or 3584 blocks: within 1%). Two rows per wavefront, the next row's data loaded before the
+// current row's stores, measured 0.178 against 0.181 ms at 120 VGPRs and 4 waves per SIMD (with vector index loads
+// at 94 VGPRs it had been 15% slower): too little for the second row's registers.
 template <bool NARROW, int CPL, bool MOVE>
 __global__ __launch_bounds__(kThreads) void pack_gather_kernel(GatherArgs g) {
   const int lane = threadIdx.x & 63;
