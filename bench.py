@@ -382,17 +382,18 @@ def run_power(args):
     lq = [int(x) for x in (plan.cu_q[1:] - plan.cu_q[:-1]).tolist()]
     lk = [int(x) for x in plan.k_len.tolist()]
     flops = float(sum(4.0 * a * b * H * D for a, b in zip(lq, lk)))
-    qr = scene.rotate_queries(plan, q, cos, sin)
+    # the video queries rotated and multiplied by scale * log2(e), as the layer's pack launch leaves them
+    qr = scene.pack_layer(plan, k, ek, v, ev, cos, sin, 'raw', q=q, q_scale=scene.base2_scale(D))[2]
     attn = lambda: scene.varlen(qr, kp, vp, plan.cu_q, plan.cu_k, plan.max_q, plan.max_k, k_off=plan.k_off,
                                 k_len=plan.k_len, out=ov, seg_q_src=plan.seg_q_src, q_text=eq, o_text=ot,
-                                n_q_video=plan.n_video, sum_q=plan.sum_q, workspace=ws)
+                                n_q_video=plan.n_video, sum_q=plan.sum_q, workspace=ws, q_prescaled=True)
     # the same call on operands with two mantissa bits (bf16 bits 4..0 cleared): the same FLOP and schedule, less
     # MFMA switching power, so the rate it reaches at the board's limit shows how much power bounds the kernel
     low = lambda x: (x.view(torch.int16) & -32).view(torch.bfloat16)
     qr2, kp2, vp2, eq2 = low(qr), low(kp), low(vp), low(eq)
     attn2 = lambda: scene.varlen(qr2, kp2, vp2, plan.cu_q, plan.cu_k, plan.max_q, plan.max_k, k_off=plan.k_off,
                                  k_len=plan.k_len, out=ov, seg_q_src=plan.seg_q_src, q_text=eq2, o_text=ot,
-                                 n_q_video=plan.n_video, sum_q=plan.sum_q, workspace=ws)
+                                 n_q_video=plan.n_video, sum_q=plan.sum_q, workspace=ws, q_prescaled=True)
     n_g = 16384
     a = torch.randn(n_g, n_g, generator=g, device=dev).to(torch.bfloat16)
     b = torch.randn(n_g, n_g, generator=g, device=dev).to(torch.bfloat16)
@@ -652,14 +653,16 @@ def main():
     ov = torch.empty_like(q)
     ot = torch.empty(Le, H, D, dtype=torch.bfloat16, device=dev)
     ws = plan.workspace(H, D)
-    # the attention kernel as the step runs it: video queries already rotated (qbuf), read in place, the own-frame
-    # values read in place from v
+    # the attention kernel as the step runs it: video queries already rotated and multiplied by scale * log2(e)
+    # (qbuf; head_dim 128), read in place, the own-frame values read in place from v
+    base2 = D == 128
     attn_of = lambda p: (lambda: scene.varlen(qbuf, kbuf, vbuf, p.cu_q, p.cu_k, p.max_q, p.max_k, k_off=p.k_off,
                                               k_len=p.k_len, out=ov, seg_q_src=p.seg_q_src, q_text=eq, o_text=ot,
                                               n_q_video=p.n_video, sum_q=p.sum_q, workspace=ws, v_tok=v,
-                                              v_lead=p.v_lead, v_row=p.v_row, v_runs=p.v_runs))
+                                              v_lead=p.v_lead, v_row=p.v_row, v_runs=p.v_runs, q_prescaled=base2))
     # the step's one pack launch: K rows (rotated), the V rows not read in place, the video queries rotated once
-    pack_of = lambda p: (lambda: scene.pack_layer(p, k, ek, v, ev, cos, sin, 'raw', kbuf, vbuf, q=q, qbuf=qbuf))
+    pack_of = lambda p: (lambda: scene.pack_layer(p, k, ek, v, ev, cos, sin, 'raw', kbuf, vbuf, q=q, qbuf=qbuf,
+                                                  q_scale=scene.base2_scale(D) if base2 else None))
     attn, pack = attn_of(plan), pack_of(plan)
     qpk = torch.empty(plan.sum_q, H, D, dtype=torch.bfloat16, device=dev)
     scat = lambda: scene.scatter(plan, qpk, ov, ot)

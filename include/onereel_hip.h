@@ -187,6 +187,8 @@ typedef struct or_pack_args {
   int64_t n_rope_rows;
   int32_t H;
   int32_t D;
+  float q_scale;              /* nonzero: each rotated query element is multiplied by q_scale in fp32 before its one
+                                 rounding to bf16 (scale * log2(e) for or_varlen_args.q_prescaled); 0: not scaled */
 } or_pack_args;
 
 /* Replaces the same code as or_pack_gather and or_rotate_rows together (hunyuan15.py:164,168,183-191,225;
@@ -263,6 +265,11 @@ typedef struct or_varlen_args {
                                (n = 0: unused). Only their whole key blocks (inside the segment, its key count and
                                v_tok_rows) are read in place, the other keys' values from v (a layout's v_runs, with
                                the values packed per its v_src) */
+  int32_t q_prescaled;      /* optional, head_dim 128 without q_rope: nonzero when the rows of q (not q_text) hold
+                               scale * log2(e) * q, rounded once to bf16 (or_pack_layer's query rotation with q_scale
+                               = scale * log2(e)); their segments then take the scores as base-2 exponents, without
+                               the multiply per score. The results are those of the unscaled queries up to that
+                               rounding. Every query row of a segment must be on one side of n_q_video. */
 } or_varlen_args;
 
 /* Bytes of device workspace or_varlen_fwd needs for this many segments, packed queries and heads: the work-item

@@ -53,7 +53,7 @@ class VarlenArgs(ctypes.Structure):
                 ('max_q', i32), ('max_k', i32), ('H', i32), ('D', i32), ('scale', ctypes.c_float),
                 ('workspace', vp), ('workspace_bytes', i64), ('q_row_step', i32), ('v_tok', vp), ('v_lead', vp),
                 ('v_row', vp), ('v_tok_rows', i64), ('k_len_head', vp), ('k_tok', vp), ('k_lead', vp),
-                ('k_tok_rows', i64), ('v_runs', vp)]
+                ('k_tok_rows', i64), ('v_runs', vp), ('q_prescaled', i32)]
 
 
 class PackArgs(ctypes.Structure):
@@ -62,7 +62,8 @@ class PackArgs(ctypes.Structure):
                 ('v_src', vp), ('n_keys', i64), ('k_dst', vp), ('k_out', vp), ('v_out', vp), ('q', vp),
                 ('q_row_stride', i64),
                 ('q_src', vp), ('q_rope', vp), ('n_queries', i64), ('q_out', vp), ('q_out_row_stride', i64),
-                ('cos_table', vp), ('sin_table', vp), ('n_rope_rows', i64), ('H', i32), ('D', i32)]
+                ('cos_table', vp), ('sin_table', vp), ('n_rope_rows', i64), ('H', i32), ('D', i32),
+                ('q_scale', ctypes.c_float)]
 
 
 # every exported symbol with its ctypes signature: include/onereel_hip.h

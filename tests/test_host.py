@@ -209,6 +209,24 @@ def test_varlen_argument_errors_without_gpu():
         L.check(L.lib().or_pack_gather(1, 1, None, None, 4096, 4096, 0, 1, None, None, None, None, 0, 1, 64, 128, 1,
                                        None, None), 'or_pack_gather')
     assert L.lib().or_varlen_workspace_size(8, 51392, 16, 128) > 0
+    # pre-multiplied queries: the base-2 key loop is the head_dim 128 kernel's, and the queries must not be rotated
+    # on the load (the rotation would round them again)
+    a = L.VarlenArgs()
+    a.H, a.n_seg, a.sum_q, a.q_prescaled = 1, 1, 1, 1
+    a.q = a.k = a.v = a.o = 0x10000
+    a.cu_q = a.cu_k = 0x20000
+    for D, rope, msg in ((64, None, 'q_prescaled needs head_dim 128'), (128, 0x30000, 'no q_rope')):
+        a.D, a.q_rope, a.cos_table, a.sin_table, a.n_rope_rows = D, rope, 0x40000, 0x50000, 10
+        a.q_row_stride = a.k_row_stride = a.o_row_stride = D
+        with pytest.raises(L.HipPathError, match=msg):
+            L.check(L.lib().or_varlen_fwd(ctypes.byref(a), None), 'or_varlen_fwd')
+    p = L.PackArgs()
+    p.H, p.D, p.n_queries, p.q_scale = 16, 128, 4, float('inf')
+    p.q, p.q_src, p.q_rope, p.q_out, p.cos_table, p.sin_table, p.n_rope_rows = (0x10000, 0x20000, 0x30000, 0x40000,
+                                                                                  0x50000, 0x60000, 10)
+    p.q_row_stride = p.q_out_row_stride = 2048
+    with pytest.raises(L.HipPathError, match='q_scale must be finite'):
+        L.check(L.lib().or_pack_layer(ctypes.byref(p), None), 'or_pack_layer')
 
 
 def test_product_has_no_cpu_fallback():
@@ -441,3 +459,29 @@ def test_bench_refuses_several_gpus_and_bad_shares():
     r = subprocess.run([sys.executable, str(root / 'bench.py'), '--share', '3/3', '--no-cpu'], capture_output=True,
                        text=True, timeout=300, cwd=root)
     assert r.returncode != 0 and 'rank R in [0, P)' in r.stdout + r.stderr
+
+
+def test_abi_structs_match_the_header(tmp_path):
+    """the ctypes argument structs have the C header's field offsets and sizes (gcc on the header itself)"""
+    import shutil
+    import subprocess
+    if shutil.which('gcc') is None:
+        pytest.skip('needs gcc')
+    pairs = [('or_layout_desc', L.LayoutDesc), ('or_layout_sizes', L.LayoutSizes), ('or_layout_out', L.LayoutOut),
+             ('or_varlen_args', L.VarlenArgs), ('or_pack_args', L.PackArgs)]
+    lines = ['#include <stddef.h>', '#include <stdio.h>', f'#include "{ROOT / "include" / "onereel_hip.h"}"',
+             'int main(void) {']
+    for cname, cls in pairs:
+        lines.append(f'  printf("{cname} sizeof %zu\\n", sizeof({cname}));')
+        for f in cls._fields_:
+            lines.append(f'  printf("{cname} {f[0]} %zu\\n", offsetof({cname}, {f[0]}));')
+    lines += ['  return 0;', '}']
+    src, exe = tmp_path / 'abi.c', tmp_path / 'abi'
+    src.write_text('\n'.join(lines) + '\n')
+    subprocess.run(['gcc', '-std=c11', '-o', str(exe), str(src)], check=True)
+    got = dict(l.rsplit(' ', 1) for l in subprocess.run([str(exe)], check=True, capture_output=True,
+                                                        text=True).stdout.splitlines())
+    for cname, cls in pairs:
+        assert int(got[f'{cname} sizeof']) == ctypes.sizeof(cls), cname
+        for f in cls._fields_:
+            assert int(got[f'{cname} {f[0]}']) == getattr(cls, f[0]).offset, (cname, f[0])
