@@ -307,17 +307,20 @@ def run_bounded_memory(args):
     shape: one layer call = representative choice (warm-started k-means) + the foreign representatives' index arrays +
     the pack of the local rows past each piece's in-place run and of the representatives + one multi-head varlen call
     (local keys and values of the leading run read in place), timed in steady state: after the first call, whose
-    k-means runs 50 iterations, and `warmup` (default 3) more calls"""
+    k-means runs 50 iterations, and `warmup` (default 3) more calls. The video queries carry scale * log2(e), as the
+    processors' rotation leaves them (q_scaled_rows), the sentence queries not"""
     import torch
     import torch.nn.functional as F
     from onereel_amd.layout import SceneLayout
     from onereel_amd.memory import BoundaryMemory, MemoryAttention, frame_plan
+    from onereel_amd.scene import base2_scale
     dev = torch.device('cuda:0')
     torch.cuda.set_device(dev)
     lay = SceneLayout(LENGTHS, halo=0)
     S, Le = lay.n_frames * T, sum(COUNTS)
     g = torch.Generator(device=dev).manual_seed(0)
     q, k, v = (torch.randn(S + Le, H, D, generator=g, device=dev).to(torch.bfloat16) for _ in range(3))
+    q[:S] = (q[:S].float() * base2_scale(D)).to(torch.bfloat16)
     tr, c = [], 0
     for n in COUNTS:
         tr.append((c, c + n))
@@ -330,15 +333,15 @@ def run_bounded_memory(args):
     st = torch.cuda.current_stream(dev)
     a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     a.record(st)
-    mem(key, q, k, v, plan)
+    mem(key, q, k, v, plan, q_scaled_rows=S)
     b.record(st)
     b.synchronize()
     t_first = a.elapsed_time(b)
     warm = 3 if args.warmup is None else args.warmup
     for _ in range(warm):
-        mem(key, q, k, v, plan)
+        mem(key, q, k, v, plan, q_scaled_rows=S)
     reps = max(3, args.kernel_reps)
-    t_call = time_events(lambda: mem(key, q, k, v, plan), reps, st)
+    t_call = time_events(lambda: mem(key, q, k, v, plan, q_scaled_rows=S), reps, st)
     # useful FLOPs of the attention: each piece and head reads its local keys plus the foreign representatives
     rep, valid = BoundaryMemory(M).select(key, k[plan.cand])
     rep_scene = plan.owner[rep]

@@ -395,9 +395,11 @@ def zero_text_padding(plan: ScopePlan, ot: torch.Tensor):
     return ot
 
 
-def rotate_queries(plan: ScopePlan, q, cos, sin, out=None):
+def rotate_queries(plan: ScopePlan, q, cos, sin, out=None, q_scale=None):
     """every video query row rotated at its scene-RoPE table row, in token order (or_rotate_rows over the plan's
-    packed queries; text rows are not rotated and stay in the text tensor): [F*T, H, D] bf16"""
+    packed queries; text rows are not rotated and stay in the text tensor): [F*T, H, D] bf16. With q_scale, each
+    rotated element multiplied by it in fp32 before its rounding to bf16 (or_pack_layer's query job alone), for
+    varlen(..., q_prescaled=True) with q_scale = base2_scale(D)."""
     H, D = q.shape[1], q.shape[2]
     _check_bf16(q, out)
     _, qs = _rows2d(q, H, D)
@@ -410,9 +412,18 @@ def rotate_queries(plan: ScopePlan, q, cos, sin, out=None):
     _, os_ = _rows2d(out, H, D)
     if out.shape[0] < plan.n_video:
         raise L.HipValueError(f'out holds {out.shape[0]} rows, the layout has {plan.n_video} video rows')
-    L.check(L.lib().or_rotate_rows(q.data_ptr(), qs, plan.n_video, plan.q_src.data_ptr(), plan.q_rope.data_ptr(),
-                                   cos.data_ptr(), sin.data_ptr(), n_rows, plan.sum_q, H, D, out.data_ptr(), os_,
-                                   L.stream_handle(q.device)), 'or_rotate_rows')
+    if q_scale is None:
+        L.check(L.lib().or_rotate_rows(q.data_ptr(), qs, plan.n_video, plan.q_src.data_ptr(), plan.q_rope.data_ptr(),
+                                       cos.data_ptr(), sin.data_ptr(), n_rows, plan.sum_q, H, D, out.data_ptr(), os_,
+                                       L.stream_handle(q.device)), 'or_rotate_rows')
+        return out
+    a = L.PackArgs()
+    a.n_video = plan.n_video
+    a.q, a.q_row_stride, a.q_src, a.q_rope = q.data_ptr(), qs, plan.q_src.data_ptr(), plan.q_rope.data_ptr()
+    a.n_queries, a.q_out, a.q_out_row_stride = plan.sum_q, out.data_ptr(), os_
+    a.cos_table, a.sin_table, a.n_rope_rows = cos.data_ptr(), sin.data_ptr(), n_rows
+    a.H, a.D, a.q_scale = H, D, float(q_scale)
+    L.check(L.lib().or_pack_layer(ctypes.byref(a), L.stream_handle(q.device)), 'or_pack_layer')
     return out
 
 
