@@ -311,11 +311,13 @@ int or_lse_merge(float* o, float* lse, const void* o_s, const float* lse_s, int6
  * y[2i+1] c; fp32 throughout, one rounding to bf16. q and k (k may be NULL) in one launch. Rows: bf16 with the given
  * strides (elements); cos / sin: fp32 [n_rope_rows, D], table row rope_row[r] (rope_row NULL: row r; out of range:
  * no rotation). With n_rope_rows = 0 and no tables it is the RMSNorm alone (the norm_q / norm_k of diffusers'
- * Wan cross-attention processor, which wan.py:83-87 calls per scene). D must divide 512 and C be a multiple of 512. */
+ * Wan cross-attention processor, which wan.py:83-87 calls per scene). D must divide 512 and C be a multiple of 512.
+ * q_scale (finite; 0: none) multiplies the query outputs before their rounding, e.g. scale * log2(e) for
+ * or_varlen_args.q_prescaled. */
 int or_rmsnorm_rope(const void* q, const void* k, const void* wq, const void* wk, int64_t q_row_stride,
                     int64_t k_row_stride, int64_t n_rows, int32_t C, int32_t D, float eps, const float* cos_table,
                     const float* sin_table, const int32_t* rope_row, int64_t n_rope_rows, void* q_out, void* k_out,
-                    int64_t qo_row_stride, int64_t ko_row_stride, void* stream);
+                    int64_t qo_row_stride, int64_t ko_row_stride, float q_scale, void* stream);
 
 /* Replaces the pooling of FrameMemory.collect (src/onereel/frame_memory.py:76-85, index_add_ of one layer's video rows
  * into per-frame sums and counts): for the frame-major rows r of hs (bf16, row stride row_stride elements, C wide),

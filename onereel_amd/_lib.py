@@ -79,7 +79,7 @@ SIGNATURES = {
     'or_varlen_fwd_noalloc': (i32, [ctypes.POINTER(VarlenArgs), vp]),
     'or_lse_merge': (i32, [vp, vp, vp, vp, i64, i32, i32, i64, i64, vp]),
     'or_rmsnorm_rope': (i32, [vp, vp, vp, vp, i64, i64, i64, i32, i32, ctypes.c_float, vp, vp, vp, i64, vp, vp, i64,
-                              i64, vp]),
+                              i64, ctypes.c_float, vp]),
     'or_frame_pool': (i32, [vp, i64, i32, i64, i64, i32, i32, vp, vp, vp]),
     'or_frame_select': (i32, [vp, i32, i32, vp, i32, i32, i32, vp, vp, vp]),
     'or_memory_select_workspace_size': (i64, [i32, i32, i32, i32, i32]),

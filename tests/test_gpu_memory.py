@@ -305,6 +305,7 @@ def test_wan_self_attention_routes_the_bounded_memory():
     lay = SceneLayout([3, 4, 2], halo=0)
     S = lay.n_frames * T
     ctx = W.Context(lay, T=T, memory=M)
+    ctx2 = W.Context(lay, T=T, memory=M)       # the same calls with pre-multiplied queries (its own memory state)
     twin = BoundaryMemory(M)
     cand, owner = candidates(lay, T, 'cpu')
     empty = torch.zeros(0, H, D, dtype=torch.bfloat16)
@@ -317,6 +318,10 @@ def test_wan_self_attention_routes_the_bounded_memory():
         rv, _ = OM.masked_reference(q, k, v, empty, empty, empty, lay.ranges, T, cand[rep], owner[rep], valid,
                                     [(0, 0)] * 3)
         assert_close(o, rv, what=f'wan memory call {call}')
+        # as the processor runs it: the queries multiplied by D^-0.5 log2 e (the base-2 key loop)
+        qs = (q.float() * base2_scale(D)).to(torch.bfloat16)
+        o2 = W.memory_self(ctx2, qs.to(DEV), k.to(DEV), v.to(DEV), 4, q_prescaled=True).cpu()
+        assert_close(o2, rv, what=f'wan memory call {call}, pre-multiplied queries')
 
 
 def test_select_matches_oracle_at_480p_shape():
