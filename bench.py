@@ -307,20 +307,17 @@ def run_bounded_memory(args):
     shape: one layer call = representative choice (warm-started k-means) + the foreign representatives' index arrays +
     the pack of the local rows past each piece's in-place run and of the representatives + one multi-head varlen call
     (local keys and values of the leading run read in place), timed in steady state: after the first call, whose
-    k-means runs 50 iterations, and `warmup` (default 3) more calls. The video queries carry scale * log2(e), as the
-    processors' rotation leaves them (q_scaled_rows), the sentence queries not"""
+    k-means runs 50 iterations, and `warmup` (default 3) more calls"""
     import torch
     import torch.nn.functional as F
     from onereel_amd.layout import SceneLayout
     from onereel_amd.memory import BoundaryMemory, MemoryAttention, frame_plan
-    from onereel_amd.scene import base2_scale
     dev = torch.device('cuda:0')
     torch.cuda.set_device(dev)
     lay = SceneLayout(LENGTHS, halo=0)
     S, Le = lay.n_frames * T, sum(COUNTS)
     g = torch.Generator(device=dev).manual_seed(0)
     q, k, v = (torch.randn(S + Le, H, D, generator=g, device=dev).to(torch.bfloat16) for _ in range(3))
-    q[:S] = (q[:S].float() * base2_scale(D)).to(torch.bfloat16)
     tr, c = [], 0
     for n in COUNTS:
         tr.append((c, c + n))
@@ -333,15 +330,15 @@ def run_bounded_memory(args):
     st = torch.cuda.current_stream(dev)
     a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     a.record(st)
-    mem(key, q, k, v, plan, q_scaled_rows=S)
+    mem(key, q, k, v, plan)
     b.record(st)
     b.synchronize()
     t_first = a.elapsed_time(b)
     warm = 3 if args.warmup is None else args.warmup
     for _ in range(warm):
-        mem(key, q, k, v, plan, q_scaled_rows=S)
+        mem(key, q, k, v, plan)
     reps = max(3, args.kernel_reps)
-    t_call = time_events(lambda: mem(key, q, k, v, plan, q_scaled_rows=S), reps, st)
+    t_call = time_events(lambda: mem(key, q, k, v, plan), reps, st)
     # useful FLOPs of the attention: each piece and head reads its local keys plus the foreign representatives
     rep, valid = BoundaryMemory(M).select(key, k[plan.cand])
     rep_scene = plan.owner[rep]
@@ -385,18 +382,17 @@ def run_power(args):
     lq = [int(x) for x in (plan.cu_q[1:] - plan.cu_q[:-1]).tolist()]
     lk = [int(x) for x in plan.k_len.tolist()]
     flops = float(sum(4.0 * a * b * H * D for a, b in zip(lq, lk)))
-    # the video queries rotated and multiplied by scale * log2(e), as the layer's pack launch leaves them
-    qr = scene.pack_layer(plan, k, ek, v, ev, cos, sin, 'raw', q=q, q_scale=scene.base2_scale(D))[2]
+    qr = scene.rotate_queries(plan, q, cos, sin)
     attn = lambda: scene.varlen(qr, kp, vp, plan.cu_q, plan.cu_k, plan.max_q, plan.max_k, k_off=plan.k_off,
                                 k_len=plan.k_len, out=ov, seg_q_src=plan.seg_q_src, q_text=eq, o_text=ot,
-                                n_q_video=plan.n_video, sum_q=plan.sum_q, workspace=ws, q_prescaled=True)
+                                n_q_video=plan.n_video, sum_q=plan.sum_q, workspace=ws)
     # the same call on operands with two mantissa bits (bf16 bits 4..0 cleared): the same FLOP and schedule, less
     # MFMA switching power, so the rate it reaches at the board's limit shows how much power bounds the kernel
     low = lambda x: (x.view(torch.int16) & -32).view(torch.bfloat16)
     qr2, kp2, vp2, eq2 = low(qr), low(kp), low(vp), low(eq)
     attn2 = lambda: scene.varlen(qr2, kp2, vp2, plan.cu_q, plan.cu_k, plan.max_q, plan.max_k, k_off=plan.k_off,
                                  k_len=plan.k_len, out=ov, seg_q_src=plan.seg_q_src, q_text=eq2, o_text=ot,
-                                 n_q_video=plan.n_video, sum_q=plan.sum_q, workspace=ws, q_prescaled=True)
+                                 n_q_video=plan.n_video, sum_q=plan.sum_q, workspace=ws)
     n_g = 16384
     a = torch.randn(n_g, n_g, generator=g, device=dev).to(torch.bfloat16)
     b = torch.randn(n_g, n_g, generator=g, device=dev).to(torch.bfloat16)
@@ -656,16 +652,14 @@ def main():
     ov = torch.empty_like(q)
     ot = torch.empty(Le, H, D, dtype=torch.bfloat16, device=dev)
     ws = plan.workspace(H, D)
-    # the attention kernel as the step runs it: video queries already rotated and multiplied by scale * log2(e)
-    # (qbuf; head_dim 128), read in place, the own-frame values read in place from v
-    base2 = D == 128
+    # the attention kernel as the step runs it: video queries already rotated (qbuf), read in place, the own-frame
+    # values read in place from v
     attn_of = lambda p: (lambda: scene.varlen(qbuf, kbuf, vbuf, p.cu_q, p.cu_k, p.max_q, p.max_k, k_off=p.k_off,
                                               k_len=p.k_len, out=ov, seg_q_src=p.seg_q_src, q_text=eq, o_text=ot,
                                               n_q_video=p.n_video, sum_q=p.sum_q, workspace=ws, v_tok=v,
-                                              v_lead=p.v_lead, v_row=p.v_row, v_runs=p.v_runs, q_prescaled=base2))
+                                              v_lead=p.v_lead, v_row=p.v_row, v_runs=p.v_runs))
     # the step's one pack launch: K rows (rotated), the V rows not read in place, the video queries rotated once
-    pack_of = lambda p: (lambda: scene.pack_layer(p, k, ek, v, ev, cos, sin, 'raw', kbuf, vbuf, q=q, qbuf=qbuf,
-                                                  q_scale=scene.base2_scale(D) if base2 else None))
+    pack_of = lambda p: (lambda: scene.pack_layer(p, k, ek, v, ev, cos, sin, 'raw', kbuf, vbuf, q=q, qbuf=qbuf))
     attn, pack = attn_of(plan), pack_of(plan)
     qpk = torch.empty(plan.sum_q, H, D, dtype=torch.bfloat16, device=dev)
     scat = lambda: scene.scatter(plan, qpk, ov, ot)

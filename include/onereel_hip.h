@@ -187,8 +187,6 @@ typedef struct or_pack_args {
   int64_t n_rope_rows;
   int32_t H;
   int32_t D;
-  float q_scale;              /* nonzero: each rotated query element is multiplied by q_scale in fp32 before its one
-                                 rounding to bf16 (scale * log2(e) for or_varlen_args.q_prescaled); 0: not scaled */
 } or_pack_args;
 
 /* Replaces the same code as or_pack_gather and or_rotate_rows together (hunyuan15.py:164,168,183-191,225;
@@ -265,11 +263,6 @@ typedef struct or_varlen_args {
                                (n = 0: unused). Only their whole key blocks (inside the segment, its key count and
                                v_tok_rows) are read in place, the other keys' values from v (a layout's v_runs, with
                                the values packed per its v_src) */
-  int32_t q_prescaled;      /* optional, head_dim 128 without q_rope: nonzero when the rows of q (not q_text) hold
-                               scale * log2(e) * q, rounded once to bf16 (or_pack_layer's query rotation with q_scale
-                               = scale * log2(e)); their segments then take the scores as base-2 exponents, without
-                               the multiply per score. The results are those of the unscaled queries up to that
-                               rounding. Every query row of a segment must be on one side of n_q_video. */
 } or_varlen_args;
 
 /* Bytes of device workspace or_varlen_fwd needs for this many segments, packed queries and heads: the work-item
@@ -311,13 +304,11 @@ int or_lse_merge(float* o, float* lse, const void* o_s, const float* lse_s, int6
  * y[2i+1] c; fp32 throughout, one rounding to bf16. q and k (k may be NULL) in one launch. Rows: bf16 with the given
  * strides (elements); cos / sin: fp32 [n_rope_rows, D], table row rope_row[r] (rope_row NULL: row r; out of range:
  * no rotation). With n_rope_rows = 0 and no tables it is the RMSNorm alone (the norm_q / norm_k of diffusers'
- * Wan cross-attention processor, which wan.py:83-87 calls per scene). D must divide 512 and C be a multiple of 512.
- * q_scale (finite; 0: none) multiplies the query outputs before their rounding, e.g. scale * log2(e) for
- * or_varlen_args.q_prescaled. */
+ * Wan cross-attention processor, which wan.py:83-87 calls per scene). D must divide 512 and C be a multiple of 512. */
 int or_rmsnorm_rope(const void* q, const void* k, const void* wq, const void* wk, int64_t q_row_stride,
                     int64_t k_row_stride, int64_t n_rows, int32_t C, int32_t D, float eps, const float* cos_table,
                     const float* sin_table, const int32_t* rope_row, int64_t n_rope_rows, void* q_out, void* k_out,
-                    int64_t qo_row_stride, int64_t ko_row_stride, float q_scale, void* stream);
+                    int64_t qo_row_stride, int64_t ko_row_stride, void* stream);
 
 /* Replaces the pooling of FrameMemory.collect (src/onereel/frame_memory.py:76-85, index_add_ of one layer's video rows
  * into per-frame sums and counts): for the frame-major rows r of hs (bf16, row stride row_stride elements, C wide),

@@ -53,7 +53,7 @@ class VarlenArgs(ctypes.Structure):
                 ('max_q', i32), ('max_k', i32), ('H', i32), ('D', i32), ('scale', ctypes.c_float),
                 ('workspace', vp), ('workspace_bytes', i64), ('q_row_step', i32), ('v_tok', vp), ('v_lead', vp),
                 ('v_row', vp), ('v_tok_rows', i64), ('k_len_head', vp), ('k_tok', vp), ('k_lead', vp),
-                ('k_tok_rows', i64), ('v_runs', vp), ('q_prescaled', i32)]
+                ('k_tok_rows', i64), ('v_runs', vp)]
 
 
 class PackArgs(ctypes.Structure):
@@ -62,8 +62,7 @@ class PackArgs(ctypes.Structure):
                 ('v_src', vp), ('n_keys', i64), ('k_dst', vp), ('k_out', vp), ('v_out', vp), ('q', vp),
                 ('q_row_stride', i64),
                 ('q_src', vp), ('q_rope', vp), ('n_queries', i64), ('q_out', vp), ('q_out_row_stride', i64),
-                ('cos_table', vp), ('sin_table', vp), ('n_rope_rows', i64), ('H', i32), ('D', i32),
-                ('q_scale', ctypes.c_float)]
+                ('cos_table', vp), ('sin_table', vp), ('n_rope_rows', i64), ('H', i32), ('D', i32)]
 
 
 # every exported symbol with its ctypes signature: include/onereel_hip.h
@@ -79,7 +78,7 @@ SIGNATURES = {
     'or_varlen_fwd_noalloc': (i32, [ctypes.POINTER(VarlenArgs), vp]),
     'or_lse_merge': (i32, [vp, vp, vp, vp, i64, i32, i32, i64, i64, vp]),
     'or_rmsnorm_rope': (i32, [vp, vp, vp, vp, i64, i64, i64, i32, i32, ctypes.c_float, vp, vp, vp, i64, vp, vp, i64,
-                              i64, ctypes.c_float, vp]),
+                              i64, vp]),
     'or_frame_pool': (i32, [vp, i64, i32, i64, i64, i32, i32, vp, vp, vp]),
     'or_frame_select': (i32, [vp, i32, i32, vp, i32, i32, i32, vp, vp, vp]),
     'or_memory_select_workspace_size': (i64, [i32, i32, i32, i32, i32]),

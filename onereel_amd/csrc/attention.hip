@@ -16,8 +16,6 @@
 // - head_dim 128: attn8_kernel, 64 queries per wavefront (one wavefront per SIMD), O in AGPRs, key loop in generated
 //   asm. head_dim 64: attn4_kernel, 32 queries per wavefront, two wavefronts per SIMD.
 // - Softmax in base 2, p = 2^(c (s - m)) with c = scale * log2(e), and a running max m raised only when needed.
-//   With q_prescaled the video query rows already hold c q (rounded once to bf16 from the fp32 rotation that made
-//   them), so their scores are base-2 exponents and the key loop takes p = 2^(s - m) without a multiply per score.
 // - Optional RoPE on the Q load (table row per packed query), with the rounding of diffusers apply_rotary_emb.
 #include <math.h>
 #include <stdlib.h>
@@ -96,8 +94,6 @@ struct AttnArgs {
   int64_t n_ktok;
   // value events of the segments with value runs (kVEvents int4 per segment, written by the planner)
   const int4* v_events;
-  // the rows of q below n_q_video hold c q: their items run the base-2 key loop (head_dim 128)
-  int32_t q_prescaled;
 };
 
 // the list a work item without further value events points its key loop at: sentinels only
@@ -1051,45 +1047,33 @@ void attn8_kernel(AttnArgs a, int32_t* ws) {
     }
     const int valid = Lk - (nb - 1) * kBKB - 16 * h;
     const uint64_t kaddr2 = kblock(2);   // K block 2, where the prologue's ring fill starts
-    float mo0, mo1, lo0, lo1;   // per query: the running max of the scores, and the row sum relative to it
-    // the item's queries are the video rows of q (every row of a segment is on one side of n_q_video): with
-    // q_prescaled they hold c q, and the base-2 loop leaves out the multiply per score
-    const bool base2 = a.q_prescaled && q_src0 < a.n_q_video;
-#define ONEREEL_ATTN8_LOOP(ASM)                                                                                     \
-  asm volatile(ASM                                                                                                 \
-               : [mo0] "=&v"(mo0), [mo1] "=&v"(mo1), [lo0] "=&v"(lo0), [lo1] "=&v"(lo1)                             \
-               : [qa0] "v"(qa[0]), [qa1] "v"(qa[1]), [c] "s"(a.c), [nb] "s"(nb), [valid] "v"(valid), [kb] "v"(kb),  \
-                 [vb] "v"(vb), [vk0] "v"(voff[0]), [vk1] "v"(voff[1]), [vv0] "v"(voff[2]), [vv1] "v"(voff[3]),      \
-                 [sbase] "s"(sbase), [bb] "s"(bb), [kb_lo] "s"((uint32_t)kaddr2),                                  \
-                 [kb_hi] "s"((uint32_t)(kaddr2 >> 32)), [vb_lo] "s"((uint32_t)vaddr),                               \
-                 [vb_hi] "s"((uint32_t)(vaddr >> 32)), [rem0] "s"(rem0), [remk] "s"(rem0 - 2 * bb),                 \
-                 [op0] "v"(op[0]), [op1] "v"(op[1]), [ok0] "v"(ok[0]), [ok1] "v"(ok[1]),                            \
-                 [f32] "s"(__builtin_amdgcn_readfirstlane(ways > 1 ? 1 : 0)),                                      \
-                 [dead] "s"(__builtin_amdgcn_readfirstlane(q0 >= Lq ? 1 : 0)), [vsw] "s"(vsw), [nbav] "s"(vnext),   \
-                 [ksw] "s"(ksw), [nbak] "s"(kr.nba), [vlist] "s"(vlist_u), [hoff] "s"(hoff), [b0] "s"(b0)           \
-               : ONEREEL_RING64_CLOBBERS)
-    if (base2)
-      ONEREEL_ATTN8_LOOP(ONEREEL_RING64_ASM_BASE2);
-    else
-      ONEREEL_ATTN8_LOOP(ONEREEL_RING64_ASM);
-#undef ONEREEL_ATTN8_LOOP
-    // the running max in natural-log units: m scale, or m ln 2 for base-2 scores
-    const float mscale = base2 ? 0.6931471805599453f : a.scale;
+    float mo0, mo1, lo0, lo1;   // per query: the running max of q k^T, and the row sum relative to it
+    asm volatile(ONEREEL_RING64_ASM
+                 : [mo0] "=&v"(mo0), [mo1] "=&v"(mo1), [lo0] "=&v"(lo0), [lo1] "=&v"(lo1)
+                 : [qa0] "v"(qa[0]), [qa1] "v"(qa[1]), [c] "s"(a.c), [nb] "s"(nb), [valid] "v"(valid), [kb] "v"(kb),
+                   [vb] "v"(vb), [vk0] "v"(voff[0]), [vk1] "v"(voff[1]), [vv0] "v"(voff[2]), [vv1] "v"(voff[3]),
+                   [sbase] "s"(sbase), [bb] "s"(bb), [kb_lo] "s"((uint32_t)kaddr2), [kb_hi] "s"((uint32_t)(kaddr2 >> 32)),
+                   [vb_lo] "s"((uint32_t)vaddr), [vb_hi] "s"((uint32_t)(vaddr >> 32)), [rem0] "s"(rem0), [remk] "s"(rem0 - 2 * bb),
+                   [op0] "v"(op[0]), [op1] "v"(op[1]), [ok0] "v"(ok[0]), [ok1] "v"(ok[1]),
+                   [f32] "s"(__builtin_amdgcn_readfirstlane(ways > 1 ? 1 : 0)),
+                   [dead] "s"(__builtin_amdgcn_readfirstlane(q0 >= Lq ? 1 : 0)), [vsw] "s"(vsw), [nbav] "s"(vnext),
+                   [ksw] "s"(ksw), [nbak] "s"(kr.nba), [vlist] "s"(vlist_u), [hoff] "s"(hoff), [b0] "s"(b0)
+                 : ONEREEL_RING64_CLOBBERS);
     // the next item's queries are in a128..a191 unless they must be rotated on the load
     have_q = nit >= 0 && !a.q_rope;
     it = nit == kLater ? claim(false) : nit;
     if (ways <= 1) {
       if (a.lse && h == 0) {
-        if (ok[0]) a.lse[(int64_t)head * a.sum_q + q_beg + q0 + l32] = mo0 * mscale + logf(lo0);
-        if (ok[1]) a.lse[(int64_t)head * a.sum_q + q_beg + q0 + 32 + l32] = mo1 * mscale + logf(lo1);
+        if (ok[0]) a.lse[(int64_t)head * a.sum_q + q_beg + q0 + l32] = mo0 * a.scale + logf(lo0);
+        if (ok[1]) a.lse[(int64_t)head * a.sum_q + q_beg + q0 + 32 + l32] = mo1 * a.scale + logf(lo1);
       }
       continue;
     }
     // a part of a split item: its lse next to its O / l (merge_kernel combines the parts)
     float* part_lse = a.split_lse + (int64_t)(sidx * ways + part) * kSplitRows;
     if (h == 0) {
-      if (ok[0]) part_lse[w * WQ + l32] = mo0 * mscale + logf(lo0);
-      if (ok[1]) part_lse[w * WQ + 32 + l32] = mo1 * mscale + logf(lo1);
+      if (ok[0]) part_lse[w * WQ + l32] = mo0 * a.scale + logf(lo0);
+      if (ok[1]) part_lse[w * WQ + 32 + l32] = mo1 * a.scale + logf(lo1);
     }
   }
 }
@@ -1242,8 +1226,6 @@ int check_args(const or_varlen_args& x, const char* fn) {
     return fail_arg("%s: k_tok needs k_lead, v_row, k_tok_rows >= 0 and 16-byte alignment", fn);
   if (x.v_runs && (!x.v_tok || x.D != 128 || x.k_len_head))
     return fail_arg("%s: v_runs needs v_tok and head_dim 128 (and no k_len_head)", fn);
-  if (x.q_prescaled && (x.D != 128 || x.q_rope))
-    return fail_arg("%s: q_prescaled needs head_dim 128 (and no q_rope)", fn);
   return 0;
 }
 
@@ -1297,7 +1279,6 @@ int launch_varlen(const or_varlen_args& x, void* wsp, int64_t cap, hipStream_t s
   a.split_lse = (float*)((char*)wsp + wl.lse);
   a.split_o = (float*)((char*)wsp + wl.o);
   a.v_events = (const int4*)((char*)wsp + wl.ev);
-  a.q_prescaled = x.q_prescaled ? 1 : 0;
   VRunArgs vra;
   vra.runs = x.v_tok ? x.v_runs : nullptr;
   vra.v_tok = (uint64_t)x.v_tok;

@@ -24,31 +24,6 @@ constexpr int kMaxChunksPerLane = 8;  // rows up to 64 lanes * 8 * 8 elements = 
 // 16-byte store that bypasses the caches (global_store_dwordx4 ... nt)
 __device__ __forceinline__ void store_nt(uint16_t* p, u32x4 v) { __builtin_nontemporal_store(v, (u32x4*)p); }
 
-// rotate8 (sign +1) with each rotated element multiplied by `mul` in fp32 before its one rounding to bf16: the
-// queries of an attention call that takes its scores as base-2 exponents (mul = scale * log2(e))
-__device__ __forceinline__ u32x4 rotate8_mul(u32x4 v, const Tab8& t, float mul) {
-  float c[8] = {t.c0[0], t.c0[1], t.c0[2], t.c0[3], t.c1[0], t.c1[1], t.c1[2], t.c1[3]};
-  float s[8] = {t.s0[0], t.s0[1], t.s0[2], t.s0[3], t.s1[0], t.s1[1], t.s1[2], t.s1[3]};
-  u32x4 r;
-#pragma unroll
-  for (int p = 0; p < 4; ++p) {
-    float x0 = bf2f((uint16_t)(v[p] & 0xffffu)), x1 = bf2f((uint16_t)(v[p] >> 16));
-    float y0, y1;
-    rot_pair(x0, x1, c[2 * p], c[2 * p + 1], s[2 * p], s[2 * p + 1], y0, y1);
-    r[p] = pack2(y0 * mul, y1 * mul);
-  }
-  return r;
-}
-
-// 8 bf16 multiplied by `mul` in fp32 and rounded to bf16 (a row the table leaves unrotated)
-__device__ __forceinline__ u32x4 scale8(u32x4 v, float mul) {
-  u32x4 r;
-#pragma unroll
-  for (int p = 0; p < 4; ++p)
-    r[p] = pack2(bf2f((uint16_t)(v[p] & 0xffffu)) * mul, bf2f((uint16_t)(v[p] >> 16)) * mul);
-  return r;
-}
-
 // One job of the row kernel: n_rows rows, row r read from src_idx[r] of [video ; text] (none where src_idx[r] < 0),
 // rotated per rope_row / move_from, written to packed row dst_idx[r] (r without dst_idx) of a_out (in_place: to its
 // own source row of a_out, row stride out_stride, and text rows skipped); the second source's row b_idx[r] (src_idx[r]
@@ -69,7 +44,6 @@ struct RowJob {
   int64_t out_stride;
   int64_t n_rows;
   int in_place;
-  float mul;   // nonzero: every written a row multiplied by mul in fp32 before its rounding to bf16 (0: as read)
 };
 
 // rows [0, job[0].n_rows) run job 0, the next job[1].n_rows rows job 1 (one launch for the K/V pack and the query
@@ -105,7 +79,6 @@ struct RowWork {
   uint16_t* ao;
   uint16_t* bo;
   int rope, mfrom;
-  float mul;
   bool live, rot;
   Tab8 tr, tm;
   u32x4 va[CPL], vb[CPL];
@@ -159,7 +132,6 @@ __device__ __forceinline__ void row_load(const GatherArgs& g, int64_t rr, int64_
   if (rope >= g.n_rope_rows || mfrom >= g.n_rope_rows) rope = mfrom = -1;
   w.rope = rope;
   w.mfrom = mfrom;
-  w.mul = J.mul;
   const int row_elems = g.H * g.D;
 #pragma unroll
   for (int i = 0; i < CPL; ++i) {
@@ -198,9 +170,7 @@ __device__ __forceinline__ void row_store(const GatherArgs& g, const RowLanes& r
           if (move) w.tm = load_tab8(g.cos_t, g.sin_t, (int64_t)w.mfrom * g.D + d0);
         }
         if (move) x = rotate8(x, w.tm, -1.0f);
-        x = w.mul != 0.0f ? rotate8_mul(x, w.tr, w.mul) : rotate8(x, w.tr, 1.0f);
-      } else if (w.mul != 0.0f) {
-        x = scale8(x, w.mul);
+        x = rotate8(x, w.tr, 1.0f);
       }
       store_nt(w.ao + 8 * c, x);
       if (w.bo) store_nt(w.bo + 8 * c, w.vb[i]);
@@ -455,7 +425,6 @@ extern "C" int or_pack_layer(const or_pack_args* p, void* stream) {
       return fail_arg("or_pack_layer: query row strides must cover H * D elements");
     if (!aligned16(x.q) || !aligned16(x.q_out) || x.q_row_stride % 8 || x.q_out_row_stride % 8)
       return fail_arg("or_pack_layer: pointers must be 16-byte aligned and row strides multiples of 8 elements");
-    if (!(fabsf(x.q_scale) < __builtin_inff())) return fail_arg("or_pack_layer: q_scale must be finite");
   }
   GatherArgs g{};
   if (x.n_keys > 0)
@@ -464,7 +433,7 @@ extern "C" int or_pack_layer(const or_pack_args* p, void* stream) {
   if (x.n_queries > 0)
     g.job[1] = RowJob{(const uint16_t*)x.q, (const uint16_t*)x.q, nullptr, nullptr, x.q_row_stride, x.q_row_stride,
                       x.q_src, nullptr, nullptr, x.q_rope, nullptr, (uint16_t*)x.q_out, nullptr, x.q_out_row_stride,
-                      x.n_queries, 1, x.q_scale};
+                      x.n_queries, 1};
   g.n_video = x.n_video;
   g.cos_t = x.cos_table;
   g.sin_t = x.sin_table;

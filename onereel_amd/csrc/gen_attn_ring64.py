@@ -24,11 +24,7 @@ that item, or of this item when the next one is not claimed yet: the 16 loads ar
 are not queued behind its O stores in the in-order vmcnt.
 S = q k^T - m comes out of the MFMAs (the first of each block accumulates onto -m), so P = 2^(c S), c = scale *
 log2(e), takes one v_mul_f32 and one v_exp_f32 per score: the fp32 scores of FlashAttention's exp2(s c - m c), with
-the subtraction folded into the accumulator. The loop is emitted twice: ONEREEL_RING64_ASM as above, and
-ONEREEL_RING64_ASM_BASE2 for queries that already hold c q (rounded once to bf16 where they were rotated in fp32), whose
-scores are base-2 exponents: P = 2^S, one v_exp_f32 per score and no multiply (the layer's video queries; measured
-2.0-2.3% faster at the 480p layer: the board is at its power limit, and the multiplies' share of it goes to the
-clock). The running max m and the rescale's 2^(-d) are then in the same base-2 units.
+the subtraction folded into the accumulator.
 
 Schedule of iteration j (32 keys; R-slot rings of K and V blocks in LDS, 8 KiB per slot):
     phase A  MFMA steps k = 0..3: S(j+1) += K(j+1)_k Q_k^T for both query blocks, O += V(j-1)_k P(j-1)_k; the VALU
@@ -265,10 +261,9 @@ def v_advance(R):
 
 
 class Kernel:
-    def __init__(self, ring, base2=False):
+    def __init__(self, ring):
         assert ring in (4, 6, 8)
         self.R = ring
-        self.base2 = base2            # queries pre-multiplied by c: the scores are base-2 exponents (no v_mul)
         self.VBASE = ring * SLOT      # V ring after the K ring
 
     # ---- pieces ------------------------------------------------------------------------------------------------
@@ -315,20 +310,15 @@ class Kernel:
                       [vr(lo, 2)])
 
     def softmax(self, par, qb):
-        """P(par, qb) = bf16(2^(c S)) (bf16(2^S) in the base-2 form) and LS(qb) = fp32 sum of the unrounded values:
-        list of (asm, reads, writes, trans)"""
+        """P(par, qb) = bf16(2^(c S)) and LS(qb) = fp32 sum of the unrounded values: list of (asm, reads, writes,
+        trans)"""
         T = lambda r: T0 + (r % 4)
 
         def mul(p):
-            if self.base2:
-                return []
             return [(f'v_mul_f32_e32 v{T(r)}, %[c], v{S(par, qb, r)}', [v(S(par, qb, r))], [v(T(r))], False)
                     for r in (2 * p, 2 * p + 1)]
 
         def exp(p):
-            if self.base2:
-                return [(f'v_exp_f32_e32 v{T(r)}, v{S(par, qb, r)}', [v(S(par, qb, r))], [v(T(r))], True)
-                        for r in (2 * p, 2 * p + 1)]
             return [(f'v_exp_f32_e32 v{T(r)}, v{T(r)}', [v(T(r))], [v(T(r))], True) for r in (2 * p, 2 * p + 1)]
 
         def tail(p):
@@ -345,8 +335,7 @@ class Kernel:
             return out
 
         # pair p: c*S, 2^(c*S) one pair ahead of its cvt and adds (no transcendental result is read by the next
-        # instruction); a pair's T registers are rewritten only after its tail has read them (exp(p + 1) writes the
-        # registers of pair p - 1, after tail(p - 1))
+        # instruction); a pair's T registers are rewritten only after its tail has read them
         ops = mul(0)
         for p in range(8):
             ops += exp(p)
@@ -512,8 +501,8 @@ class Kernel:
 
     def rescale_block(self, par):
         """entered after the MFMAs of the iteration (20 wait states before S or the accumulators are touched): the
-        running max moves up by d = max(block max, 0) >= 0; O and l scale by 2^(-c d) (2^(-d) in the base-2 form);
-        S(j), S(j+1) (accumulated onto the old -m) and -m shift by -d; P(j) and its row sums are recomputed"""
+        running max moves up by d = max(block max, 0) >= 0; O and l scale by 2^(-c d); S(j), S(j+1) (accumulated onto
+        the old -m) and -m shift by -d; P(j) and its row sums are recomputed"""
         npar = par ^ 1
         e = Emitter()
         e.label(f'.Lrescale{par}_%=')
@@ -522,11 +511,8 @@ class Kernel:
         for qb in range(2):
             self.row_max(e, par, qb, d, alpha)
             e.valu(f'v_max_f32_e32 v{d}, 0, v{d}', [v(d)], [v(d)])
-            if self.base2:
-                e.valu(f'v_exp_f32_e64 v{alpha}, -v{d}', [v(d)], [v(alpha)], trans=True)
-            else:
-                e.valu(f'v_mul_f32_e32 v{alpha}, %[c], v{d}', [v(d)], [v(alpha)])
-                e.valu(f'v_exp_f32_e64 v{alpha}, -v{alpha}', [v(alpha)], [v(alpha)], trans=True)
+            e.valu(f'v_mul_f32_e32 v{alpha}, %[c], v{d}', [v(d)], [v(alpha)])
+            e.valu(f'v_exp_f32_e64 v{alpha}, -v{alpha}', [v(alpha)], [v(alpha)], trans=True)
             e.valu(f'v_add_f32_e32 v{M0 + qb}, v{M0 + qb}, v{d}', [v(M0 + qb), v(d)], [v(M0 + qb)])
             for r in range(16):
                 for reg in (S(par, qb, r), S(npar, qb, r), MCV(qb) + r):
@@ -788,13 +774,10 @@ class Kernel:
         return lines
 
 
-def asm_body(lines):
-    return '\n'.join(f'  "{l}\\n\\t"' if not l.endswith(':') else f'  "{l}\\n"' for l in lines)
-
-
 def render(ring):
-    body = asm_body(Kernel(ring).generate())
-    body2 = asm_body(Kernel(ring, base2=True).generate())
+    k = Kernel(ring)
+    lines = k.generate()
+    body = '\n'.join(f'  "{l}\\n\\t"' if not l.endswith(':') else f'  "{l}\\n"' for l in lines)
     clob = ', '.join(f'"v{i}"' for i in range(FIRST_FIXED, 256)) + ', ' + ', '.join(f'"a{i}"' for i in range(192))
     clob += ', ' + ', '.join(f'"s{i}"' for i in range(64, LAST_SGPR + 1)) + ', "vcc", "scc", "memory"'
     qload = ' \\\n  '.join(f'"{l}\\n\\t"' for l in Kernel.q_prefetch())
@@ -814,9 +797,6 @@ def render(ring):
 #define ONEREEL_RING64 {ring}
 #define ONEREEL_RING64_ASM \\
 {body.replace(chr(10), " " + chr(92) + chr(10))}
-// the same loop for queries pre-multiplied by c = scale * log2(e): P = 2^S, no multiply per score (%[c] unused)
-#define ONEREEL_RING64_ASM_BASE2 \\
-{body2.replace(chr(10), " " + chr(92) + chr(10))}
 #define ONEREEL_RING64_CLOBBERS {clob}
 // an item's queries into the key loop's registers a128..a191 (query block qb, k-step k at a[128 + 32 qb + 4 k : +3]):
 // loaded from the lane's two rows (%[qa0], %[qa1]), or written from four dwords x[0..3] per (qb, k) (qb and k

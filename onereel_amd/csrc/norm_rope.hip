@@ -7,8 +7,7 @@
 // (cos[..., 0::2], sin[..., 1::2]):
 //   out[2i] = y[2i] c - y[2i+1] s,   out[2i+1] = y[2i] s + y[2i+1] c,
 // cast to bf16 (type_as(x)). Here the whole chain is fp32 with one rounding at the end, as the compiled graph computes
-// it; the bf16 input is read once and the bf16 output written once. With q_scale the query outputs are multiplied by
-// it before that rounding (scale * log2(e): queries for the attention kernel's base-2 key loop).
+// it; the bf16 input is read once and the bf16 output written once.
 //
 // HBM-bound: 2 * C * 2 bytes per row and tensor, plus the row's cos / sin entries (2 * D * 4 bytes, shared by its
 // heads). One wavefront per row: each lane holds C / 512 16-byte chunks, the sum of squares is reduced across the
@@ -37,7 +36,6 @@ struct NormRopeArgs {
   int64_t n_rows, n_rope_rows;
   int C, D;
   float eps;
-  float mul[2];                  // q / k outputs times mul before their rounding (1: as computed)
 };
 
 // One row's inputs: its bf16 words, and this lane's cos / sin entries (d0 = 8 lane mod D, pairs 2p, 2p + 1).
@@ -75,7 +73,6 @@ __device__ __forceinline__ void norm_rope_row(const NormRopeArgs& g, int which, 
     }
   }
   const float inv = 1.0f / sqrtf(wave_sum(ss) / (float)g.C + g.eps);
-  const float m = g.mul[which];
   uint16_t* op = g.out[which] + r * g.out_stride[which];
 #pragma unroll
   for (int i = 0; i < NCH; ++i) {
@@ -87,7 +84,7 @@ __device__ __forceinline__ void norm_rope_row(const NormRopeArgs& g, int which, 
 #pragma clang fp contract(off)
       const float y0 = bf2f((uint16_t)(in.x[i][p] & 0xffffu)) * inv * bf2f((uint16_t)(wv[p] & 0xffffu));
       const float y1 = bf2f((uint16_t)(in.x[i][p] >> 16)) * inv * bf2f((uint16_t)(wv[p] >> 16));
-      o[p] = pack2((y0 * in.c[p] - y1 * in.s[p]) * m, (y0 * in.s[p] + y1 * in.c[p]) * m);
+      o[p] = pack2(y0 * in.c[p] - y1 * in.s[p], y0 * in.s[p] + y1 * in.c[p]);
     }
     __builtin_nontemporal_store(o, (u32x4*)(op + e));
   }
@@ -119,7 +116,7 @@ extern "C" int or_rmsnorm_rope(const void* q, const void* k, const void* wq, con
                                int64_t k_row_stride, int64_t n_rows, int32_t C, int32_t D, float eps,
                                const float* cos_table, const float* sin_table, const int32_t* rope_row,
                                int64_t n_rope_rows, void* q_out, void* k_out, int64_t qo_row_stride,
-                               int64_t ko_row_stride, float q_scale, void* stream) {
+                               int64_t ko_row_stride, void* stream) {
   if (n_rows < 0) return fail_arg("or_rmsnorm_rope: n_rows < 0");
   if (D < 8 || D % 8 || 512 % D || C % 512 || C < 512 || C > 64 * 8 * kMaxChunks)
     return fail_arg("or_rmsnorm_rope: need D a multiple of 8 dividing 512 and C a multiple of 512 up to %d "
@@ -130,7 +127,6 @@ extern "C" int or_rmsnorm_rope(const void* q, const void* k, const void* wq, con
     return fail_arg("or_rmsnorm_rope: n_rope_rows > 0 needs the cos / sin tables");
   if (n_rope_rows < 0) return fail_arg("or_rmsnorm_rope: n_rope_rows < 0");
   if (k && (!wk || !k_out)) return fail_arg("or_rmsnorm_rope: k needs wk and k_out");
-  if (!(fabsf(q_scale) < __builtin_inff())) return fail_arg("or_rmsnorm_rope: q_scale must be finite");
   if (q_row_stride < C || qo_row_stride < C || (k && (k_row_stride < C || ko_row_stride < C)))
     return fail_arg("or_rmsnorm_rope: row strides must cover C elements");
   const uintptr_t al = (uintptr_t)q | (uintptr_t)wq | (uintptr_t)q_out | (uintptr_t)(k ? k : q) |
@@ -156,8 +152,6 @@ extern "C" int or_rmsnorm_rope(const void* q, const void* k, const void* wq, con
   g.C = C;
   g.D = D;
   g.eps = eps;
-  g.mul[0] = q_scale != 0.0f ? q_scale : 1.0f;
-  g.mul[1] = 1.0f;
   int64_t blocks = (n_rows + kWaves - 1) / kWaves;
   if (blocks > 256 * 8) blocks = 256 * 8;
   const dim3 grid((unsigned)blocks, k ? 2 : 1);

@@ -20,7 +20,7 @@ from . import _lib as L
 from .frame_memory import FrameMemory
 from .layout import SceneLayout
 from .memory import BoundaryMemory, MemoryAttention, frame_plan
-from .scene import ScopePlan, base2_scale, rotate_queries, scene_attention
+from .scene import ScopePlan, rotate_queries, scene_attention
 
 
 @dataclass
@@ -139,16 +139,15 @@ def memory_attention(ctx: Context) -> MemoryAttention:
     return ctx._mem
 
 
-def rotate_tokens(ctx: Context, x: torch.Tensor, cos, sin, q_scale=None) -> torch.Tensor:
+def rotate_tokens(ctx: Context, x: torch.Tensor, cos, sin) -> torch.Tensor:
     """x [F*T, H, D] rotated at every video token's rotary row (its scene row with scene_rope), in token order: the
-    q / k RoPE of Processor.__call__ (hunyuan15.py:183-191) as one or_rotate_rows launch (q_scale: the rotated
-    elements multiplied by it before their rounding to bf16, as scene.rotate_queries)"""
+    q / k RoPE of Processor.__call__ (hunyuan15.py:183-191) as one or_rotate_rows launch"""
     lay = ctx.layout
     key = ('tokens', tuple(lay.lengths), ctx.T, ctx.scene_rope, tuple(ctx.rope_lengths or ()), str(x.device))
     if key not in ctx._cache:
         ctx._cache[key] = ScopePlan(SceneLayout(list(lay.lengths), halo=0), ctx.T, None, 0, ctx.scene_rope,
                                     ctx.rope_lengths, False, False, x.device)
-    return rotate_queries(ctx._cache[key], x, cos, sin, q_scale=q_scale)
+    return rotate_queries(ctx._cache[key], x, cos, sin)
 
 
 class Processor:
@@ -172,12 +171,8 @@ class Processor:
             ek = attn.norm_added_k(ek)
         eq, ek, ev = (x[0].to(torch.bfloat16) for x in (eq, ek, ev))
         if ctx.memory:
-            # the video queries leave the rotation multiplied by scale * log2(e) (head_dim 128): the attention kernel
-            # then takes their scores as base-2 exponents
-            base2 = q.shape[-1] == 128
-            q = rotate_tokens(ctx, q, cos, sin, q_scale=base2_scale(q.shape[-1]) if base2 else None)
-            k = rotate_tokens(ctx, k, cos, sin)
-            hs, ehs = self.memory(q, k, v, eq, ek, ev, q_scaled=base2)
+            q, k = rotate_tokens(ctx, q, cos, sin), rotate_tokens(ctx, k, cos, sin)
+            hs, ehs = self.memory(q, k, v, eq, ek, ev)
         else:
             hs, ehs = self.scene_raw(q, k, v, eq, ek, ev, cos, sin)
         hs = attn.to_out[1](attn.to_out[0](hs.flatten(1, 2)[None].to(hidden_states.dtype)))
@@ -200,12 +195,11 @@ class Processor:
         cos, sin = ctx._rot_full if adjacent else (None, None)
         return scene_attention(plan, q, k, v, eq, ek, ev, cos, sin, mode='rotated', fused=ctx.fused)
 
-    def memory(self, q, k, v, eq, ek, ev, q_scaled=False):
+    def memory(self, q, k, v, eq, ek, ev):
         """the bounded cross-scene memory on one GPU (hunyuan15.py:305-334, world 1): q / k already rotated. Every
         scene's video queries read its frames, its sentence and M representatives per head of the other scenes'
         boundary keys; its sentence queries read its frames and its sentence. Returns (video out, text out); text
-        rows past the valid tokens are zero. q_scaled: q holds the rotated queries times base2_scale(D) (head_dim
-        128), the text queries eq as they are."""
+        rows past the valid tokens are zero."""
         ctx, T, lay = self.ctx, self.ctx.T, self.ctx.layout
         mem = memory_attention(ctx)
         Sq = q.shape[0]
@@ -216,6 +210,5 @@ class Processor:
             pieces = [(j, lo * T, hi * T) for j, (lo, hi) in enumerate(lay.ranges)]
             mem.plans[pk] = frame_plan(lay, T, torch.arange(Sq), k.shape[0], pieces, ctx.text_ranges(),
                                        set(range(lay.n_scenes)), Sq, q.device)
-        out = mem((self.layer, ctx.cond()), torch.cat([q, eq]), torch.cat([k, ek]), torch.cat([v, ev]), mem.plans[pk],
-                  q_scaled_rows=Sq if q_scaled else 0)
+        out = mem((self.layer, ctx.cond()), torch.cat([q, eq]), torch.cat([k, ek]), torch.cat([v, ev]), mem.plans[pk])
         return out[:Sq], out[Sq:]

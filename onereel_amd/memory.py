@@ -220,7 +220,6 @@ class _Static:
             for c in qlen:
                 cu.append(cu[-1] + c)
         self.cu_q, self.sum_q = t32(cu), cu[-1]
-        self.first = first
         if self.in_place:
             self.seg_q_src = t32([first[i] * H + h for h in range(H) for i in range(n)])
             self.first_q = t32(first)
@@ -351,11 +350,8 @@ class MemoryAttention:
             self._static[key] = hit
         return hit[1]
 
-    def __call__(self, key, q, k, v, p: Plan, q_scaled_rows: int = 0) -> torch.Tensor:
-        """q [Sq, H, D], k / v [L, H, D] bf16 on the GPU -> [Sq, H, D] (rows outside the plan's queries are zero).
-        q_scaled_rows = n > 0 (head_dim 128, a plan whose pieces are ranges of q, none across row n): q's first n rows
-        hold the queries times scale * log2(e) (scene.base2_scale), whose pieces then run the attention kernel's
-        base-2 key loop; the other rows are plain queries."""
+    def __call__(self, key, q, k, v, p: Plan) -> torch.Tensor:
+        """q [Sq, H, D], k / v [L, H, D] bf16 on the GPU -> [Sq, H, D] (rows outside the plan's queries are zero)"""
         Sq, H, D = q.shape
         Lk = k.shape[0]
         if k.shape[1:] != (H, D) or v.shape != k.shape:
@@ -370,16 +366,10 @@ class MemoryAttention:
                                   f'takes at most 4096')
         if st.max_key_row >= Lk:
             raise L.HipValueError(f'the plan reads key row {st.max_key_row}, the key buffer has {Lk} rows')
-        n_ps = int(q_scaled_rows)
-        if n_ps:
-            if D != 128 or not st.in_place or n_ps > Sq:
-                raise L.HipValueError('q_scaled_rows needs head_dim 128 and a plan whose pieces are ranges of q')
-            if any(f < n_ps < f + c for f, c in zip(st.first, st.qlen)):
-                raise L.HipValueError(f'a piece of the plan crosses row {n_ps} (q_scaled_rows)')
         rep, valid = self.memory._select(key, k, st.cand32, st.B, H, D)
         M = rep.shape[1]
         if st.in_place and not self.head_major:
-            return self._multi_head(st, q, k, v, rep, valid, M, n_ps)
+            return self._multi_head(st, q, k, v, rep, valid, M)
         k_off, kidx = st.slots(M)
         k_len = torch.empty(st.n * H, dtype=torch.int32, device=dev)
         L.check(L.lib().or_memory_index(rep.data_ptr(), valid.data_ptr(), st.cand64.data_ptr(), st.owner64.data_ptr(),
@@ -392,11 +382,8 @@ class MemoryAttention:
         if st.in_place:
             out = torch.empty_like(q) if st.covers_all else torch.zeros_like(q)
             qv, ov = q.view(Sq * H, 1, D), out.view(Sq * H, 1, D)
-            # with q_scaled_rows the plain rows are read as the text rows past n_q_video (the same rows of q)
-            nv = n_ps * H if n_ps else Sq * H
             varlen(qv, kp, vp, st.cu_q, None, st.max_q, max_k, k_off=k_off, k_len=k_len, out=ov,
-                   seg_q_src=st.seg_q_src, q_text=qv[nv:], o_text=ov[nv:], n_q_video=nv, sum_q=st.sum_q,
-                   q_row_step=H, q_prescaled=n_ps > 0)
+                   seg_q_src=st.seg_q_src, n_q_video=Sq * H, sum_q=st.sum_q, q_row_step=H)
             return out
         qp = gather_rows(q.view(Sq * H, 1, D), st.qidx, check=False)
         o = varlen(qp, kp, vp, st.cu_q, None, st.max_q, max_k, k_off=k_off, k_len=k_len)
@@ -404,7 +391,7 @@ class MemoryAttention:
         scatter_rows(o, st.qidx, out.view(Sq * H, 1, D), check=False)
         return out
 
-    def _multi_head(self, st: _Static, q, k, v, rep, valid, M: int, n_ps: int = 0) -> torch.Tensor:
+    def _multi_head(self, st: _Static, q, k, v, rep, valid, M: int) -> torch.Tensor:
         """every piece one multi-head segment: its local keys (the leading run of token rows, whole key blocks of it,
         read in place from k / v, the rest packed as whole rows) then, per head, that head's representatives of the
         other scenes in its own head slot"""
@@ -429,9 +416,7 @@ class MemoryAttention:
             pack_job(k, v, mh['src'], mh['dst'], kp, vp)
         pack_job(k.view(Lk * H, 1, D), v.view(Lk * H, 1, D), fsrc, fdst, kp.view(R * H, 1, D), vp.view(R * H, 1, D))
         out = torch.empty_like(q) if st.covers_all else torch.zeros_like(q)
-        nv = n_ps if n_ps else Sq
         varlen(q, kp, vp, st.cu_piece, None, st.max_q, mh['max_k'], k_off=mh['k_off'], k_len=mh['k_len'], out=out,
-               seg_q_src=st.first_q, q_text=q[nv:], o_text=out[nv:], n_q_video=nv, sum_q=sum(st.qlen), v_tok=v,
-               v_lead=mh['lead'], v_row=mh['v_row'], k_tok=k, k_lead=mh['lead'], k_len_head=k_len_head,
-               q_prescaled=n_ps > 0)
+               seg_q_src=st.first_q, n_q_video=Sq, sum_q=sum(st.qlen), v_tok=v, v_lead=mh['lead'],
+               v_row=mh['v_row'], k_tok=k, k_lead=mh['lead'], k_len_head=k_len_head)
         return out

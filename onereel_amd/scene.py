@@ -282,7 +282,7 @@ def scatter_rows(packed: torch.Tensor, idx: torch.Tensor, out: torch.Tensor, che
 def varlen(q, k, v, cu_q, cu_k, max_q, max_k, *, k_off=None, k_len=None, out=None, lse=None, seg_q_src=None,
            q_text=None, o_text=None, n_q_video=None, q_rope=None, cos=None, sin=None, sum_q=None, workspace=None,
            scale=None, noalloc=False, q_row_step=1, v_tok=None, v_lead=None, v_row=None, k_len_head=None,
-           k_tok=None, k_lead=None, v_runs=None, q_prescaled=False):
+           k_tok=None, k_lead=None, v_runs=None):
     """or_varlen_fwd on torch tensors. Returns out (allocated [Nq, H, D] when not given). noalloc=True calls
     or_varlen_fwd_noalloc instead: no workspace, the library's fixed per-GPU array (calls must not overlap on a GPU).
     q_row_step > 1 (with seg_q_src): query i of segment s is row seg_q_src[s] + i * q_row_step of q and of out.
@@ -290,9 +290,7 @@ def varlen(q, k, v, cu_q, cu_k, max_q, max_k, *, k_off=None, k_len=None, out=Non
     of k), the others rows k_off[s] + v_lead[s].. of v; k_tok with k_lead (and v_row) likewise for the keys.
     v_runs [n_seg * VALUE_RUNS * 3] (with v_tok, head_dim 128): further runs of each segment's values in v_tok, entry
     (key offset, key count, token row), whose whole key blocks are read in place.
-    k_len_head [n_seg * H] (with k_len): head h of segment s attends to its first k_len_head[s * H + h] keys.
-    q_prescaled (head_dim 128, no q_rope): the rows of q (not q_text) hold base2_scale(D, scale) * q rounded once to
-    bf16 (pack_layer's q_scale); their scores are then base-2 exponents and the kernel skips its multiply per score."""
+    k_len_head [n_seg * H] (with k_len): head h of segment s attends to its first k_len_head[s * H + h] keys."""
     H, D = k.shape[1], k.shape[2]
     _check_bf16(q, k, v, q_text, out, o_text)
     _, qs = _rows2d(q, H, D)
@@ -318,8 +316,6 @@ def varlen(q, k, v, cu_q, cu_k, max_q, max_k, *, k_off=None, k_len=None, out=Non
             raise L.HipValueError('v_runs needs v_tok and head_dim 128 (and no k_len_head)')
         if v_runs.numel() != n_seg_of(cu_q) * L.VALUE_RUNS * 3:
             raise L.HipValueError(f'v_runs needs {L.VALUE_RUNS} (offset, count, row) entries per segment')
-    if q_prescaled and (D != 128 or q_rope is not None):
-        raise L.HipValueError('q_prescaled needs head_dim 128 (and no q_rope)')
     if k_tok is not None:
         _check_bf16(k_tok)
         if k_lead is None or v_row is None:
@@ -352,7 +348,6 @@ def varlen(q, k, v, cu_q, cu_k, max_q, max_k, *, k_off=None, k_len=None, out=Non
     a.n_seg, a.sum_q, a.max_q, a.max_k, a.H, a.D = int(n_seg), int(sum_q), int(max_q), int(max_k), H, D
     a.scale = float(D ** -0.5 if scale is None else scale)
     a.q_row_step = int(q_row_step)
-    a.q_prescaled = 1 if q_prescaled else 0
     if v_tok is not None:
         a.v_tok, a.v_lead, a.v_row, a.v_tok_rows = v_tok.data_ptr(), v_lead.data_ptr(), v_row.data_ptr(), v_tok.shape[0]
     a.v_runs = L.ptr(v_runs)
@@ -395,11 +390,9 @@ def zero_text_padding(plan: ScopePlan, ot: torch.Tensor):
     return ot
 
 
-def rotate_queries(plan: ScopePlan, q, cos, sin, out=None, q_scale=None):
+def rotate_queries(plan: ScopePlan, q, cos, sin, out=None):
     """every video query row rotated at its scene-RoPE table row, in token order (or_rotate_rows over the plan's
-    packed queries; text rows are not rotated and stay in the text tensor): [F*T, H, D] bf16. With q_scale, each
-    rotated element multiplied by it in fp32 before its rounding to bf16 (or_pack_layer's query job alone), for
-    varlen(..., q_prescaled=True) with q_scale = base2_scale(D)."""
+    packed queries; text rows are not rotated and stay in the text tensor): [F*T, H, D] bf16"""
     H, D = q.shape[1], q.shape[2]
     _check_bf16(q, out)
     _, qs = _rows2d(q, H, D)
@@ -412,33 +405,18 @@ def rotate_queries(plan: ScopePlan, q, cos, sin, out=None, q_scale=None):
     _, os_ = _rows2d(out, H, D)
     if out.shape[0] < plan.n_video:
         raise L.HipValueError(f'out holds {out.shape[0]} rows, the layout has {plan.n_video} video rows')
-    if q_scale is None:
-        L.check(L.lib().or_rotate_rows(q.data_ptr(), qs, plan.n_video, plan.q_src.data_ptr(), plan.q_rope.data_ptr(),
-                                       cos.data_ptr(), sin.data_ptr(), n_rows, plan.sum_q, H, D, out.data_ptr(), os_,
-                                       L.stream_handle(q.device)), 'or_rotate_rows')
-        return out
-    a = L.PackArgs()
-    a.n_video = plan.n_video
-    a.q, a.q_row_stride, a.q_src, a.q_rope = q.data_ptr(), qs, plan.q_src.data_ptr(), plan.q_rope.data_ptr()
-    a.n_queries, a.q_out, a.q_out_row_stride = plan.sum_q, out.data_ptr(), os_
-    a.cos_table, a.sin_table, a.n_rope_rows = cos.data_ptr(), sin.data_ptr(), n_rows
-    a.H, a.D, a.q_scale = H, D, float(q_scale)
-    L.check(L.lib().or_pack_layer(ctypes.byref(a), L.stream_handle(q.device)), 'or_pack_layer')
+    L.check(L.lib().or_rotate_rows(q.data_ptr(), qs, plan.n_video, plan.q_src.data_ptr(), plan.q_rope.data_ptr(),
+                                   cos.data_ptr(), sin.data_ptr(), n_rows, plan.sum_q, H, D, out.data_ptr(), os_,
+                                   L.stream_handle(q.device)), 'or_rotate_rows')
     return out
 
 
-def base2_scale(D, scale=None):
-    """the factor q_prescaled queries carry: scale * log2(e) in fp32, scale = D^-0.5 by default (the kernel's c)"""
-    f32 = lambda x: ctypes.c_float(x).value
-    return f32(f32(D ** -0.5 if scale is None else scale) * f32(1.4426950408889634))
-
-
 def pack_layer(plan: ScopePlan, k, ek, v, ev, cos=None, sin=None, mode='raw', kbuf=None, vbuf=None, q=None,
-               qbuf=None, values_in_place=True, q_scale=None):
+               qbuf=None, values_in_place=True):
     """One launch of or_pack_layer: the plan's packed keys (rotated per `mode`, as pack_rows) into kbuf, the values
     into vbuf (only the rows the attention call does not read in place when values_in_place: plan.v_src), and, when q
-    is given, the video queries rotated once in token order into qbuf (as rotate_queries; with q_scale, each rotated
-    element multiplied by it in fp32 before its rounding to bf16). Returns (kbuf, vbuf, qbuf)."""
+    is given, the video queries rotated once in token order into qbuf (as rotate_queries). Returns (kbuf, vbuf,
+    qbuf)."""
     H, D = k.shape[1], k.shape[2]
     _check_bf16(k, ek, v, ev, q, kbuf, vbuf, qbuf)
     _, vs = _rows2d(k, H, D)
@@ -485,7 +463,6 @@ def pack_layer(plan: ScopePlan, k, ek, v, ev, cos=None, sin=None, mode='raw', kb
         a.n_queries, a.q_out, a.q_out_row_stride = plan.sum_q, qbuf.data_ptr(), qos
     a.cos_table, a.sin_table, a.n_rope_rows = L.ptr(cos), L.ptr(sin), n_rows
     a.H, a.D = H, D
-    a.q_scale = 0.0 if q_scale is None else float(q_scale)
     L.check(L.lib().or_pack_layer(ctypes.byref(a), L.stream_handle(k.device)), 'or_pack_layer')
     return kbuf, vbuf, qbuf
 
@@ -495,8 +472,7 @@ def scene_attention(plan: ScopePlan, q, k, v, eq, ek, ev, cos=None, sin=None, mo
     """(ov, ot) of one scene-attention layer. q / k / v [F*T, H, D] and eq / ek / ev [Le, H, D] bf16 on the GPU.
 
     fused=True: one pack launch (K rows, the V rows not read in place, and the video queries rotated once when
-    mode is 'raw' and rotate_q='pre', into qbuf when given; at head_dim 128 multiplied by base2_scale(D) on the way,
-    so that the attention kernel takes their scores as base-2 exponents), then the attention call with Q read in place, the
+    mode is 'raw' and rotate_q='pre', into qbuf when given), then the attention call with Q read in place, the
     own-frame values and the shared frames' values (value runs, head_dim 128) read in place from v (values_in_place,
     when v's rows are H * D elements apart, as the packed rows are) and the outputs written in place. rotate_q='load' rotates the queries on the attention kernel's Q load instead.
     fused=False: the reference's data flow (Q, K, V packed, one varlen call on packed tensors, write-back by the
@@ -525,14 +501,13 @@ def scene_attention(plan: ScopePlan, q, k, v, eq, ek, ev, cos=None, sin=None, mo
         # head_dim such a plan packs every value
         in_place = (bool(values_in_place) and v.dim() == 3 and v.stride(0) == H * D and v.is_contiguous()
                     and (plan.v_runs is None or D == 128))
-        base2 = pre and D == 128
         kp, vp, qr = pack_layer(plan, k, ek, v, ev, cos, sin, mode, kbuf, vbuf, q=q if pre else None, qbuf=qbuf,
-                                values_in_place=in_place, q_scale=base2_scale(D) if base2 else None)
+                                values_in_place=in_place)
         vi = dict(v_tok=v, v_lead=plan.v_lead, v_row=plan.v_row, v_runs=plan.v_runs) if in_place else {}
         varlen(qr if pre else q, kp, vp, plan.cu_q, plan.cu_k, plan.max_q, plan.max_k, k_off=plan.k_off,
                k_len=plan.k_len, out=ov, seg_q_src=plan.seg_q_src, q_text=eq, o_text=ot, n_q_video=plan.n_video,
                q_rope=plan.q_rope if on_load else None, cos=cos, sin=sin, sum_q=plan.sum_q,
-               workspace=plan.workspace(H, D), q_prescaled=base2, **vi)
+               workspace=plan.workspace(H, D), **vi)
         if ot is not None:
             zero_text_padding(plan, ot)
     else:

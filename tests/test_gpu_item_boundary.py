@@ -170,64 +170,3 @@ def test_many_items_with_value_runs(monkeypatch):
     o = scene.varlen(q.to(DEV), k.to(DEV), vp.to(DEV), t32(cq), t32(ck), max(lq), max(lk), v_tok=vtok.to(DEV),
                      v_lead=t32(lead), v_row=t32(rows), v_runs=t32(tab.reshape(-1)))
     assert_close(o.cpu(), OA.packed_attention(q, k, v, cq, ck), what='O, value runs')
-
-
-@pytest.mark.parametrize('blocks,few', [(1, False), (4, False), (4, True)])
-def test_many_items_base2_and_plain_queries(monkeypatch, blocks, few):
-    """q_prescaled: the segments whose queries are rows of q (pre-multiplied by c = D^-0.5 log2 e, rounded once) run
-    the base-2 key loop, those whose queries are rows of q_text the loop that multiplies each score by c. Segments of
-    the two kinds interleaved on 1 or 4 work-groups (each item's key loop loading the next item's queries, of either
-    kind, at its exit), and with few long segments the key-split parts of both kinds merged by their lse. O and lse of
-    every row against the fp32 oracle on the queries as passed (the base-2 scores 2^(c q k) = e^(c q k ln 2)), O also
-    against the oracle on the unscaled queries"""
-    monkeypatch.setenv('ONEREEL_ATTN_MAX_BLOCKS', str(blocks))
-    H, D = 8 if not few else 2, 128
-    if few:
-        lq, lk = [300, 40, 260], [5000, 3000, 4000]      # 10 items on 4 work-groups: the last 2 split by keys
-    else:
-        lq, lk = _many_items(41 + blocks)
-    rng = np.random.default_rng(61 + blocks)
-    video = rng.integers(0, 2, len(lq)).astype(bool)
-    video[0], video[1] = True, False
-    q_raw = rand_bf16((sum(lq), H, D), 600)
-    k = rand_bf16((sum(lk), H, D), 601)
-    v = rand_bf16((sum(lk), H, D), 602)
-    cq, ck = np.cumsum([0] + lq), np.cumsum([0] + lk)
-    c = scene.base2_scale(D)
-    # video segments' queries in q (multiplied by c), text segments' in q_text, each in segment order
-    vid = [s for s in range(len(lq)) if video[s]]
-    txt = [s for s in range(len(lq)) if not video[s]]
-    qv = torch.cat([q_raw[cq[s]:cq[s + 1]] for s in vid]).float().mul(c).to(torch.bfloat16)
-    qt = torch.cat([q_raw[cq[s]:cq[s + 1]] for s in txt])
-    nv = qv.shape[0]
-    offs, a, b = [], 0, 0
-    for s in range(len(lq)):
-        if video[s]:
-            offs.append(a)
-            a += lq[s]
-        else:
-            offs.append(nv + b)
-            b += lq[s]
-    print(f'item boundaries, base-2 and plain loops: {blocks} work-groups, lq={lq}, lk={lk}, '
-          f'video={video.astype(int).tolist()}', flush=True)
-    t32 = lambda x: torch.tensor(np.asarray(x), dtype=torch.int32, device=DEV)
-    ov = torch.empty(nv, H, D, dtype=torch.bfloat16, device=DEV)
-    ot = torch.empty(qt.shape[0], H, D, dtype=torch.bfloat16, device=DEV)
-    lse = torch.empty(H, sum(lq), dtype=torch.float32, device=DEV)
-    ws = torch.zeros(int(L.lib().or_varlen_workspace_size(len(lq), sum(lq), H, D)), dtype=torch.uint8, device=DEV)
-    scene.varlen(qv.to(DEV), k.to(DEV), v.to(DEV), t32(cq), t32(ck), max(lq), max(lk), out=ov, lse=lse,
-                 seg_q_src=t32(offs), q_text=qt.to(DEV), o_text=ot, n_q_video=nv, sum_q=sum(lq), workspace=ws,
-                 q_prescaled=True)
-    assert (int(ws.view(torch.int32)[3]) > 0) == few
-    # packed order: segment s's rows of the outputs, and its queries as the kernel saw them (fp32)
-    o = torch.cat([(ov if video[s] else ot)[offs[s] - (0 if video[s] else nv):][:lq[s]].cpu() for s in
-                   range(len(lq))]).float()
-    ln2_sqrt_d = float(np.log(2.0)) * D ** 0.5
-    q_seen = torch.cat([qv[offs[s]:offs[s] + lq[s]].float() * ln2_sqrt_d if video[s] else
-                        qt[offs[s] - nv:offs[s] - nv + lq[s]].float() for s in range(len(lq))])
-    assert_close(o, OA.packed_attention(q_seen, k, v, cq, ck), what='O, base-2 and plain items')
-    assert_close(o, OA.packed_attention(q_raw, k, v, cq, ck), what='O vs the unscaled queries')
-    lref = _lse_ref(q_seen, k, cq, ck, D)
-    fin = torch.isfinite(lref)
-    assert torch.equal(torch.isfinite(lse.cpu()), fin)
-    assert (lse.cpu()[fin] - lref[fin]).abs().max() < 2e-3

@@ -13,10 +13,8 @@ import pytest
 import torch
 
 from helpers import assert_close
-from onereel_amd import _lib as L
 from onereel_amd.layout import SceneLayout
 from onereel_amd.memory import BoundaryMemory, MemoryAttention, candidates, frame_plan, make_plan
-from onereel_amd.scene import base2_scale
 from oracle import memory as OM
 
 pytestmark = [pytest.mark.gpu, pytest.mark.skipif(not torch.cuda.is_available(), reason='needs the GPU')]
@@ -305,7 +303,6 @@ def test_wan_self_attention_routes_the_bounded_memory():
     lay = SceneLayout([3, 4, 2], halo=0)
     S = lay.n_frames * T
     ctx = W.Context(lay, T=T, memory=M)
-    ctx2 = W.Context(lay, T=T, memory=M)       # the same calls with pre-multiplied queries (its own memory state)
     twin = BoundaryMemory(M)
     cand, owner = candidates(lay, T, 'cpu')
     empty = torch.zeros(0, H, D, dtype=torch.bfloat16)
@@ -318,10 +315,6 @@ def test_wan_self_attention_routes_the_bounded_memory():
         rv, _ = OM.masked_reference(q, k, v, empty, empty, empty, lay.ranges, T, cand[rep], owner[rep], valid,
                                     [(0, 0)] * 3)
         assert_close(o, rv, what=f'wan memory call {call}')
-        # as the processor runs it: the queries multiplied by D^-0.5 log2 e (the base-2 key loop)
-        qs = (q.float() * base2_scale(D)).to(torch.bfloat16)
-        o2 = W.memory_self(ctx2, qs.to(DEV), k.to(DEV), v.to(DEV), 4, q_prescaled=True).cpu()
-        assert_close(o2, rv, what=f'wan memory call {call}, pre-multiplied queries')
 
 
 def test_select_matches_oracle_at_480p_shape():
@@ -389,39 +382,3 @@ def test_multi_head_and_single_head_forms_agree(lengths, T, H, D, M):
         a = mh(('l', True), q, k, v, plan)
         b = sh(('l', True), q, k, v, plan)
         assert torch.equal(a, b), (call, (a.float() - b.float()).abs().max().item())
-
-
-@pytest.mark.parametrize('lengths,T,H,M', [([6, 1, 3], 16, 4, 5), ([8] * 4, 1590, 16, 128)])
-def test_memory_attention_prescaled_video_queries(lengths, T, H, M):
-    """q_scaled_rows: the video queries multiplied by c = D^-0.5 log2 e before their rounding run the attention
-    kernel's base-2 key loop, the sentence queries (the rows past them) the multiplying loop. The multi-head and the
-    single-head forms give the same bits, and both the fp32 oracle's outputs on the unscaled queries; a row count
-    that cuts a piece is refused"""
-    print(f'memory attention, pre-multiplied video queries: lengths={lengths} T={T} H={H} M={M}', flush=True)
-    D = 128
-    lay = SceneLayout(lengths, halo=0)
-    S = lay.n_frames * T
-    counts = [128] * len(lengths) if T > 100 else [5, 7, 3]
-    tr, c = [], 0
-    for x in counts:
-        tr.append((c, c + x))
-        c += x
-    plan = frame_plan(lay, T, torch.arange(S), S, [(j, lo * T, hi * T) for j, (lo, hi) in enumerate(lay.ranges)], tr,
-                      set(range(lay.n_scenes)), S, DEV)
-    mh, sh = MemoryAttention(BoundaryMemory(M)), MemoryAttention(BoundaryMemory(M), head_major=True)
-    g = torch.Generator(device=DEV).manual_seed(90)
-    q, k, v = (torch.randn(S + c, H, D, generator=g, device=DEV).to(torch.bfloat16) for _ in range(3))
-    qs = q.clone()
-    qs[:S] = (q[:S].float() * base2_scale(D)).to(torch.bfloat16)
-    a = mh(('l', True), qs, k, v, plan, q_scaled_rows=S)
-    b = sh(('l', True), qs, k, v, plan, q_scaled_rows=S)
-    assert torch.equal(a, b), (a.float() - b.float()).abs().max().item()
-    rows, owner = candidates(lay, T, 'cpu')
-    rep, valid = BoundaryMemory(M).select(('l', True), k[rows.to(DEV)])
-    ref = _piece_reference(q.cpu(), k.cpu(), v.cpu(), _frame_pieces(lay, T, S, tr), rows, owner, rep.cpu(),
-                           valid.cpu(), sample=12 if T > 100 else None)
-    out = a.cpu()
-    for i, (qr, o) in ref.items():
-        assert_close(out[qr], o, what=f'pre-multiplied video queries, piece {i}')
-    with pytest.raises(L.HipValueError, match='crosses row'):
-        mh(('l', True), qs, k, v, plan, q_scaled_rows=S - 1)

@@ -75,13 +75,6 @@ def test_processors_match_the_oracle_inside_the_model():
     qq, kk = wan._qk(q, k, blk.attn1.norm_q.weight, blk.attn1.norm_k.weight, blk.attn1.norm_q.eps, *rot, 4)
     o = wan.self_ranges(model.ctx, qq[0].contiguous(), kk[0].contiguous(), v[0].unflatten(1, (4, -1)).contiguous())
     assert_close(o.cpu(), ref_o, what='dit self-attention')
-    # as the processor runs it: the queries leave _qk multiplied by D^-0.5 log2 e, the kernel's base-2 key loop
-    from onereel_amd.scene import base2_scale
-    qs, _ = wan._qk(q, k, blk.attn1.norm_q.weight, blk.attn1.norm_k.weight, blk.attn1.norm_q.eps, *rot, 4,
-                    q_scale=base2_scale(128))
-    o2 = wan.self_ranges(model.ctx, qs[0].contiguous(), kk[0].contiguous(), v[0].unflatten(1, (4, -1)).contiguous(),
-                         q_prescaled=True)
-    assert_close(o2.cpu(), ref_o, what='dit self-attention, pre-multiplied queries')
     assert (got.float() - ref_out.float()).abs().max() < 5e-2
     ctx_text = model.text_out(torch.nn.functional.gelu(model.text_in(text), approximate='tanh'))[None]
     got = model.p_cross(blk.attn2, x, encoder_hidden_states=ctx_text)

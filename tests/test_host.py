@@ -209,24 +209,6 @@ def test_varlen_argument_errors_without_gpu():
         L.check(L.lib().or_pack_gather(1, 1, None, None, 4096, 4096, 0, 1, None, None, None, None, 0, 1, 64, 128, 1,
                                        None, None), 'or_pack_gather')
     assert L.lib().or_varlen_workspace_size(8, 51392, 16, 128) > 0
-    # pre-multiplied queries: the base-2 key loop is the head_dim 128 kernel's, and the queries must not be rotated
-    # on the load (the rotation would round them again)
-    a = L.VarlenArgs()
-    a.H, a.n_seg, a.sum_q, a.q_prescaled = 1, 1, 1, 1
-    a.q = a.k = a.v = a.o = 0x10000
-    a.cu_q = a.cu_k = 0x20000
-    for D, rope, msg in ((64, None, 'q_prescaled needs head_dim 128'), (128, 0x30000, 'no q_rope')):
-        a.D, a.q_rope, a.cos_table, a.sin_table, a.n_rope_rows = D, rope, 0x40000, 0x50000, 10
-        a.q_row_stride = a.k_row_stride = a.o_row_stride = D
-        with pytest.raises(L.HipPathError, match=msg):
-            L.check(L.lib().or_varlen_fwd(ctypes.byref(a), None), 'or_varlen_fwd')
-    p = L.PackArgs()
-    p.H, p.D, p.n_queries, p.q_scale = 16, 128, 4, float('inf')
-    p.q, p.q_src, p.q_rope, p.q_out, p.cos_table, p.sin_table, p.n_rope_rows = (0x10000, 0x20000, 0x30000, 0x40000,
-                                                                                  0x50000, 0x60000, 10)
-    p.q_row_stride = p.q_out_row_stride = 2048
-    with pytest.raises(L.HipPathError, match='q_scale must be finite'):
-        L.check(L.lib().or_pack_layer(ctypes.byref(p), None), 'or_pack_layer')
 
 
 def test_product_has_no_cpu_fallback():
