@@ -10,7 +10,9 @@
 //
 // HBM-bound: per element 4 B of o read and written and 2 B of o_s read. One thread per 8 consecutive elements of a
 // (row, head) pair, each computing the pair's weights from its two lse scalars; a second launch then writes the new
-// lse (the first reads the old one in every thread of a pair).
+// lse (the first reads the old one in every thread of a pair). Writing it from the first launch instead, one 4-byte
+// store per pair at head-major addresses, measured 0.216 against 0.187 ms at 51 392 rows x 16 heads x 128 (the
+// second launch writes the lse rows contiguously); non-temporal stores of o changed nothing.
 #include <math.h>
 
 #include "common.h"
