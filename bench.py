@@ -16,6 +16,11 @@ cpu_baseline: the oracle's packing plus torch SDPA per scope in fp32 on the host
 gemm_reference: torch.matmul (hipBLASLt) of two bf16 16384 x 16384 N(0, 1) matrices in the same run: what the
 vendor's dense bf16 GEMM reaches on this GPU with data of the same distribution. MI355X throttles its clock under
 MFMA load (power limit), and MFMA power depends on the operand bits, so this is the practical MFMA ceiling here.
+mfma_ceiling: a loop of nothing but bf16 MFMAs on N(0, 1) operands held in registers (libonereel_bench.so), one
+wavefront per SIMD on every CU, in the same run: what the matrix cores sustain under the power limit with no memory
+traffic, LDS or softmax at all; and the same loop with an exact softmax's VALU work per MFMA beside it (the
+exponential, its scale, the row sum, the bf16 conversion); attention_frac and attention_frac_of_softmax_valu are the
+attention kernel's rate over each.
 copy_reference: a device-to-device copy of the pack's size (torch copy_) with cold caches, in the same run: the
 practical ceiling of the HBM-bound pack and scatter kernels.
 
@@ -27,6 +32,7 @@ rank of a P-GPU run computes once its K/V rows are local, on this one GPU.
 from __future__ import annotations
 
 import argparse
+import ctypes
 import hashlib
 import json
 import os
@@ -145,6 +151,47 @@ def gemm_reference(n=16384, reps=5):
     torch.cuda.empty_cache()
     return dict(what=f'torch.matmul bf16 {n}x{n}x{n}, N(0,1) inputs (hipBLASLt), same run', ms=round(ms, 4),
                 tflops=round(tflops, 1), frac_bf16_peak=round(tflops / PEAK_BF16_TFLOPS, 4))
+
+
+def mfma_ceiling_call(mode=0, iters=80000):
+    """(call, FLOP per call) of or_mfma_ceiling: one work-group of four wavefronts per CU, each running `iters`
+    iterations of 8 bf16 MFMAs on N(0, 1) operands held in registers (~12-16 ms per call at the throttled clock);
+    mode 2 adds an exact softmax's VALU work per MFMA"""
+    import torch
+    from onereel_amd import _lib as L
+    blocks = torch.cuda.get_device_properties(0).multi_processor_count
+    g = torch.Generator(device='cuda').manual_seed(2)
+    ops = torch.randn(1 << 19, generator=g, device='cuda').to(torch.bfloat16)   # 65536 vectors of 8
+    out = torch.empty(blocks * 256, dtype=torch.float32, device='cuda')
+    st = torch.cuda.current_stream()
+
+    def call():
+        L.bench_check(L.bench_lib().or_mfma_ceiling(ops.data_ptr(), ops.numel() // 8, out.data_ptr(), blocks, iters,
+                                                    mode, ctypes.c_void_p(st.cuda_stream)), 'or_mfma_ceiling')
+    return call, float(blocks) * 4 * iters * 8 * 32768
+
+
+def mfma_ceiling(reps=10):
+    """TFLOP/s of the register-only MFMA loop (libonereel_bench.so) in both bf16 MFMA shapes, and in the attention
+    kernel's shape beside an exact softmax's VALU work per MFMA (one v_mul_f32, one v_exp_f32, one v_add_f32, half a
+    v_cvt_pk_bf16_f32: what the attention kernel does per score), best of three timings of `reps` calls after three
+    warm-up calls: what the matrix cores sustain on this GPU under its power limit with N(0, 1) operands"""
+    import torch
+    st = torch.cuda.current_stream()
+    res = {}
+    for mode, name in ((0, '32x32x16'), (1, '16x16x32'), (2, 'softmax_valu')):
+        call, fl = mfma_ceiling_call(mode)
+        for _ in range(3):
+            call()
+        torch.cuda.synchronize()
+        ms = min(time_events(call, reps, st) for _ in range(3))
+        res[name] = (ms, fl / ms / 1e9)
+    ms, tf = res['32x32x16']
+    return dict(what='register-only loop of v_mfma_f32_32x32x16_bf16 (the attention kernel\'s MFMA) on N(0,1) bf16 '
+                     'operands, one wavefront per SIMD on every CU, no memory traffic, same run',
+                ms=round(ms, 4), tflops=round(tf, 1), frac_bf16_peak=round(tf / PEAK_BF16_TFLOPS, 4),
+                tflops_16x16x32=round(res['16x16x32'][1], 1),
+                tflops_with_softmax_valu=round(res['softmax_valu'][1], 1))
 
 
 def copy_reference(nbytes, reps, stream, flush):
@@ -356,8 +403,9 @@ def run_bounded_memory(args):
 
 def run_power(args):
     """board power and clocks while the headline layer's attention kernel runs back to back (about 8 s), then while
-    the bf16 GEMM reference does, then the attention kernel again on operands with two mantissa bits, sampled with
-    amd-smi every ~0.25 s: whether each sits at the board's power limit and at what clock. One JSON line: per phase the median socket power, the mean over samples of the XCDs' mean
+    the bf16 GEMM reference does, then the attention kernel again on operands with two mantissa bits, then the
+    register-only MFMA loop alone and beside an exact softmax's VALU work (or_mfma_ceiling modes 0 and 2), sampled
+    with amd-smi every ~0.25 s: whether each sits at the board's power limit and at what clock. One JSON line: per phase the median socket power, the mean over samples of the XCDs' mean
     clock, and the kernel's ms per call and TFLOP/s over the phase."""
     import statistics
     import subprocess
@@ -421,8 +469,11 @@ def run_power(args):
                unit='W', n_gpus=1, data='synthetic',
                config=dict(workload='hunyuan15-480p-4scene-attention-kernel-vs-gemm16384', sampler='amd-smi metric '
                            '-p -c, every ~0.25 s'))
+    ceil, ceil_fl = mfma_ceiling_call(0)
+    ceil2, ceil2_fl = mfma_ceiling_call(2)
     for name, fn, fl in (('attention', attn, flops), ('gemm_reference', gemm, 2.0 * n_g ** 3),
-                         ('attention_two_mantissa_bits', attn2, flops)):
+                         ('attention_two_mantissa_bits', attn2, flops), ('mfma_ceiling', ceil, ceil_fl),
+                         ('mfma_ceiling_with_softmax_valu', ceil2, ceil2_fl)):
         fn()
         torch.cuda.synchronize()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -747,6 +798,9 @@ def main():
         out['copy_reference'] = copy_ref
     if headline and not args.no_gemm_ref:
         out['gemm_reference'] = gemm_reference()
+        mc = out['mfma_ceiling'] = mfma_ceiling()
+        mc['attention_frac'] = round(kernels['attention']['tflops'] / mc['tflops'], 4)
+        mc['attention_frac_of_softmax_valu'] = round(kernels['attention']['tflops'] / mc['tflops_with_softmax_valu'], 4)
     if headline and not args.no_cpu:
         out['cpu_baseline'] = cpu_baseline()
     print(json.dumps(out), flush=True)

@@ -15,6 +15,8 @@ import torch  # noqa: F401  (loads the HIP runtime the library binds to)
 LIB_PATH = Path(os.environ.get('ONEREEL_HIP_LIB', Path(__file__).resolve().parent / 'libonereel_hip.so'))
 # the DiT harness's elementwise kernels (include/onereel_dit.h), not on the scene-attention path
 DIT_LIB_PATH = Path(__file__).resolve().parent / 'libonereel_dit.so'
+# bench.py's measurement kernels (include/onereel_bench.h), not on the scene-attention path
+BENCH_LIB_PATH = Path(__file__).resolve().parent / 'libonereel_bench.so'
 
 OR_MAX_SCENES = 64
 OR_MAX_EXTRA = 512
@@ -97,8 +99,14 @@ DIT_SIGNATURES = {
                                              vp]),
 }
 
+# libonereel_bench.so: include/onereel_bench.h
+BENCH_SIGNATURES = {
+    'or_mfma_ceiling': (i32, [vp, i64, vp, i32, i32, i32, vp]),
+}
+
 _lib = None
 _dit_lib = None
+_bench_lib = None
 
 
 class HipPathError(RuntimeError):
@@ -146,6 +154,23 @@ def dit_lib():
     return _dit_lib
 
 
+def bench_lib():
+    """the measurement library (it loads libonereel_hip.so beside it and reports errors through its or_last_error,
+    which bench_check reads through this handle)"""
+    global _bench_lib
+    if _bench_lib is None:
+        lib()
+        if not BENCH_LIB_PATH.exists():
+            raise RuntimeError(f'{BENCH_LIB_PATH} is not built: run python -m onereel_amd.build')
+        h = ctypes.CDLL(str(BENCH_LIB_PATH))
+        for name, (res, args) in BENCH_SIGNATURES.items():
+            f = getattr(h, name)
+            f.restype, f.argtypes = res, args
+        h.or_last_error.restype, h.or_last_error.argtypes = ctypes.c_char_p, []
+        _bench_lib = h
+    return _bench_lib
+
+
 def check(rc: int, what: str):
     if rc != 0:
         msg = lib().or_last_error().decode()
@@ -155,6 +180,12 @@ def check(rc: int, what: str):
 def dit_check(rc: int, what: str):
     if rc != 0:
         msg = dit_lib().or_last_error().decode()
+        raise HipPathError(f'{what} failed ({rc}): {msg}')
+
+
+def bench_check(rc: int, what: str):
+    if rc != 0:
+        msg = bench_lib().or_last_error().decode()
         raise HipPathError(f'{what} failed ({rc}): {msg}')
 
 

@@ -1,5 +1,6 @@
-"""Build libonereel_hip.so (gfx950) in-tree with hipcc: one object per HIP source, then one shared library; and
-libonereel_dit.so, the DiT harness's elementwise kernels, linked against it.
+"""Build libonereel_hip.so (gfx950) in-tree with hipcc: one object per HIP source, then one shared library; and,
+linked against it, libonereel_dit.so (the DiT harness's elementwise kernels) and libonereel_bench.so (bench.py's
+measurement kernels).
 
     python -m onereel_amd.build            # or __graft_entry__.build()
 """
@@ -16,9 +17,11 @@ CSRC = PKG / 'csrc'
 INCLUDE = PKG.parent / 'include'
 LIB = PKG / 'libonereel_hip.so'
 DIT_LIB = PKG / 'libonereel_dit.so'
+BENCH_LIB = PKG / 'libonereel_bench.so'
 OBJ = PKG / 'csrc' / '_obj'
 SOURCES = ['layout.hip', 'gather.hip', 'attention.hip', 'merge.hip', 'norm_rope.hip', 'frame_memory.hip', 'memory.hip']
 DIT_SOURCES = ['dit_fused.hip']
+BENCH_SOURCES = ['mfma_ceiling.hip']
 # attention: no NaN operands reach the softmax max, so fmax needs no quieting of its inputs (v_max3_f32 directly)
 SOURCE_FLAGS = {'attention.hip': ['-fno-honor-nans']}
 ARCH = os.environ.get('ONEREEL_ARCH', 'gfx950')
@@ -47,21 +50,25 @@ def build(verbose: bool = False) -> Path:
     _run([sys.executable, str(CSRC / 'gen_attn_ring64.py'), '--out', str(CSRC / 'attn_ring64.inc')])
     objs = [OBJ / (s.replace('.hip', '.o')) for s in SOURCES]
     dit_objs = [OBJ / (s.replace('.hip', '.o')) for s in DIT_SOURCES]
+    bench_objs = [OBJ / (s.replace('.hip', '.o')) for s in BENCH_SOURCES]
 
     def one(src_obj):
         src, obj = src_obj
         return _run([HIPCC, *FLAGS, *SOURCE_FLAGS.get(src, []), '-c', str(CSRC / src), '-o', str(obj)])
 
-    with ThreadPoolExecutor(max_workers=len(SOURCES) + len(DIT_SOURCES)) as ex:
-        logs = list(ex.map(one, zip(SOURCES + DIT_SOURCES, objs + dit_objs)))
+    srcs = SOURCES + DIT_SOURCES + BENCH_SOURCES
+    with ThreadPoolExecutor(max_workers=len(srcs)) as ex:
+        logs = list(ex.map(one, zip(srcs, objs + dit_objs + bench_objs)))
     tmp = LIB.with_suffix('.so.tmp')
     logs.append(_run([HIPCC, f'--offload-arch={ARCH}', '-shared', '-fPIC', *map(str, objs), '-o', str(tmp)]))
     os.replace(tmp, LIB)
-    # the harness library resolves the error helpers from libonereel_hip.so, found beside it at run time
-    tmp = DIT_LIB.with_suffix('.so.tmp')
-    logs.append(_run([HIPCC, f'--offload-arch={ARCH}', '-shared', '-fPIC', *map(str, dit_objs), '-L', str(PKG),
-                      '-l:libonereel_hip.so', "-Wl,-rpath,$ORIGIN", '-o', str(tmp)]))
-    os.replace(tmp, DIT_LIB)
+    # the harness and measurement libraries resolve the error helpers from libonereel_hip.so, found beside them at
+    # run time
+    for out, lib_objs in ((DIT_LIB, dit_objs), (BENCH_LIB, bench_objs)):
+        tmp = out.with_suffix('.so.tmp')
+        logs.append(_run([HIPCC, f'--offload-arch={ARCH}', '-shared', '-fPIC', *map(str, lib_objs), '-L', str(PKG),
+                          '-l:libonereel_hip.so', "-Wl,-rpath,$ORIGIN", '-o', str(tmp)]))
+        os.replace(tmp, out)
     if verbose:
         for l in logs:
             if l.strip():

@@ -101,6 +101,12 @@ def test_library_exports_every_declared_symbol():
     for s in dit:
         assert not hasattr(h, s), s
         assert hasattr(L.dit_lib(), s), s
+    # so do bench.py's measurement kernels
+    bench = _header_symbols('onereel_bench.h')
+    assert bench and set(bench) == set(L.BENCH_SIGNATURES) and not set(bench) & (set(syms) | set(dit))
+    for s in bench:
+        assert not hasattr(h, s), s
+        assert hasattr(L.bench_lib(), s), s
 
 
 def _random_layout(rng):
@@ -285,6 +291,22 @@ def test_fused_residual_layernorm_argument_errors_without_gpu():
     for kw, msg in ((dict(C=100), 'multiple of 8'), (dict(C=9000), 'multiple of 8'), (dict(a=None), 'a must be'),
                     (dict(a=a + 8), 'a must be'), (dict(a_stride=256), 'a must be'), (dict(out=x), 'must not be'),
                     (dict(out=a), 'must not be'), (dict(x=x + 4), '16-byte aligned')):
+        with pytest.raises(L.HipPathError, match=msg):
+            call(**kw)
+
+
+def test_mfma_ceiling_argument_errors_without_gpu():
+    """or_mfma_ceiling (libonereel_bench.so) refuses missing or misaligned buffers, a bad operand count, grid,
+    iteration count or mode before it launches anything"""
+    f = L.bench_lib().or_mfma_ceiling
+    ops, out = 0x10000, 0x20000
+
+    def call(ops=ops, n=64, out=out, blocks=256, iters=800, mode=0):
+        return L.bench_check(f(ops, n, out, blocks, iters, mode, None), 'or_mfma_ceiling')
+    for kw, msg in ((dict(ops=None), 'required'), (dict(out=None), 'required'), (dict(n=0), 'n_vec'),
+                    (dict(ops=ops + 8), 'aligned'), (dict(out=out + 2), 'aligned'), (dict(blocks=0), 'blocks'),
+                    (dict(blocks=70000), 'blocks'), (dict(iters=12), 'multiple of 8'), (dict(iters=0), 'multiple of 8'),
+                    (dict(mode=3), 'mode')):
         with pytest.raises(L.HipPathError, match=msg):
             call(**kw)
 
