@@ -489,3 +489,29 @@ def test_abi_structs_match_the_header(tmp_path):
         assert int(got[f'{cname} sizeof']) == ctypes.sizeof(cls), cname
         for f in cls._fields_:
             assert int(got[f'{cname} {f[0]}']) == getattr(cls, f[0]).offset, (cname, f[0])
+
+
+def test_drop_in_varlen_rejects_bad_offsets_and_ranges_without_gpu():
+    """attention.varlen / varlen_lse / overlapping_ranges check caller offsets and key ranges on the host before any
+    launch: the kernels index q / k / v rows by them without bounds checks"""
+    import torch
+    from onereel_amd import attention as A
+    q = torch.zeros(10, 2, 64, dtype=torch.bfloat16)
+    k = torch.zeros(12, 2, 64, dtype=torch.bfloat16)
+    cu = lambda *x: torch.tensor(x, dtype=torch.int32)
+    A.check_cu_seqlens(cu(0, 4, 10), 10, 6, 'cu_q')          # good offsets pass
+    for c, n, mx, msg in ((cu(1, 4, 10), 10, 9, 'start at 0'), (cu(0, 5, 3), 10, 9, 'not decrease'),
+                          (cu(0, 4, 11), 10, 9, 'at most at 10'), (cu(0, 4, 10), 10, 5, 'exceeds'),
+                          (cu(0), 10, 9, 'at least 2')):
+        with pytest.raises(L.HipValueError, match=msg):
+            A.check_cu_seqlens(c, n, mx, 'cu_q')
+    with pytest.raises(L.HipValueError, match='cu_k'):
+        A.varlen(q, k, k, cu(0, 4, 10), cu(0, 6, 13), 6, 7)
+    with pytest.raises(L.HipValueError, match='one offset per segment'):
+        A.varlen_lse(q, k, k, cu(0, 4, 10), cu(0, 12), 6, 12)
+    with pytest.raises(L.HipValueError, match='inside the 12 rows'):
+        A.overlapping_ranges(q, k, k, [(0, 4), (4, 10)], [(0, 6), (6, 13)])
+    with pytest.raises(L.HipValueError, match='inside the 12 rows'):
+        A.overlapping_ranges(q, k, k, [(0, 4), (4, 10)], [(5, 3), (0, 2)])
+    with pytest.raises(L.HipValueError, match='pair up'):
+        A.overlapping_ranges(q, k, k, [(0, 4), (4, 10)], [(0, 6)])
