@@ -15,9 +15,10 @@ roofline: the attention kernel alone, timed with HIP events on the stream it run
 cpu_baseline: the oracle's packing plus torch SDPA per scope in fp32 on the host cores, on a sample of heads.
 gemm_reference: torch.matmul (hipBLASLt) of two bf16 16384 x 16384 N(0, 1) matrices in the same run: what the
 vendor's dense bf16 GEMM reaches on this GPU with data of the same distribution. MI355X throttles its clock under
-MFMA load (power limit), and MFMA power depends on the operand bits, so this is the practical MFMA ceiling here.
+MFMA load (power and current management), and MFMA power depends on the operand bits, so this is the practical MFMA
+ceiling here.
 mfma_ceiling: a loop of nothing but bf16 MFMAs on N(0, 1) operands held in registers (libonereel_bench.so), one
-wavefront per SIMD on every CU, in the same run: what the matrix cores sustain under the power limit with no memory
+wavefront per SIMD on every CU, in the same run: what the matrix cores sustain at the throttled clock with no memory
 traffic, LDS or softmax at all; and the same loop with an exact softmax's VALU work per MFMA beside it (the
 exponential, its scale, the row sum, the bf16 conversion); attention_frac and attention_frac_of_softmax_valu are the
 attention kernel's rate over each.
@@ -175,7 +176,7 @@ def mfma_ceiling(reps=10):
     """TFLOP/s of the register-only MFMA loop (libonereel_bench.so) in both bf16 MFMA shapes, and in the attention
     kernel's shape beside an exact softmax's VALU work per MFMA (one v_mul_f32, one v_exp_f32, one v_add_f32, half a
     v_cvt_pk_bf16_f32: what the attention kernel does per score), best of three timings of `reps` calls after three
-    warm-up calls: what the matrix cores sustain on this GPU under its power limit with N(0, 1) operands"""
+    warm-up calls: what the matrix cores sustain on this GPU at its throttled clock with N(0, 1) operands"""
     import torch
     st = torch.cuda.current_stream()
     res = {}
@@ -405,7 +406,7 @@ def run_power(args):
     """board power and clocks while the headline layer's attention kernel runs back to back (about 8 s), then while
     the bf16 GEMM reference does, then the attention kernel again on operands with two mantissa bits, then the
     register-only MFMA loop alone and beside an exact softmax's VALU work (or_mfma_ceiling modes 0 and 2), sampled
-    with amd-smi every ~0.25 s: whether each sits at the board's power limit and at what clock. One JSON line: per phase the median socket power, the mean over samples of the XCDs' mean
+    with amd-smi every ~0.25 s: at what power and clock each runs. One JSON line: per phase the median socket power, the mean over samples of the XCDs' mean
     clock, and the kernel's ms per call and TFLOP/s over the phase."""
     import statistics
     import subprocess

@@ -16,7 +16,7 @@
 extern "C" {
 #endif
 
-/* The matrix cores' own ceiling under the board's power limit, alone and beside an exact softmax's VALU work:
+/* The matrix cores' own ceiling at the board's throttled clock, alone and beside an exact softmax's VALU work:
  * `blocks` work-groups of four wavefronts (one wavefront per SIMD when blocks is the CU count) each load 8 A and 8 B
  * operand registers of 8 bf16 from `operands` (n_vec vectors of 8 bf16, read at lane-dependent indices modulo n_vec)
  * and then run `iters` iterations of 8 dense bf16 MFMAs with no memory access and no LDS, cycling through the
