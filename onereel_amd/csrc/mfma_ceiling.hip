@@ -3,10 +3,10 @@
 // board's power and current management lowers the clock under MFMA load, and MFMA power depends on the operand bits,
 // so with N(0, 1) operands this rate, not the nominal 2.4 GHz peak, bounds every bf16 kernel; the attention kernel is
 // read against it. The operands stay in registers and rotate so that consecutive MFMAs read different registers, as a
-// kernel's K / Q and V / P operands do. Mode 2 adds, per MFMA, the VALU work an exact softmax does per score in a kernel that
-// computes 64 queries x 32 keys per 32 MFMAs of this shape: p = 2^(c s) (one v_mul_f32 and one v_exp_f32), the row
-// sum l += p (one v_add_f32) and every second MFMA one v_cvt_pk_bf16_f32 of two p; on independent registers, so
-// that the MFMA issue never waits on them.
+// kernel's K / Q and V / P operands do. Mode 2 adds, per MFMA, the VALU work an exact softmax does per score in a
+// kernel that computes 64 queries x 32 keys per 32 MFMAs of this shape: p = 2^(c s) (one v_mul_f32 and one
+// v_exp_f32), the row sum l += p (one v_add_f32) and every second MFMA one v_cvt_pk_bf16_f32 of two p; on independent
+// registers, so that the MFMA issue never waits on them.
 #include "../../include/onereel_bench.h"
 #include "common.h"
 
