@@ -107,7 +107,8 @@ extern "C" int or_mfma_ceiling(const void* operands, int64_t n_vec, float* out, 
   if (((uintptr_t)operands & 15) || ((uintptr_t)out & 3))
     return fail_arg("or_mfma_ceiling: operands must be 16-byte aligned and out 4-byte aligned");
   if (blocks < 1 || blocks > 65536) return fail_arg("or_mfma_ceiling: blocks must be in [1, 65536] (got %d)", blocks);
-  if (iters < 8 || iters % 8) return fail_arg("or_mfma_ceiling: iters must be a positive multiple of 8 (got %d)", iters);
+  if (iters < 8 || iters % 8)
+    return fail_arg("or_mfma_ceiling: iters must be a positive multiple of 8 (got %d)", iters);
   if (mode < 0 || mode > 2)
     return fail_arg("or_mfma_ceiling: mode must be 0 (32x32x16), 1 (16x16x32) or 2 (32x32x16 with softmax VALU work)");
   const bf16x8* in = (const bf16x8*)operands;
