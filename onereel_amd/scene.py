@@ -153,6 +153,17 @@ def _rows2d(x: torch.Tensor, H: int, D: int):
     return x, x.stride(0)
 
 
+def _with_row_stride(x: torch.Tensor, stride: int) -> torch.Tensor:
+    """x [rows, H, D] itself when its rows are `stride` elements apart, else a copy of its rows laid out that way (the
+    attention call reads video and text query rows with one row stride)"""
+    if x.stride(0) == stride:
+        return x
+    rows, H, D = x.shape
+    buf = torch.empty(rows, stride, dtype=x.dtype, device=x.device)[:, :H * D].view(rows, H, D)
+    buf.copy_(x)
+    return buf
+
+
 def _check_bf16(*xs):
     for x in xs:
         if x is not None and (x.dtype != torch.bfloat16 or not x.is_cuda):
@@ -504,8 +515,12 @@ def scene_attention(plan: ScopePlan, q, k, v, eq, ek, ev, cos=None, sin=None, mo
         kp, vp, qr = pack_layer(plan, k, ek, v, ev, cos, sin, mode, kbuf, vbuf, q=q if pre else None, qbuf=qbuf,
                                 values_in_place=in_place)
         vi = dict(v_tok=v, v_lead=plan.v_lead, v_row=plan.v_row, v_runs=plan.v_runs) if in_place else {}
-        varlen(qr if pre else q, kp, vp, plan.cu_q, plan.cu_k, plan.max_q, plan.max_k, k_off=plan.k_off,
-               k_len=plan.k_len, out=ov, seg_q_src=plan.seg_q_src, q_text=eq, o_text=ot, n_q_video=plan.n_video,
+        qq = qr if pre else q
+        # the text queries in the video queries' row stride (a copy of the Le text rows when q and eq are views with
+        # different strides, e.g. a head range of wider rows whose video queries were rotated into a new buffer)
+        et = _with_row_stride(eq, qq.stride(0)) if eq is not None and eq.shape[0] else eq
+        varlen(qq, kp, vp, plan.cu_q, plan.cu_k, plan.max_q, plan.max_k, k_off=plan.k_off,
+               k_len=plan.k_len, out=ov, seg_q_src=plan.seg_q_src, q_text=et, o_text=ot, n_q_video=plan.n_video,
                q_rope=plan.q_rope if on_load else None, cos=cos, sin=sin, sum_q=plan.sum_q,
                workspace=plan.workspace(H, D), **vi)
         if ot is not None:

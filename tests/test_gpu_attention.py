@@ -334,6 +334,41 @@ def test_scene_layer_repeatable_at_480p(rotate_q):
         assert torch.equal(ov2, ov) and torch.equal(ot2, ot)
 
 
+@pytest.mark.parametrize('rotate_q', ['pre', 'load'])
+def test_scene_layer_head_chunks_at_480p(rotate_q):
+    """heads are independent (the reference checks its path bit-exact across head chunkings 1/2/3/4/16,
+    tests/dist_onereel_kv_chunks.py:29-37): the 480p layer run on chunks of the heads, through views of the same
+    q / k / v / text rows (row stride 16 heads), gives the full layer's rows for those heads. Bit for bit while the
+    chunk's call has at least 4 rounds of work items on the GPU (16 and 8 heads: 12.75 and 6.4 rounds), where items are
+    cut exactly as in the full call; the chunks of 4, 3, 2 and 1 heads have fewer rounds, so the planner splits their
+    last items by keys and merges the parts in fp32, which rounds differently: within a bf16 step of the full layer.
+    The views' rows are wider than their heads: with rotate_q='pre' the rotated video queries land in a new buffer of
+    narrower rows, and the layer lays the text queries out likewise"""
+    case = layout_case('hunyuan480p')
+    g = [x.to(DEV) for x in _layer_inputs(case, 5)]
+    lay = SceneLayout(case['lengths'], halo=case['halo'], sides=case['sides'], extra=case['extra'])
+    plan = scene.ScopePlan(lay, case['T'], case['counts'], case['Le'], case['scene_rope'], None, True, True, DEV,
+                           text_keys_in_place=True)
+    print(f'layer hunyuan480p, all 16 heads, rotate_q={rotate_q}', flush=True)
+    ov, ot = scene.scene_attention(plan, *g[:6], g[6], g[7], mode='raw', fused=True, rotate_q=rotate_q)
+    H = case['H']
+    for size in (8, 4, 3, 2, 1):
+        lo = 0
+        while lo < H:
+            hi = min(lo + size, H)
+            print(f'layer hunyuan480p, heads [{lo}, {hi})', flush=True)
+            cv, ct = scene.scene_attention(plan, *(x[:, lo:hi] for x in g[:6]), g[6], g[7], mode='raw', fused=True,
+                                           rotate_q=rotate_q)
+            if size == 8:
+                assert torch.equal(cv, ov[:, lo:hi]) and torch.equal(ct, ot[:, lo:hi]), (lo, hi)
+            else:
+                for got, want in ((cv, ov[:, lo:hi]), (ct, ot[:, lo:hi])):
+                    d = (got.float() - want.float()).abs()
+                    assert d.max().item() <= 2 ** -7 * max(1.0, want.float().abs().max().item()), (lo, hi)
+                    assert d.mean().item() <= 1e-4, (lo, hi)
+            lo = hi
+
+
 @pytest.mark.parametrize('name,P,per_seg', [('cpu_plumbing', 3, None), ('hunyuan480p', 3, 32),
                                             ('uneven_K4', 5, 24)])
 def test_scene_layer_rank_shares(name, P, per_seg):
